@@ -1,0 +1,290 @@
+/*
+ * microinfer_hip.h — the C ABI of the MI355X-native paged mixed-precision
+ * KV-cache library (libmicroinfer_hip.so).
+ *
+ * This is the drop-in boundary for the reference's one native module,
+ * `_microinfer` and its submodule `_microinfer.device`
+ * (lecuong1502/Semantic-Aware_Adaptive_KV_Cache_Precision:
+ * src/core_kernels/bindings.cpp:427-669, bindings_device.cpp:251-993).
+ * Every entry point is `extern "C"` with plain pointers and sizes; the
+ * Python shim `microinfer._microinfer` re-presents the reference's surface on
+ * top of it through ctypes. Each declaration cites the reference interface it
+ * replaces.
+ *
+ * Conventions.
+ *   - Every function returns an mi_status; 0 is success. On failure
+ *     mi_last_error() gives the message of the calling thread's last failure.
+ *     The status picks the exception class the shim raises, as the
+ *     reference's bindings map C++ exceptions (bindings.cpp:546-554).
+ *   - "device" pointers are device-visible addresses (hipMalloc'd memory, or
+ *     pinned host memory mapped for the device); "host" pointers are host
+ *     memory. fp16 data is passed as raw 16-bit storage.
+ *   - `stream` is a hipStream_t (0 = the null stream, which every object of
+ *     the runtime uses). Launchers enqueue and return without synchronising;
+ *     execution errors surface at the next synchronising call
+ *     (reference: device_ops.h:20-28).
+ *   - Tiers: 0 FP16, 1 INT8, 2 INT4, 3 INT2 (reference: paged_kv_cache.h:16-25).
+ *     A page-table tier of 0xFF is a page no query reads (device_ops.h:91-96).
+ */
+#ifndef MICROINFER_HIP_H
+#define MICROINFER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mi_status {
+  MI_OK = 0,
+  MI_ERR_INVALID = 1,       /* std::invalid_argument -> ValueError            */
+  MI_ERR_RANGE = 2,         /* std::out_of_range -> IndexError                */
+  MI_ERR_NOT_FOUND = 3,     /* PageNotFound -> KeyError subclass              */
+  MI_ERR_OPEN_PAGE = 4,     /* OpenPage -> ValueError subclass                */
+  MI_ERR_OUT_OF_MEMORY = 5, /* OutOfMemory -> MemoryError subclass            */
+  MI_ERR_LOGIC = 6,         /* std::logic_error -> RuntimeError               */
+  MI_ERR_FULL = 7,          /* std::length_error "... is full" -> ValueError  */
+  MI_ERR_DEVICE = 8         /* a HIP runtime error -> RuntimeError            */
+} mi_status;
+
+typedef struct mi_cache mi_cache;           /* PagedKVCache   */
+typedef struct mi_kv_pages mi_kv_pages;     /* device.KVPages */
+typedef struct mi_scores mi_scores;         /* device.ImportanceScores */
+typedef struct mi_shadows mi_shadows;       /* device.ShadowStore */
+typedef struct mi_rope_table mi_rope_table; /* device.RopeTable */
+
+/* The calling thread's last error message ("" if none). */
+const char *mi_last_error(void);
+/* The library's build string: arch and flags. */
+const char *mi_build_info(void);
+
+/* ---- device and memory --------------------------------------------------
+ * reference: device.cu:14-34 (device_name, device_memory_info),
+ * device_tensor.cu:14-152 (DeviceTensor/DeviceFloats RAII storage),
+ * paged_kv_cache.cu:46-60 (allocation_granularity). */
+int mi_device_count(int *count);
+int mi_device_name(char *out, size_t capacity);
+int mi_runtime_version(int *version);
+int mi_memory_info(size_t *free_bytes, size_t *total_bytes);
+int mi_granule_bytes(size_t *out);
+int mi_malloc(void **out, size_t bytes);
+int mi_free(void *ptr);
+/* kind: 0 host-to-device, 1 device-to-host, 2 device-to-device. Synchronous. */
+int mi_memcpy(void *dst, const void *src, size_t bytes, int kind);
+int mi_memset(void *dst, int value, size_t bytes);
+int mi_synchronize(void);
+/* Timing on the stream a kernel runs on (hipEvent). */
+int mi_event_create(void **event);
+int mi_event_destroy(void *event);
+int mi_event_record(void *event, void *stream);
+int mi_event_elapsed_ms(void *start, void *end, float *ms);
+/* Streams and graphs. A created stream has the default priority and orders
+ * with the null stream. mi_set_stream picks the stream the runtime objects
+ * (KVPages, PagedKVCache, ImportanceScores, RopeTable) launch on from the
+ * calling thread; NULL is the null stream. A graph captures the launches made
+ * on a stream between begin and end (hipStreamBeginCapture, thread-local
+ * mode), to replay a launch-bound sequence, such as a decode step's attention
+ * over every layer, with one launch. No counterpart in the reference, which
+ * launches everything on the legacy default stream (device_ops.h:20-28). */
+int mi_stream_create(void **stream);
+int mi_stream_destroy(void *stream);
+int mi_stream_synchronize(void *stream);
+int mi_set_stream(void *stream);
+int mi_graph_begin(void *stream);
+int mi_graph_end(void *stream, void **exec);
+int mi_graph_launch(void *exec, void *stream);
+int mi_graph_destroy(void *exec);
+/* Host conversions of the library's own rounding, for tests:
+ * fp64 -> nearest fp16 bits in one rounding, and a group's stored scale
+ * (reference: quant.cu:44-56 scale_of). Need no device. */
+uint16_t mi_half_bits_from_double(double x);
+uint16_t mi_scale_bits_of(float lo, float hi, int bits);
+
+/* ---- quantised pages ----------------------------------------------------
+ * reference: quant.h:45-59 QuantisedPageLayout, quant.cu:358-392. */
+typedef struct mi_page_layout {
+  int bits;
+  size_t key_codes, value_codes, key_scales, key_zeros, value_scales, value_zeros;
+  size_t metadata_bytes, page_bytes;
+  double effective_bits;
+} mi_page_layout;
+int mi_quantised_page_layout(int tier, int page_tokens, int kv_heads, int head_dim,
+                             mi_page_layout *out);
+/* An FP16 page's bytes (reference: kv_pages.cu:62-66 page_bytes_for). */
+size_t mi_fp16_page_bytes(int page_tokens, size_t kv_width);
+/* One page (reference: quant.cu:403-417 device::quantise_page): keys and
+ * values (page_tokens, kv_heads, head_dim) fp16 on the device, `filled`
+ * positions of them; fewer than page_tokens is MI_ERR_OPEN_PAGE. */
+int mi_quantise_page(const void *keys, const void *values, void *page, int tier,
+                     int page_tokens, int filled, int kv_heads, int head_dim, void *stream);
+/* A batch (reference: quant.cu:419-436 device::quantise_pages): page i from
+ * rows[i] (an FP16 page, keys then values) into pages[i]; both tables in
+ * device-visible memory; a row may be mapped pinned host memory. */
+int mi_quantise_pages(const void *const *rows, void *const *pages, int count, int tier,
+                      int page_tokens, int kv_heads, int head_dim, void *stream);
+/* reference: quant.cu:438-450 device::dequantise_page. */
+int mi_dequantise_page(const void *page, void *keys, void *values, int tier, int page_tokens,
+                       int kv_heads, int head_dim, void *stream);
+
+/* ---- attention ----------------------------------------------------------
+ * reference: device_ops.h:61-147; attention.cu:1047-1142. Layout of q and
+ * out (seq_q, heads, head_dim) fp16; k_bias (kv_heads, head_dim) fp16 or
+ * NULL; rope a RopeTable's fp32 {cos, sin} (positions, head_dim/2, 2), read
+ * only with k_bias. `partials` (mi_attention_partials_floats floats) lets a
+ * long launch split its keys; NULL splits nothing. */
+size_t mi_attention_partials_floats(int head_dim);
+int mi_attention_split(int seq_q, int seq_k, int heads, int kv_heads, int page_tokens,
+                       int *splits, int *split_keys);
+/* Contiguous k, v (seq_k, kv_heads, head_dim) (reference: device::attention). */
+int mi_attention(const void *q, const void *k, const void *v, const void *k_bias,
+                 const float *rope, int rope_positions, void *out, int seq_q, int seq_k, int heads,
+                 int kv_heads, int head_dim, float *partials, void *stream);
+/* Through an FP16 page table of `pages` addresses (reference:
+ * device::attention_paged). `mass` (heads, pages) fp32 or NULL. */
+int mi_attention_paged(const void *q, const unsigned long long *pages, int page_tokens,
+                       const void *k_bias, const float *rope, int rope_positions, void *out,
+                       int seq_q, int seq_k, int heads, int kv_heads, int head_dim, float *mass,
+                       float *partials, void *stream);
+/* A cache that seals, read causally (reference: device::attention_paged_causal,
+ * attention.cu:1091-1142): `sealed` and `tiers` the layer's table;
+ * may_be_at_mask bit t set if a page may be at tier t; `open` the FP16 page
+ * holding the own page's rows before seq_k - seq_q; chunk_k/chunk_v the
+ * seq_q rows the queries brought. `scores`, if given, is the layer's row of
+ * importance scores, into which the step's mass is folded with `alpha`
+ * (reference: importance_scores.cu:74-98) in the same pass. */
+int mi_attention_paged_causal(const void *q, const unsigned long long *sealed,
+                              const uint8_t *tiers, int may_be_at_mask, const void *open,
+                              const void *chunk_k, const void *chunk_v, int page_tokens,
+                              const void *k_bias, const float *rope, int rope_positions, void *out,
+                              int seq_q, int seq_k, int heads, int kv_heads, int head_dim,
+                              float *mass, float *scores, float alpha, float *partials,
+                              void *stream);
+
+/* ---- pages, rows and scores ----------------------------------------------
+ * reference: page_copy.cu:41-70, kv_pages.cu:47-60, importance_scores.cu:18-50. */
+int mi_copy_pages(const void *const *from, void *const *to, size_t bytes, int count, void *stream);
+int mi_store_pages(const void *keys, const void *values, const unsigned long long *pages,
+                   int page_tokens, size_t row, int start, int n, void *stream);
+int mi_fill_f32(float *out, size_t count, float value, void *stream);
+int mi_fold_scores(float *scores, const float *mass, int heads, int pages, float alpha,
+                   void *stream);
+
+/* ---- RoPE, RMSNorm, SwiGLU ------------------------------------------------
+ * reference: rope.cu:57-68, rope_table.cu:18-68, rmsnorm.cu:87-109,
+ * swiglu.cu:41-52, residual.cu (add). */
+int mi_rope(const void *x, const int32_t *positions, void *out, int seq, int heads, int head_dim,
+            double theta, void *stream);
+int mi_rope_table_fill(float *table, int positions, int head_dim, double theta, void *stream);
+int mi_rmsnorm(const void *x, int x_is_f32, const void *weight, void *out, int rows, int hidden,
+               float eps, void *stream);
+int mi_swiglu(const void *gate, const void *up, void *out, size_t count, void *stream);
+int mi_add(const void *a, const void *b, void *out, size_t count, void *stream);
+
+/* ---- PagedKVCache: the per-tier VMM allocator ------------------------------
+ * reference: paged_kv_cache.h:112-227, bindings.cpp:579-668. Keys are
+ * (layer, page_index) int pairs. */
+int mi_cache_create(const size_t page_bytes[4], const size_t capacity_pages[4], mi_cache **out);
+void mi_cache_destroy(mi_cache *cache);
+int mi_cache_allocate(mi_cache *cache, int layer, int page, int tier);
+int mi_cache_free(mi_cache *cache, int layer, int page);
+/* keys: n (layer, page) pairs, 2n ints. */
+int mi_cache_free_pages(mi_cache *cache, const int *keys, size_t n);
+int mi_cache_replace(mi_cache *cache, int layer, int page, int staged_layer, int staged_page);
+/* quads: n (layer, page, staged_layer, staged_page), 4n ints. */
+int mi_cache_replace_pages(mi_cache *cache, const int *quads, size_t n);
+int mi_cache_write(mi_cache *cache, int layer, int page, const void *host, size_t bytes);
+int mi_cache_read(mi_cache *cache, int layer, int page, void *host, size_t bytes);
+int mi_cache_locate(mi_cache *cache, int layer, int page, int *tier, size_t *slot);
+int mi_cache_contains(mi_cache *cache, int layer, int page, int *out);
+/* The tier's keys in slot order: up to `capacity` pairs into keys (2 ints
+ * each); *count receives the number held. */
+int mi_cache_pages(mi_cache *cache, int tier, int *keys, size_t capacity, size_t *count);
+int mi_cache_page_bytes(mi_cache *cache, int tier, size_t *out);
+int mi_cache_reserved_bytes(mi_cache *cache, int tier, size_t *out);
+int mi_cache_mapped_bytes(mi_cache *cache, int tier, size_t *out);
+int mi_cache_keep_spare_granules(mi_cache *cache, int tier, size_t granules);
+int mi_cache_spare_granules(mi_cache *cache, int tier, size_t *out);
+int mi_cache_granule_bytes(mi_cache *cache, size_t *out);
+/* Test hook (no counterpart in the reference; the reference forces the
+ * same paths by exhausting VRAM): the next n granule maps fail as out of
+ * memory. */
+int mi_debug_fail_next_granules(int n);
+
+/* ---- ShadowStore ------------------------------------------------------------
+ * reference: shadow_store.h:23-85, bindings_device.cpp:652-686. */
+int mi_shadows_create(size_t page_bytes, mi_shadows **out);
+void mi_shadows_destroy(mi_shadows *s);
+int mi_shadows_take(mi_shadows *s, int layer, int page, const void *device_page);
+int mi_shadows_contains(mi_shadows *s, int layer, int page, int *out);
+int mi_shadows_read(mi_shadows *s, int layer, int page, void *host, size_t bytes);
+int mi_shadows_count(mi_shadows *s, size_t *out);
+int mi_shadows_bytes(mi_shadows *s, size_t *out);
+
+/* ---- ImportanceScores --------------------------------------------------------
+ * reference: importance_scores.h:27-66, bindings_device.cpp:601-650. */
+int mi_scores_create(int layers, int max_pages, float alpha, mi_scores **out);
+void mi_scores_destroy(mi_scores *s);
+int mi_scores_fold(mi_scores *s, int layer, const float *mass, int heads, int pages);
+int mi_scores_download(mi_scores *s, float *host, size_t count);
+int mi_scores_upload(mi_scores *s, const float *host, int layers, int max_pages);
+int mi_scores_layer_row(mi_scores *s, int layer, float **row);
+int mi_scores_info(mi_scores *s, int *layers, int *max_pages, float *alpha, size_t *downloads);
+
+/* ---- RopeTable ----------------------------------------------------------------
+ * reference: rope_table.h:25-44, bindings_device.cpp:529-566. */
+int mi_rope_table_create(int head_dim, double theta, mi_rope_table **out);
+void mi_rope_table_destroy(mi_rope_table *t);
+int mi_rope_table_cover(mi_rope_table *t, int positions);
+int mi_rope_table_info(mi_rope_table *t, int *positions, const float **data);
+
+/* ---- KVPages: the cache manager ---------------------------------------------------
+ * reference: kv_pages.h:105-412, bindings_device.cpp:688-978. tier_map: a
+ * flat array of `map_rows` rows, row l holding row_lengths[l] tiers; NULL for
+ * none. halves: 0 Both, 1 Keys, 2 Values. The allocator must outlive it. */
+int mi_kv_create(mi_cache *allocator, int layers, int page_tokens, int kv_heads, int head_dim,
+                 int tier, int halves, const int *tier_map, const int *row_lengths, int map_rows,
+                 int always_seal, mi_kv_pages **out);
+void mi_kv_destroy(mi_kv_pages *kv);
+int mi_kv_seals_for(int tier, const int *tier_map, const int *row_lengths, int map_rows,
+                    int always_seal, int *out);
+int mi_kv_reserve(mi_kv_pages *kv, int tokens);
+/* keys, values: (n, kv_width) fp16 on the device. */
+int mi_kv_store(mi_kv_pages *kv, int layer, const void *keys, const void *values, int start, int n);
+/* reference: KVPages::attention (kv_pages.cu:901-947) with, beyond it,
+ * `scores`/`alpha`: the step's mass folded into the layer's importance
+ * scores in the same launch sequence. */
+int mi_kv_attention(mi_kv_pages *kv, int layer, const void *q, const void *k_bias,
+                    mi_rope_table *rope, void *out, int seq_q, int seq_k, int heads, int kv_heads,
+                    int head_dim, const void *keys, const void *values, float *mass, float *scores,
+                    float alpha, float *partials);
+int mi_kv_downgrade(mi_kv_pages *kv, int layer, int page, int target);
+int mi_kv_upgrade(mi_kv_pages *kv, int layer, int page, int target);
+/* triples: n (layer, page, target tier), 3n ints. */
+int mi_kv_move_pages(mi_kv_pages *kv, const int *triples, size_t n);
+int mi_kv_evict(mi_kv_pages *kv, int layer, int page);
+int mi_kv_mask(mi_kv_pages *kv, int layer, int page);
+int mi_kv_page_tier(mi_kv_pages *kv, int layer, int page, int *tier);
+int mi_kv_has_shadow(mi_kv_pages *kv, int layer, int page, int *out);
+int mi_kv_shadow(mi_kv_pages *kv, int layer, int page, void *host, size_t bytes);
+/* Per-page arrays (layers, pages_per_layer): tiers as page_tiers gives them
+ * (evicted = 4), and shadowed / evicted flags. */
+int mi_kv_page_tiers(mi_kv_pages *kv, int8_t *out, size_t capacity);
+int mi_kv_flags(mi_kv_pages *kv, int which, uint8_t *out, size_t capacity);
+typedef struct mi_kv_info {
+  int layers, page_tokens, kv_heads, head_dim, pages_per_layer, capacity_tokens;
+  int tier, halves, storage_tier, seals, born_at_one_tier;
+  size_t page_bytes, kv_width, shadow_count, shadow_bytes;
+} mi_kv_info;
+int mi_kv_info_get(mi_kv_pages *kv, mi_kv_info *out);
+int mi_kv_birth_tier(mi_kv_pages *kv, int layer, int page, int *tier);
+/* last_move: has, layer, page, from, to; bytes; seconds. */
+int mi_kv_last_move(mi_kv_pages *kv, int *has, int *ints4, size_t *bytes2, double *seconds2);
+int mi_kv_last_batch(mi_kv_pages *kv, int *has, size_t *moves, size_t *shadows_taken,
+                     double *seconds);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MICROINFER_HIP_H */

@@ -1,0 +1,255 @@
+// Shared definitions of the MI355X KV-cache library: tiers, the quantised
+// page layout, error types, and the fp16 helpers the kernels share.
+//
+// Everything here is written for gfx950 (wave64, CDNA4) and the HIP runtime;
+// host and device code both include it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+namespace mi
+{
+
+  // The four precision tiers, highest first (reference: paged_kv_cache.h:16-25).
+  enum Tier : int
+  {
+    kFP16 = 0,
+    kINT8 = 1,
+    kINT4 = 2,
+    kINT2 = 3,
+  };
+  constexpr int kTierCount = 4;
+  // A page-table tier entry no query reads: evicted or masked
+  // (reference: device_ops.h:91-96).
+  constexpr std::uint8_t kUnreadPage = 0xFF;
+
+  inline const char *tier_name(int tier)
+  {
+    switch (tier)
+    {
+    case kFP16: return "FP16";
+    case kINT8: return "INT8";
+    case kINT4: return "INT4";
+    case kINT2: return "INT2";
+    }
+    return "an unknown tier";
+  }
+  // A lower tier has fewer bits a value: a larger number.
+  inline bool is_lower(int a, int b) { return a > b; }
+
+  // ---- errors ---------------------------------------------------------------
+  // Each maps to one status code of the C ABI and one Python exception class
+  // of the shim (reference: bindings.cpp:546-554, check.h:18-57).
+  struct InvalidArgument : std::runtime_error { using std::runtime_error::runtime_error; };
+  struct OutOfRange : std::runtime_error { using std::runtime_error::runtime_error; };
+  struct PageNotFound : std::runtime_error { using std::runtime_error::runtime_error; };
+  struct OpenPageError : std::runtime_error { using std::runtime_error::runtime_error; };
+  struct OutOfMemory : std::runtime_error { using std::runtime_error::runtime_error; };
+  struct LogicError : std::runtime_error { using std::runtime_error::runtime_error; };
+  struct Full : std::runtime_error { using std::runtime_error::runtime_error; };
+  struct DeviceError : std::runtime_error { using std::runtime_error::runtime_error; };
+
+  inline void hip_check(hipError_t e, const char *what)
+  {
+    if (e == hipSuccess)
+    {
+      return;
+    }
+    const std::string msg = std::string(what) + ": " + hipGetErrorString(e);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+    {
+      (void)hipGetLastError(); // an allocation failure is not sticky
+      throw OutOfMemory(msg);
+    }
+    throw DeviceError(msg);
+  }
+
+  // ---- the quantised page layout ----------------------------------------------
+  // Regions back to back, W = kv_heads * head_dim (reference: quant.h:28-44):
+  // key codes (P rows of W codes), value codes (the same), key scales (W fp16),
+  // key zeros (W), value scales (P * kv_heads), value zeros (P * kv_heads).
+  // Below 8 bits, 8/bits consecutive codes share a byte, the first lowest.
+  struct PageLayout
+  {
+    int bits;
+    std::size_t key_codes;
+    std::size_t value_codes;
+    std::size_t key_scales;
+    std::size_t key_zeros;
+    std::size_t value_scales;
+    std::size_t value_zeros;
+    std::size_t metadata_bytes;
+    std::size_t page_bytes;
+    double effective_bits;
+  };
+
+  inline int bits_of(int tier)
+  {
+    switch (tier)
+    {
+    case kINT8: return 8;
+    case kINT4: return 4;
+    case kINT2: return 2;
+    }
+    throw InvalidArgument("FP16 is not a quantised tier: its page has no codes and no metadata");
+  }
+
+  // The one place the layout's arithmetic is written (reference: quant.cu:358-392).
+  inline PageLayout page_layout(int tier, int page_tokens, int kv_heads, int head_dim)
+  {
+    const int bits = bits_of(tier);
+    if (page_tokens <= 0 || kv_heads <= 0 || head_dim <= 0)
+    {
+      throw InvalidArgument("page_tokens, kv_heads and head_dim must be positive, got " +
+                            std::to_string(page_tokens) + ", " + std::to_string(kv_heads) +
+                            ", " + std::to_string(head_dim));
+    }
+    if (head_dim * bits % 8 != 0)
+    {
+      throw InvalidArgument("head_dim " + std::to_string(head_dim) + " at " +
+                            std::to_string(bits) +
+                            " bits leaves a value group sharing a byte with the next");
+    }
+    const std::size_t width = static_cast<std::size_t>(kv_heads) * head_dim;
+    const std::size_t codes = static_cast<std::size_t>(page_tokens) * width * bits / 8;
+    const std::size_t key_meta = width * 2;
+    const std::size_t value_meta = static_cast<std::size_t>(page_tokens) * kv_heads * 2;
+    PageLayout l{};
+    l.bits = bits;
+    l.key_codes = 0;
+    l.value_codes = codes;
+    l.key_scales = 2 * codes;
+    l.key_zeros = l.key_scales + key_meta;
+    l.value_scales = l.key_zeros + key_meta;
+    l.value_zeros = l.value_scales + value_meta;
+    l.page_bytes = l.value_zeros + value_meta;
+    l.metadata_bytes = l.page_bytes - 2 * codes;
+    l.effective_bits = 8.0 * static_cast<double>(l.page_bytes) /
+                       static_cast<double>(2 * static_cast<std::size_t>(page_tokens) * width);
+    return l;
+  }
+
+  // An FP16 page: P rows of keys, then P rows of values (reference: kv_pages.cu:62-66).
+  inline std::size_t fp16_page_bytes(int page_tokens, std::size_t kv_width)
+  {
+    return 2 * static_cast<std::size_t>(page_tokens) * kv_width * 2;
+  }
+
+  inline std::size_t page_bytes_at(int tier, int page_tokens, int kv_heads, int head_dim)
+  {
+    return tier == kFP16
+               ? fp16_page_bytes(page_tokens, static_cast<std::size_t>(kv_heads) * head_dim)
+               : page_layout(tier, page_tokens, kv_heads, head_dim).page_bytes;
+  }
+
+  // ---- fp16 helpers -----------------------------------------------------------
+  // Round a double to the nearest fp16, ties to even, in one rounding (no
+  // detour through fp32, which could round twice). The bits of the result.
+  __host__ __device__ inline std::uint16_t half_bits_from_double(double x)
+  {
+    std::uint64_t b;
+    std::memcpy(&b, &x, sizeof(b));
+    const std::uint16_t sign = static_cast<std::uint16_t>((b >> 48) & 0x8000u);
+    const int exp = static_cast<int>((b >> 52) & 0x7ff);
+    const std::uint64_t mant = b & 0xFFFFFFFFFFFFFull;
+    if (exp == 0x7ff)
+    {
+      return static_cast<std::uint16_t>(sign | 0x7c00u | (mant != 0 ? 0x200u : 0u));
+    }
+    if (exp == 0)
+    {
+      return sign; // below 2^-1022: far under half of fp16's least subnormal
+    }
+    const int e = exp - 1023;
+    const std::uint64_t sig = mant | (1ull << 52); // value = sig * 2^(e - 52)
+    // Normal fp16 keeps 11 significant bits; a subnormal counts units of 2^-24.
+    const int shift = e >= -14 ? 42 : 28 - e;
+    if (shift > 62)
+    {
+      return sign;
+    }
+    std::uint64_t q = sig >> shift;
+    const std::uint64_t rem = sig & ((1ull << shift) - 1);
+    const std::uint64_t halfway = 1ull << (shift - 1);
+    if (rem > halfway || (rem == halfway && (q & 1u)))
+    {
+      ++q;
+    }
+    if (e >= -14)
+    {
+      int he = e + 15;
+      if (q == 2048)
+      {
+        q = 1024;
+        ++he;
+      }
+      if (he >= 31)
+      {
+        return static_cast<std::uint16_t>(sign | 0x7c00u);
+      }
+      return static_cast<std::uint16_t>(sign | (he << 10) | (q & 0x3ffu));
+    }
+    // q <= 1024; 1024 is the least normal's bit pattern, as wanted.
+    return static_cast<std::uint16_t>(sign | q);
+  }
+
+  __host__ __device__ inline float half_bits_to_float(std::uint16_t h)
+  {
+    const std::uint32_t sign = static_cast<std::uint32_t>(h & 0x8000u) << 16;
+    const int exp = (h >> 10) & 0x1f;
+    std::uint32_t mant = h & 0x3ffu;
+    std::uint32_t bits;
+    if (exp == 0x1f)
+    {
+      bits = sign | 0x7f800000u | (mant << 13);
+    }
+    else if (exp != 0)
+    {
+      bits = sign | (static_cast<std::uint32_t>(exp - 15 + 127) << 23) | (mant << 13);
+    }
+    else if (mant == 0)
+    {
+      bits = sign;
+    }
+    else
+    {
+      int e = -14;
+      while ((mant & 0x400u) == 0)
+      {
+        mant <<= 1;
+        --e;
+      }
+      bits = sign | (static_cast<std::uint32_t>(e + 127) << 23) | ((mant & 0x3ffu) << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, sizeof(f));
+    return f;
+  }
+
+  // The group's scale (reference: quant.cu:44-56): its range over the
+  // 2^bits - 1 steps, formed in fp64 and rounded to the nearest fp16, then
+  // one fp16 ulp up if that fell short of the exact value, so that the last
+  // level always reaches the maximum and no code is clamped.
+  __host__ __device__ inline std::uint16_t scale_bits_of(float lo, float hi, int bits)
+  {
+    const double levels = static_cast<double>((1 << bits) - 1);
+    const double exact = (static_cast<double>(hi) - static_cast<double>(lo)) / levels;
+    const std::uint16_t nearest = half_bits_from_double(exact);
+    if (static_cast<double>(half_bits_to_float(nearest)) >= exact)
+    {
+      return nearest;
+    }
+    return static_cast<std::uint16_t>(nearest + 1); // non-negative: next bit pattern is next up
+  }
+
+  // Largest page_tokens / head_dim / kv_heads any kernel here is built for.
+  constexpr int kMaxHeadDim = 256;
+
+} // namespace mi

@@ -1,0 +1,110 @@
+// Launchers of the library's HIP kernels. Each enqueues on `stream` and
+// returns without synchronising; launch errors throw at once, execution
+// errors surface at the next synchronising call.
+#pragma once
+
+#include "common.hpp"
+
+namespace mi
+{
+
+  // ---- requantisation (quant.hip) ------------------------------------------------
+  // Quantises `count` FP16 pages at `tier`: page i's keys from rows[i] and its
+  // values from rows[i] + values_offset bytes, into pages[i]. `rows` and
+  // `pages` are device-visible tables (pinned host memory mapped for the
+  // device is a valid row). With null tables, one page: row0 -> page0.
+  void launch_quantise_pages(const void *const *rows, void *const *pages, const void *row0,
+                             void *page0, std::ptrdiff_t values_offset, int count, int tier,
+                             int page_tokens, int kv_heads, int head_dim, hipStream_t stream);
+  void launch_dequantise_page(const void *page, void *keys, void *values, int tier,
+                              int page_tokens, int kv_heads, int head_dim, hipStream_t stream);
+
+  // ---- pages and scores (pages.hip) ----------------------------------------------
+  // from[i] -> to[i], `bytes` each, `count` pages, one launch; tables on the
+  // device. No copy may read what another writes.
+  void launch_copy_pages(const void *const *from, void *const *to, std::size_t bytes, int count,
+                         hipStream_t stream);
+  // Rows of n tokens, (n, row) fp16 keys and values, to positions
+  // [start, start + n) of an FP16 page table (P rows of keys then P of values).
+  void launch_store_pages(const void *keys, const void *values, const unsigned long long *pages,
+                          int page_tokens, std::size_t row, int start, int n, hipStream_t stream);
+  void launch_fill(float *out, std::size_t count, float value, hipStream_t stream);
+  // scores[p] = isnan(old) ? obs : alpha*obs + (1-alpha)*old with obs the
+  // head-order sum of mass[h][p] over `heads` divided by heads, every
+  // operation rounded once (reference: importance_scores.cu:31-50).
+  void launch_fold(float *scores, const float *mass, int heads, int pages, float alpha,
+                   hipStream_t stream);
+
+  // ---- pointwise (pointwise.hip) --------------------------------------------------
+  void launch_rope(const void *x, const std::int32_t *positions, void *out, int seq, int heads,
+                   int head_dim, double theta, hipStream_t stream);
+  void launch_rope_table(float *table, int positions, int head_dim, double theta,
+                         hipStream_t stream);
+  void launch_rmsnorm(const void *x, bool x_is_f32, const void *weight, void *out, int rows,
+                      int hidden, float eps, hipStream_t stream);
+  void launch_swiglu(const void *gate, const void *up, void *out, std::size_t count,
+                     hipStream_t stream);
+  void launch_add(const void *a, const void *b, void *out, std::size_t count, hipStream_t stream);
+
+  // ---- attention (attention.hip, decode.hip) -------------------------------------------
+  // Where keys and values are read from. Contiguous: k and v (seq_k, kv, hd).
+  // Paged: an FP16 page table, `pages`, P rows of keys then values. Causal:
+  // a cache that seals: sealed pages at the tier `tiers` records, the
+  // query's own page from `open` (FP16 page) before `start` and from
+  // chunk_k/chunk_v (the rows the queries brought) from `start` on.
+  enum class Layout : int
+  {
+    kContiguous = 0,
+    kPaged = 1,
+    kCausal = 2,
+  };
+
+  struct KVSource
+  {
+    Layout layout;
+    // Contiguous.
+    const std::uint16_t *k;
+    const std::uint16_t *v;
+    // Paged and causal.
+    const unsigned long long *pages;
+    const std::uint8_t *tiers;
+    const std::uint16_t *open;
+    const std::uint16_t *chunk_k;
+    const std::uint16_t *chunk_v;
+    int page_tokens;
+    int start;
+    // Which tiers a page may be at: a layout is formed for each.
+    bool may_be_at[kTierCount];
+  };
+
+  struct AttentionArgs
+  {
+    const std::uint16_t *q;   // (seq_q, heads, hd) fp16
+    std::uint16_t *out;       // (seq_q, heads, hd) fp16
+    const std::uint16_t *k_bias; // (kv_heads, hd) fp16 or null
+    const float *rope;        // {cos, sin} per (position, j < hd/2), fp32; with k_bias
+    int rope_positions;
+    int seq_q;
+    int seq_k;
+    int heads;
+    int kv_heads;
+    int head_dim;
+    float *mass;              // (heads, pages) fp32 or null; decode only
+    float *scores;            // this layer's importance scores or null; decode only
+    float alpha;
+    float *partials;          // attention_partials_floats(hd) or null: no split
+  };
+
+  // How a launch given partials splits its keys: runs and keys a run.
+  struct Split
+  {
+    int splits;
+    int split_keys;
+  };
+  Split attention_split(int seq_q, int seq_k, int heads, int kv_heads, int page_tokens);
+  std::size_t attention_partials_floats(int head_dim);
+  int device_multiprocessors();
+
+  void launch_attention(const KVSource &kv, const AttentionArgs &a, hipStream_t stream);
+
+} // namespace mi

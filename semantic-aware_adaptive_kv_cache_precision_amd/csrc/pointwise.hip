@@ -1,0 +1,218 @@
+// RoPE, the RoPE cos/sin table, RMSNorm, SwiGLU and the fp16 add, for gfx950.
+//
+// Arithmetic follows the reference:
+//   - RoPE rotate-half with the angle pos * theta^(-2j/hd) formed and reduced
+//     in fp64 (rope.cu:32-54, rope_angle.cuh:15-21); gfx950 runs fp64 at full
+//     rate, so this costs nothing here;
+//   - RMSNorm in fp32 from fp16 or fp32 input, one fp16 rounding at the store
+//     (rmsnorm.cu:33-84);
+//   - SwiGLU as g / (1 + expf(-g)) * up in fp32 (swiglu.cu:26-38).
+// Reductions are wave64: a wave's partial by DPP/shuffle, then one LDS step.
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <algorithm>
+
+namespace mi
+{
+  namespace
+  {
+
+    __device__ inline void rope_angle(double position, int j, int head_dim, double theta,
+                                      double *s, double *c)
+    {
+      const double inv_freq = pow(theta, -2.0 * static_cast<double>(j) / head_dim);
+      sincos(position * inv_freq, s, c);
+    }
+
+    // One workgroup per (token, head); a lane per rotation pair.
+    __global__ void rope_kernel(const std::uint16_t *__restrict__ x,
+                                const std::int32_t *__restrict__ positions,
+                                std::uint16_t *__restrict__ out, int heads, int head_dim,
+                                double theta)
+    {
+      const int token = blockIdx.x / heads;
+      const std::size_t base = static_cast<std::size_t>(blockIdx.x) * head_dim;
+      const int half = head_dim / 2;
+      const double pos = static_cast<double>(positions[token]);
+      for (int j = threadIdx.x; j < half; j += blockDim.x)
+      {
+        double s, c;
+        rope_angle(pos, j, head_dim, theta, &s, &c);
+        const float sf = static_cast<float>(s);
+        const float cf = static_cast<float>(c);
+        const float x1 = half_bits_to_float(x[base + j]);
+        const float x2 = half_bits_to_float(x[base + j + half]);
+        out[base + j] = __half_as_ushort(__float2half(x1 * cf - x2 * sf));
+        out[base + j + half] = __half_as_ushort(__float2half(x2 * cf + x1 * sf));
+      }
+    }
+
+    __global__ void rope_table_kernel(float *__restrict__ table, int half, int head_dim,
+                                      double theta, std::size_t count)
+    {
+      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+           i < count; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+      {
+        double s, c;
+        rope_angle(static_cast<double>(i / half), static_cast<int>(i % half), head_dim, theta, &s,
+                   &c);
+        table[2 * i] = static_cast<float>(c);
+        table[2 * i + 1] = static_cast<float>(s);
+      }
+    }
+
+    __device__ inline float widen(const std::uint16_t *x, std::size_t i)
+    {
+      return half_bits_to_float(x[i]);
+    }
+    __device__ inline float widen(const float *x, std::size_t i) { return x[i]; }
+
+    template <typename In>
+    __global__ void __launch_bounds__(256)
+        rmsnorm_kernel(const In *__restrict__ x, const std::uint16_t *__restrict__ weight,
+                       std::uint16_t *__restrict__ out, int hidden, float eps)
+    {
+      __shared__ float partial[256 / 64];
+      __shared__ float scale;
+      const std::size_t row = static_cast<std::size_t>(blockIdx.x) * hidden;
+      float acc = 0.0f;
+      for (int i = threadIdx.x; i < hidden; i += blockDim.x)
+      {
+        const float v = widen(x, row + i);
+        acc += v * v;
+      }
+      for (int offset = warpSize / 2; offset > 0; offset /= 2)
+      {
+        acc += __shfl_xor(acc, offset);
+      }
+      const int wave = threadIdx.x / warpSize;
+      if (threadIdx.x % warpSize == 0)
+      {
+        partial[wave] = acc;
+      }
+      __syncthreads();
+      if (threadIdx.x == 0)
+      {
+        float total = 0.0f;
+        for (int w = 0; w < static_cast<int>(blockDim.x / warpSize); ++w)
+        {
+          total += partial[w];
+        }
+        scale = rsqrtf(total / static_cast<float>(hidden) + eps);
+      }
+      __syncthreads();
+      for (int i = threadIdx.x; i < hidden; i += blockDim.x)
+      {
+        const float v = widen(x, row + i) * scale * half_bits_to_float(weight[i]);
+        out[row + i] = __half_as_ushort(__float2half(v));
+      }
+    }
+
+    __global__ void swiglu_kernel(const std::uint16_t *__restrict__ gate,
+                                  const std::uint16_t *__restrict__ up,
+                                  std::uint16_t *__restrict__ out, std::size_t count)
+    {
+      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+           i < count; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+      {
+        const float g = half_bits_to_float(gate[i]);
+        const float silu = g / (1.0f + expf(-g));
+        out[i] = __half_as_ushort(__float2half(silu * half_bits_to_float(up[i])));
+      }
+    }
+
+    __global__ void add_kernel(const std::uint16_t *a, const std::uint16_t *b, std::uint16_t *out,
+                               std::size_t count)
+    {
+      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+           i < count; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+      {
+        out[i] = __half_as_ushort(__float2half(half_bits_to_float(a[i]) + half_bits_to_float(b[i])));
+      }
+    }
+
+    int grid_for(std::size_t count, int threads)
+    {
+      return static_cast<int>(std::max<std::size_t>(
+          1, std::min<std::size_t>((count + threads - 1) / threads, 65536)));
+    }
+
+  } // namespace
+
+  void launch_rope(const void *x, const std::int32_t *positions, void *out, int seq, int heads,
+                   int head_dim, double theta, hipStream_t stream)
+  {
+    if (seq <= 0 || heads <= 0 || head_dim <= 0)
+    {
+      return;
+    }
+    hipLaunchKernelGGL(rope_kernel, dim3(seq * heads), dim3(64), 0, stream,
+                       static_cast<const std::uint16_t *>(x), positions,
+                       static_cast<std::uint16_t *>(out), heads, head_dim, theta);
+    hip_check(hipGetLastError(), "rope kernel launch");
+  }
+
+  void launch_rope_table(float *table, int positions, int head_dim, double theta,
+                         hipStream_t stream)
+  {
+    const std::size_t entries = static_cast<std::size_t>(positions) * (head_dim / 2);
+    if (entries == 0)
+    {
+      return;
+    }
+    hipLaunchKernelGGL(rope_table_kernel, dim3(grid_for(entries, 256)), dim3(256), 0, stream,
+                       table, head_dim / 2, head_dim, theta, entries);
+    hip_check(hipGetLastError(), "rope table kernel launch");
+  }
+
+  void launch_rmsnorm(const void *x, bool x_is_f32, const void *weight, void *out, int rows,
+                      int hidden, float eps, hipStream_t stream)
+  {
+    if (rows <= 0 || hidden <= 0)
+    {
+      return;
+    }
+    const auto *w = static_cast<const std::uint16_t *>(weight);
+    auto *o = static_cast<std::uint16_t *>(out);
+    if (x_is_f32)
+    {
+      hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3(rows), dim3(256), 0, stream,
+                         static_cast<const float *>(x), w, o, hidden, eps);
+    }
+    else
+    {
+      hipLaunchKernelGGL(rmsnorm_kernel<std::uint16_t>, dim3(rows), dim3(256), 0, stream,
+                         static_cast<const std::uint16_t *>(x), w, o, hidden, eps);
+    }
+    hip_check(hipGetLastError(), "rmsnorm kernel launch");
+  }
+
+  void launch_swiglu(const void *gate, const void *up, void *out, std::size_t count,
+                     hipStream_t stream)
+  {
+    if (count == 0)
+    {
+      return;
+    }
+    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(count, 256)), dim3(256), 0, stream,
+                       static_cast<const std::uint16_t *>(gate),
+                       static_cast<const std::uint16_t *>(up), static_cast<std::uint16_t *>(out),
+                       count);
+    hip_check(hipGetLastError(), "swiglu kernel launch");
+  }
+
+  void launch_add(const void *a, const void *b, void *out, std::size_t count, hipStream_t stream)
+  {
+    if (count == 0)
+    {
+      return;
+    }
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for(count, 256)), dim3(256), 0, stream,
+                       static_cast<const std::uint16_t *>(a), static_cast<const std::uint16_t *>(b),
+                       static_cast<std::uint16_t *>(out), count);
+    hip_check(hipGetLastError(), "add kernel launch");
+  }
+
+} // namespace mi

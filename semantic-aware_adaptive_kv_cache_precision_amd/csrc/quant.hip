@@ -1,0 +1,313 @@
+// Page requantisation kernels for gfx950: a batch of FP16 pages quantised to
+// INT8/INT4/INT2 in one launch, and the dequantiser.
+//
+// Arithmetic follows the reference exactly (src/core_kernels/quant.cu):
+//   - keys per (head, channel) over the page's P positions, values per
+//     (token, head) over head_dim (quant.cu:76-187);
+//   - zero-point = the group's minimum, stored exactly in fp16;
+//   - scale = scale_bits_of (fp64 range / levels, nearest fp16, one ulp up
+//     if short: quant.cu:44-56);
+//   - code = rintf((x - zero) / scale) in fp32 IEEE arithmetic, clamped,
+//     0 for a zero scale (quant.cu:60-70);
+//   - dequantised value = fp16_rn(fmaf(code, scale, zero)) (quant.cu:243-266).
+//
+// Layout of the work (MI355X-first, not the reference's two launches per
+// batch): one workgroup quantises one whole page. It streams the FP16 page
+// (possibly pinned host memory mapped for the device) into LDS once with
+// 16-byte loads, computes every group there, assembles the quantised page in
+// LDS, and writes it out with 16-byte stores. Every input byte crosses HBM or
+// the host link once and every output byte once.
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mi
+{
+  namespace
+  {
+
+    constexpr int kQuantThreads = 256;
+
+    // Copies `bytes` from src to dst by the workgroup, 16 bytes a lane where
+    // both are 16-byte aligned and the size a multiple of 16, else bytewise.
+    __device__ inline void block_copy(std::uint8_t *__restrict__ dst,
+                                      const std::uint8_t *__restrict__ src,
+                                      std::size_t bytes)
+    {
+      const bool wide = ((reinterpret_cast<std::uintptr_t>(dst) |
+                          reinterpret_cast<std::uintptr_t>(src) | bytes) &
+                         15u) == 0;
+      if (wide)
+      {
+        const std::size_t n = bytes / 16;
+        const uint4 *s = reinterpret_cast<const uint4 *>(src);
+        uint4 *d = reinterpret_cast<uint4 *>(dst);
+        for (std::size_t i = threadIdx.x; i < n; i += blockDim.x)
+        {
+          d[i] = s[i];
+        }
+      }
+      else
+      {
+        for (std::size_t i = threadIdx.x; i < bytes; i += blockDim.x)
+        {
+          dst[i] = src[i];
+        }
+      }
+    }
+
+    template <int Bits>
+    __device__ inline unsigned code_of(float x, float zero, float scale)
+    {
+      constexpr float kLevels = static_cast<float>((1 << Bits) - 1);
+      if (scale == 0.0f)
+      {
+        return 0u;
+      }
+      const float q = rintf((x - zero) / scale);
+      return static_cast<unsigned>(fminf(fmaxf(q, 0.0f), kLevels));
+    }
+
+    __device__ inline float lds_half(const std::uint16_t *p, std::size_t i)
+    {
+      return __half2float(__ushort_as_half(p[i]));
+    }
+
+    // Quantises one FP16 page already in LDS (`in`: P rows of keys then P of
+    // values, W halves each) into `out` (LDS, the layout's page_bytes).
+    template <int Bits>
+    __device__ void quantise_in_lds(const std::uint16_t *__restrict__ in,
+                                    std::uint8_t *__restrict__ out,
+                                    const PageLayout &L, int page_tokens,
+                                    int kv_heads, int head_dim)
+    {
+      constexpr int kPerByte = 8 / Bits;
+      const int width = kv_heads * head_dim;
+      const int columns = width / kPerByte;
+      const std::uint16_t *keys = in;
+      const std::uint16_t *values = in + static_cast<std::size_t>(page_tokens) * width;
+      std::uint16_t *k_scales = reinterpret_cast<std::uint16_t *>(out + L.key_scales);
+      std::uint16_t *k_zeros = reinterpret_cast<std::uint16_t *>(out + L.key_zeros);
+      std::uint16_t *v_scales = reinterpret_cast<std::uint16_t *>(out + L.value_scales);
+      std::uint16_t *v_zeros = reinterpret_cast<std::uint16_t *>(out + L.value_zeros);
+
+      // Keys: a lane owns the kPerByte channels that share a byte of every row.
+      for (int column = threadIdx.x; column < columns; column += blockDim.x)
+      {
+        const int first = column * kPerByte;
+        float lo[kPerByte], hi[kPerByte], scale[kPerByte];
+#pragma unroll
+        for (int c = 0; c < kPerByte; ++c)
+        {
+          lo[c] = INFINITY;
+          hi[c] = -INFINITY;
+        }
+        for (int t = 0; t < page_tokens; ++t)
+        {
+#pragma unroll
+          for (int c = 0; c < kPerByte; ++c)
+          {
+            const float x = lds_half(keys, static_cast<std::size_t>(t) * width + first + c);
+            lo[c] = fminf(lo[c], x);
+            hi[c] = fmaxf(hi[c], x);
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < kPerByte; ++c)
+        {
+          const std::uint16_t s = scale_bits_of(lo[c], hi[c], Bits);
+          k_scales[first + c] = s;
+          k_zeros[first + c] = __half_as_ushort(__float2half(lo[c]));
+          scale[c] = half_bits_to_float(s);
+        }
+        for (int t = 0; t < page_tokens; ++t)
+        {
+          unsigned byte = 0;
+#pragma unroll
+          for (int c = 0; c < kPerByte; ++c)
+          {
+            const float x = lds_half(keys, static_cast<std::size_t>(t) * width + first + c);
+            byte |= code_of<Bits>(x, lo[c], scale[c]) << (c * Bits);
+          }
+          out[L.key_codes + static_cast<std::size_t>(t) * columns + column] =
+              static_cast<std::uint8_t>(byte);
+        }
+      }
+
+      // Values: a wave per (token, head) group, lanes reducing its range.
+      const int lane = threadIdx.x % warpSize;
+      const int wave = threadIdx.x / warpSize;
+      const int waves = blockDim.x / warpSize;
+      const int groups = page_tokens * kv_heads;
+      const int bytes = head_dim / kPerByte;
+      for (int group = wave; group < groups; group += waves)
+      {
+        const std::uint16_t *x = values + static_cast<std::size_t>(group) * head_dim;
+        float lo = INFINITY, hi = -INFINITY;
+        for (int i = lane; i < head_dim; i += warpSize)
+        {
+          const float v = lds_half(x, i);
+          lo = fminf(lo, v);
+          hi = fmaxf(hi, v);
+        }
+        for (int offset = warpSize / 2; offset > 0; offset /= 2)
+        {
+          lo = fminf(lo, __shfl_xor(lo, offset));
+          hi = fmaxf(hi, __shfl_xor(hi, offset));
+        }
+        const std::uint16_t s = scale_bits_of(lo, hi, Bits);
+        if (lane == 0)
+        {
+          v_scales[group] = s;
+          v_zeros[group] = __half_as_ushort(__float2half(lo));
+        }
+        const float scale = half_bits_to_float(s);
+        std::uint8_t *codes = out + L.value_codes + static_cast<std::size_t>(group) * bytes;
+        for (int b = lane; b < bytes; b += warpSize)
+        {
+          unsigned byte = 0;
+#pragma unroll
+          for (int c = 0; c < kPerByte; ++c)
+          {
+            byte |= code_of<Bits>(lds_half(x, b * kPerByte + c), lo, scale) << (c * Bits);
+          }
+          codes[b] = static_cast<std::uint8_t>(byte);
+        }
+      }
+    }
+
+    // One workgroup per page: page blockIdx.x + first of the batch.
+    template <int Bits>
+    __global__ void __launch_bounds__(kQuantThreads)
+        quantise_pages_kernel(const void *const *__restrict__ rows,
+                              void *const *__restrict__ pages, const void *row0, void *page0,
+                              std::ptrdiff_t values_offset, PageLayout L, int page_tokens,
+                              int kv_heads, int head_dim)
+    {
+      extern __shared__ uint4 lds_raw[];
+      const std::size_t half_bytes =
+          static_cast<std::size_t>(page_tokens) * kv_heads * head_dim * 2;
+      const std::size_t in_bytes = 2 * half_bytes;
+      std::uint16_t *in = reinterpret_cast<std::uint16_t *>(lds_raw);
+      std::uint8_t *out = reinterpret_cast<std::uint8_t *>(lds_raw) + ((in_bytes + 15) / 16) * 16;
+      // A batch names its pages in tables; a single page comes by value.
+      const auto *src = static_cast<const std::uint8_t *>(rows ? rows[blockIdx.x] : row0);
+      auto *dst = static_cast<std::uint8_t *>(pages ? pages[blockIdx.x] : page0);
+      block_copy(reinterpret_cast<std::uint8_t *>(in), src, half_bytes);
+      block_copy(reinterpret_cast<std::uint8_t *>(in) + half_bytes, src + values_offset,
+                 half_bytes);
+      __syncthreads();
+      quantise_in_lds<Bits>(in, out, L, page_tokens, kv_heads, head_dim);
+      __syncthreads();
+      block_copy(dst, out, L.page_bytes);
+    }
+
+    // One half of a quantised page back to fp16, a thread per code byte.
+    // Element e of the half is row e / width; its group is its channel,
+    // e % width, for keys, and its (token, head), e / head_dim, for values.
+    template <int Bits, bool PerChannel>
+    __global__ void dequantise_kernel(const std::uint8_t *__restrict__ codes,
+                                      const std::uint16_t *__restrict__ scales,
+                                      const std::uint16_t *__restrict__ zeros,
+                                      std::uint16_t *__restrict__ out, std::size_t bytes,
+                                      int width, int head_dim)
+    {
+      constexpr int kPerByte = 8 / Bits;
+      constexpr unsigned kMask = (1u << Bits) - 1;
+      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+           i < bytes; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+      {
+        const unsigned byte = codes[i];
+#pragma unroll
+        for (int c = 0; c < kPerByte; ++c)
+        {
+          const std::size_t e = i * kPerByte + c;
+          const std::size_t group = PerChannel ? e % width : e / head_dim;
+          const float q = static_cast<float>((byte >> (c * Bits)) & kMask);
+          const float v = fmaf(q, half_bits_to_float(scales[group]),
+                               half_bits_to_float(zeros[group]));
+          out[e] = __half_as_ushort(__float2half_rn(v));
+        }
+      }
+    }
+
+    template <typename F>
+    void with_bits(int tier, F &&f)
+    {
+      switch (tier)
+      {
+      case kINT8: f(std::integral_constant<int, 8>{}); return;
+      case kINT4: f(std::integral_constant<int, 4>{}); return;
+      case kINT2: f(std::integral_constant<int, 2>{}); return;
+      }
+      throw InvalidArgument("FP16 is not a quantised tier: its page has no codes and no metadata");
+    }
+
+    std::size_t quant_lds_bytes(const PageLayout &L, int page_tokens, int kv_heads, int head_dim)
+    {
+      const std::size_t in = fp16_page_bytes(page_tokens, static_cast<std::size_t>(kv_heads) * head_dim);
+      return ((in + 15) / 16) * 16 + ((L.page_bytes + 15) / 16) * 16;
+    }
+
+    // LDS a workgroup may take on gfx950.
+    constexpr std::size_t kMaxLds = 160 * 1024;
+
+  } // namespace
+
+  void launch_quantise_pages(const void *const *rows, void *const *pages, const void *row0,
+                             void *page0, std::ptrdiff_t values_offset, int count, int tier,
+                             int page_tokens, int kv_heads, int head_dim, hipStream_t stream)
+  {
+    const PageLayout L = page_layout(tier, page_tokens, kv_heads, head_dim);
+    if (count <= 0)
+    {
+      return;
+    }
+    const std::size_t lds = quant_lds_bytes(L, page_tokens, kv_heads, head_dim);
+    if (lds > kMaxLds)
+    {
+      throw InvalidArgument("a page of " + std::to_string(page_tokens) + " positions at " +
+                            std::to_string(kv_heads * head_dim) +
+                            " elements does not fit one workgroup's LDS to quantise");
+    }
+    with_bits(tier, [&](auto bits) {
+      constexpr int B = decltype(bits)::value;
+      auto kernel = quantise_pages_kernel<B>;
+      if (lds > 64 * 1024)
+      {
+        hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds)),
+                  "hipFuncSetAttribute quantise LDS");
+      }
+      // A grid's x dimension holds far more than any batch of pages.
+      hipLaunchKernelGGL(kernel, dim3(count), dim3(kQuantThreads), lds, stream, rows, pages, row0,
+                         page0, values_offset, L, page_tokens, kv_heads, head_dim);
+      hip_check(hipGetLastError(), "quantise pages kernel launch");
+    });
+  }
+
+  void launch_dequantise_page(const void *page, void *keys, void *values, int tier,
+                              int page_tokens, int kv_heads, int head_dim, hipStream_t stream)
+  {
+    const PageLayout L = page_layout(tier, page_tokens, kv_heads, head_dim);
+    const std::size_t bytes = L.value_codes - L.key_codes;
+    const int width = kv_heads * head_dim;
+    const auto *p = static_cast<const std::uint8_t *>(page);
+    const auto meta = [p](std::size_t off) { return reinterpret_cast<const std::uint16_t *>(p + off); };
+    const int threads = 256;
+    const int blocks = static_cast<int>(std::min<std::size_t>((bytes + threads - 1) / threads, 4096));
+    with_bits(tier, [&](auto bits) {
+      constexpr int B = decltype(bits)::value;
+      hipLaunchKernelGGL((dequantise_kernel<B, true>), dim3(blocks), dim3(threads), 0, stream,
+                         p + L.key_codes, meta(L.key_scales), meta(L.key_zeros),
+                         static_cast<std::uint16_t *>(keys), bytes, width, head_dim);
+      hip_check(hipGetLastError(), "dequantise keys kernel launch");
+      hipLaunchKernelGGL((dequantise_kernel<B, false>), dim3(blocks), dim3(threads), 0, stream,
+                         p + L.value_codes, meta(L.value_scales), meta(L.value_zeros),
+                         static_cast<std::uint16_t *>(values), bytes, width, head_dim);
+      hip_check(hipGetLastError(), "dequantise values kernel launch");
+    });
+  }
+
+} // namespace mi

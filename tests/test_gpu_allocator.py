@@ -1,0 +1,117 @@
+"""The VMM page allocator on the device against the oracle's slot model:
+slot order, page contents, mapped granules, rollback. GPU parity tests."""
+
+import numpy as np
+import pytest
+
+from conftest import announce
+from oracle import slots
+
+pytestmark = pytest.mark.gpu
+
+
+def mi():
+    from microinfer import _microinfer
+    return _microinfer
+
+
+def test_random_operations_match_the_slot_model():
+    m = mi()
+    granule = m.granule_bytes()
+    announce("granule", granule)
+    assert granule > 0
+    # Page sizes as fractions of the granule, as the reference's tests use
+    # (tests/test_paged_kv_cache.py:1-87), and capacity for several granules.
+    page_bytes = [granule // 3 // 16 * 16, granule // 5 // 16 * 16, granule // 7 // 16 * 16, 4096]
+    cap = [40, 40, 40, 40]
+    alloc = m.PagedKVCache(page_bytes, cap)
+    model = slots.Slots(page_bytes, cap, granule)
+    rng = np.random.default_rng(0)
+    held = {}
+    for step in range(300):
+        op = rng.integers(0, 6)
+        keys = list(held)
+        if op <= 2 or not keys:
+            key = (int(rng.integers(0, 3)), int(rng.integers(-20, 30)))
+            tier = int(rng.integers(0, 4))
+            if key in held or len(model.slots[tier]) == cap[tier]:
+                continue
+            data = rng.integers(0, 256, page_bytes[tier], dtype=np.uint8)
+            alloc.allocate(key[0], key[1], tier)
+            alloc.write(key[0], key[1], data)
+            model.allocate(key, tier, data=data)
+            held[key] = data
+        elif op == 3:
+            key = keys[rng.integers(0, len(keys))]
+            alloc.free(*key)
+            model.free(key)
+            del held[key]
+        elif op == 4:
+            n = int(rng.integers(1, min(8, len(keys)) + 1))
+            chosen = [keys[i] for i in rng.choice(len(keys), n, replace=False)]
+            alloc.free_pages(chosen)
+            model.free_pages(chosen)
+            for key in chosen:
+                del held[key]
+        else:
+            n = int(rng.integers(1, min(4, len(keys)) + 1))
+            chosen = [keys[i] for i in rng.choice(len(keys), n, replace=False)]
+            pairs = []
+            for i, key in enumerate(chosen):
+                stage = (key[0], -100 - i)
+                tier = int(rng.integers(0, 4))
+                if len(model.slots[tier]) == cap[tier]:
+                    continue
+                data = rng.integers(0, 256, page_bytes[tier], dtype=np.uint8)
+                alloc.allocate(stage[0], stage[1], tier)
+                alloc.write(stage[0], stage[1], data)
+                model.allocate(stage, tier, data=data)
+                pairs.append((key, stage))
+                held[key] = data
+            if pairs:
+                alloc.replace_pages(pairs)
+                model.replace_pages(pairs)
+        if step % 25 == 0 or step == 299:
+            announce("allocator step", step)
+            for t in range(4):
+                assert alloc.pages(t) == model.slots[t], (step, t)
+                assert alloc.mapped_bytes(t) == model.mapped_bytes(t), (step, t)
+            for key, data in held.items():
+                np.testing.assert_array_equal(alloc.read(*key), data)
+
+
+def test_a_failed_granule_rolls_back_and_full_is_refused():
+    m = mi()
+    granule = m.granule_bytes()
+    alloc = m.PagedKVCache([granule, granule, granule, granule], [3, 0, 0, 1])
+    alloc.allocate(0, 0, 0)
+    mapped = alloc.mapped_bytes(0)
+    m.fail_next_granules(1)
+    with pytest.raises(m.OutOfMemory):
+        alloc.allocate(0, 1, 0)
+    m.fail_next_granules(0)
+    assert (0, 1) not in alloc and alloc.mapped_bytes(0) == mapped
+    alloc.allocate(0, 1, 0)
+    alloc.allocate(0, 2, 0)
+    with pytest.raises(ValueError, match="full"):
+        alloc.allocate(0, 3, 0)
+    with pytest.raises(KeyError):
+        alloc.free(5, 5)
+    with pytest.raises(ValueError, match="already"):
+        alloc.allocate(0, 1, 0)
+
+
+def test_spare_granules_are_kept_mapped_beyond_the_tail():
+    m = mi()
+    granule = m.granule_bytes()
+    alloc = m.PagedKVCache([granule // 2] * 4, [16, 16, 16, 16])
+    alloc.allocate(0, 0, 2)
+    assert alloc.mapped_bytes(2) == granule
+    alloc.keep_spare_granules(2, 2)
+    assert alloc.spare_granules(2) == 2 and alloc.mapped_bytes(2) == 3 * granule
+    for i in range(1, 5):
+        alloc.allocate(0, i, 2)
+    assert alloc.mapped_bytes(2) == 5 * granule
+    for i in range(5):
+        alloc.free(0, i)
+    assert alloc.mapped_bytes(2) == 2 * granule

@@ -1,0 +1,155 @@
+"""Attention kernels against the float64 oracle: contiguous layout, GQA,
+the key bias, causal masking, split-K.
+
+GPU parity tests (tolerance: conftest.ATTN_RTOL, 1e-3 relative)."""
+
+import numpy as np
+import pytest
+
+from conftest import announce, assert_attention_close, each, fp16_exact
+from oracle import attention as att
+from oracle import pointwise
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {"qwen2.5-0.5b": (14, 2, 64, 1e6), "qwen2.5-1.5b": (12, 2, 128, 1e6),
+          "llama-3.2-1b": (32, 8, 64, 5e5)}
+
+
+def mi():
+    from microinfer import _microinfer
+    return _microinfer
+
+
+def qkv(seq_q, seq_k, heads, kv_heads, hd, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return (fp16_exact(scale * rng.standard_normal((seq_q, heads, hd))),
+            fp16_exact(rng.standard_normal((seq_k, kv_heads, hd))),
+            fp16_exact(rng.standard_normal((seq_k, kv_heads, hd))))
+
+
+def test_contiguous_attention_is_the_float64_reference():
+    m = mi()
+
+    def check(name, seq_q, seq_k):
+        heads, kv, hd, _ = SHAPES[name]
+        announce("attention", name, seq_q, seq_k)
+        q, k, v = qkv(seq_q, seq_k, heads, kv, hd, seed=seq_q * 1000 + seq_k, scale=2.0)
+        got = m.attention(q, k, v)
+        want, _ = att.attention64(q, k, v)
+        assert_attention_close(got, want, f"{name} {seq_q}x{seq_k}")
+
+    cases = [(n, sq, sk) for n in SHAPES for sq, sk in
+             ((1, 1), (1, 31), (1, 32), (1, 33), (1, 700), (1, 4099), (16, 16), (17, 40),
+              (37, 300))]
+    each(cases, check)
+
+
+def test_grouped_query_heads_read_their_own_kv_head():
+    """Each KV head's values are a constant of its own: a query head's
+    output is the constant of KV head h // group, whatever its scores."""
+    m = mi()
+    heads, kv, hd = 12, 3, 64
+    rng = np.random.default_rng(1)
+    q = fp16_exact(rng.standard_normal((1, heads, hd)))
+    k = fp16_exact(rng.standard_normal((50, kv, hd)))
+    v = np.zeros((50, kv, hd), np.float32)
+    for h in range(kv):
+        v[:, h, :] = h + 1
+    got = m.attention(q, k, v)
+    for h in range(heads):
+        np.testing.assert_array_equal(got[0, h], np.full(hd, h // (heads // kv) + 1, np.float32))
+
+
+def test_the_key_bias_completes_each_key():
+    """k_bias (kv_heads, hd) completes key j as k + RoPE(k_bias, j)
+    (reference attention.cu:104-116), against the whole key in float64."""
+    m = mi()
+    for name in ("qwen2.5-0.5b", "qwen2.5-1.5b"):
+        heads, kv, hd, theta = SHAPES[name]
+        for seq_q, seq_k in ((1, 99), (40, 40)):
+            announce("key bias", name, seq_q, seq_k)
+            rng = np.random.default_rng(seq_k)
+            q = fp16_exact(rng.standard_normal((seq_q, heads, hd)))
+            k = fp16_exact(0.3 * rng.standard_normal((seq_k, kv, hd)))
+            v = fp16_exact(rng.standard_normal((seq_k, kv, hd)))
+            bias = fp16_exact(3 * rng.standard_normal((kv, hd)))
+            got = m.attention(q, k, v, k_bias=bias, theta=theta)
+            want, _ = att.attention64(q, k, v, k_bias=bias, theta=theta)
+            assert_attention_close(got, want, f"bias {name}")
+
+
+def test_a_nan_in_a_future_key_does_not_leak():
+    m = mi()
+    heads, kv, hd = 4, 2, 64
+    q, k, v = qkv(3, 10, heads, kv, hd, seed=3)
+    k[9], v[9] = np.nan, np.nan
+    # Queries at positions 7, 8 and 9: only the last sees key 9.
+    got = m.attention(q, k, v)
+    assert np.isfinite(got[:2]).all()
+    want, _ = att.attention64(q[:2], k[:9], v[:9])
+    assert_attention_close(got[:2], want, "masked NaN")
+
+
+def test_split_launches_match_the_reference_and_the_unsplit_one():
+    """A long decode launch splits its keys into runs (device.attention with
+    partials); without partials it does not. Both are the reference."""
+    m = mi()
+    d = m.device
+    heads, kv, hd, _ = SHAPES["qwen2.5-1.5b"]
+    seq_k = 5000
+    splits, keys = d.attention_split(1, seq_k, heads, kv, 0)
+    assert splits > 1, "the case must split"
+    q, k, v = qkv(1, seq_k, heads, kv, hd, seed=9)
+    want, _ = att.attention64(q, k, v)
+    outs = []
+    for partials in (d.empty_f32(d.attention_partials(hd)), None):
+        announce("split", partials is not None)
+        out = d.empty(q.size)
+        d.attention(m.upload_fp16(q), m.upload_fp16(k), m.upload_fp16(v), None, None, out, 1,
+                    seq_k, heads, kv, hd, partials)
+        outs.append(out.to_numpy().reshape(q.shape))
+        assert_attention_close(outs[-1], want, "split" if partials else "unsplit")
+
+
+def test_rope_rmsnorm_swiglu_are_the_float64_references():
+    m = mi()
+    rng = np.random.default_rng(0)
+    # RoPE: positions past 2048 and at the end of the window (tests/test_rope.py:30-41).
+    for heads, hd in ((14, 64), (2, 128)):
+        announce("rope", heads, hd)
+        pos = np.array([0, 1, 31, 2047, 2049, 16384, 32767], np.int32)
+        x = fp16_exact(rng.standard_normal((len(pos), heads, hd)))
+        got = m.rope(x, pos, 1e6)
+        want = pointwise.rope(x, pos, 1e6)
+        ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+        assert np.all(np.abs(got - want) <= 2 * ulp + 1e-6 * np.abs(x).max())
+    for hidden in (896, 2048):
+        announce("rmsnorm", hidden)
+        x = fp16_exact(rng.standard_normal((3, hidden)))
+        w = fp16_exact(rng.uniform(0.5, 1.5, hidden))
+        got = m.rmsnorm(x, w, 1e-6)
+        want = pointwise.rmsnorm(x, w, 1e-6)
+        ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+        assert np.all(np.abs(got - want) <= ulp)
+    announce("swiglu")
+    g = fp16_exact(4 * rng.standard_normal((2, 8192)))
+    u = fp16_exact(rng.standard_normal((2, 8192)))
+    got = m.swiglu(g, u)
+    want = pointwise.swiglu(g, u)
+    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= ulp)
+
+
+def test_rope_table_is_fp64_cos_sin_rounded():
+    m = mi()
+    t = m.device.RopeTable(128, 1e6)
+    t.cover(3000)
+    table = t.to_numpy()
+    assert table.shape[0] >= 3000
+    pos = np.arange(table.shape[0])[:, None]
+    inv = 1e6 ** (-np.arange(64) * 2.0 / 128)
+    ang = pos * inv[None, :]
+    for got, want in ((table[..., 0], np.cos(ang)), (table[..., 1], np.sin(ang))):
+        ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+        assert np.all(np.abs(got - want) <= ulp)

@@ -1,0 +1,354 @@
+"""The cache manager on the device: sealing, causal mixed-tier attention with
+per-page mass and the fused EWMA, downgrades, upgrades and batched moves,
+against the oracle.
+
+GPU parity tests. Bytes, tiers and shadows are compared to the bit; attention
+outputs and masses to the 1e-3 bar; the fused scores to the bit against the
+oracle's fold of the kernel's own masses."""
+
+import numpy as np
+import pytest
+
+from conftest import (announce, assert_attention_close, assert_mass_close, each, fp16_exact)
+from oracle import attention as att
+from oracle import ewma, quant
+
+pytestmark = pytest.mark.gpu
+
+LAYERS = 2
+
+
+def mi():
+    from microinfer import _microinfer
+    return _microinfer
+
+
+def page_sizes(P, kv, hd):
+    return [quant.page_bytes(t, kv, hd, P) for t in range(4)]
+
+
+def pages_for(P, kv, hd, tier=0, tier_map=None, always_seal=False, capacity=4096):
+    m = mi()
+    cap = [capacity] * 4
+    cap[0] += LAYERS * 2 + 8
+    alloc = m.PagedKVCache(page_sizes(P, kv, hd), cap)
+    cache = m.device.KVPages(alloc, LAYERS, P, kv, hd, tier, m.device.Halves.Both,
+                             tier_map or [], always_seal)
+    return alloc, cache
+
+
+def put(x):
+    return mi().upload_fp16(np.ascontiguousarray(x, np.float32).reshape(-1))
+
+
+def normal(rng, *shape):
+    return fp16_exact(rng.standard_normal(shape))
+
+
+def store_in_runs(cache, layer, k, v, runs):
+    start = 0
+    for n in runs:
+        cache.reserve(start + n)
+        cache.store(layer, put(k[start:start + n]), put(v[start:start + n]), start, n)
+        start += n
+    return start - runs[-1]
+
+
+def sealed_pages(alloc, layer, n):
+    pages, tiers = [], []
+    for i in range(n):
+        pages.append(alloc.read(layer, i))
+        tiers.append(int(alloc.locate(layer, i)[0]))
+    return pages, tiers
+
+
+def test_sealed_pages_are_quantise_page_s_bytes_however_rows_arrive():
+    """A full page holds, byte for byte, the oracle's quantise_page of its
+    rows at its birth tier, whether its positions came in one store, one at a
+    time, or in runs that begin and end mid-page (P = 16, 32, 48)."""
+    def check(P, tier, runs_name):
+        kv, hd = 2, 64
+        rng = np.random.default_rng(P + tier)
+        seq = 3 * P + 5
+        k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+        runs = {"one": [seq], "single": [1] * seq, "ragged": [P // 2 + 1, P + 3, seq - (3 * P // 2 + 4)]}[runs_name]
+        announce("seal", P, tier, runs_name)
+        alloc, cache = pages_for(P, kv, hd, tier)
+        store_in_runs(cache, 1, k, v, runs)
+        for i in range(seq // P):
+            kp = k[i * P:(i + 1) * P].astype(np.float16)
+            vp = v[i * P:(i + 1) * P].astype(np.float16)
+            want = quant.fp16_page(kp, vp) if tier == 0 else quant.quantise_page(kp, vp, tier, P)
+            np.testing.assert_array_equal(alloc.read(1, i), want)
+
+    each([(P, t, r) for P in (16, 32, 48) for t in (1, 2, 3)
+          for r in ("one", "single", "ragged")], check)
+    # An FP16 cache that seals (always_seal) copies its rows.
+    for P in (16, 32):
+        kv, hd = 2, 64
+        rng = np.random.default_rng(3)
+        k, v = normal(rng, 2 * P, kv, hd), normal(rng, 2 * P, kv, hd)
+        alloc, cache = pages_for(P, kv, hd, 0, always_seal=True)
+        store_in_runs(cache, 0, k, v, [P - 3, P + 3])
+        for i in range(2):
+            want = quant.fp16_page(k[i * P:(i + 1) * P].astype(np.float16),
+                                   v[i * P:(i + 1) * P].astype(np.float16))
+            np.testing.assert_array_equal(alloc.read(0, i), want)
+
+
+def decode_case(P, kv, hd, heads, tier_map, seq, seed, bias=False, theta=1e6):
+    m = mi()
+    rng = np.random.default_rng(seed)
+    k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+    k[:, :, rng.choice(hd, 2, replace=False)] *= 10
+    k = fp16_exact(k)
+    alloc, cache = pages_for(P, kv, hd, 0, tier_map=tier_map, always_seal=True)
+    store_in_runs(cache, 0, k, v, [seq - 1, 1])
+    q = normal(rng, 1, heads, hd)
+    b = fp16_exact(3 * rng.standard_normal((kv, hd))) if bias else None
+    return m, alloc, cache, k, v, q, b
+
+
+def oracle_decode(alloc, P, kv, hd, k, v, q, bias=None, theta=1e6):
+    seq = len(k)
+    own = (seq - 1) // P
+    pages, tiers = sealed_pages(alloc, 0, own)
+    return att.causal_decode(q, pages, tiers, k[own * P:], v[own * P:], kv, hd, P,
+                             k_bias=bias, theta=theta)
+
+
+def run_decode(m, cache, k, v, q, heads, kv, hd, bias=None, theta=1e6, mass=True, partials=True,
+               scores=None):
+    d = m.device
+    seq = len(k)
+    P = cache.page_tokens
+    pages = -(-seq // P)
+    rope = None
+    if bias is not None:
+        rope = d.RopeTable(hd, theta)
+        rope.cover(seq)
+    out = d.empty(heads * hd)
+    mbuf = d.empty_f32(heads * pages) if mass else None
+    part = d.empty_f32(d.attention_partials(hd)) if partials else None
+    cache.attention(0, put(q), put(bias) if bias is not None else None, rope, out, 1, seq, heads,
+                    kv, hd, put(k[-1:]), put(v[-1:]), mbuf, part, scores=scores)
+    got = out.to_numpy().reshape(1, heads, hd)
+    return got, (mbuf.to_numpy().reshape(heads, pages) if mass else None)
+
+
+def test_decode_over_mixed_tiers_is_the_oracle():
+    """One decode query over a cache whose pages were born at every tier,
+    own page FP16 from the open page and the row it brought: output and
+    per-page masses against the float64 causal view."""
+    def check(P, shape, seq, bias):
+        heads, kv, hd = shape
+        cycle = [1, 0, 3, 2]
+        tmap = [[cycle[i % 4] for i in range(seq // P + 1)] for _ in range(LAYERS)]
+        announce("decode mixed", P, shape, seq, bias)
+        m, alloc, cache, k, v, q, b = decode_case(P, kv, hd, heads, tmap, seq, seed=seq, bias=bias)
+        for partials in (True, False):
+            got, mass = run_decode(m, cache, k, v, q, heads, kv, hd, b, partials=partials)
+            want, want_mass = oracle_decode(alloc, P, kv, hd, k, v, q, b)
+            assert_attention_close(got, want, f"P={P} {shape} seq={seq} partials={partials}")
+            assert_mass_close(mass, want_mass, "mass")
+            np.testing.assert_allclose(mass.sum(1), 1.0, atol=1e-5)
+
+    cases = [(32, (12, 2, 128), 32 * 9 + 7, False), (32, (14, 2, 64), 32 * 40 + 1, True),
+             (16, (14, 2, 64), 16 * 20 + 5, False), (48, (12, 2, 128), 48 * 7 + 20, False),
+             (32, (32, 8, 64), 32 * 33, False), (32, (12, 2, 128), 32 * 300 + 31, False)]
+    each(cases, check)
+
+
+def test_asking_for_the_mass_changes_no_output_bit():
+    for P in (16, 32):
+        for tier in (0, 2):
+            announce("mass off", P, tier)
+            tmap = [[tier] * 20 for _ in range(LAYERS)]
+            m, alloc, cache, k, v, q, _ = decode_case(P, 2, 64, 14, tmap, P * 12 + 3, seed=P)
+            on, _ = run_decode(m, cache, k, v, q, 14, 2, 64, mass=True)
+            off, _ = run_decode(m, cache, k, v, q, 14, 2, 64, mass=False)
+            np.testing.assert_array_equal(on, off)
+
+
+def test_the_fused_ewma_is_the_oracle_fold_of_the_kernel_s_masses():
+    """Decode steps with the scores folded in the same pass: the scores
+    equal, to the bit, the oracle's fp32 fold (importance_scores.cu:31-50) of
+    the masses the same kernel wrote; and the masses are the float64 ones."""
+    m = mi()
+    d = m.device
+    P, heads, kv, hd = 32, 12, 2, 128
+    rng = np.random.default_rng(21)
+    seq0 = P * 10 + 4
+    total = seq0 + 40
+    k, v = normal(rng, total, kv, hd), normal(rng, total, kv, hd)
+    tmap = [[(i * 7) % 4 for i in range(total // P + 1)] for _ in range(LAYERS)]
+    alloc, cache = pages_for(P, kv, hd, 0, tier_map=tmap, always_seal=True)
+    max_pages = total // P + 2
+    scores = d.ImportanceScores(LAYERS, max_pages)
+    store_in_runs(cache, 0, k[:seq0], v[:seq0], [seq0])
+    steps = []
+    for t in range(seq0, total):
+        cache.reserve(t + 1)
+        cache.store(0, put(k[t:t + 1]), put(v[t:t + 1]), t, 1)
+        q = normal(rng, 1, heads, hd)
+        announce("ewma step", t)
+        got, mass = run_decode(m, cache, k[:t + 1], v[:t + 1], q, heads, kv, hd, scores=scores)
+        steps.append((0, mass.astype(np.float32)))
+        if t % 13 == 0:
+            want, want_mass = oracle_decode(alloc, P, kv, hd, k[:t + 1], v[:t + 1], q)
+            assert_attention_close(got, want, f"step {t}")
+            assert_mass_close(mass, want_mass, f"step {t}")
+    np.testing.assert_array_equal(scores.download(), ewma.host_ewma(steps, LAYERS, max_pages))
+
+
+def test_downgrade_upgrade_and_moves_are_quantise_of_the_shadow():
+    """A page at tier T is quantise_page(FP16, T) of its shadow; a page back
+    at FP16 is its shadow; a batch leaves every byte, tier and shadow as the
+    per-page path does (tests/test_batched_moves.py:98-126)."""
+    m = mi()
+    P, kv, hd = 32, 2, 128
+    rng = np.random.default_rng(5)
+    seq = P * 12
+    k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+    plan = [(0, 1, 2), (0, 3, 3), (1, 0, 1), (1, 5, 2), (0, 7, 3), (1, 11, 2)]
+    caches = []
+    for batched in (False, True):
+        alloc, cache = pages_for(P, kv, hd, 0, always_seal=True)
+        for layer in range(LAYERS):
+            store_in_runs(cache, layer, k, v, [seq])
+        announce("moves", "batched" if batched else "per-page")
+        if batched:
+            cache.move_pages(plan)
+            assert cache.last_batch["moves"] == len(plan)
+            assert cache.last_batch["shadows_taken"] == len(plan)
+        else:
+            for layer, page, tier in plan:
+                cache.downgrade(layer, page, tier)
+        caches.append((alloc, cache))
+    for (alloc, cache), name in zip(caches, ("per-page", "batched")):
+        for layer, page, tier in plan:
+            shadow = cache.shadow(layer, page)
+            kp = k[page * P:(page + 1) * P].astype(np.float16)
+            vp = v[page * P:(page + 1) * P].astype(np.float16)
+            np.testing.assert_array_equal(shadow, quant.fp16_page(kp, vp))
+            assert cache.page_tier(layer, page) == tier
+            np.testing.assert_array_equal(alloc.read(layer, page),
+                                          quant.quantise_page(kp, vp, tier, P), err_msg=name)
+    a0, c0 = caches[0]
+    a1, c1 = caches[1]
+    np.testing.assert_array_equal(c0.page_tiers(), c1.page_tiers())
+    for layer in range(LAYERS):
+        for page in range(12):
+            np.testing.assert_array_equal(a0.read(layer, page), a1.read(layer, page))
+    # Up again, and across: from the shadows, per page and in a batch.
+    up = [(0, 1, 0), (0, 3, 1), (1, 5, 3)]
+    for layer, page, tier in up:
+        c0.upgrade(layer, page, tier) if tier < plan_tier(plan, layer, page) else \
+            c0.downgrade(layer, page, tier)
+    c1.move_pages(up)
+    for alloc, cache in caches:
+        for layer, page, tier in up:
+            kp = k[page * P:(page + 1) * P].astype(np.float16)
+            vp = v[page * P:(page + 1) * P].astype(np.float16)
+            want = quant.fp16_page(kp, vp) if tier == 0 else quant.quantise_page(kp, vp, tier, P)
+            np.testing.assert_array_equal(alloc.read(layer, page), want)
+            assert cache.page_tier(layer, page) == tier
+
+
+def plan_tier(plan, layer, page):
+    return next(t for l, p, t in plan if l == layer and p == page)
+
+
+def test_refusals_leave_every_byte_unchanged():
+    m = mi()
+    P, kv, hd = 32, 2, 64
+    rng = np.random.default_rng(6)
+    k, v = normal(rng, P * 4, kv, hd), normal(rng, P * 4, kv, hd)
+    alloc, cache = pages_for(P, kv, hd, 0, always_seal=True)
+    for layer in range(LAYERS):
+        store_in_runs(cache, layer, k, v, [P * 4])
+    cache.downgrade(0, 1, 2)
+    before = [[alloc.read(l, p) for p in range(4)] for l in range(LAYERS)]
+    tiers = cache.page_tiers().copy()
+    with pytest.raises(ValueError, match="lower"):
+        cache.downgrade(0, 1, 1)
+    with pytest.raises(ValueError, match="higher"):
+        cache.upgrade(0, 2, 1)
+    with pytest.raises(ValueError, match="twice"):
+        cache.move_pages([(0, 2, 3), (0, 2, 2)])
+    with pytest.raises(ValueError, match="already"):
+        cache.move_pages([(0, 2, 0)])
+    with pytest.raises(ValueError, match="not a page of positions"):
+        cache.move_pages([(0, 9, 2)])
+    m.fail_next_granules(1)
+    with pytest.raises(m.OutOfMemory):
+        cache.move_pages([(0, 0, 3), (1, 3, 3), (1, 2, 1)])
+    m.fail_next_granules(0)
+    np.testing.assert_array_equal(cache.page_tiers(), tiers)
+    for l in range(LAYERS):
+        for p in range(4):
+            np.testing.assert_array_equal(alloc.read(l, p), before[l][p])
+
+
+def test_an_evicted_page_reads_as_a_masked_one_to_the_bit():
+    """tests/test_split_attention.py:295-319: attention over a cache with a
+    page evicted is, to the bit, attention over the same cache with it
+    masked; its mass is 0."""
+    m = mi()
+    P, heads, kv, hd = 32, 12, 2, 128
+    rng = np.random.default_rng(8)
+    seq = P * 20 + 3
+    k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+    q = normal(rng, 1, heads, hd)
+    outs = []
+    for how in ("evict", "mask"):
+        alloc, cache = pages_for(P, kv, hd, 2)
+        store_in_runs(cache, 0, k, v, [seq - 1, 1])
+        for page in (3, 4, 11):
+            getattr(cache, how)(0, page)
+        announce("unread", how)
+        got, mass = run_decode(m, cache, k, v, q, heads, kv, hd)
+        assert np.all(mass[:, [3, 4, 11]] == 0)
+        outs.append(got)
+        if how == "mask":
+            pages, tiers = sealed_pages(alloc, 0, seq // P)
+            for p in (3, 4, 11):
+                tiers[p] = quant.UNREAD
+            want, want_mass = att.causal_decode(q, pages, tiers, k[(seq // P) * P:],
+                                                v[(seq // P) * P:], kv, hd, P)
+            assert_attention_close(got, want, "masked")
+            assert_mass_close(mass, want_mass, "masked mass")
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+def test_full_size_config3_layer_against_the_oracle():
+    """BASELINE config 3 at its full size on one layer: 32K positions of
+    Qwen2.5-1.5B shape, tiers 20/30/40/10 by seeded importance, built by
+    storing all rows (pages sealed at birth tier in batched launches), then
+    one decode with the fused mass and EWMA, against the float64 oracle."""
+    from microinfer import workloads as w
+    m = mi()
+    d = m.device
+    shape = w.QWEN_15B
+    P, seq = 32, 32768
+    rng = np.random.default_rng(0)
+    outliers = w.outlier_channels(rng, shape.kv_width)
+    k, v = w.kv_rows(rng, seq, shape, outliers)
+    tmap = [w.tiers_by_importance(np.random.default_rng(0), seq // P - 1, w.MIX_CONFIG3).tolist()]
+    tmap = tmap * LAYERS
+    alloc, cache = pages_for(P, shape.kv_heads, shape.head_dim, 0, tier_map=tmap,
+                             always_seal=True, capacity=1100 * LAYERS)
+    announce("config3 full layer: store")
+    store_in_runs(cache, 0, k.astype(np.float32), v.astype(np.float32), [seq - 1, 1])
+    counts = np.bincount(cache.page_tiers()[0][:seq // P - 1], minlength=4)
+    assert list(counts) == [205, 307, 409, 102]
+    q = fp16_exact(rng.standard_normal((1, shape.heads, shape.head_dim)))
+    scores = d.ImportanceScores(LAYERS, seq // P)
+    announce("config3 full layer: decode")
+    got, mass = run_decode(m, cache, k.astype(np.float32), v.astype(np.float32), q, shape.heads,
+                           shape.kv_heads, shape.head_dim, scores=scores)
+    want, want_mass = oracle_decode(alloc, P, shape.kv_heads, shape.head_dim, k, v, q)
+    assert_attention_close(got, want, "config3")
+    assert_mass_close(mass, want_mass, "config3 mass")
+    np.testing.assert_array_equal(scores.download()[0],
+                                  ewma.host_ewma([(0, mass.astype(np.float32))], 1, seq // P)[0])
