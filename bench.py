@@ -159,7 +159,8 @@ def requant_plan(m, shape, context, seed=0, layers=None):
     up_s = time.perf_counter() - t0
     # Bit-exactness spot check of a few moved pages against the oracle.
     from oracle import quant
-    for layer, page, tier in (down[0], down[n4], up[0]):
+    for layer, page, _ in (down[0], down[n4], down[-1], up[0], up[-1]):
+        tier = int(cache.page_tier(layer, page))
         shadow = cache.shadow(layer, page)
         kp, vp = quant.read_fp16_page(shadow, P, shape.kv_heads, shape.head_dim)
         if not np.array_equal(alloc.read(layer, page), quant.quantise_page(kp, vp, tier, P)):
@@ -250,7 +251,6 @@ def main() -> int:
     requant = None
     if not args.no_requant:
         t0 = time.perf_counter()
-        del cache, alloc
         requant = requant_plan(m, shape, context, layers=layers)
         log(f"requant plan in {time.perf_counter() - t0:.1f}s: {requant}")
 

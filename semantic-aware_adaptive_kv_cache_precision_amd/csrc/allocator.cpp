@@ -31,6 +31,29 @@ namespace mi
       prop.location.id = device;
       return prop;
     }
+
+    // The unit each tier's range is backed and released in: the driver's
+    // recommended granularity, and at least 2 MiB, as a whole multiple of its
+    // minimum. On MI355X the minimum is 4 KiB; a 32K-context cache mapped at
+    // that would take hundreds of thousands of physical allocations, past
+    // what the driver hands out (hipMemCreate then fails with VRAM free), so
+    // the allocator maps 2 MiB granules, the reference's own.
+    constexpr std::size_t kMinGranule = std::size_t{2} << 20;
+
+    std::size_t mapping_unit(const hipMemAllocationProp &prop)
+    {
+      std::size_t minimum = 0, recommended = 0;
+      hip_check(hipMemGetAllocationGranularity(&minimum, &prop, hipMemAllocationGranularityMinimum),
+                "hipMemGetAllocationGranularity");
+      if (hipMemGetAllocationGranularity(&recommended, &prop,
+                                         hipMemAllocationGranularityRecommended) != hipSuccess)
+      {
+        (void)hipGetLastError();
+        recommended = minimum;
+      }
+      const std::size_t unit = std::max({minimum, recommended, kMinGranule});
+      return minimum > 0 ? round_up(unit, minimum) : unit;
+    }
   } // namespace
 
   namespace
@@ -71,11 +94,7 @@ namespace mi
   {
     int device = 0;
     hip_check(hipGetDevice(&device), "hipGetDevice");
-    hipMemAllocationProp prop = device_prop(device);
-    std::size_t granule = 0;
-    hip_check(hipMemGetAllocationGranularity(&granule, &prop, hipMemAllocationGranularityMinimum),
-              "hipMemGetAllocationGranularity");
-    return granule;
+    return mapping_unit(device_prop(device));
   }
 
   PagedKVCache::PagedKVCache(const std::array<std::size_t, kTierCount> &page_bytes,
@@ -90,8 +109,7 @@ namespace mi
     }
     hip_check(hipGetDevice(&device_), "hipGetDevice");
     prop_ = device_prop(device_);
-    hip_check(hipMemGetAllocationGranularity(&granule_, &prop_, hipMemAllocationGranularityMinimum),
-              "hipMemGetAllocationGranularity");
+    granule_ = mapping_unit(prop_);
     try
     {
       for (int t = 0; t < kTierCount; ++t)

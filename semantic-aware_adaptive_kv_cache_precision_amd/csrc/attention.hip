@@ -52,7 +52,7 @@ namespace mi
       int head_dim;
       int own;                  // the query tile's own page (causal)
 
-      __device__ static float h2f(std::uint16_t h) { return half_bits_to_float(h); }
+      __device__ static float h2f(std::uint16_t h) { return mi::h2f(h); }
 
       template <int Bits>
       __device__ static void dequant(const std::uint8_t *page, const PageLayout &L, int t,
@@ -153,8 +153,8 @@ namespace mi
       const int half = head_dim / 2;
       const int j = d < half ? d : d - half;
       const float *cs = rope + 2 * (static_cast<std::size_t>(position) * half + j);
-      const float b1 = half_bits_to_float(bias[j]);
-      const float b2 = half_bits_to_float(bias[j + half]);
+      const float b1 = h2f(bias[j]);
+      const float b2 = h2f(bias[j + half]);
       return d < half ? b1 * cs[0] - b2 * cs[1] : b2 * cs[0] + b1 * cs[1];
     }
 
@@ -216,7 +216,7 @@ namespace mi
       {
         const int r = i / hd;
         const int d = i % hd;
-        q_s[i] = stored(r) ? half_bits_to_float(a.q[query_of(r) * token_stride +
+        q_s[i] = stored(r) ? h2f(a.q[query_of(r) * token_stride +
                                                     static_cast<std::size_t>(head_of(r)) * hd + d]) *
                                  scale
                            : 0.0f;
@@ -415,56 +415,85 @@ namespace mi
     // Folds the runs: M = max m_s, w_s = exp(m_s - M), out = sum(w o) / sum(w l);
     // a page's mass, relative to its run's m, is weighed by its run's w and
     // divided by the same sum (reference: attention.cu:754-815; no carry, as
-    // runs are whole pages here). One block a (query, head).
-    __global__ void combine_kernel(const float *__restrict__ partials, std::uint16_t *__restrict__ out,
-                                   int seq_q, int heads, int head_dim, int splits, int split_keys,
-                                   float *__restrict__ mass, int page_tokens, int seq_k)
+    // runs are whole pages here). One block a (query, head); a thread a run,
+    // the sums over runs taken through LDS, never by one thread alone.
+    constexpr int kCombineThreads = 256;
+    constexpr int kCombineDims = 32;
+
+    __global__ void __launch_bounds__(kCombineThreads)
+        combine_kernel(const float *__restrict__ partials, std::uint16_t *__restrict__ out,
+                       int seq_q, int heads, int head_dim, int splits, int split_keys,
+                       float *__restrict__ mass, int page_tokens, int seq_k)
     {
-      extern __shared__ float weight_s[];
+      extern __shared__ float s_w[]; // a weight per run
+      __shared__ float s_red[kCombineThreads / 64];
+      __shared__ float s_acc[kCombineThreads][kCombineDims + 1];
       const int query = blockIdx.x / heads;
       const int head = blockIdx.x % heads;
+      const int t = threadIdx.x;
       const std::size_t sf = slot_floats(head_dim);
       const auto slot = [&](int s) {
         return partials + ((static_cast<std::size_t>(s) * seq_q + query) * heads + head) * sf;
       };
-      if (threadIdx.x == 0)
+      float top = -INFINITY;
+      for (int s = t; s < splits; s += kCombineThreads)
       {
-        float m = -INFINITY;
-        for (int s = 0; s < splits; ++s)
-        {
-          m = fmaxf(m, slot(s)[0]);
-        }
-        float l = 0.0f;
-        for (int s = 0; s < splits; ++s)
-        {
-          const float w = expf(slot(s)[0] - m);
-          weight_s[s] = w;
-          l += slot(s)[1] * w;
-        }
-        weight_s[splits] = l;
+        top = fmaxf(top, slot(s)[0]);
       }
-      __syncthreads();
-      const float l = weight_s[splits];
-      for (int d = threadIdx.x; d < head_dim; d += blockDim.x)
+      top = block_reduce<true>(top, s_red);
+      float l = 0.0f;
+      for (int s = t; s < splits; s += kCombineThreads)
       {
-        float acc = 0.0f;
-        for (int s = 0; s < splits; ++s)
+        // A run none of whose keys this row reads weighs exactly 0.
+        const float w = expf(slot(s)[0] - top);
+        s_w[s] = w;
+        l += slot(s)[1] * w;
+      }
+      l = block_reduce<false>(l, s_red);
+      for (int d0 = 0; d0 < head_dim; d0 += kCombineDims)
+      {
+        const int n = min(kCombineDims, head_dim - d0);
+        float acc[kCombineDims];
+        for (int d = 0; d < kCombineDims; ++d)
         {
-          acc += slot(s)[2 + d] * weight_s[s];
+          acc[d] = 0.0f;
         }
-        out[(static_cast<std::size_t>(query) * heads + head) * head_dim + d] =
-            __half_as_ushort(__float2half(acc / l));
+        for (int s = t; s < splits; s += kCombineThreads)
+        {
+          const float *p = slot(s) + 2 + d0;
+          for (int d = 0; d < n; ++d)
+          {
+            acc[d] += p[d] * s_w[s];
+          }
+        }
+        __syncthreads();
+        for (int d = 0; d < kCombineDims; ++d)
+        {
+          s_acc[t][d] = acc[d];
+        }
+        __syncthreads();
+        if (t < n)
+        {
+          float sum = 0.0f;
+          for (int u = 0; u < kCombineThreads; ++u)
+          {
+            sum += s_acc[u][t];
+          }
+          out[(static_cast<std::size_t>(query) * heads + head) * head_dim + d0 + t] =
+              __half_as_ushort(__float2half(sum / l));
+        }
       }
       if (mass == nullptr)
       {
         return;
       }
+      __syncthreads();
       const int pages = (seq_k + page_tokens - 1) / page_tokens;
       float *head_mass = mass + static_cast<std::size_t>(head) * pages;
-      for (int page = threadIdx.x; page < pages; page += blockDim.x)
+      for (int page = t; page < pages; page += kCombineThreads)
       {
         const int s = page * page_tokens / split_keys;
-        head_mass[page] = head_mass[page] * weight_s[s] / l;
+        head_mass[page] = head_mass[page] * s_w[s] / l;
       }
     }
 
@@ -680,8 +709,8 @@ namespace mi
     hip_check(hipGetLastError(), "attention kernel launch");
     if (s.splits > 1)
     {
-      hipLaunchKernelGGL(combine_kernel, dim3(a.seq_q * a.heads), dim3(kThreads),
-                         (s.splits + 1) * sizeof(float), stream, a.partials, a.out, a.seq_q,
+      hipLaunchKernelGGL(combine_kernel, dim3(a.seq_q * a.heads), dim3(kCombineThreads),
+                         s.splits * sizeof(float), stream, a.partials, a.out, a.seq_q,
                          a.heads, a.head_dim, s.splits, s.split_keys, mass, rd.src.page_tokens,
                          a.seq_k);
       hip_check(hipGetLastError(), "attention combine kernel launch");

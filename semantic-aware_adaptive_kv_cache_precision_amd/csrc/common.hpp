@@ -233,6 +233,36 @@ namespace mi
     return f;
   }
 
+  // fp16 bits to fp32 on the device: the hardware conversion, exact
+  // (subnormals included, fp16 denormals being on in HIP's default mode).
+  __device__ inline float h2f(std::uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+  // A block's max or sum of one float per thread, returned to every thread.
+  // `scratch` holds a float per wave. Every thread of the block must call it.
+  template <bool kMax>
+  __device__ inline float block_reduce(float v, float *scratch)
+  {
+    for (int offset = warpSize / 2; offset > 0; offset /= 2)
+    {
+      const float o = __shfl_xor(v, offset);
+      v = kMax ? fmaxf(v, o) : v + o;
+    }
+    const int wave = threadIdx.x / warpSize;
+    const int waves = (blockDim.x + warpSize - 1) / warpSize;
+    __syncthreads();
+    if (threadIdx.x % warpSize == 0)
+    {
+      scratch[wave] = v;
+    }
+    __syncthreads();
+    v = scratch[0];
+    for (int w = 1; w < waves; ++w)
+    {
+      v = kMax ? fmaxf(v, scratch[w]) : v + scratch[w];
+    }
+    return v;
+  }
+
   // The group's scale (reference: quant.cu:44-56): its range over the
   // 2^bits - 1 steps, formed in fp64 and rounded to the nearest fp16, then
   // one fp16 ulp up if that fell short of the exact value, so that the last

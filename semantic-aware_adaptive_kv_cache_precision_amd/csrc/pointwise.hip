@@ -42,8 +42,8 @@ namespace mi
         rope_angle(pos, j, head_dim, theta, &s, &c);
         const float sf = static_cast<float>(s);
         const float cf = static_cast<float>(c);
-        const float x1 = half_bits_to_float(x[base + j]);
-        const float x2 = half_bits_to_float(x[base + j + half]);
+        const float x1 = h2f(x[base + j]);
+        const float x2 = h2f(x[base + j + half]);
         out[base + j] = __half_as_ushort(__float2half(x1 * cf - x2 * sf));
         out[base + j + half] = __half_as_ushort(__float2half(x2 * cf + x1 * sf));
       }
@@ -65,7 +65,7 @@ namespace mi
 
     __device__ inline float widen(const std::uint16_t *x, std::size_t i)
     {
-      return half_bits_to_float(x[i]);
+      return h2f(x[i]);
     }
     __device__ inline float widen(const float *x, std::size_t i) { return x[i]; }
 
@@ -105,7 +105,7 @@ namespace mi
       __syncthreads();
       for (int i = threadIdx.x; i < hidden; i += blockDim.x)
       {
-        const float v = widen(x, row + i) * scale * half_bits_to_float(weight[i]);
+        const float v = widen(x, row + i) * scale * h2f(weight[i]);
         out[row + i] = __half_as_ushort(__float2half(v));
       }
     }
@@ -117,9 +117,9 @@ namespace mi
       for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
            i < count; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
       {
-        const float g = half_bits_to_float(gate[i]);
+        const float g = h2f(gate[i]);
         const float silu = g / (1.0f + expf(-g));
-        out[i] = __half_as_ushort(__float2half(silu * half_bits_to_float(up[i])));
+        out[i] = __half_as_ushort(__float2half(silu * h2f(up[i])));
       }
     }
 
@@ -129,7 +129,7 @@ namespace mi
       for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
            i < count; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
       {
-        out[i] = __half_as_ushort(__float2half(half_bits_to_float(a[i]) + half_bits_to_float(b[i])));
+        out[i] = __half_as_ushort(__float2half(h2f(a[i]) + h2f(b[i])));
       }
     }
 

@@ -456,7 +456,7 @@ def attention(q, k, v, k_bias=None, theta: float = 0.0) -> np.ndarray:
     seq_k, kv_heads, _ = k.shape
     out = DeviceTensor(q.size)
     dq, dk, dv = upload_fp16(q), upload_fp16(k), upload_fp16(v)
-    partials = FloatTensor(attention_partials(hd))
+    partials = FloatTensor(_attention_partials(hd))
     table = None
     bias = None
     if k_bias is not None:

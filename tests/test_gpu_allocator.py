@@ -115,3 +115,28 @@ def test_spare_granules_are_kept_mapped_beyond_the_tail():
     for i in range(5):
         alloc.free(0, i)
     assert alloc.mapped_bytes(2) == 2 * granule
+
+
+def test_footprint_at_32k_is_the_reference_measurement():
+    """experiments/logs/benchmark.jsonl:48-51: a 28-layer Qwen2.5-1.5B cache
+    reserved for 32K positions maps exactly the reference's measured bytes at
+    every tier (whole 2 MiB granules per tier range, two FP16 open pages a
+    layer once the cache seals)."""
+    import json
+    from conftest import GOLDEN
+    from oracle import quant
+    m = mi()
+    d = m.device
+    f = json.loads((GOLDEN / "known_answers.json").read_text())["footprint_32k_1_5b"]
+    assert m.granule_bytes() == f["granule"]
+    sizes = [quant.page_bytes(t, 2, 128) for t in range(4)]
+    for tier, name in enumerate(("FP16", "INT8", "INT4", "INT2")):
+        announce("footprint", name)
+        cap = [0, 0, 0, 0]
+        cap[tier] = f["layers"] * 1024
+        cap[0] += f["layers"] * 2
+        alloc = m.PagedKVCache(sizes, cap)
+        cache = d.KVPages(alloc, f["layers"], 32, 2, 128, tier)
+        cache.reserve(f["context"])
+        assert sum(alloc.mapped_bytes(t) for t in range(4)) == f["bytes"][name]
+        del cache, alloc

@@ -79,16 +79,31 @@ def test_the_key_bias_completes_each_key():
             assert_attention_close(got, want, f"bias {name}")
 
 
-def test_a_nan_in_a_future_key_does_not_leak():
+def test_attention_is_causal_and_a_nan_key_does_not_leak():
+    """tests/test_attention.py:215-242: changing every key and value after
+    position i moves no bit of query i's output; a NaN in a masked key does
+    not leak; position 0 attends to itself alone."""
     m = mi()
-    heads, kv, hd = 4, 2, 64
-    q, k, v = qkv(3, 10, heads, kv, hd, seed=3)
-    k[9], v[9] = np.nan, np.nan
-    # Queries at positions 7, 8 and 9: only the last sees key 9.
-    got = m.attention(q, k, v)
-    assert np.isfinite(got[:2]).all()
-    want, _ = att.attention64(q[:2], k[:9], v[:9])
-    assert_attention_close(got[:2], want, "masked NaN")
+    heads, kv, hd, _ = SHAPES["qwen2.5-0.5b"]
+    rng = np.random.default_rng(2)
+    for seq in (29, 69):
+        q, k, v = qkv(seq, seq, heads, kv, hd, seed=1)
+        base = m.attention(q, k, v)
+        for i in (0, 1, 16, seq - 2):
+            announce("causal", seq, i)
+            k2, v2 = k.copy(), v.copy()
+            k2[i + 1:] = fp16_exact(1000 * rng.standard_normal(k2[i + 1:].shape))
+            v2[i + 1:] = fp16_exact(1000 * rng.standard_normal(v2[i + 1:].shape))
+            moved = m.attention(q, k2, v2)
+            np.testing.assert_array_equal(moved[:i + 1], base[:i + 1])
+            assert not np.array_equal(moved[i + 1:], base[i + 1:])
+    q, k, v = qkv(41, 41, heads, kv, hd, seed=5)
+    base = m.attention(q, k, v)
+    k2 = k.copy()
+    k2[-1] = np.nan
+    np.testing.assert_array_equal(m.attention(q, k2, v)[:-1], base[:-1])
+    q, k, v = qkv(3, 3, heads, kv, hd, seed=6)
+    np.testing.assert_array_equal(m.attention(q, k, v)[0], np.repeat(v[0], heads // kv, axis=0))
 
 
 def test_split_launches_match_the_reference_and_the_unsplit_one():

@@ -154,9 +154,34 @@ def test_decode_over_mixed_tiers_is_the_oracle():
             np.testing.assert_allclose(mass.sum(1), 1.0, atol=1e-5)
 
     cases = [(32, (12, 2, 128), 32 * 9 + 7, False), (32, (14, 2, 64), 32 * 40 + 1, True),
+             (32, (14, 2, 64), 32 * 40 + 1, False), (32, (12, 2, 128), 32 * 2 + 1, False),
              (16, (14, 2, 64), 16 * 20 + 5, False), (48, (12, 2, 128), 48 * 7 + 20, False),
              (32, (32, 8, 64), 32 * 33, False), (32, (12, 2, 128), 32 * 300 + 31, False)]
     each(cases, check)
+
+
+def test_decode_over_a_cache_that_does_not_seal_is_the_oracle():
+    """An FP16 cache that never seals (config 2's layout: every page FP16 in
+    the page table, the last one partly filled): one decode query with its
+    masses, against float64 over the same keys and values."""
+    m = mi()
+    d = m.device
+    for heads, kv, hd, seq in ((14, 2, 64, 8192 - 5), (12, 2, 128, 32 * 37 + 1), (14, 2, 64, 20)):
+        announce("paged fp16 decode", heads, kv, hd, seq)
+        rng = np.random.default_rng(seq)
+        k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+        alloc, cache = pages_for(32, kv, hd, 0)
+        assert not cache.seals
+        store_in_runs(cache, 0, k, v, [seq - 1, 1])
+        q = normal(rng, 1, heads, hd)
+        pages = -(-seq // 32)
+        out, mass = d.empty(heads * hd), d.empty_f32(heads * pages)
+        cache.attention(0, put(q), None, None, out, 1, seq, heads, kv, hd, None, None, mass,
+                        d.empty_f32(d.attention_partials(hd)))
+        want, w = att.attention64(q, k, v)
+        assert_attention_close(out.to_numpy().reshape(1, heads, hd), want, "paged")
+        assert_mass_close(mass.to_numpy().reshape(heads, pages), att.page_mass(w[:, 0], 32),
+                          "paged mass")
 
 
 def test_asking_for_the_mass_changes_no_output_bit():
