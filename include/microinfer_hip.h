@@ -258,6 +258,19 @@ int mi_kv_attention(mi_kv_pages *kv, int layer, const void *q, const void *k_bia
                     mi_rope_table *rope, void *out, int seq_q, int seq_k, int heads, int kv_heads,
                     int head_dim, const void *keys, const void *values, float *mass, float *scores,
                     float alpha, float *partials);
+/* Beyond the reference (which attends one layer a call, kv_pages.cu:901-947):
+ * one decode query per head for `layers` consecutive layers in one launch,
+ * for callers holding several layers' queries at once. Layer first_layer + i
+ * reads q + i*q_stride, its own rows at keys/values + i*kv_stride, and writes
+ * out + i*out_stride, mass + i*mass_stride, scores + i*scores_stride
+ * (strides in elements; mass and scores may be NULL). Results equal
+ * mi_kv_attention's for each layer with seq_q 1, no key bias, split. */
+int mi_kv_attention_layers(mi_kv_pages *kv, int first_layer, int layers, const void *q,
+                           long long q_stride, void *out, long long out_stride, int seq_k,
+                           int heads, int kv_heads, int head_dim, const void *keys,
+                           const void *values, long long kv_stride, float *mass,
+                           long long mass_stride, float *scores, long long scores_stride,
+                           float alpha);
 int mi_kv_downgrade(mi_kv_pages *kv, int layer, int page, int target);
 int mi_kv_upgrade(mi_kv_pages *kv, int layer, int page, int target);
 /* triples: n (layer, page, target tier), 3n ints. */

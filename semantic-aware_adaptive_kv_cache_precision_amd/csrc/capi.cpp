@@ -903,6 +903,24 @@ int mi_kv_attention(mi_kv_pages *kv, int layer, const void *q, const void *k_bia
   });
 }
 
+int mi_kv_attention_layers(mi_kv_pages *kv, int first_layer, int layers, const void *q,
+                           long long q_stride, void *out, long long out_stride, int seq_k,
+                           int heads, int kv_heads, int head_dim, const void *keys,
+                           const void *values, long long kv_stride, float *mass,
+                           long long mass_stride, float *scores, long long scores_stride,
+                           float alpha)
+{
+  return guarded([&] {
+    if (q == nullptr || out == nullptr)
+    {
+      throw mi::InvalidArgument("q and out must be device pointers, got null");
+    }
+    kv->impl.attention_layers(first_layer, layers, q, q_stride, out, out_stride, seq_k, heads,
+                              kv_heads, head_dim, keys, values, kv_stride, mass, mass_stride,
+                              scores, scores_stride, alpha);
+  });
+}
+
 int mi_kv_downgrade(mi_kv_pages *kv, int layer, int page, int target)
 {
   return guarded([&] { kv->impl.downgrade(layer, page, target); });

@@ -107,4 +107,31 @@ namespace mi
 
   void launch_attention(const KVSource &kv, const AttentionArgs &a, hipStream_t stream);
 
+  // The decode fast path (decode.hip) over `layers` consecutive layers of one
+  // cache in one launch. Layer first_layer + i reads its page addresses and
+  // tiers at kv.pages / kv.tiers + (first_layer + i) * table_stride, its open
+  // page at open_table[first_layer + i] (kv.open when open_table is null),
+  // and its q, chunk rows, output, mass and scores at i times the strides
+  // (in elements) from the AttentionArgs / KVSource bases. AttentionArgs'
+  // partials are not read: the fast path keeps its own workspace.
+  struct DecodeLayers
+  {
+    bool split; // a wave a page and a combine; else a workgroup a KV head
+    int first_layer;
+    int layers;
+    long long table_stride;
+    const unsigned long long *open_table;
+    long long q_stride;
+    long long chunk_stride;
+    long long out_stride;
+    long long mass_stride;
+    long long scores_stride;
+  };
+  // Whether the fast path takes this decode: one query, no key bias, 32-token
+  // pages, head_dim 64 or 128, a group of at most 16 heads, 16-byte aligned
+  // rows and page regions.
+  bool decode_fast_applies(const KVSource &kv, const AttentionArgs &a);
+  void launch_decode_layers(const KVSource &kv, const AttentionArgs &a, const DecodeLayers &ls,
+                            hipStream_t stream);
+
 } // namespace mi

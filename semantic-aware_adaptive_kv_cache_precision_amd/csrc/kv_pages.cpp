@@ -1083,4 +1083,117 @@ namespace mi
     launch_attention(kv, a, runtime_stream());
   }
 
+  const unsigned long long *KVPages::open_table()
+  {
+    std::vector<unsigned long long> now(static_cast<std::size_t>(layers_));
+    for (int l = 0; l < layers_; ++l)
+    {
+      now[l] = reinterpret_cast<unsigned long long>(open_page(l, attend_open_[l]));
+    }
+    if (open_table_ == nullptr)
+    {
+      open_table_ = std::make_unique<DeviceBuffer>(now.size() * sizeof(unsigned long long));
+    }
+    if (now != open_uploaded_)
+    {
+      hip_check(hipMemcpy(open_table_->raw(), now.data(), now.size() * sizeof(unsigned long long),
+                          hipMemcpyHostToDevice),
+                "hipMemcpy open-page table host-to-device");
+      open_uploaded_ = now;
+    }
+    return open_table_->as<const unsigned long long>();
+  }
+
+  void KVPages::attention_layers(int first_layer, int layers, const void *q, long long q_stride,
+                                 void *out, long long out_stride, int seq_k, int heads,
+                                 int kv_heads, int head_dim, const void *keys, const void *values,
+                                 long long kv_stride, float *mass, long long mass_stride,
+                                 float *scores, long long scores_stride, float alpha)
+  {
+    if (layers < 0 || first_layer < 0 || first_layer + layers > layers_)
+    {
+      throw OutOfRange("layers [" + std::to_string(first_layer) + ", " +
+                       std::to_string(first_layer + layers) + ") are not all in this cache's " +
+                       std::to_string(layers_));
+    }
+    if (layers == 0)
+    {
+      return;
+    }
+    if (static_cast<std::size_t>(kv_heads) * head_dim != kv_width_)
+    {
+      throw InvalidArgument("kv_heads * head_dim is " + std::to_string(kv_heads * head_dim) +
+                            "; this cache holds " + std::to_string(kv_width_) + " per token");
+    }
+    if (seq_k <= 0 || seq_k > capacity_tokens())
+    {
+      throw OutOfRange("seq_k " + std::to_string(seq_k) + " is not within the " +
+                       std::to_string(capacity_tokens()) + " positions on pages");
+    }
+    if (seals_ && (keys == nullptr || values == nullptr))
+    {
+      throw InvalidArgument("attention at a quantised tier reads each query's own page from the "
+                            "rows the queries stored; pass them");
+    }
+    if (seals_ && !open_pages_)
+    {
+      throw LogicError("attention before any position was reserved");
+    }
+    KVSource kv{};
+    kv.page_tokens = page_tokens_;
+    AttentionArgs a{};
+    a.q = static_cast<const std::uint16_t *>(q);
+    a.out = static_cast<std::uint16_t *>(out);
+    a.seq_q = 1;
+    a.seq_k = seq_k;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.mass = mass;
+    a.scores = scores;
+    a.alpha = alpha;
+    const LayerTable base = resolve(0);
+    kv.pages = base.pages;
+    if (seals_)
+    {
+      kv.layout = Layout::kCausal;
+      kv.tiers = base.tiers;
+      kv.open = open_page(first_layer, attend_open_[first_layer]);
+      kv.chunk_k = static_cast<const std::uint16_t *>(keys);
+      kv.chunk_v = static_cast<const std::uint16_t *>(values);
+      kv.start = seq_k - 1;
+      for (int t = 0; t < kTierCount; ++t)
+      {
+        kv.may_be_at[t] = may_be_at_[t];
+      }
+    }
+    else
+    {
+      kv.layout = Layout::kPaged;
+      kv.may_be_at[kFP16] = true;
+    }
+    if (decode_fast_applies(kv, a))
+    {
+      DecodeLayers ls{};
+      ls.split = true;
+      ls.first_layer = first_layer;
+      ls.layers = layers;
+      ls.table_stride = table_stride_;
+      ls.open_table = seals_ ? open_table() : nullptr;
+      ls.q_stride = q_stride;
+      ls.chunk_stride = kv_stride;
+      ls.out_stride = out_stride;
+      ls.mass_stride = mass_stride;
+      ls.scores_stride = scores_stride;
+      launch_decode_layers(kv, a, ls, runtime_stream());
+      return;
+    }
+    throw InvalidArgument("attention over several layers in one launch takes one query per "
+                          "head, 32-token pages, head_dim 64 or 128 and at most 16 query heads "
+                          "per KV head, 16-byte aligned; got head_dim " +
+                          std::to_string(head_dim) + ", " + std::to_string(heads) + "/" +
+                          std::to_string(kv_heads) + " heads, " + std::to_string(page_tokens_) +
+                          "-token pages");
+  }
+
 } // namespace mi

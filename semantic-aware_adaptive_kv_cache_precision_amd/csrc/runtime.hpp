@@ -266,6 +266,14 @@ namespace mi
     void attention(int layer, const void *q, const void *k_bias, const RopeTable *rope, void *out,
                    int seq_q, int seq_k, int heads, int kv_heads, int head_dim, const void *keys,
                    const void *values, float *mass, float *scores, float alpha, float *partials);
+    // One decode step of `layers` consecutive layers in one launch: layer
+    // first_layer + i reads its q, chunk rows and writes its output, mass and
+    // scores at i times the strides (elements) from the bases; always split.
+    void attention_layers(int first_layer, int layers, const void *q, long long q_stride,
+                          void *out, long long out_stride, int seq_k, int heads, int kv_heads,
+                          int head_dim, const void *keys, const void *values,
+                          long long kv_stride, float *mass, long long mass_stride,
+                          float *scores, long long scores_stride, float alpha);
     void downgrade(int layer, int page, int target);
     void upgrade(int layer, int page, int target);
     void move_pages(const std::vector<PageMove> &moves);
@@ -318,6 +326,8 @@ namespace mi
     std::size_t bytes_at(int tier) const;
     void require_page_size(int tier, const char *what) const;
     std::uint16_t *open_page(int layer, int which);
+    // Every layer's open page as the next attention reads it, on the device.
+    const unsigned long long *open_table();
     static std::string page_name(PageKey key);
 
     PagedKVCache &allocator_;
@@ -350,6 +360,8 @@ namespace mi
     int table_stride_ = 0;
     int resolved_pages_ = -1;
     std::uint64_t resolved_generation_ = 0;
+    std::unique_ptr<DeviceBuffer> open_table_;
+    std::vector<unsigned long long> open_uploaded_;
     // Address tables for batched launches, grown as needed.
     std::unique_ptr<DeviceBuffer> batch_table_;
   };

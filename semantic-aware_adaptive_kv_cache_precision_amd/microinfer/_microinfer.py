@@ -31,6 +31,7 @@ if not _LIB_PATH.exists():
 lib = C.CDLL(str(_LIB_PATH))
 
 _vp, _sz, _i, _f, _d = C.c_void_p, C.c_size_t, C.c_int, C.c_float, C.c_double
+_ll = C.c_longlong
 _ip, _szp, _fp = C.POINTER(C.c_int), C.POINTER(C.c_size_t), C.POINTER(C.c_float)
 
 
@@ -135,6 +136,8 @@ SIGNATURES = {
     "mi_kv_store": ((_vp, _i, _vp, _vp, _i, _i), C.c_int),
     "mi_kv_attention": ((_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _f,
                          _vp), C.c_int),
+    "mi_kv_attention_layers": ((_vp, _i, _i, _vp, _ll, _vp, _ll, _i, _i, _i, _i, _vp, _vp, _ll,
+                                _vp, _ll, _vp, _ll, _f), C.c_int),
     "mi_kv_downgrade": ((_vp, _i, _i, _i), C.c_int),
     "mi_kv_upgrade": ((_vp, _i, _i, _i), C.c_int),
     "mi_kv_move_pages": ((_vp, _ip, _sz), C.c_int),
@@ -318,6 +321,23 @@ def granule_bytes() -> int:
     g = C.c_size_t()
     _check(lib.mi_granule_bytes(C.byref(g)))
     return g.value
+
+
+def copy_pages(sources, destinations, nbytes: int) -> None:
+    """Copies nbytes from each device address in `sources` to the matching
+    one in `destinations`, all in one launch of the batched page copy
+    (page_copy.cu:41-70), on the null stream, then waits for it. No copy
+    may read what another writes."""
+    src = np.ascontiguousarray(sources, np.uint64).reshape(-1)
+    dst = np.ascontiguousarray(destinations, np.uint64).reshape(-1)
+    if src.size != dst.size:
+        raise ValueError(f"{src.size} sources for {dst.size} destinations")
+    if src.size == 0:
+        return
+    tables = _Storage(16 * src.size)
+    _h2d(tables.ptr, np.concatenate([src, dst]))
+    _check(lib.mi_copy_pages(tables.ptr, tables.ptr + 8 * src.size, nbytes, src.size, None))
+    synchronize()  # the tables are freed on return
 
 
 def synchronize() -> None:
@@ -888,6 +908,38 @@ class KVPages:
         _check(lib.mi_kv_attention(self._h, layer, qa, ba, rope._h if rope is not None else None,
                                    oa, seq_q, seq_k, heads, kv_heads, head_dim, ka, va, ma, sa,
                                    alpha, pa))
+
+    def attention_layers(self, first_layer: int, layers: int, q, out, seq_k: int, heads: int,
+                         kv_heads: int, head_dim: int, keys=None, values=None, mass=None,
+                         scores=None):
+        """Beyond the reference's surface: one decode query per head for
+        `layers` consecutive layers in one launch. q and out hold (layers,
+        heads, head_dim) fp16, keys/values (layers, kv_width) (the query's
+        own rows), mass (layers, heads, pages) floats; `scores` an
+        ImportanceScores whose rows first_layer.. take the fold. Each layer's
+        results equal attention(layer, ..., seq_q=1, partials=...)'s."""
+        _non_negative(layers, "layers")
+        per_q = heads * head_dim
+        width = kv_heads * head_dim
+        qa = _need(_span(q), layers * per_q, "q")
+        oa = _need(_span(out), layers * per_q, "out")
+        ka = _need(_span(keys), layers * width, "keys") if keys is not None else None
+        va = _need(_span(values), layers * width, "values") if values is not None else None
+        pages = -(-seq_k // self.page_tokens)
+        ma = None
+        if mass is not None:
+            if mass.numel < layers * heads * pages:
+                raise ValueError(f"the per-page attention mass of {layers} layers needs "
+                                 f"{layers * heads * pages} floats; got {mass.numel}")
+            ma = mass.address
+        sa, stride, alpha = None, 0, 0.0
+        if scores is not None:
+            if pages > scores.max_pages:
+                raise ValueError(f"{pages} pages; the scores hold up to {scores.max_pages}")
+            sa, stride, alpha = scores.row(first_layer), scores.max_pages, scores.alpha
+        _check(lib.mi_kv_attention_layers(self._h, first_layer, layers, qa, per_q, oa, per_q,
+                                          seq_k, heads, kv_heads, head_dim, ka, va, width, ma,
+                                          heads * pages, sa, stride, alpha))
 
     def page_tier(self, layer: int, page: int) -> Tier:
         t = C.c_int()

@@ -226,6 +226,62 @@ def test_the_fused_ewma_is_the_oracle_fold_of_the_kernel_s_masses():
     np.testing.assert_array_equal(scores.download(), ewma.host_ewma(steps, LAYERS, max_pages))
 
 
+def test_one_launch_over_several_layers_is_each_layer_s_own_launch():
+    """attention_layers, beyond the reference (several layers' decode queries
+    in one launch), gives to the bit what one split attention call a layer
+    gives: outputs, masses and the scores folded over two steps; and the
+    first and last layers match the oracle. Also a sub-range of layers, and
+    a range past the cache refused."""
+    m = mi()
+    d = m.device
+    P, heads, kv, hd, L = 32, 12, 2, 128, 3
+    for seq in (32 * 9 + 7, 32 * 64, 33):
+        announce("layers in one launch", seq)
+        rng = np.random.default_rng(seq)
+        cap = [4096] * 4
+        cap[0] += L * 2 + 8
+        alloc = m.PagedKVCache(page_sizes(P, kv, hd), cap)
+        tmap = [[(i * 5 + l) % 4 for i in range(seq // P + 1)] for l in range(L)]
+        cache = d.KVPages(alloc, L, P, kv, hd, 0, d.Halves.Both, tmap, True)
+        k, v = normal(rng, L, seq, kv, hd), normal(rng, L, seq, kv, hd)
+        for l in range(L):
+            store_in_runs(cache, l, k[l], v[l], [seq - 1, 1])
+        pages = -(-seq // P)
+        max_pages = pages + 1
+        together, alone = d.ImportanceScores(L, max_pages), d.ImportanceScores(L, max_pages)
+        part = d.empty_f32(d.attention_partials(hd))
+        own_k, own_v = put(k[:, -1]), put(v[:, -1])
+        for step in range(2):
+            q = normal(rng, L, heads, hd)
+            out, mass = d.empty(L * heads * hd), d.empty_f32(L * heads * pages)
+            cache.attention_layers(0, L, put(q), out, seq, heads, kv, hd, own_k, own_v, mass,
+                                   scores=together)
+            got = out.to_numpy().reshape(L, heads, hd)
+            got_mass = mass.to_numpy()[:L * heads * pages].reshape(L, heads, pages)
+            for l in range(L):
+                o1, m1 = d.empty(heads * hd), d.empty_f32(heads * pages)
+                cache.attention(l, put(q[l]), None, None, o1, 1, seq, heads, kv, hd,
+                                put(k[l, -1:]), put(v[l, -1:]), m1, part, scores=alone)
+                np.testing.assert_array_equal(got[l], o1.to_numpy().reshape(heads, hd))
+                np.testing.assert_array_equal(got_mass[l], m1.to_numpy().reshape(heads, pages))
+            np.testing.assert_array_equal(together.download(), alone.download())
+        own = (seq - 1) // P
+        for l in (0, L - 1):
+            sealed, tiers = sealed_pages(alloc, l, own)
+            want, want_mass = att.causal_decode(q[l:l + 1], sealed, tiers, k[l, own * P:],
+                                                v[l, own * P:], kv, hd, P)
+            assert_attention_close(got[l:l + 1], want, f"layer {l} seq={seq}")
+            assert_mass_close(got_mass[l], want_mass, f"layer {l} mass")
+        # Layers 1 and 2 alone: the same bits as in the three-layer launch.
+        out2 = d.empty(2 * heads * hd)
+        cache.attention_layers(1, 2, put(q[1:]), out2, seq, heads, kv, hd, put(k[1:, -1]),
+                               put(v[1:, -1]))
+        np.testing.assert_array_equal(out2.to_numpy().reshape(2, heads, hd), got[1:])
+        with pytest.raises(IndexError):
+            cache.attention_layers(2, 2, put(q[1:]), out2, seq, heads, kv, hd, put(k[1:, -1]),
+                                   put(v[1:, -1]))
+
+
 def test_downgrade_upgrade_and_moves_are_quantise_of_the_shadow():
     """A page at tier T is quantise_page(FP16, T) of its shadow; a page back
     at FP16 is its shadow; a batch leaves every byte, tier and shadow as the
