@@ -171,6 +171,36 @@ def requant_plan(m, shape, context, seed=0, layers=None):
             "shadows_taken": cache.last_batch and len(down)}
 
 
+def copy_peak(m, page=32768, count=32768, reps=10) -> float:
+    """The achieved HBM rate of a plain device copy (1 GiB read + 1 GiB
+    written a launch, the batched page-copy kernel), GB/s of read + write."""
+    arena = m.DeviceArena(2 * page * count)
+    src = [arena.address + i * page for i in range(count)]
+    copy = m.PageCopy(src, [a + page * count for a in src], page)
+    copy.launch()
+    m.synchronize()
+    timer = m.Timer()
+    timer.start()
+    for _ in range(reps):
+        copy.launch()
+    timer.stop()
+    m.synchronize()
+    return 2 * page * count * reps / (timer.elapsed_ms() * 1e-3) / 1e9
+
+
+def profiled_traffic(path=REPO / "profiles" / "decode_attention_config3_hbm_bytes.md"):
+    """HBM bytes one layer's decode launch pair moves, from the committed
+    counter summary of this bench (FETCH_SIZE and WRITE_SIZE per dispatch,
+    scaled by the copy reference); None when the summary is absent."""
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_layer:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -198,6 +228,8 @@ def main() -> int:
         m.copy_pages(src, [a + page * count for a in src], page)
         log(f"copied {page * count} bytes in one copy_pages launch")
         return 0
+    copy_gbs = copy_peak(m)
+    log(f"device copy: {copy_gbs:.0f} GB/s (read + write)")
     shape = w.QWEN_15B
     context = 32768
     layers = args.layers or shape.layers
@@ -332,7 +364,12 @@ def main() -> int:
         "pct_hbm_peak": round(100 * gbs / PEAK_GBS, 2),
         "bytes_per_step": step_bytes,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / PEAK_GBS, 4), "traffic": profiled_traffic(),
+                     "kernel": "decode_pages_kernel + decode_combine_kernel, one layer's "
+                               "launch pair; achieved = algorithmic bytes a layer / live "
+                               "per-layer time (HIP events on the graph's stream)",
+                     "algorithmic_bytes_per_layer": round(step_bytes / layers),
+                     "measured_copy_gb_per_s": round(copy_gbs, 1)},
         "one_launch_all_layers": {"us_per_token": round(ms_all * 1e3 * shape.layers / layers, 2),
                                   "gb_per_s": round(gbs_all, 1),
                                   "pct_hbm_peak": round(100 * gbs_all / PEAK_GBS, 2),

@@ -18,5 +18,4 @@ Modules:
   ewma       the importance-score EWMA in fp32, in the device's order
   slots      the tail-swap page allocator and its granule accounting
   pointwise  RoPE, RMSNorm, SwiGLU float64 references
-  workloads  the seeded synthetic KV of the benchmark configurations
 """

@@ -323,21 +323,31 @@ def granule_bytes() -> int:
     return g.value
 
 
+class PageCopy:
+    """A batch of page copies (page_copy.cu:41-70): nbytes from each device
+    address in `sources` to the matching one in `destinations`, the address
+    tables uploaded once; launch() enqueues the one batched copy on the null
+    stream. No copy may read what another writes."""
+
+    def __init__(self, sources, destinations, nbytes: int):
+        src = np.ascontiguousarray(sources, np.uint64).reshape(-1)
+        dst = np.ascontiguousarray(destinations, np.uint64).reshape(-1)
+        if src.size != dst.size:
+            raise ValueError(f"{src.size} sources for {dst.size} destinations")
+        self.count, self.nbytes = int(src.size), int(nbytes)
+        self._tables = _Storage(max(16 * src.size, 16))
+        _h2d(self._tables.ptr, np.concatenate([src, dst]))
+
+    def launch(self) -> None:
+        if self.count:
+            _check(lib.mi_copy_pages(self._tables.ptr, self._tables.ptr + 8 * self.count,
+                                     self.nbytes, self.count, None))
+
+
 def copy_pages(sources, destinations, nbytes: int) -> None:
-    """Copies nbytes from each device address in `sources` to the matching
-    one in `destinations`, all in one launch of the batched page copy
-    (page_copy.cu:41-70), on the null stream, then waits for it. No copy
-    may read what another writes."""
-    src = np.ascontiguousarray(sources, np.uint64).reshape(-1)
-    dst = np.ascontiguousarray(destinations, np.uint64).reshape(-1)
-    if src.size != dst.size:
-        raise ValueError(f"{src.size} sources for {dst.size} destinations")
-    if src.size == 0:
-        return
-    tables = _Storage(16 * src.size)
-    _h2d(tables.ptr, np.concatenate([src, dst]))
-    _check(lib.mi_copy_pages(tables.ptr, tables.ptr + 8 * src.size, nbytes, src.size, None))
-    synchronize()  # the tables are freed on return
+    """One batched copy of nbytes per (source, destination), waited for."""
+    PageCopy(sources, destinations, nbytes).launch()
+    synchronize()
 
 
 def synchronize() -> None:
