@@ -306,29 +306,29 @@ def main() -> int:
     stream.synchronize()
     gbs_all = step_bytes / (ms_all * 1e-3) / 1e9
     log(f"one launch over {layers} layers: {ms_all * 1e3:.1f} us/step, {gbs_all:.0f} GB/s")
-    got_all = out_all.to_numpy().reshape(layers, heads * hd)
-    for layer in range(layers):
-        if not np.array_equal(got_all[layer], outs[layer].to_numpy()):
-            raise AssertionError(f"layer {layer}: the all-layer launch differs from its own")
-    if not np.array_equal(scores_all.download(), scores.download()):
-        # Both folded warmup + steps + the eager call: the same number of times.
-        raise AssertionError("the all-layer launch's scores differ from the per-layer ones")
+    got_all = out_all.to_numpy().reshape(layers, 1, heads, hd)
 
-    # Parity of the timed path on the first and last layer.
+    # Parity of both timed paths against the oracle on three layers.
     from oracle import attention as att
-    for layer in (0, layers - 1):
+    for layer in sorted({0, layers // 2, layers - 1}):
         sealed = context // P - 1
         pages = [alloc.read(layer, i) for i in range(sealed)]
         tiers = [int(alloc.locate(layer, i)[0]) for i in range(sealed)]
         k, v = host_rows[layer]
         q = qs[layer].raw().reshape(1, heads, hd)
-        want, _ = att.causal_decode(q, pages, tiers, k[sealed * P:], v[sealed * P:],
-                                    shape.kv_heads, hd, P)
-        got = outs[layer].to_numpy().reshape(1, heads, hd)
-        err = np.abs(got - want) / (np.abs(want) + 1e-4 * np.abs(want).max())
-        if err.max() > 1e-3:
-            raise AssertionError(f"layer {layer}: timed output off the oracle by {err.max():.3g}")
-    log("parity of the timed path: ok")
+        want, _, bound = att.causal_decode(q, pages, tiers, k[sealed * P:], v[sealed * P:],
+                                           shape.kv_heads, hd, P, with_bound=True)
+        # The reference's error gate (tests/ulp_gate.py, tests/test_attention.py:58-115)
+        # held to 1e-3: relative error floored at fp16's least normal and where the
+        # fp32 error bound spends the budget.
+        floor = np.maximum(att.FP16_MIN_NORMAL, bound / 1e-3)
+        for name, got in (("per-layer", outs[layer].to_numpy().reshape(1, heads, hd)),
+                          ("one-launch", got_all[layer])):
+            err = np.abs(got - want) / np.maximum(np.abs(want), floor)
+            if err.max() >= 1e-3 or err.mean() >= 2.0**-11:
+                raise AssertionError(f"layer {layer}: the {name} output is off the oracle: "
+                                     f"max {err.max():.3g}, mean {err.mean():.3g}")
+    log("parity of both timed paths: ok")
 
     requant = None
     if not args.no_requant:

@@ -263,8 +263,9 @@ int mi_kv_attention(mi_kv_pages *kv, int layer, const void *q, const void *k_bia
  * for callers holding several layers' queries at once. Layer first_layer + i
  * reads q + i*q_stride, its own rows at keys/values + i*kv_stride, and writes
  * out + i*out_stride, mass + i*mass_stride, scores + i*scores_stride
- * (strides in elements; mass and scores may be NULL). Results equal
- * mi_kv_attention's for each layer with seq_q 1, no key bias, split. */
+ * (strides in elements; mass and scores may be NULL). Results are
+ * mi_kv_attention's for each layer (seq_q 1, no key bias) within the
+ * attention tolerance: the pages are split among waves differently. */
 int mi_kv_attention_layers(mi_kv_pages *kv, int first_layer, int layers, const void *q,
                            long long q_stride, void *out, long long out_stride, int seq_k,
                            int heads, int kv_heads, int head_dim, const void *keys,

@@ -81,6 +81,42 @@ def attention64(q, k, v, k_bias=None, theta: float = 0.0, unread=None, positions
     return out, p
 
 
+#: fp32's unit roundoff, and the smallest normal fp16: the two constants of
+#: the reference's error gate (tests/ulp_gate.py:28-38).
+FP32_REL_ULP = 2.0**-24
+FP16_MIN_NORMAL = 6.103515625e-05
+
+
+def attention_bound(q, k, v, weights, k_bias=None, theta: float = 0.0, unread=None,
+                    positions=None):
+    """Per output element, the absolute error an fp32-accumulating kernel
+    may carry (tests/test_attention.py:58-107): the fp32 sum over the
+    visible keys, sqrt(n) * u32 * terms with terms = sum_j p_j |v_j|, plus
+    the fp32 scores' rounding, sqrt(hd) * u32 * (largest sum_d |q_d k_d| /
+    sqrt(hd) over the visible keys), weighing the same terms. `weights` are
+    attention64's. Returns (seq_q, heads, hd)."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    seq_q, heads, hd = q.shape
+    seq_k = k.shape[0]
+    if k_bias is not None:
+        k = k + rotated_bias(k_bias, seq_k, theta)
+    if positions is None:
+        positions = np.arange(seq_q) + (seq_k - seq_q)
+    positions = np.asarray(positions)
+    kk, vv = expand_kv(heads, k), expand_kv(heads, v)
+    terms = np.einsum("hqk,khd->qhd", weights, np.abs(vv))
+    score_terms = np.einsum("qhd,khd->hqk", np.abs(q), np.abs(kk)) / np.sqrt(hd)
+    masked = np.arange(seq_k)[None, :] > positions[:, None]
+    if unread is not None:
+        masked = masked | np.asarray(unread, bool)[None, :]
+    score_terms[:, masked] = 0.0
+    score_terms = score_terms.max(axis=-1).T[..., None]
+    visible = (positions + 1)[:, None, None]
+    return (np.sqrt(visible) + np.sqrt(hd) * score_terms) * FP32_REL_ULP * terms
+
+
 def page_mass(weights: np.ndarray, page_tokens: int) -> np.ndarray:
     """(heads, seq_k) softmax weights of one query -> (heads, pages), each
     page's share (tests/test_attention_mass.py:68-86)."""
@@ -118,17 +154,21 @@ def read_sealed(pages, tiers, kv_heads: int, head_dim: int, page_tokens: int):
 
 
 def causal_decode(q, sealed_pages, tiers, own_k, own_v, kv_heads: int, head_dim: int,
-                  page_tokens: int, k_bias=None, theta: float = 0.0):
+                  page_tokens: int, k_bias=None, theta: float = 0.0, with_bound: bool = False):
     """One decode query over a cache that seals (tests/test_quantised_pages.py:86-105):
     the sealed pages before its own at their tiers, then its own page's rows
     as they came, `own_k`/`own_v` (n_own, kv, hd), the last of them the
-    query's own position. Returns (out (1, heads, hd), mass (heads, pages))."""
+    query's own position. Returns (out (1, heads, hd), mass (heads, pages)),
+    and attention_bound's error bound third when `with_bound`."""
     K, V, unread = read_sealed(sealed_pages, tiers, kv_heads, head_dim, page_tokens)
     k = np.concatenate([K, np.asarray(own_k, np.float64)])
     v = np.concatenate([V, np.asarray(own_v, np.float64)])
     flags = np.concatenate([unread, np.zeros(len(own_k), bool)])
     out, w = attention64(q, k, v, k_bias, theta, unread=flags)
-    return out, page_mass(w[:, -1, :], page_tokens)
+    mass = page_mass(w[:, -1, :], page_tokens)
+    if not with_bound:
+        return out, mass
+    return out, mass, attention_bound(q, k, v, w, k_bias, theta, unread=flags)
 
 
 def attention_bruteforce(q, k, v):

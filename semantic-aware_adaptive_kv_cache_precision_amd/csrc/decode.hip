@@ -107,11 +107,31 @@ namespace mi
       int pages_per_wave;
       int splits;
       float scale; // 1/sqrt(hd) * log2 e: scores in base-2 units
-      float *partials;   // [launch layer][kv_heads][splits][group][2 + hd]
+      // Streaming launches: the (layer, KV head, page) units split into
+      // stream_waves equal contiguous ranges, one a wave; a group's splits are
+      // the waves whose ranges meet it. 0: fixed splits of pages_per_wave * 8.
+      long long stream_units;
+      int stream_waves;
+      float *partials;   // [launch layer][kv_heads][splits][group][kSlotHead + hd]
       float *page_stats; // [launch layer][heads][pages][2]: each page's max and sum
     };
 
     __device__ inline half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
+
+    // 2^x as the one hardware instruction (v_exp_f32): softmax weights and
+    // rescale factors, where a result below 2^-126 weighs nothing.
+    __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+    // P enters P.V scaled by 2^14 (exact), so that its fp16 high and low
+    // parts stay normal numbers for every weight above 2^-17 of the running
+    // maximum, however far a page's own maximum sits below it; o carries the
+    // same factor until it leaves the wave.
+    constexpr float kPScale = 16384.0f;
+    constexpr float kPUnscale = 1.0f / 16384.0f;
+
+    // A partial slot: m, l, then padding to 128 bytes, then the HD outputs,
+    // so that each 32-channel chunk of o is one aligned 128-byte line.
+    constexpr int kSlotHead = 32;
 
     __device__ inline f32x4 mfma(half8 a, half8 b, f32x4 c)
     {
@@ -284,7 +304,7 @@ namespace mi
 #pragma unroll
       for (int e = 0; e < 8; ++e)
       {
-        pv[e] = exp2f(sc[e] - m_from);
+        pv[e] = exp2_fast(sc[e] - m_from);
         l_page += pv[e];
       }
       l_page += __shfl_xor(l_page, 16);
@@ -304,20 +324,25 @@ namespace mi
       {
         const float m_new = fmaxf(run.m, m_page);
         const float m_new_from = m_new == -INFINITY ? 0.0f : m_new;
-        const float f_old = exp2f(run.m - m_new_from);
-        f_page = exp2f(m_page - m_new_from);
+        const float f_old = exp2_fast(run.m - m_new_from);
+        f_page = exp2_fast(m_page - m_new_from);
         run.l = run.l * f_old + l_page * f_page;
-        run.m = m_new;
-#pragma unroll
-        for (int db = 0; db < HD / 16; ++db)
+        // o needs rescaling only where this page raised a head's maximum.
+        if (__builtin_amdgcn_ballot_w64(m_page > run.m) != 0)
         {
-          run.o[db] *= f_old;
+#pragma unroll
+          for (int db = 0; db < HD / 16; ++db)
+          {
+            run.o[db] *= f_old;
+          }
         }
+        run.m = m_new;
       }
+      const float p_scale = f_page * kPScale;
 #pragma unroll
       for (int e = 0; e < 8; ++e)
       {
-        const float pe = pv[e] * f_page;
+        const float pe = pv[e] * p_scale;
         const _Float16 hi = static_cast<_Float16>(pe);
         p_hi[e] = hi;
         p_lo[e] = static_cast<_Float16>(pe - static_cast<float>(hi));
@@ -355,81 +380,53 @@ namespace mi
       }
     }
 
-    // A page at INT8/INT4/INT2. `meta` is this wave's 4 * HD bytes of LDS.
+    // The per-lane codes and value metadata of one quantised page: rows r
+    // and 16 + r, the lane's run of channels.
     template <int HD, int Bits>
-    __device__ inline void quantised_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
-                                          const std::uint8_t *page, const PageLayout &L,
-                                          std::size_t W, int kvh, int kv_heads, int lane,
-                                          unsigned *meta)
+    struct QuantRaw
+    {
+      static constexpr int kRowWords = (HD / 4) * Bits / 8 / 4;
+      unsigned kc[2][kRowWords];
+      unsigned vc[2][kRowWords];
+      unsigned vs[2];
+      unsigned vz[2];
+    };
+
+    // q.K^T, softmax and P.V of a quantised page from its raw codes. `ks` and
+    // `kz` point at the KV head's key scales and key zeros (HD halves each)
+    // in LDS, read 32 channels at a time.
+    template <int HD, int Bits>
+    __device__ inline void quantised_compute(Running<HD> &run, const PageCtx &c, const half8 *qb,
+                                             const QuantRaw<HD, Bits> &raw, const unsigned *ks,
+                                             const unsigned *kz)
     {
       constexpr int S = HD / 32;
       constexpr int kRun = HD / 4;
-      constexpr int kRowBytes = kRun * Bits / 8;
-      constexpr int kRowWords = kRowBytes / 4;
-      constexpr int kMetaLanes = HD / 4; // 8 bytes (4 channels) a lane, a region
       const int r = c.r, g = c.g;
-      const std::size_t ch0 = static_cast<std::size_t>(kvh) * HD + g * kRun;
-      // Every load first: codes of both rows, the key scales and zeros (two
-      // regions, a lane's 8 bytes each), the rows' value scales and zeros.
-      unsigned kc[2][kRowWords], vc[2][kRowWords];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-      {
-        const std::size_t at = (static_cast<std::size_t>(kb * 16 + r) * W + ch0) * Bits / 8;
-        load_words<kRowBytes>(kc[kb], page + L.key_codes + at);
-        load_words<kRowBytes>(vc[kb], page + L.value_codes + at);
-      }
-      u32x2 km = {0u, 0u};
-      const bool meta_lane = lane < 2 * kMetaLanes;
-      if (meta_lane)
-      {
-        const std::size_t region = lane < kMetaLanes ? L.key_scales : L.key_zeros;
-        km = *((g_u32x2)(page + region + 2 * static_cast<std::size_t>(kvh) * HD +
-                         8 * (lane % kMetaLanes)));
-      }
-      unsigned vs[2], vz[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-      {
-        const std::size_t grp = static_cast<std::size_t>(kb * 16 + r) * kv_heads + kvh;
-        vs[kb] = *((g_u16)(page + L.value_scales + 2 * grp));
-        vz[kb] = *((g_u16)(page + L.value_zeros + 2 * grp));
-      }
-      // The key scales and zeros through LDS: [scales HD halves][zeros HD].
-      // LDS operations of one wave complete in order; the fences keep the
-      // compiler from moving the reads above the write.
-      if (meta_lane)
-      {
-        *reinterpret_cast<u32x2 *>(meta + 2 * lane) = km;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // q.K^T a step at a time.
       f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
       for (int s = 0; s < S; ++s)
       {
-        const u32x4 ks = *reinterpret_cast<const u32x4 *>(meta + (g * kRun + 8 * s) / 2);
-        const u32x4 kz = *reinterpret_cast<const u32x4 *>(meta + (HD + g * kRun + 8 * s) / 2);
+        const u32x4 s2 = *reinterpret_cast<const u32x4 *>(ks + (g * kRun + 8 * s) / 2);
+        const u32x4 z2 = *reinterpret_cast<const u32x4 *>(kz + (g * kRun + 8 * s) / 2);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
         {
           unsigned w0, w1 = 0;
           if constexpr (Bits == 8)
           {
-            w0 = kc[kb][2 * s];
-            w1 = kc[kb][2 * s + 1];
+            w0 = raw.kc[kb][2 * s];
+            w1 = raw.kc[kb][2 * s + 1];
           }
           else if constexpr (Bits == 4)
           {
-            w0 = kc[kb][s];
+            w0 = raw.kc[kb][s];
           }
           else
           {
-            w0 = kc[kb][s / 2] >> (16 * (s & 1));
+            w0 = raw.kc[kb][s / 2] >> (16 * (s & 1));
           }
-          acc[kb] = mfma(dequant_step<Bits>(w0, w1, ks, kz), qb[s], acc[kb]);
+          acc[kb] = mfma(dequant_step<Bits>(w0, w1, s2, z2), qb[s], acc[kb]);
         }
       }
       half8 p_hi, p_lo;
@@ -439,7 +436,7 @@ namespace mi
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
       {
-        const unsigned sp = vs[kb] | (vs[kb] << 16), zp = vz[kb] | (vz[kb] << 16);
+        const unsigned sp = raw.vs[kb] | (raw.vs[kb] << 16), zp = raw.vz[kb] | (raw.vz[kb] << 16);
         sv[kb] = u32x4{sp, sp, sp, sp};
         zv[kb] = u32x4{zp, zp, zp, zp};
       }
@@ -453,16 +450,16 @@ namespace mi
           unsigned w0, w1 = 0;
           if constexpr (Bits == 8)
           {
-            w0 = vc[kb][2 * s];
-            w1 = vc[kb][2 * s + 1];
+            w0 = raw.vc[kb][2 * s];
+            w1 = raw.vc[kb][2 * s + 1];
           }
           else if constexpr (Bits == 4)
           {
-            w0 = vc[kb][s];
+            w0 = raw.vc[kb][s];
           }
           else
           {
-            w0 = vc[kb][s / 2] >> (16 * (s & 1));
+            w0 = raw.vc[kb][s / 2] >> (16 * (s & 1));
           }
           v[kb] = dequant_step<Bits>(w0, w1, sv[kb], zv[kb]);
         }
@@ -470,31 +467,81 @@ namespace mi
       }
     }
 
-    // A page of FP16 rows: keys at k0/k1 (rows r and 16 + r, the lane's run),
-    // values at v0/v1, loaded after the scores so no page is held twice.
-    // Rows past the last key may hold anything: their scores are masked, and
-    // their values zeroed so that a non-finite one cannot reach P.V.
-    template <int HD>
-    __device__ inline void fp16_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
-                                     const std::uint16_t *k0, const std::uint16_t *k1,
-                                     const std::uint16_t *v0, const std::uint16_t *v1)
+    // A page at INT8/INT4/INT2, read from global memory. `meta` is this
+    // wave's 4 * HD bytes of LDS: the key scales and zeros pass through it.
+    template <int HD, int Bits>
+    __device__ inline void quantised_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
+                                          const std::uint8_t *page, const PageLayout &L,
+                                          std::size_t W, int kvh, int kv_heads, int lane,
+                                          unsigned *meta)
     {
-      constexpr int S = HD / 32;
-      half8 k[2][S];
-      load_fp16_run<HD>(k[0], k0);
-      load_fp16_run<HD>(k[1], k1);
-      f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+      using Raw = QuantRaw<HD, Bits>;
+      constexpr int kRun = HD / 4;
+      constexpr int kRowBytes = Raw::kRowWords * 4;
+      constexpr int kMetaLanes = HD / 4; // 8 bytes (4 channels) a lane, a region
+      const int r = c.r, g = c.g;
+      const std::size_t ch0 = static_cast<std::size_t>(kvh) * HD + g * kRun;
+      // Every load first: codes of both rows, the key scales and zeros (two
+      // regions, a lane's 8 bytes each), the rows' value scales and zeros.
+      Raw raw;
 #pragma unroll
-      for (int s = 0; s < S; ++s)
+      for (int kb = 0; kb < 2; ++kb)
+      {
+        const std::size_t at = (static_cast<std::size_t>(kb * 16 + r) * W + ch0) * Bits / 8;
+        load_words<kRowBytes>(raw.kc[kb], page + L.key_codes + at);
+        load_words<kRowBytes>(raw.vc[kb], page + L.value_codes + at);
+      }
+      u32x2 km = {0u, 0u};
+      const bool meta_lane = lane < 2 * kMetaLanes;
+      if (meta_lane)
+      {
+        const std::size_t region = lane < kMetaLanes ? L.key_scales : L.key_zeros;
+        km = *((g_u32x2)(page + region + 2 * static_cast<std::size_t>(kvh) * HD +
+                         8 * (lane % kMetaLanes)));
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+      {
+        const std::size_t grp = static_cast<std::size_t>(kb * 16 + r) * kv_heads + kvh;
+        raw.vs[kb] = *((g_u16)(page + L.value_scales + 2 * grp));
+        raw.vz[kb] = *((g_u16)(page + L.value_zeros + 2 * grp));
+      }
+      // The key scales and zeros through LDS: [scales HD halves][zeros HD].
+      // LDS operations of one wave complete in order; the fences keep the
+      // compiler from moving the reads above the write.
+      if (meta_lane)
+      {
+        *reinterpret_cast<u32x2 *>(meta + 2 * lane) = km;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      quantised_compute<HD, Bits>(run, c, qb, raw, meta, meta + HD / 2);
+    }
+
+    // q.K^T of an FP16 page's two 16-row blocks.
+    template <int HD>
+    __device__ inline void fp16_scores(f32x4 (&acc)[2], const half8 (&k)[2][HD / 32],
+                                       const half8 *qb)
+    {
+      acc[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      acc[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < HD / 32; ++s)
       {
         acc[0] = mfma(k[0][s], qb[s], acc[0]);
         acc[1] = mfma(k[1][s], qb[s], acc[1]);
       }
-      half8 p_hi, p_lo;
-      softmax_page<HD>(acc, c, run, p_hi, p_lo);
-      half8 v[2][S];
-      load_fp16_run<HD>(v[0], v0);
-      load_fp16_run<HD>(v[1], v1);
+    }
+
+    // P.V of an FP16 page. Rows past the last key may hold anything: their
+    // scores are masked, and their values zeroed so that a non-finite one
+    // cannot reach P.V.
+    template <int HD>
+    __device__ inline void fp16_values(Running<HD> &run, const PageCtx &c, half8 (&v)[2][HD / 32],
+                                       half8 p_hi, half8 p_lo)
+    {
+      constexpr int S = HD / 32;
       if (c.partial)
       {
 #pragma unroll
@@ -515,6 +562,28 @@ namespace mi
       {
         pv_step<HD>(run, s, v[0][s], v[1][s], c.r, c.g, p_hi, p_lo);
       }
+    }
+
+    // A page of FP16 rows from global memory: keys at k0/k1 (rows r and
+    // 16 + r, the lane's run), values at v0/v1, loaded after the scores so
+    // that no page is held twice.
+    template <int HD>
+    __device__ inline void fp16_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
+                                     const std::uint16_t *k0, const std::uint16_t *k1,
+                                     const std::uint16_t *v0, const std::uint16_t *v1)
+    {
+      constexpr int S = HD / 32;
+      half8 k[2][S];
+      load_fp16_run<HD>(k[0], k0);
+      load_fp16_run<HD>(k[1], k1);
+      f32x4 acc[2];
+      fp16_scores<HD>(acc, k, qb);
+      half8 p_hi, p_lo;
+      softmax_page<HD>(acc, c, run, p_hi, p_lo);
+      half8 v[2][S];
+      load_fp16_run<HD>(v[0], v0);
+      load_fp16_run<HD>(v[1], v1);
+      fp16_values<HD>(run, c, v, p_hi, p_lo);
     }
 
     template <int HD>
@@ -674,7 +743,8 @@ namespace mi
 #pragma unroll
             for (int i2 = 0; i2 < 4; ++i2)
             {
-              s_o[(wave * G + r) * kRow + out_channel<HD>(s, h, g, i2)] = run.o[2 * s + h][i2];
+              s_o[(wave * G + r) * kRow + out_channel<HD>(s, h, g, i2)] =
+                  run.o[2 * s + h][i2] * kPUnscale;
             }
           }
         }
@@ -690,7 +760,7 @@ namespace mi
           top = fmaxf(top, s_m[w * G + h]);
         }
         const float from = top == -INFINITY ? 0.0f : top;
-        s_w[threadIdx.x] = exp2f(s_m[threadIdx.x] - from);
+        s_w[threadIdx.x] = exp2_fast(s_m[threadIdx.x] - from);
         if (threadIdx.x < G)
         {
           s_w[kWaves * G + h] = top;
@@ -699,7 +769,7 @@ namespace mi
       __syncthreads();
       float *part = a.partials +
                     ((static_cast<std::size_t>(li) * a.kv_heads + kvh) * a.splits + split) * G *
-                        (HD + 2);
+                        (kSlotHead + HD);
       for (int idx = threadIdx.x; idx < G * (HD + 2); idx += kThreads)
       {
         const int h = idx / (HD + 2);
@@ -715,7 +785,7 @@ namespace mi
             acc += v * s_w[w * G + h];
           }
         }
-        part[idx] = acc;
+        part[h * (kSlotHead + HD) + (col < 2 ? col : kSlotHead + col - 2)] = acc;
       }
     }
 
@@ -725,6 +795,588 @@ namespace mi
       return (static_cast<std::size_t>(kWaves) * hd + 3 * kWaves * group + group +
               static_cast<std::size_t>(kWaves) * group * (hd + 4)) *
              sizeof(float);
+    }
+
+    // ---- the streaming kernel: several layers in one launch ----------------
+
+    typedef __attribute__((address_space(3))) void *lds_void;
+    // Word 3 of a raw buffer descriptor on gfx9-family parts (gfx950).
+    constexpr int kBufferWord3 = 0x00020000;
+    typedef const __attribute__((address_space(1))) void *global_void;
+
+    // Direct global-to-LDS copies (global_load_lds): lane l's 16 (or 4)
+    // bytes land at block + 16 l (4 l); `block` must be wave-uniform.
+    __device__ inline void dma16(const void *src, void *block)
+    {
+      __builtin_amdgcn_global_load_lds((global_void)src, (lds_void)block, 16, 0, 0);
+    }
+    __device__ inline void dma4(const void *src, void *block)
+    {
+      __builtin_amdgcn_global_load_lds((global_void)src, (lds_void)block, 4, 0, 0);
+    }
+    // s_waitcnt vmcnt(0): every copy into LDS has landed.
+    __device__ inline void wait_copies()
+    {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // s_waitcnt lgkmcnt(0): every LDS read has returned, so its slot may be
+    // overwritten.
+    __device__ inline void wait_reads()
+    {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    __device__ inline u32x4 lds16(const void *block, int lane)
+    {
+      return *reinterpret_cast<const u32x4 *>(static_cast<const std::uint8_t *>(block) + 16 * lane);
+    }
+    __device__ inline unsigned lds4(const void *block, int lane)
+    {
+      return *reinterpret_cast<const unsigned *>(static_cast<const std::uint8_t *>(block) + 4 * lane);
+    }
+
+    // Where a quantised page's pieces sit in a wave's LDS slot. Codes go in
+    // 1 KiB blocks of 16 bytes a lane when a lane's row run is a multiple of
+    // 16 bytes, else in 256-byte blocks of 4 bytes a lane; both in the order
+    // the lanes read them. Then the KV head's key scales, key zeros (a
+    // 256-byte block each) and the page's value scales and zeros.
+    template <int HD, int Bits>
+    struct SlotLayout
+    {
+      static constexpr int kRowWords = QuantRaw<HD, Bits>::kRowWords;
+      static constexpr bool kWide = kRowWords % 4 == 0;
+      static constexpr int kBlocksARow = kWide ? kRowWords / 4 : kRowWords;
+      static constexpr int kBlock = kWide ? 1024 : 256;
+      static constexpr int kCodes = 4 * kBlocksARow * kBlock; // K rows r, 16+r; V rows
+      static constexpr int kKeyScales = kCodes;
+      static constexpr int kKeyZeros = kCodes + 256;
+      static constexpr int kValueMeta = kCodes + 512;
+    };
+
+    // The bytes of one (page, KV head) unit a wave's slot must hold, and the
+    // slot's size: an FP16 unit (4 rows of the lane's run, 16 bytes a lane a
+    // step) is the largest.
+    template <int HD>
+    constexpr int stream_slot_bytes()
+    {
+      return 4 * (HD / 32) * 1024;
+    }
+
+    struct Unit
+    {
+      int li;   // layer within the launch
+      int kvh;
+      int page;
+    };
+
+    __device__ inline Unit unit_of(long long u, int kv_heads, int pages)
+    {
+      const long long group = u / pages;
+      return {static_cast<int>(group / kv_heads), static_cast<int>(group % kv_heads),
+              static_cast<int>(u - group * pages)};
+    }
+
+    // Range of wave w: units [w U / W, (w+1) U / W).
+    __host__ __device__ inline long long range_start(long long w, long long units, int waves)
+    {
+      return w * units / waves;
+    }
+
+    // The wave whose range holds unit x.
+    __host__ __device__ inline int wave_of(long long x, long long units, int waves)
+    {
+      long long w = x * waves / units;
+      while (w + 1 < waves && range_start(w + 1, units, waves) <= x)
+      {
+        ++w;
+      }
+      while (w > 0 && range_start(w, units, waves) > x)
+      {
+        --w;
+      }
+      return static_cast<int>(w);
+    }
+
+    // Splits of (layer li, KV head kvh): fixed, or the streaming waves that
+    // meet its pages; and the split a streaming wave writes for it.
+    __host__ __device__ inline int group_splits(const DecodeArgs &a, int li, int kvh)
+    {
+      if (a.stream_waves == 0)
+      {
+        return a.splits;
+      }
+      const long long base = (static_cast<long long>(li) * a.kv_heads + kvh) * a.pages;
+      return wave_of(base + a.pages - 1, a.stream_units, a.stream_waves) -
+             wave_of(base, a.stream_units, a.stream_waves) + 1;
+    }
+
+    // Issues the copies of unit `u` (address `page`, tier `tier`) into `slot`.
+    template <int HD>
+    __device__ inline void stream_copy(const DecodeArgs &a, const Unit &u, const std::uint8_t *page,
+                                       int tier, std::uint8_t *slot, int lane)
+    {
+      constexpr int S = HD / 32;
+      constexpr int kRun = HD / 4;
+      const int r = lane & 15, g = lane >> 4;
+      const std::size_t W = static_cast<std::size_t>(a.kv_heads) * HD;
+      const std::size_t run0 = static_cast<std::size_t>(u.kvh) * HD + g * kRun;
+      const auto quantised = [&](auto bits_tag) {
+        constexpr int Bits = decltype(bits_tag)::value;
+        using SL = SlotLayout<HD, Bits>;
+        const PageLayout &L = a.lay[Bits == 8 ? kINT8 : Bits == 4 ? kINT4 : kINT2];
+        // One buffer over the page (reads past it return zeros); each lane's
+        // row offset once, the regions and rows as scalar offsets, the steps
+        // as immediates.
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<std::uint8_t *>(page), 0, static_cast<int>(L.page_bytes), kBufferWord3);
+        const int lane_row = static_cast<int>((r * W + run0) * Bits / 8);
+        const int row16 = static_cast<int>(16 * W * Bits / 8);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) // keys, values
+        {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+          {
+            const int region =
+                static_cast<int>(half == 0 ? L.key_codes : L.value_codes) + kb * row16;
+#pragma unroll
+            for (int i = 0; i < SL::kBlocksARow; ++i)
+            {
+              std::uint8_t *block = slot + ((half * 2 + kb) * SL::kBlocksARow + i) * SL::kBlock;
+              if constexpr (SL::kWide)
+              {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)block, 16, lane_row,
+                                                         region + 16 * i, 0, 0);
+              }
+              else
+              {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)block, 4, lane_row,
+                                                         region + 4 * i, 0, 0);
+              }
+            }
+          }
+        }
+        // Key scales and zeros of this KV head: HD halves each, 4 bytes a lane.
+        const int meta_off = 4 * (lane % (HD / 2));
+        const int kvh_meta = 2 * u.kvh * HD;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)(slot + SL::kKeyScales), 4, meta_off,
+                                                 static_cast<int>(L.key_scales) + kvh_meta, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)(slot + SL::kKeyZeros), 4, meta_off,
+                                                 static_cast<int>(L.key_zeros) + kvh_meta, 0, 0);
+        // Value scales then value zeros, all KV heads: 64 * kv bytes each,
+        // contiguous in the page (zeros follow scales).
+        const int words = 16 * a.kv_heads;
+        for (int b = 0; b < (2 * words + 63) / 64; ++b)
+        {
+          const int w = b * 64 + lane;
+          const int wc = w < 2 * words ? w : 2 * words - 1;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)(slot + SL::kValueMeta + 256 * b),
+                                                   4, 4 * wc, static_cast<int>(L.value_scales),
+                                                   0, 0);
+        }
+      };
+      if (tier != kOwnPage && tier >= kINT8 && tier <= kINT2)
+      {
+        switch (tier)
+        {
+        case kINT8:
+          quantised(std::integral_constant<int, 8>{});
+          break;
+        case kINT4:
+          quantised(std::integral_constant<int, 4>{});
+          break;
+        default:
+          quantised(std::integral_constant<int, 2>{});
+          break;
+        }
+        return;
+      }
+      if (tier != kOwnPage)
+      {
+        // FP16 rows: keys r, 16+r then values r, 16+r, the lane's run, a
+        // 16-byte step at a time, through one buffer over the page.
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<std::uint8_t *>(page), 0, static_cast<int>(4 * kPageTokens * W),
+            kBufferWord3);
+        const int lane_row = static_cast<int>((r * W + run0) * 2);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+          const int row = static_cast<int>(((j / 2) * kPageTokens + (j % 2) * 16) * W * 2);
+#pragma unroll
+          for (int st = 0; st < S; ++st)
+          {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)(slot + (j * S + st) * 1024), 16,
+                                                     lane_row, row + 16 * st, 0, 0);
+          }
+        }
+        return;
+      }
+      // The own page: rows before `start` from the open page, the rest from
+      // the chunk; rows past the last key read row 0.
+      const int layer = a.first_layer + u.li;
+      const auto *open = a.open_table != nullptr
+                             ? reinterpret_cast<const std::uint16_t *>(a.open_table[layer])
+                             : a.open;
+      const int last = a.seq_k - 1 - u.page * kPageTokens;
+      const int t_start = a.start - u.page * kPageTokens;
+      const std::uint16_t *ck = a.chunk_k + u.li * a.chunk_stride;
+      const std::uint16_t *cv = a.chunk_v + u.li * a.chunk_stride;
+      const std::uint16_t *rows[4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+      {
+        const int t = kb * 16 + r;
+        const int tt = t <= last ? t : 0;
+        if (tt < t_start)
+        {
+          rows[kb] = open + static_cast<std::size_t>(tt) * W + run0;
+          rows[2 + kb] = open + static_cast<std::size_t>(kPageTokens + tt) * W + run0;
+        }
+        else
+        {
+          rows[kb] = ck + static_cast<std::size_t>(tt - t_start) * W + run0;
+          rows[2 + kb] = cv + static_cast<std::size_t>(tt - t_start) * W + run0;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+      {
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+        {
+          dma16(rows[j] + 8 * st, slot + (j * S + st) * 1024);
+        }
+      }
+    }
+
+    // Reads a quantised unit's codes and value metadata from the slot.
+    template <int HD, int Bits>
+    __device__ inline void stream_read_quantised(QuantRaw<HD, Bits> &raw, const std::uint8_t *slot,
+                                                 int lane, int kvh, int kv_heads)
+    {
+      using SL = SlotLayout<HD, Bits>;
+      const int r = lane & 15;
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+      {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+        {
+          unsigned *dst = half == 0 ? raw.kc[kb] : raw.vc[kb];
+#pragma unroll
+          for (int i = 0; i < SL::kBlocksARow; ++i)
+          {
+            const std::uint8_t *block =
+                slot + ((half * 2 + kb) * SL::kBlocksARow + i) * SL::kBlock;
+            if constexpr (SL::kWide)
+            {
+              const u32x4 v = lds16(block, lane);
+              dst[4 * i + 0] = v.x;
+              dst[4 * i + 1] = v.y;
+              dst[4 * i + 2] = v.z;
+              dst[4 * i + 3] = v.w;
+            }
+            else
+            {
+              dst[i] = lds4(block, lane);
+            }
+          }
+        }
+      }
+      const auto *vmeta = reinterpret_cast<const std::uint16_t *>(slot + SL::kValueMeta);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+      {
+        const int grp = (kb * 16 + r) * kv_heads + kvh;
+        raw.vs[kb] = vmeta[grp];
+        raw.vz[kb] = vmeta[32 * kv_heads + grp];
+      }
+    }
+
+    // Writes a wave's running softmax as the partial of its group's split.
+    template <int HD>
+    __device__ inline void stream_flush(const DecodeArgs &a, const Running<HD> &run, int li, int kvh,
+                                        int split, int r, int g)
+    {
+      const int G = a.group;
+      if (r >= G)
+      {
+        return;
+      }
+      float *part = a.partials +
+                    (((static_cast<std::size_t>(li) * a.kv_heads + kvh) * a.splits + split) * G + r) *
+                        (kSlotHead + HD);
+      if (g == 0)
+      {
+        part[0] = run.m;
+        part[1] = run.l;
+      }
+#pragma unroll
+      for (int s = 0; s < HD / 32; ++s)
+      {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+        {
+          *reinterpret_cast<f32x4 *>(part + kSlotHead + out_channel<HD>(s, h, g, 0)) =
+              run.o[2 * s + h] * kPUnscale;
+        }
+      }
+    }
+
+    // A quantised unit from the slot: codes and value metadata to registers,
+    // the key scales and zeros to the wave's metadata area (out of the
+    // slot), then `next` (which reuses the slot), then the arithmetic.
+    template <int HD, int Bits, typename Next>
+    __device__ inline void stream_quantised(Running<HD> &run, const PageCtx &c, const half8 *qb,
+                                            const std::uint8_t *slot, std::uint8_t *meta,
+                                            int lane, int kvh, int kv_heads, const Next &next)
+    {
+      using SL = SlotLayout<HD, Bits>;
+      QuantRaw<HD, Bits> raw;
+      stream_read_quantised<HD, Bits>(raw, slot, lane, kvh, kv_heads);
+      const u32x2 km = *reinterpret_cast<const u32x2 *>(slot + SL::kKeyScales + 8 * lane);
+      *reinterpret_cast<u32x2 *>(meta + 8 * lane) = km;
+      next();
+      quantised_compute<HD, Bits>(run, c, qb, raw, reinterpret_cast<const unsigned *>(meta),
+                                  reinterpret_cast<const unsigned *>(meta + 256));
+    }
+
+    // Each wave takes an equal contiguous range of (layer, KV head, page)
+    // units (at most 64, and at most two groups) and walks it with one unit
+    // in flight: the next unit's bytes are copied into the wave's LDS slot by
+    // global_load_lds while the current one, already in registers, is
+    // computed. A wave writes one partial per group it touches.
+    template <int HD>
+    __global__ void __launch_bounds__(kThreads) decode_stream_kernel(DecodeArgs a)
+    {
+      constexpr int S = HD / 32;
+      constexpr int DB = HD / 16;
+      constexpr int kRun = HD / 4;
+      extern __shared__ float lds[];
+      const int lane = threadIdx.x & 63;
+      const int wave = threadIdx.x >> 6;
+      const int r = lane & 15;
+      const int g = lane >> 4;
+      const int G = a.group;
+      const int gw = blockIdx.x * kWaves + wave;
+      if (gw >= a.stream_waves)
+      {
+        return;
+      }
+      const long long u0 = range_start(gw, a.stream_units, a.stream_waves);
+      const long long u1 = range_start(gw + 1, a.stream_units, a.stream_waves);
+      const int n = static_cast<int>(u1 - u0);
+      if (n <= 0)
+      {
+        return;
+      }
+      std::uint8_t *slot = reinterpret_cast<std::uint8_t *>(lds) + wave * stream_slot_bytes<HD>();
+      std::uint8_t *meta =
+          reinterpret_cast<std::uint8_t *>(lds) + kWaves * stream_slot_bytes<HD>() + wave * 512;
+      const int own = a.causal ? (a.seq_k - 1) / kPageTokens : -1;
+
+      // Every unit's address and tier, a lane a unit, read once.
+      unsigned long long my_addr = 0;
+      int my_tier = kFP16;
+      if (lane < n)
+      {
+        const Unit u = unit_of(u0 + lane, a.kv_heads, a.pages);
+        const long long at = static_cast<long long>(a.first_layer + u.li) * a.table_stride + u.page;
+        if (a.causal)
+        {
+          my_tier = u.page < own ? static_cast<int>(a.tiers[at]) : kOwnPage;
+        }
+        if (my_tier != kUnreadPage && my_tier != kOwnPage)
+        {
+          my_addr = a.table[at];
+        }
+      }
+      const auto addr_of = [&](int i) {
+        return reinterpret_cast<const std::uint8_t *>(
+            (static_cast<unsigned long long>(__builtin_amdgcn_readlane(
+                 static_cast<unsigned>(my_addr >> 32), i))
+             << 32) |
+            static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<unsigned>(my_addr), i)));
+      };
+      const auto tier_of = [&](int i) { return __builtin_amdgcn_readlane(my_tier, i); };
+
+      Running<HD> run;
+      run.m = -INFINITY;
+      run.l = 0.0f;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+      {
+        run.o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      half8 qb[S];
+      int seg_group = -1;
+      bool first = true;
+
+      {
+        const int t = tier_of(0);
+        if (t != kUnreadPage)
+        {
+          stream_copy<HD>(a, unit_of(u0, a.kv_heads, a.pages), addr_of(0), t, slot, lane);
+        }
+      }
+      Unit u = unit_of(u0, a.kv_heads, a.pages);
+      for (int i = 0; i < n; ++i)
+      {
+        if (i > 0)
+        {
+          // The next unit: the next page, or the next group's first.
+          if (++u.page == a.pages)
+          {
+            u.page = 0;
+            if (++u.kvh == a.kv_heads)
+            {
+              u.kvh = 0;
+              ++u.li;
+            }
+          }
+        }
+        const int group = u.li * a.kv_heads + u.kvh;
+        if (group != seg_group)
+        {
+          seg_group = group;
+          first = true;
+          const std::uint16_t *q_row =
+              a.q + u.li * a.q_stride + static_cast<std::size_t>(u.kvh * G + (r < G ? r : 0)) * HD +
+              g * kRun;
+          load_fp16_run<HD>(qb, q_row);
+          if (r >= G)
+          {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+            {
+              qb[s] = as_half8(u32x4{0u, 0u, 0u, 0u});
+            }
+          }
+        }
+        const int tier = tier_of(i);
+        PageCtx c;
+        c.r = r;
+        c.g = g;
+        c.group = G;
+        c.last = a.seq_k - 1 - u.page * kPageTokens;
+        c.partial = c.last < kPageTokens - 1;
+        c.first = first;
+        c.scale = a.scale;
+        c.stat = a.page_stats +
+                 ((static_cast<std::size_t>(u.li) * a.heads + u.kvh * G + r) * a.pages + u.page) * 2;
+        // The next unit's copies go out as soon as this one is out of LDS.
+        const auto next = [&]() {
+          wait_reads();
+          if (i + 1 < n)
+          {
+            const int t = tier_of(i + 1);
+            if (t != kUnreadPage)
+            {
+              Unit v = u;
+              if (++v.page == a.pages)
+              {
+                v.page = 0;
+                if (++v.kvh == a.kv_heads)
+                {
+                  v.kvh = 0;
+                  ++v.li;
+                }
+              }
+              stream_copy<HD>(a, v, addr_of(i + 1), t, slot, lane);
+            }
+          }
+        };
+        wait_copies();
+        switch (tier)
+        {
+        case kUnreadPage:
+          next();
+          if (g == 0 && r < G)
+          {
+            c.stat[0] = -INFINITY;
+            c.stat[1] = 0.0f;
+          }
+          break;
+        case kINT8:
+          stream_quantised<HD, 8>(run, c, qb, slot, meta, lane, u.kvh, a.kv_heads, next);
+          first = false;
+          break;
+        case kINT4:
+          stream_quantised<HD, 4>(run, c, qb, slot, meta, lane, u.kvh, a.kv_heads, next);
+          first = false;
+          break;
+        case kINT2:
+          stream_quantised<HD, 2>(run, c, qb, slot, meta, lane, u.kvh, a.kv_heads, next);
+          first = false;
+          break;
+        default:
+        {
+          half8 k[2][S], v[2][S];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+          {
+#pragma unroll
+            for (int st = 0; st < S; ++st)
+            {
+              const half8 x = as_half8(lds16(slot + (j * S + st) * 1024, lane));
+              if (j < 2)
+              {
+                k[j][st] = x;
+              }
+              else
+              {
+                v[j - 2][st] = x;
+              }
+            }
+          }
+          next();
+          f32x4 acc[2];
+          fp16_scores<HD>(acc, k, qb);
+          half8 p_hi, p_lo;
+          softmax_page<HD>(acc, c, run, p_hi, p_lo);
+          fp16_values<HD>(run, c, v, p_hi, p_lo);
+          first = false;
+          break;
+        }
+        }
+        // The group's last unit in this wave's range: its partial.
+        const bool group_ends = i + 1 == n || u.page + 1 == a.pages;
+        if (group_ends)
+        {
+          const long long base = static_cast<long long>(group) * a.pages;
+          const int split = gw - wave_of(base, a.stream_units, a.stream_waves);
+          if (first)
+          {
+            // Every unit of the segment was unread: an empty partial.
+            run.m = -INFINITY;
+            run.l = 0.0f;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+            {
+              run.o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+          }
+          stream_flush<HD>(a, run, u.li, u.kvh, split, r, g);
+          run.m = -INFINITY;
+          run.l = 0.0f;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+          {
+            run.o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          }
+        }
+      }
+    }
+
+    // LDS of decode_stream_kernel, bytes: a slot and a metadata area a wave.
+    template <int HD>
+    constexpr std::size_t stream_kernel_lds()
+    {
+      return static_cast<std::size_t>(kWaves) * (stream_slot_bytes<HD>() + 512);
     }
 
     constexpr int kCombineThreads = 256;
@@ -738,7 +1390,7 @@ namespace mi
     {
       const float next = fmaxf(top, m);
       const float from = next == -INFINITY ? 0.0f : next;
-      sum = sum * exp2f(top - from) + l * exp2f(m - from);
+      sum = sum * exp2_fast(top - from) + l * exp2_fast(m - from);
       top = next;
     }
 
@@ -795,7 +1447,7 @@ namespace mi
       const auto slot = [&](int h, int s) {
         return a.partials +
                (((static_cast<std::size_t>(li) * a.kv_heads + h / G) * a.splits + s) * G + h % G) *
-                   (HD + 2);
+                   (kSlotHead + HD);
       };
       constexpr int kChunks = HD / kCombineDims;
       if (static_cast<int>(blockIdx.x) < a.heads * kChunks)
@@ -804,9 +1456,10 @@ namespace mi
         const int d0 = (blockIdx.x % kChunks) * kCombineDims;
         const int c = t % kCombineDims;
         const int j = t / kCombineDims;
+        const int splits = group_splits(a, li, h / G);
         // This thread's running max, output channel and sum over its splits.
         float top = -INFINITY, acc = 0.0f, l = 0.0f;
-        for (int s0 = j; s0 < a.splits; s0 += kSplitLanes * kLoadsAhead)
+        for (int s0 = j; s0 < splits; s0 += kSplitLanes * kLoadsAhead)
         {
           float mv[kLoadsAhead], lv[kLoadsAhead], ov[kLoadsAhead];
 #pragma unroll
@@ -816,12 +1469,12 @@ namespace mi
             mv[i] = -INFINITY;
             lv[i] = 0.0f;
             ov[i] = 0.0f;
-            if (s < a.splits)
+            if (s < splits)
             {
               const float *p = slot(h, s);
               mv[i] = p[0];
               lv[i] = p[1];
-              ov[i] = p[2 + d0 + c];
+              ov[i] = p[kSlotHead + d0 + c];
             }
           }
           float next = top;
@@ -831,13 +1484,13 @@ namespace mi
             next = fmaxf(next, mv[i]);
           }
           const float from = next == -INFINITY ? 0.0f : next;
-          const float keep = exp2f(top - from);
+          const float keep = exp2_fast(top - from);
           acc *= keep;
           l *= keep;
 #pragma unroll
           for (int i = 0; i < kLoadsAhead; ++i)
           {
-            const float w = exp2f(mv[i] - from);
+            const float w = exp2_fast(mv[i] - from);
             acc += ov[i] * w;
             l += lv[i] * w;
           }
@@ -846,7 +1499,7 @@ namespace mi
         // Across the block: the common max, then every thread's share at it.
         const float all = block_reduce<true>(top, s_red);
         const float from = all == -INFINITY ? 0.0f : all;
-        const float keep = exp2f(top - from);
+        const float keep = exp2_fast(top - from);
         s_acc[j][c] = acc * keep;
         if (c == 0)
         {
@@ -867,6 +1520,23 @@ namespace mi
         }
         return;
       }
+      // This block's page: its (max, sum) of the first kHeadsAPass heads and
+      // its old score are loaded now, while the head totals are formed.
+      const int page = (blockIdx.x - a.heads * kChunks) * kCombineThreads + t;
+      const bool has_page = page < a.pages;
+      const float *stats = a.page_stats + static_cast<std::size_t>(li) * a.heads * a.pages * 2;
+      float *scores = a.scores != nullptr ? a.scores + li * a.scores_stride : nullptr;
+      const float old = has_page && scores != nullptr ? scores[page] : 0.0f;
+      float2 st0[kHeadsAPass];
+#pragma unroll
+      for (int i = 0; i < kHeadsAPass; ++i)
+      {
+        if (has_page && i < a.heads)
+        {
+          st0[i] = *reinterpret_cast<const float2 *>(
+              stats + (static_cast<std::size_t>(i) * a.pages + page) * 2);
+        }
+      }
       // Every head's whole max and sum: a 16-lane row a head, each lane
       // folding every 16th split (its loads issued ahead), then the row
       // reduced with DPP moves.
@@ -877,7 +1547,8 @@ namespace mi
         float top = -INFINITY, sum = 0.0f;
         if (h < a.heads)
         {
-          for (int s0 = q; s0 < a.splits; s0 += 16 * kLoadsAhead)
+          const int splits = group_splits(a, li, h / G);
+          for (int s0 = q; s0 < splits; s0 += 16 * kLoadsAhead)
           {
             float mv[kLoadsAhead], lv[kLoadsAhead];
 #pragma unroll
@@ -886,7 +1557,7 @@ namespace mi
               const int s = s0 + 16 * i;
               mv[i] = -INFINITY;
               lv[i] = 0.0f;
-              if (s < a.splits)
+              if (s < splits)
               {
                 const float2 ml = *reinterpret_cast<const float2 *>(slot(h, s));
                 mv[i] = ml.x;
@@ -902,7 +1573,7 @@ namespace mi
         }
         const float all = row16_max(top);
         const float from = all == -INFINITY ? 0.0f : all;
-        const float total = row16_sum(sum * exp2f(top - from));
+        const float total = row16_sum(sum * exp2_fast(top - from));
         if (q == 0 && h < a.heads)
         {
           s_top[h] = from;
@@ -910,15 +1581,11 @@ namespace mi
         }
       }
       __syncthreads();
-      const int page = (blockIdx.x - a.heads * kChunks) * kCombineThreads + t;
-      if (page >= a.pages)
+      if (!has_page)
       {
         return;
       }
-      const float *stats = a.page_stats + static_cast<std::size_t>(li) * a.heads * a.pages * 2;
       float *mass = a.mass != nullptr ? a.mass + li * a.mass_stride : nullptr;
-      float *scores = a.scores != nullptr ? a.scores + li * a.scores_stride : nullptr;
-      const float old = scores != nullptr ? scores[page] : 0.0f; // loaded ahead of the masses
       float total = 0.0f;
       for (int h0 = 0; h0 < a.heads; h0 += kHeadsAPass)
       {
@@ -927,7 +1594,11 @@ namespace mi
 #pragma unroll
         for (int i = 0; i < kHeadsAPass; ++i)
         {
-          if (h0 + i < a.heads)
+          if (h0 == 0)
+          {
+            st[i] = st0[i];
+          }
+          else if (h0 + i < a.heads)
           {
             st[i] = *reinterpret_cast<const float2 *>(
                 stats + (static_cast<std::size_t>(h0 + i) * a.pages + page) * 2);
@@ -939,7 +1610,7 @@ namespace mi
           const int h = h0 + i;
           if (h < a.heads)
           {
-            const float share = st[i].y * exp2f(st[i].x - s_top[h]) / s_sum[h];
+            const float share = st[i].y * exp2_fast(st[i].x - s_top[h]) / s_sum[h];
             if (mass != nullptr)
             {
               mass[static_cast<std::size_t>(h) * a.pages + page] = share;
@@ -1057,9 +1728,32 @@ namespace mi
     d.pages = pages;
     // Scores in base-2 units: the softmax weights are exp2 of them.
     d.scale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(a.head_dim)));
-    // A page a wave, so a launch has a wave for every page of every KV head,
-    // or, unsplit, one workgroup a KV head.
-    if (ls.split)
+    // One layer: a page a wave, so a launch has a wave for every page of
+    // every KV head (or, unsplit, one workgroup a KV head). Several layers:
+    // the streaming kernel, equal ranges of units a wave.
+    const bool streaming = ls.split && ls.layers > 1;
+    int stream_blocks = 0;
+    if (streaming)
+    {
+      const long long units = static_cast<long long>(ls.layers) * a.kv_heads * pages;
+      const int per_cu = 1; // 2 waves a SIMD (registers); LDS holds a slot a wave
+      long long waves = static_cast<long long>(device_multiprocessors()) * per_cu * kWaves;
+      waves = std::max(waves, (units + 63) / 64); // at most 64 units a wave
+      waves = std::min(waves, units);             // no wave without a unit
+      d.stream_units = units;
+      d.stream_waves = static_cast<int>(waves);
+      stream_blocks = static_cast<int>((waves + kWaves - 1) / kWaves);
+      d.pages_per_wave = 0;
+      d.splits = 1;
+      for (int li = 0; li < ls.layers; ++li)
+      {
+        for (int kvh = 0; kvh < a.kv_heads; ++kvh)
+        {
+          d.splits = std::max(d.splits, group_splits(d, li, kvh));
+        }
+      }
+    }
+    else if (ls.split)
     {
       d.pages_per_wave = 1;
       d.splits = (pages + kWaves - 1) / kWaves;
@@ -1070,7 +1764,7 @@ namespace mi
       d.splits = 1;
     }
     const std::size_t part = static_cast<std::size_t>(ls.layers) * a.kv_heads * d.splits * group *
-                             (a.head_dim + 2);
+                             (kSlotHead + a.head_dim);
     const std::size_t stats = static_cast<std::size_t>(ls.layers) * a.heads * pages * 2;
     float *ws = decode_workspace(part + stats);
     d.partials = ws;
@@ -1078,18 +1772,32 @@ namespace mi
     const int mass_blocks = (a.mass != nullptr || a.scores != nullptr)
                                 ? (pages + kCombineThreads - 1) / kCombineThreads
                                 : 0;
-    const auto run = [&](auto pages_kernel, auto combine_kernel, int hd) {
-      const std::size_t lds = pages_kernel_lds(group, hd);
-      if (lds > 64 * 1024)
+    const auto run = [&](auto pages_kernel, auto stream_kernel, auto combine_kernel, int hd,
+                         std::size_t stream_lds) {
+      if (stream_blocks > 0)
       {
-        hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(pages_kernel),
+        hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(stream_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      static_cast<int>(lds)),
-                  "hipFuncSetAttribute decode LDS");
+                                      static_cast<int>(stream_lds)),
+                  "hipFuncSetAttribute decode stream LDS");
+        hipLaunchKernelGGL(stream_kernel, dim3(stream_blocks), dim3(kThreads), stream_lds, stream,
+                           d);
+        hip_check(hipGetLastError(), "decode stream kernel launch");
       }
-      hipLaunchKernelGGL(pages_kernel, dim3(d.splits, a.kv_heads, ls.layers), dim3(kThreads), lds,
-                         stream, d);
-      hip_check(hipGetLastError(), "decode pages kernel launch");
+      else
+      {
+        const std::size_t lds = pages_kernel_lds(group, hd);
+        if (lds > 64 * 1024)
+        {
+          hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(pages_kernel),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds)),
+                    "hipFuncSetAttribute decode LDS");
+        }
+        hipLaunchKernelGGL(pages_kernel, dim3(d.splits, a.kv_heads, ls.layers), dim3(kThreads),
+                           lds, stream, d);
+        hip_check(hipGetLastError(), "decode pages kernel launch");
+      }
       hipLaunchKernelGGL(combine_kernel,
                          dim3(a.heads * (hd / kCombineDims) + mass_blocks, ls.layers),
                          dim3(kCombineThreads), 0, stream, d);
@@ -1097,11 +1805,13 @@ namespace mi
     };
     if (a.head_dim == 128)
     {
-      run(decode_pages_kernel<128>, decode_combine_kernel<128>, 128);
+      run(decode_pages_kernel<128>, decode_stream_kernel<128>, decode_combine_kernel<128>, 128,
+          stream_kernel_lds<128>());
     }
     else
     {
-      run(decode_pages_kernel<64>, decode_combine_kernel<64>, 64);
+      run(decode_pages_kernel<64>, decode_stream_kernel<64>, decode_combine_kernel<64>, 64,
+          stream_kernel_lds<64>());
     }
   }
 

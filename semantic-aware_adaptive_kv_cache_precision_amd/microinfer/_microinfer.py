@@ -927,7 +927,8 @@ class KVPages:
         heads, head_dim) fp16, keys/values (layers, kv_width) (the query's
         own rows), mass (layers, heads, pages) floats; `scores` an
         ImportanceScores whose rows first_layer.. take the fold. Each layer's
-        results equal attention(layer, ..., seq_q=1, partials=...)'s."""
+        results are attention(layer, ..., seq_q=1)'s within the attention
+        tolerance (the streamed launch splits the pages differently)."""
         _non_negative(layers, "layers")
         per_q = heads * head_dim
         width = kv_heads * head_dim

@@ -114,7 +114,7 @@ def oracle_decode(alloc, P, kv, hd, k, v, q, bias=None, theta=1e6):
     own = (seq - 1) // P
     pages, tiers = sealed_pages(alloc, 0, own)
     return att.causal_decode(q, pages, tiers, k[own * P:], v[own * P:], kv, hd, P,
-                             k_bias=bias, theta=theta)
+                             k_bias=bias, theta=theta, with_bound=True)
 
 
 def run_decode(m, cache, k, v, q, heads, kv, hd, bias=None, theta=1e6, mass=True, partials=True,
@@ -148,8 +148,9 @@ def test_decode_over_mixed_tiers_is_the_oracle():
         m, alloc, cache, k, v, q, b = decode_case(P, kv, hd, heads, tmap, seq, seed=seq, bias=bias)
         for partials in (True, False):
             got, mass = run_decode(m, cache, k, v, q, heads, kv, hd, b, partials=partials)
-            want, want_mass = oracle_decode(alloc, P, kv, hd, k, v, q, b)
-            assert_attention_close(got, want, f"P={P} {shape} seq={seq} partials={partials}")
+            want, want_mass, bound = oracle_decode(alloc, P, kv, hd, k, v, q, b)
+            assert_attention_close(got, want, f"P={P} {shape} seq={seq} partials={partials}",
+                                   bound)
             assert_mass_close(mass, want_mass, "mass")
             np.testing.assert_allclose(mass.sum(1), 1.0, atol=1e-5)
 
@@ -179,7 +180,8 @@ def test_decode_over_a_cache_that_does_not_seal_is_the_oracle():
         cache.attention(0, put(q), None, None, out, 1, seq, heads, kv, hd, None, None, mass,
                         d.empty_f32(d.attention_partials(hd)))
         want, w = att.attention64(q, k, v)
-        assert_attention_close(out.to_numpy().reshape(1, heads, hd), want, "paged")
+        assert_attention_close(out.to_numpy().reshape(1, heads, hd), want, "paged",
+                               att.attention_bound(q, k, v, w))
         assert_mass_close(mass.to_numpy().reshape(heads, pages), att.page_mass(w[:, 0], 32),
                           "paged mass")
 
@@ -220,24 +222,28 @@ def test_the_fused_ewma_is_the_oracle_fold_of_the_kernel_s_masses():
         got, mass = run_decode(m, cache, k[:t + 1], v[:t + 1], q, heads, kv, hd, scores=scores)
         steps.append((0, mass.astype(np.float32)))
         if t % 13 == 0:
-            want, want_mass = oracle_decode(alloc, P, kv, hd, k[:t + 1], v[:t + 1], q)
-            assert_attention_close(got, want, f"step {t}")
+            want, want_mass, bound = oracle_decode(alloc, P, kv, hd, k[:t + 1], v[:t + 1], q)
+            assert_attention_close(got, want, f"step {t}", bound)
             assert_mass_close(mass, want_mass, f"step {t}")
     np.testing.assert_array_equal(scores.download(), ewma.host_ewma(steps, LAYERS, max_pages))
 
 
-def test_one_launch_over_several_layers_is_each_layer_s_own_launch():
+def test_one_launch_over_several_layers_matches_each_layer_and_the_oracle():
     """attention_layers, beyond the reference (several layers' decode queries
-    in one launch), gives to the bit what one split attention call a layer
-    gives: outputs, masses and the scores folded over two steps; and the
-    first and last layers match the oracle. Also a sub-range of layers, and
-    a range past the cache refused."""
+    in one launch, streamed through LDS a page at a time), against each
+    layer's own split attention call and the float64 oracle, at the 1e-3 bar,
+    over mixed tiers, 1.5B / 0.5B / Llama head shapes; the scores folded over
+    two steps equal, to the bit, the oracle's fold of the launch's own masses.
+    Also a sub-range of layers, a cache that does not seal, and a range past
+    the cache refused."""
     m = mi()
     d = m.device
-    P, heads, kv, hd, L = 32, 12, 2, 128, 3
-    for seq in (32 * 9 + 7, 32 * 64, 33):
-        announce("layers in one launch", seq)
-        rng = np.random.default_rng(seq)
+    P, L = 32, 3
+    cases = [((12, 2, 128), 32 * 9 + 7), ((12, 2, 128), 32 * 64), ((12, 2, 128), 33),
+             ((14, 2, 64), 32 * 40 + 1), ((32, 8, 64), 32 * 17 + 30)]
+    for (heads, kv, hd), seq in cases:
+        announce("layers in one launch", heads, kv, hd, seq)
+        rng = np.random.default_rng(seq + hd)
         cap = [4096] * 4
         cap[0] += L * 2 + 8
         alloc = m.PagedKVCache(page_sizes(P, kv, hd), cap)
@@ -248,38 +254,68 @@ def test_one_launch_over_several_layers_is_each_layer_s_own_launch():
             store_in_runs(cache, l, k[l], v[l], [seq - 1, 1])
         pages = -(-seq // P)
         max_pages = pages + 1
-        together, alone = d.ImportanceScores(L, max_pages), d.ImportanceScores(L, max_pages)
+        scores = d.ImportanceScores(L, max_pages)
         part = d.empty_f32(d.attention_partials(hd))
         own_k, own_v = put(k[:, -1]), put(v[:, -1])
+        own = (seq - 1) // P
+        folded = []
         for step in range(2):
             q = normal(rng, L, heads, hd)
             out, mass = d.empty(L * heads * hd), d.empty_f32(L * heads * pages)
             cache.attention_layers(0, L, put(q), out, seq, heads, kv, hd, own_k, own_v, mass,
-                                   scores=together)
+                                   scores=scores)
             got = out.to_numpy().reshape(L, heads, hd)
             got_mass = mass.to_numpy()[:L * heads * pages].reshape(L, heads, pages)
+            oracle = {}
             for l in range(L):
+                folded.append((l, got_mass[l].astype(np.float32)))
+                sealed, tiers = sealed_pages(alloc, l, own)
+                want, want_mass, bound = att.causal_decode(q[l:l + 1], sealed, tiers,
+                                                           k[l, own * P:], v[l, own * P:], kv, hd,
+                                                           P, with_bound=True)
+                oracle[l] = (want, bound)
+                assert_attention_close(got[l:l + 1], want, f"layer {l} seq={seq}", bound)
+                assert_mass_close(got_mass[l], want_mass, f"layer {l} mass")
+                # The layer's own launch meets the same bar.
                 o1, m1 = d.empty(heads * hd), d.empty_f32(heads * pages)
                 cache.attention(l, put(q[l]), None, None, o1, 1, seq, heads, kv, hd,
-                                put(k[l, -1:]), put(v[l, -1:]), m1, part, scores=alone)
-                np.testing.assert_array_equal(got[l], o1.to_numpy().reshape(heads, hd))
-                np.testing.assert_array_equal(got_mass[l], m1.to_numpy().reshape(heads, pages))
-            np.testing.assert_array_equal(together.download(), alone.download())
-        own = (seq - 1) // P
-        for l in (0, L - 1):
-            sealed, tiers = sealed_pages(alloc, l, own)
-            want, want_mass = att.causal_decode(q[l:l + 1], sealed, tiers, k[l, own * P:],
-                                                v[l, own * P:], kv, hd, P)
-            assert_attention_close(got[l:l + 1], want, f"layer {l} seq={seq}")
-            assert_mass_close(got_mass[l], want_mass, f"layer {l} mass")
-        # Layers 1 and 2 alone: the same bits as in the three-layer launch.
+                                put(k[l, -1:]), put(v[l, -1:]), m1, part)
+                assert_attention_close(o1.to_numpy().reshape(1, heads, hd), want,
+                                       f"layer {l} own launch", bound)
+                assert_mass_close(m1.to_numpy().reshape(heads, pages), want_mass,
+                                  f"layer {l} own launch mass")
+            np.testing.assert_array_equal(scores.download(),
+                                          ewma.host_ewma(folded, L, max_pages))
+        # Layers 1 and 2 alone.
         out2 = d.empty(2 * heads * hd)
         cache.attention_layers(1, 2, put(q[1:]), out2, seq, heads, kv, hd, put(k[1:, -1]),
                                put(v[1:, -1]))
-        np.testing.assert_array_equal(out2.to_numpy().reshape(2, heads, hd), got[1:])
+        two = out2.to_numpy().reshape(2, heads, hd)
+        for i, l in enumerate((1, 2)):
+            assert_attention_close(two[i:i + 1], oracle[l][0], f"layers 1-2: {l}", oracle[l][1])
         with pytest.raises(IndexError):
             cache.attention_layers(2, 2, put(q[1:]), out2, seq, heads, kv, hd, put(k[1:, -1]),
                                    put(v[1:, -1]))
+    # A cache that does not seal: every page FP16 in the table, the last partly filled.
+    heads, kv, hd, seq = 14, 2, 64, 32 * 20 + 9
+    announce("layers in one launch, no seal", seq)
+    rng = np.random.default_rng(5)
+    cap = [4096] * 4
+    cap[0] += L * 2 + 8
+    alloc = m.PagedKVCache(page_sizes(P, kv, hd), cap)
+    cache = d.KVPages(alloc, L, P, kv, hd, 0, d.Halves.Both, [], False)
+    assert not cache.seals
+    k, v = normal(rng, L, seq, kv, hd), normal(rng, L, seq, kv, hd)
+    for l in range(L):
+        store_in_runs(cache, l, k[l], v[l], [seq])
+    q = normal(rng, L, heads, hd)
+    out = d.empty(L * heads * hd)
+    cache.attention_layers(0, L, put(q), out, seq, heads, kv, hd)
+    got = out.to_numpy().reshape(L, heads, hd)
+    for l in range(L):
+        want, w = att.attention64(q[l:l + 1], k[l], v[l])
+        assert_attention_close(got[l:l + 1], want, f"no-seal layer {l}",
+                               att.attention_bound(q[l:l + 1], k[l], v[l], w))
 
 
 def test_downgrade_upgrade_and_moves_are_quantise_of_the_shadow():
@@ -395,9 +431,10 @@ def test_an_evicted_page_reads_as_a_masked_one_to_the_bit():
             pages, tiers = sealed_pages(alloc, 0, seq // P)
             for p in (3, 4, 11):
                 tiers[p] = quant.UNREAD
-            want, want_mass = att.causal_decode(q, pages, tiers, k[(seq // P) * P:],
-                                                v[(seq // P) * P:], kv, hd, P)
-            assert_attention_close(got, want, "masked")
+            want, want_mass, bound = att.causal_decode(q, pages, tiers, k[(seq // P) * P:],
+                                                       v[(seq // P) * P:], kv, hd, P,
+                                                       with_bound=True)
+            assert_attention_close(got, want, "masked", bound)
             assert_mass_close(mass, want_mass, "masked mass")
     np.testing.assert_array_equal(outs[0], outs[1])
 
@@ -428,8 +465,8 @@ def test_full_size_config3_layer_against_the_oracle():
     announce("config3 full layer: decode")
     got, mass = run_decode(m, cache, k.astype(np.float32), v.astype(np.float32), q, shape.heads,
                            shape.kv_heads, shape.head_dim, scores=scores)
-    want, want_mass = oracle_decode(alloc, P, shape.kv_heads, shape.head_dim, k, v, q)
-    assert_attention_close(got, want, "config3")
+    want, want_mass, bound = oracle_decode(alloc, P, shape.kv_heads, shape.head_dim, k, v, q)
+    assert_attention_close(got, want, "config3", bound)
     assert_mass_close(mass, want_mass, "config3 mass")
     np.testing.assert_array_equal(scores.download()[0],
                                   ewma.host_ewma([(0, mass.astype(np.float32))], 1, seq // P)[0])

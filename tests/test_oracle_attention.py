@@ -103,3 +103,22 @@ def test_causal_decode_reads_sealed_pages_at_their_tiers():
     np.testing.assert_allclose(out, want, rtol=1e-12, atol=1e-14)
     np.testing.assert_allclose(mass, att.page_mass(w[:, 0], P), rtol=1e-12, atol=1e-15)
     assert mass.shape == (heads, 4)
+
+
+def test_error_bound_is_the_reference_formula_by_hand():
+    """attention_bound (tests/test_attention.py:58-107) on a case worked by
+    hand: two visible keys with equal scores (weights 1/2 each), so terms =
+    (|v0| + |v1|) / 2 per channel and the largest score term is the bigger
+    of sum_d |q_d k_jd| / sqrt(hd); a third key past the query is masked and
+    must not count."""
+    hd = 4
+    q = np.array([[[1.0, -2.0, 0.5, 0.0]]])
+    k = np.array([[[1.0, 0.0, 0.0, 0.0]], [[1.0, 0.0, 0.0, 0.0]], [[9.0, 9.0, 9.0, 9.0]]])
+    v = np.array([[[1.0, -3.0, 0.0, 2.0]], [[-1.0, 1.0, 4.0, 0.0]], [[100.0] * 4]])
+    out, w = att.attention64(q, k, v, positions=np.array([1]))
+    assert np.allclose(w[0, 0], [0.5, 0.5, 0.0])
+    bound = att.attention_bound(q, k, v, w, positions=np.array([1]))
+    terms = (np.abs(v[0, 0]) + np.abs(v[1, 0])) / 2
+    score_terms = max(np.abs(q[0, 0] * k[0, 0]).sum(), np.abs(q[0, 0] * k[1, 0]).sum()) / 2.0
+    want = (np.sqrt(2) + np.sqrt(hd) * score_terms) * 2.0**-24 * terms
+    np.testing.assert_allclose(bound[0, 0], want, rtol=1e-12)
