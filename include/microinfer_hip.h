@@ -19,8 +19,9 @@
  *   - "device" pointers are device-visible addresses (hipMalloc'd memory, or
  *     pinned host memory mapped for the device); "host" pointers are host
  *     memory. fp16 data is passed as raw 16-bit storage.
- *   - `stream` is a hipStream_t (0 = the null stream, which every object of
- *     the runtime uses). Launchers enqueue and return without synchronising;
+ *   - `stream` is a hipStream_t; 0 = the runtime's current stream, which
+ *     every object of the runtime uses (the null stream unless
+ *     mi_set_stream names another). Launchers enqueue and return without synchronising;
  *     execution errors surface at the next synchronising call
  *     (reference: device_ops.h:20-28).
  *   - Tiers: 0 FP16, 1 INT8, 2 INT4, 3 INT2 (reference: paged_kv_cache.h:16-25).
@@ -66,6 +67,8 @@ const char *mi_build_info(void);
 int mi_device_count(int *count);
 int mi_device_name(char *out, size_t capacity);
 int mi_runtime_version(int *version);
+/* reference: device.cu:10-17 cuda_driver_version (renamed: the HIP driver's). */
+int mi_driver_version(int *version);
 int mi_memory_info(size_t *free_bytes, size_t *total_bytes);
 int mi_granule_bytes(size_t *out);
 int mi_malloc(void **out, size_t bytes);
@@ -180,6 +183,40 @@ int mi_rmsnorm(const void *x, int x_is_f32, const void *weight, void *out, int r
                float eps, void *stream);
 int mi_swiglu(const void *gate, const void *up, void *out, size_t count, void *stream);
 int mi_add(const void *a, const void *b, void *out, size_t count, void *stream);
+
+/* ---- Dense projections, embedding, logits ---------------------------------
+ * fp16 operands, fp32 accumulation through hipBLASLt; W is (out, in) as the
+ * checkpoint stores it, and y = x W^T.
+ * mi_linear replaces device::linear (linear.cu:99-114; bindings_device.cpp:
+ * 411-428, and the NumPy `linear`, bindings.cpp:513-517): y (rows, out) fp16,
+ * the bias (out) fp16 or null added in fp32 before the one rounding.
+ * mi_linear_f32 replaces device::linear_fp32_out (linear.cu:116-125) and,
+ * with accumulate != 0, linear_accumulate (:127-138; bindings_device.cpp:
+ * 351-365): out (rows, out) fp32 = or += x W^T. */
+int mi_linear(const void *x, const void *weight, const void *bias, void *out, int rows,
+              int in_features, int out_features, void *stream);
+int mi_linear_f32(const void *x, const void *weight, float *out, int accumulate, int rows,
+                  int in_features, int out_features, void *stream);
+/* reference: embed.cu:60-76, bindings_device.cpp:321-334 (embed_f32) and
+ * :383-396 (embed): out (count, hidden) = table rows ids[i], fp16 or widened
+ * to fp32 (out_is_f32); an id outside [0, vocab) gives a zero row. */
+int mi_embed(const int32_t *ids, int count, const void *table, void *out, int out_is_f32,
+             int hidden, int vocab, void *stream);
+/* reference: argmax.cu:71-81. out[r] = the index of row r's largest value,
+ * the lowest on a tie; cols for a row with no value >= -FLT_MAX. */
+int mi_argmax_rows(const float *x, int rows, int cols, int32_t *out, void *stream);
+/* reference: bindings_device.cpp:109-195. scratch_elements: fp16 elements of
+ * scratch that logits or greedy need for `rows` rows (fp32 logits, then the
+ * int32 ids). mi_logits: fp32 logits of x's rows [first_row, first_row +
+ * rows) through the (vocab, hidden) head, copied to host_out (rows, vocab),
+ * synchronously. mi_greedy: each row's argmax id to host_ids; a row with no
+ * finite logit fails with MI_ERR_LOGIC ("no finite logit"). Both run on the
+ * runtime's current stream. */
+int mi_scratch_elements(int rows, int vocab, size_t *out);
+int mi_logits(const void *x, const void *head, void *scratch, size_t scratch_elements,
+              int first_row, int rows, int hidden, int vocab, float *host_out);
+int mi_greedy(const void *x, const void *head, void *scratch, size_t scratch_elements,
+              int first_row, int rows, int hidden, int vocab, int32_t *host_ids);
 
 /* ---- PagedKVCache: the per-tier VMM allocator ------------------------------
  * reference: paged_kv_cache.h:112-227, bindings.cpp:579-668. Keys are

@@ -18,4 +18,5 @@ Modules:
   ewma       the importance-score EWMA in fp32, in the device's order
   slots      the tail-swap page allocator and its granule accounting
   pointwise  RoPE, RMSNorm, SwiGLU float64 references
+  dense      float64 projection with its term magnitudes, embed, argmax
 """

@@ -21,7 +21,10 @@ LIBRARY = HERE / "microinfer" / "libmicroinfer_hip.so"
 ARCH = os.environ.get("MI_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["quant.hip", "pages.hip", "pointwise.hip", "attention.hip", "decode.hip",
-           "allocator.cpp", "kv_pages.cpp", "capi.cpp"]
+           "dense.hip", "linear.cpp", "allocator.cpp", "kv_pages.cpp", "capi.cpp"]
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+# The dense projections call hipBLASLt.
+LIBS = [f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lhipblaslt"]
 
 # Bit-exact arithmetic needs IEEE fp32 with nothing fused behind our back:
 # no contraction, no fast-math, denormals kept. Packed fp32 instructions are
@@ -53,7 +56,7 @@ def build(verbose: bool = False) -> Path:
         objects = list(pool.map(compile_one, SOURCES))
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-           *map(str, objects)]
+           *map(str, objects), *LIBS]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{result.stderr}")

@@ -67,7 +67,12 @@ namespace
     catch (...) { return fail(MI_ERR_LOGIC, "unknown error"); }
   }
 
-  hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+  // A null stream argument is the runtime's current stream (the null stream
+  // unless mi_set_stream named another), so every launch follows it.
+  hipStream_t as_stream(void *s)
+  {
+    return s != nullptr ? static_cast<hipStream_t>(s) : mi::runtime_stream();
+  }
 
   void need(const void *p, const char *what)
   {
@@ -178,6 +183,11 @@ int mi_device_name(char *out, size_t capacity)
 int mi_runtime_version(int *version)
 {
   return guarded([&] { mi::hip_check(hipRuntimeGetVersion(version), "hipRuntimeGetVersion"); });
+}
+
+int mi_driver_version(int *version)
+{
+  return guarded([&] { mi::hip_check(hipDriverGetVersion(version), "hipDriverGetVersion"); });
 }
 
 int mi_memory_info(size_t *free_bytes, size_t *total_bytes)
@@ -588,6 +598,131 @@ int mi_swiglu(const void *gate, const void *up, void *out, size_t count, void *s
 int mi_add(const void *a, const void *b, void *out, size_t count, void *stream)
 {
   return guarded([&] { mi::launch_add(a, b, out, count, as_stream(stream)); });
+}
+
+// ---- dense projections, embedding, logits ----------------------------------------
+
+namespace
+{
+  std::size_t scratch_elements_of(int rows, int vocab)
+  {
+    if (rows < 0 || vocab < 0)
+    {
+      throw mi::InvalidArgument("scratch is sized for rows >= 0 and vocab >= 0");
+    }
+    const std::size_t bytes = static_cast<std::size_t>(rows) * vocab * sizeof(float) +
+                              static_cast<std::size_t>(rows) * sizeof(std::int32_t);
+    return (bytes + 1) / 2;
+  }
+
+  // Rows [first_row, first_row + rows) of x through the (vocab, hidden) head,
+  // fp32 logits into the scratch.
+  float *logits_into(const void *x, const void *head, void *scratch, size_t scratch_elements,
+                     int first_row, int rows, int hidden, int vocab, hipStream_t stream)
+  {
+    if (first_row < 0 || rows < 0)
+    {
+      throw mi::InvalidArgument("first_row and rows are >= 0; got " + std::to_string(first_row) +
+                                " and " + std::to_string(rows));
+    }
+    if (scratch_elements < scratch_elements_of(rows, vocab))
+    {
+      throw mi::InvalidArgument("scratch holds " + std::to_string(scratch_elements) +
+                                ", and the logits of " + std::to_string(rows) + " rows need " +
+                                std::to_string(scratch_elements_of(rows, vocab)));
+    }
+    need(x, "x");
+    need(head, "head");
+    need(scratch, "scratch");
+    auto *out = static_cast<float *>(scratch);
+    const auto *rows_x =
+        static_cast<const std::uint16_t *>(x) + static_cast<std::size_t>(first_row) * hidden;
+    mi::linear_float(rows_x, head, out, false, rows, hidden, vocab, stream);
+    return out;
+  }
+}
+
+int mi_linear(const void *x, const void *weight, const void *bias, void *out, int rows,
+              int in_features, int out_features, void *stream)
+{
+  return guarded([&] {
+    mi::linear_half(x, weight, bias, out, rows, in_features, out_features, as_stream(stream));
+  });
+}
+
+int mi_linear_f32(const void *x, const void *weight, float *out, int accumulate, int rows,
+                  int in_features, int out_features, void *stream)
+{
+  return guarded([&] {
+    mi::linear_float(x, weight, out, accumulate != 0, rows, in_features, out_features,
+                     as_stream(stream));
+  });
+}
+
+int mi_embed(const int32_t *ids, int count, const void *table, void *out, int out_is_f32,
+             int hidden, int vocab, void *stream)
+{
+  return guarded([&] {
+    mi::launch_embed(ids, count, table, out, out_is_f32 != 0, hidden, vocab, as_stream(stream));
+  });
+}
+
+int mi_argmax_rows(const float *x, int rows, int cols, int32_t *out, void *stream)
+{
+  return guarded([&] { mi::launch_argmax_rows(x, rows, cols, out, as_stream(stream)); });
+}
+
+int mi_scratch_elements(int rows, int vocab, size_t *out)
+{
+  return guarded([&] { *out = scratch_elements_of(rows, vocab); });
+}
+
+int mi_logits(const void *x, const void *head, void *scratch, size_t scratch_elements,
+              int first_row, int rows, int hidden, int vocab, float *host_out)
+{
+  return guarded([&] {
+    const hipStream_t stream = mi::runtime_stream();
+    const float *dev = logits_into(x, head, scratch, scratch_elements, first_row, rows, hidden,
+                                   vocab, stream);
+    const std::size_t bytes = static_cast<std::size_t>(rows) * vocab * sizeof(float);
+    if (bytes > 0)
+    {
+      mi::hip_check(hipMemcpyAsync(host_out, dev, bytes, hipMemcpyDeviceToHost, stream),
+                    "hipMemcpyAsync logits device-to-host");
+      mi::hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize logits");
+    }
+  });
+}
+
+int mi_greedy(const void *x, const void *head, void *scratch, size_t scratch_elements,
+              int first_row, int rows, int hidden, int vocab, int32_t *host_ids)
+{
+  return guarded([&] {
+    const hipStream_t stream = mi::runtime_stream();
+    const float *dev = logits_into(x, head, scratch, scratch_elements, first_row, rows, hidden,
+                                   vocab, stream);
+    if (rows == 0)
+    {
+      return;
+    }
+    auto *ids = reinterpret_cast<std::int32_t *>(static_cast<char *>(scratch) +
+                                                 static_cast<std::size_t>(rows) * vocab *
+                                                     sizeof(float));
+    mi::launch_argmax_rows(dev, rows, vocab, ids, stream);
+    mi::hip_check(hipMemcpyAsync(host_ids, ids, static_cast<std::size_t>(rows) * sizeof(int32_t),
+                                 hipMemcpyDeviceToHost, stream),
+                  "hipMemcpyAsync ids device-to-host");
+    mi::hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize greedy");
+    for (int r = 0; r < rows; ++r)
+    {
+      if (host_ids[r] >= vocab)
+      {
+        throw mi::LogicError("row " + std::to_string(first_row + r) +
+                             " has no finite logit, so there is no greedy choice; the forward "
+                             "pass produced NaN or -inf throughout");
+      }
+    }
+  });
 }
 
 // ---- PagedKVCache ------------------------------------------------------------

@@ -46,6 +46,25 @@ namespace mi
                      hipStream_t stream);
   void launch_add(const void *a, const void *b, void *out, std::size_t count, hipStream_t stream);
 
+  // ---- dense projections and their neighbours (linear.cpp, dense.hip) ------------------
+  // y = x W^T (+ bias): x (rows, in) fp16, W (out, in) fp16, y (rows, out)
+  // fp16, fp32 accumulation and one rounding; bias (out) fp16 or null.
+  void linear_half(const void *x, const void *weight, const void *bias, void *out, int rows,
+                   int in_features, int out_features, hipStream_t stream);
+  // y = x W^T in fp32, or y += x W^T when `accumulate`.
+  void linear_float(const void *x, const void *weight, float *out, bool accumulate, int rows,
+                    int in_features, int out_features, hipStream_t stream);
+  // out row t = table row ids[t] (fp16, or widened to fp32); an id outside
+  // [0, vocab) gives a zero row.
+  void launch_embed(const std::int32_t *ids, int count, const void *table, void *out,
+                    bool out_is_f32, int hidden, int vocab, hipStream_t stream);
+  // out[r] = the index of row r's largest value, the lowest on a tie; cols
+  // for a row with no value >= -FLT_MAX.
+  void launch_argmax_rows(const float *x, int rows, int cols, std::int32_t *out,
+                          hipStream_t stream);
+  // Every row of out (rows, cols) fp16 = row (cols), or zero when row is null.
+  void launch_broadcast_rows(const void *row, void *out, int rows, int cols, hipStream_t stream);
+
   // ---- attention (attention.hip, decode.hip) -------------------------------------------
   // Where keys and values are read from. Contiguous: k and v (seq_k, kv, hd).
   // Paged: an FP16 page table, `pages`, P rows of keys then values. Causal:

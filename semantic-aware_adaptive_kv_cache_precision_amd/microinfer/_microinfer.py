@@ -92,6 +92,14 @@ SIGNATURES = {
     "mi_rmsnorm": ((_vp, _i, _vp, _vp, _i, _i, _f, _vp), C.c_int),
     "mi_swiglu": ((_vp, _vp, _vp, _sz, _vp), C.c_int),
     "mi_add": ((_vp, _vp, _vp, _sz, _vp), C.c_int),
+    "mi_driver_version": ((_ip,), C.c_int),
+    "mi_linear": ((_vp, _vp, _vp, _vp, _i, _i, _i, _vp), C.c_int),
+    "mi_linear_f32": ((_vp, _vp, _vp, _i, _i, _i, _i, _vp), C.c_int),
+    "mi_embed": ((_vp, _i, _vp, _vp, _i, _i, _i, _vp), C.c_int),
+    "mi_argmax_rows": ((_vp, _i, _i, _vp, _vp), C.c_int),
+    "mi_scratch_elements": ((_i, _i, _szp), C.c_int),
+    "mi_logits": ((_vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp), C.c_int),
+    "mi_greedy": ((_vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp), C.c_int),
     "mi_cache_create": ((_szp, _szp, C.POINTER(_vp)), C.c_int),
     "mi_cache_destroy": ((_vp,), None),
     "mi_cache_allocate": ((_vp, _i, _i, _i), C.c_int),
@@ -311,6 +319,16 @@ def hip_runtime_version() -> int:
     return v.value
 
 
+def driver_version() -> int:
+    """The HIP driver's version (the reference's cuda_driver_version)."""
+    v = C.c_int()
+    _check(lib.mi_driver_version(C.byref(v)))
+    return v.value
+
+
+cuda_driver_version = driver_version
+
+
 def device_memory_info() -> dict:
     free, total = C.c_size_t(), C.c_size_t()
     _check(lib.mi_memory_info(C.byref(free), C.byref(total)))
@@ -461,6 +479,37 @@ def swiglu(gate, up) -> np.ndarray:
     dg, du, out = upload_fp16(gate), upload_fp16(up), DeviceTensor(gate.size)
     _check(lib.mi_swiglu(dg.address, du.address, out.address, gate.size, None))
     return out.to_numpy().reshape(gate.shape)
+
+
+def linear(x, weight, bias=None) -> np.ndarray:
+    """x @ weight.T + bias through hipBLASLt; weight (out_features,
+    in_features) as the checkpoint stores it. fp16 operands, fp32
+    accumulation, one fp16 rounding on store (bindings.cpp:158-215)."""
+    x = np.ascontiguousarray(x, np.float32)
+    weight = np.ascontiguousarray(weight, np.float32)
+    if x.ndim != 2:
+        raise ValueError(f"x must be 2-D (rows, in_features), got shape {_shape(x)}")
+    if weight.ndim != 2:
+        raise ValueError(f"weight must be 2-D (out_features, in_features), got shape "
+                         f"{_shape(weight)}")
+    if weight.shape[1] != x.shape[1]:
+        raise ValueError(f"weight {_shape(weight)} does not match x {_shape(x)}: weight is "
+                         f"(out_features, in_features) and x has in_features {x.shape[1]}")
+    if x.shape[1] == 0:
+        raise ValueError("in_features must be at least 1")
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, np.float32)
+        if bias.ndim != 1 or bias.shape[0] != weight.shape[0]:
+            raise ValueError(f"bias must be 1-D (out_features,) with out_features "
+                             f"{weight.shape[0]}, got shape {_shape(bias)}")
+    rows, in_features = x.shape
+    out_features = weight.shape[0]
+    dx, dw = upload_fp16(x), upload_fp16(weight)
+    db = upload_fp16(bias) if bias is not None else None
+    out = DeviceTensor(rows * out_features)
+    _check(lib.mi_linear(dx.address, dw.address, db.address if db is not None else None,
+                         out.address, rows, in_features, out_features, None))
+    return out.to_numpy().reshape(rows, out_features)
 
 
 def attention(q, k, v, k_bias=None, theta: float = 0.0) -> np.ndarray:
@@ -1099,6 +1148,71 @@ def _device_copy(source, target, count):
     _check(lib.mi_memcpy(ta, sa, 2 * count, 2))
 
 
+def _device_linear(x, weight, bias, out, rows, in_features, out_features):
+    xa = _need(_span(x), rows * in_features, "x")
+    wa = _need(_span(weight), out_features * in_features, "weight")
+    ba = _need(_span(bias), out_features, "bias") if bias is not None else None
+    oa = _need(_span(out), rows * out_features, "out")
+    _check(lib.mi_linear(xa, wa, ba, oa, rows, in_features, out_features, None))
+
+
+def _device_linear_accumulate(x, weight, out: FloatTensor, rows, in_features, out_features):
+    """out += x @ weight.T in fp32: a projection added into the residual
+    stream with no fp16 rounding (bindings_device.cpp:351-365)."""
+    xa = _need(_span(x), rows * in_features, "x")
+    wa = _need(_span(weight), out_features * in_features, "weight")
+    oa = _floats(out, rows * out_features, "out")
+    _check(lib.mi_linear_f32(xa, wa, oa, 1, rows, in_features, out_features, None))
+
+
+def _device_embed(ids: DeviceIndex, table, out, hidden, vocab):
+    ta = _need(_span(table), vocab * hidden, "table")
+    oa = _need(_span(out), ids.count * hidden, "out")
+    _check(lib.mi_embed(ids.address, ids.count, ta, oa, 0, hidden, vocab, None))
+
+
+def _device_embed_f32(ids: DeviceIndex, table, out: FloatTensor, hidden, vocab):
+    """The embedding gather, widened exactly to fp32 (bindings_device.cpp:321-334)."""
+    ta = _need(_span(table), vocab * hidden, "table")
+    oa = _floats(out, ids.count * hidden, "out")
+    _check(lib.mi_embed(ids.address, ids.count, ta, oa, 1, hidden, vocab, None))
+
+
+def scratch_elements(rows: int, vocab: int) -> int:
+    """fp16 elements of scratch that logits or greedy need for `rows` rows."""
+    out = C.c_size_t()
+    _check(lib.mi_scratch_elements(rows, vocab, C.byref(out)))
+    return out.value
+
+
+def _logits_args(x, head, scratch, first_row, rows, hidden, vocab):
+    _non_negative(first_row, "first_row")
+    _non_negative(rows, "rows")
+    xa = _need(_span(x), (first_row + rows) * hidden, "x")
+    ha = _need(_span(head), vocab * hidden, "head")
+    sp = _span(scratch)
+    sa = _need(sp, scratch_elements(rows, vocab), "scratch")
+    return xa, ha, sa, sp.count
+
+
+def logits(x, head, scratch, first_row: int, rows: int, hidden: int, vocab: int) -> np.ndarray:
+    """fp32 logits for rows [first_row, first_row + rows) of x, to the host
+    (bindings_device.cpp:133-157)."""
+    xa, ha, sa, held = _logits_args(x, head, scratch, first_row, rows, hidden, vocab)
+    out = np.empty((rows, vocab), np.float32)
+    _check(lib.mi_logits(xa, ha, sa, held, first_row, rows, hidden, vocab, out.ctypes.data))
+    return out
+
+
+def greedy(x, head, scratch, first_row: int, rows: int, hidden: int, vocab: int) -> np.ndarray:
+    """The argmax token of each row's logits, computed on the device
+    (bindings_device.cpp:161-195); a row with no finite logit raises."""
+    xa, ha, sa, held = _logits_args(x, head, scratch, first_row, rows, hidden, vocab)
+    out = np.empty(rows, np.int32)
+    _check(lib.mi_greedy(xa, ha, sa, held, first_row, rows, hidden, vocab, out.ctypes.data))
+    return out
+
+
 def _upload_f32(host) -> FloatTensor:
     h = np.ascontiguousarray(host, np.float32).reshape(-1)
     t = FloatTensor(h.size)
@@ -1115,6 +1229,10 @@ device = SimpleNamespace(
     upload_f32=_upload_f32,
     index=DeviceIndex,
     DeviceIndex=DeviceIndex,
+    embed=_device_embed,
+    embed_f32=_device_embed_f32,
+    linear=_device_linear,
+    linear_accumulate=_device_linear_accumulate,
     rmsnorm=_device_rmsnorm,
     rmsnorm_f32=_device_rmsnorm_f32,
     rope=_device_rope,
@@ -1136,6 +1254,9 @@ device = SimpleNamespace(
     shadow_upload_page=-4,
     evicted_tier=4,
     page_bytes=page_bytes,
+    scratch_elements=scratch_elements,
+    logits=logits,
+    greedy=greedy,
     synchronize=synchronize,
 )
 

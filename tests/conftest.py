@@ -88,6 +88,34 @@ def assert_mass_close(got, want, what=""):
     assert np.all(err <= bound), f"{what}: mass error {err.max():.3g}"
 
 
+#: Dense projections: the reference's per-kernel gate (tests/ulp_gate.py:
+#: 28-103) in ulps of the fp16 output, max relative error < 4 ulps and mean
+#: < 1 ulp, the denominator floored at fp16's smallest normal and, for a
+#: sum, at the magnitude where fp32 accumulation's probabilistic error
+#: sqrt(n) * 2^-24 * terms (Higham and Mary 2019) spends the whole budget.
+FP16_REL_ULP = 2.0**-11
+ULP_MAX_REL = 4 * FP16_REL_ULP
+ULP_MEAN_REL = FP16_REL_ULP
+
+
+def accumulation_floor(terms, n: int) -> np.ndarray:
+    return np.sqrt(n) * 2.0**-24 * np.asarray(terms, np.float64) / ULP_MAX_REL
+
+
+def assert_within_gate(got, want, floor=None, what=""):
+    from oracle.attention import FP16_MIN_NORMAL
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} != reference {want.shape}"
+    f = FP16_MIN_NORMAL if floor is None else np.maximum(FP16_MIN_NORMAL, floor)
+    err = np.abs(got - want) / np.maximum(np.abs(want), f)
+    assert err.max() < ULP_MAX_REL, \
+        f"{what}: max relative error {err.max():.3e} ({err.max() / FP16_REL_ULP:.2f} ulp)"
+    assert err.mean() < ULP_MEAN_REL, \
+        f"{what}: mean relative error {err.mean():.3e} ({err.mean() / FP16_REL_ULP:.2f} ulp)"
+    return err
+
+
 def announce(*what) -> None:
     """Names the case before a GPU step, flushed, so a failed run says where."""
     print("[case]", *what, flush=True)
