@@ -171,6 +171,40 @@ def causal_decode(q, sealed_pages, tiers, own_k, own_v, kv_heads: int, head_dim:
     return out, mass, attention_bound(q, k, v, w, k_bias, theta, unread=flags)
 
 
+def causal_chunk(q, sealed_pages, tiers, k_rows, v_rows, kv_heads: int, head_dim: int,
+                 page_tokens: int, k_bias=None, theta: float = 0.0, with_bound: bool = False):
+    """A chunk of queries, the last len(q) positions of the rows, over a cache
+    that seals (tests/test_quantised_pages.py:86-104): the query at position
+    x reads every page before its own at the tier recorded for it (the
+    sealed pages' bytes) and its own page's rows as they came, k_rows and
+    v_rows (seq_k, kv, hd) holding every position's rows. Returns out
+    (seq_q, heads, hd), and attention_bound's error bound second when
+    `with_bound`."""
+    q = np.asarray(q, np.float64)
+    k_rows = np.asarray(k_rows, np.float64)
+    v_rows = np.asarray(v_rows, np.float64)
+    seq_q = q.shape[0]
+    seq_k = k_rows.shape[0]
+    positions = np.arange(seq_k - seq_q, seq_k)
+    owns = positions // page_tokens
+    K, V, unread = read_sealed(sealed_pages, tiers, kv_heads, head_dim, page_tokens)
+    out = np.zeros(q.shape)
+    bound = np.zeros(q.shape)
+    for own in np.unique(owns):
+        rows = owns == own
+        first = own * page_tokens
+        last = positions[rows].max()
+        k = np.concatenate([K[:first], k_rows[first:last + 1]])
+        v = np.concatenate([V[:first], v_rows[first:last + 1]])
+        flags = np.concatenate([unread[:first], np.zeros(last + 1 - first, bool)])
+        o, w = attention64(q[rows], k, v, k_bias, theta, unread=flags, positions=positions[rows])
+        out[rows] = o
+        if with_bound:
+            bound[rows] = attention_bound(q[rows], k, v, w, k_bias, theta, unread=flags,
+                                          positions=positions[rows])
+    return (out, bound) if with_bound else out
+
+
 def attention_bruteforce(q, k, v):
     """A plain double loop, for tiny inputs only: the check on attention64."""
     q = np.asarray(q, np.float64)

@@ -21,7 +21,7 @@ LIBRARY = HERE / "microinfer" / "libmicroinfer_hip.so"
 ARCH = os.environ.get("MI_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["quant.hip", "pages.hip", "pointwise.hip", "attention.hip", "decode.hip",
-           "dense.hip", "linear.cpp", "allocator.cpp", "kv_pages.cpp", "capi.cpp"]
+           "prefill.hip", "dense.hip", "linear.cpp", "allocator.cpp", "kv_pages.cpp", "capi.cpp"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 # The dense projections call hipBLASLt.
 LIBS = [f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lhipblaslt"]

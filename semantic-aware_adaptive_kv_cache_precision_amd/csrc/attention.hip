@@ -615,6 +615,15 @@ namespace mi
 
   bool launch_decode_fast(const KVSource &kv, const AttentionArgs &a, hipStream_t stream);
 
+  void launch_attention_combine(const float *partials, std::uint16_t *out, int seq_q, int heads,
+                                int head_dim, int splits, hipStream_t stream)
+  {
+    hipLaunchKernelGGL(combine_kernel, dim3(seq_q * heads), dim3(kCombineThreads),
+                       splits * sizeof(float), stream, partials, out, seq_q, heads, head_dim,
+                       splits, 0, nullptr, 0, 0);
+    hip_check(hipGetLastError(), "attention combine kernel launch");
+  }
+
   void launch_attention(const KVSource &kv, const AttentionArgs &a, hipStream_t stream)
   {
     check_grouping(a.heads, a.kv_heads);
@@ -640,6 +649,11 @@ namespace mi
     }
     if (launch_decode_fast(kv, a, stream))
     {
+      return;
+    }
+    if (prefill_applies(kv, a))
+    {
+      launch_prefill(kv, a, stream);
       return;
     }
     const bool aligned = kv.layout == Layout::kCausal;

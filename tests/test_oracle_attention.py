@@ -122,3 +122,35 @@ def test_error_bound_is_the_reference_formula_by_hand():
     score_terms = max(np.abs(q[0, 0] * k[0, 0]).sum(), np.abs(q[0, 0] * k[1, 0]).sum()) / 2.0
     want = (np.sqrt(2) + np.sqrt(hd) * score_terms) * 2.0**-24 * terms
     np.testing.assert_allclose(bound[0, 0], want, rtol=1e-12)
+
+
+def test_causal_chunk_is_each_query_decoded_alone_and_plain_attention_at_fp16():
+    """A chunk's query at position x is causal_decode of that query over the
+    pages before its own and its own page's rows up to x; over FP16 pages the
+    whole chunk is plain causal attention over the rows. A chunk that begins
+    mid-page and crosses two page boundaries, an unread page among them."""
+    rng = np.random.default_rng(11)
+    P, kv, hd, heads = 16, 2, 8, 4
+    seq_k, seq_q = 4 * P + 3, 2 * P + 9            # positions 26 .. 66: own pages 1 .. 4
+    k = fp16_exact(rng.standard_normal((seq_k, kv, hd))).astype(np.float16)
+    v = fp16_exact(rng.standard_normal((seq_k, kv, hd))).astype(np.float16)
+    q = fp16_exact(rng.standard_normal((seq_q, heads, hd)))
+    bias = fp16_exact(3 * rng.standard_normal((kv, hd)))
+    tiers = [quant.INT2, quant.UNREAD, quant.INT8, quant.INT4]
+    pages = []
+    for p, t in enumerate(tiers):
+        kp, vp = k[p * P:(p + 1) * P], v[p * P:(p + 1) * P]
+        pages.append(quant.fp16_page(kp, vp) if t in (quant.FP16, quant.UNREAD)
+                     else quant.quantise_page(kp, vp, t, P))
+    out, bound = att.causal_chunk(q, pages, tiers, k, v, kv, hd, P, bias, 1e4, with_bound=True)
+    assert out.shape == bound.shape == q.shape and np.all(bound > 0)
+    for i in range(seq_q):
+        x = seq_k - seq_q + i
+        own = x // P
+        want, _ = att.causal_decode(q[i:i + 1], pages[:own], tiers[:own], k[own * P:x + 1],
+                                    v[own * P:x + 1], kv, hd, P, bias, 1e4)
+        np.testing.assert_allclose(out[i:i + 1], want, rtol=1e-12, atol=1e-14, err_msg=f"query {i}")
+    fp16 = [quant.fp16_page(k[p * P:(p + 1) * P], v[p * P:(p + 1) * P]) for p in range(4)]
+    plain = att.causal_chunk(q, fp16, [quant.FP16] * 4, k, v, kv, hd, P)
+    want, _ = att.attention64(q, k, v)
+    np.testing.assert_allclose(plain, want, rtol=1e-12, atol=1e-14)
