@@ -12,8 +12,10 @@ timed with hipEvents on the stream they run on. Inputs are resident in HBM
 before timing starts.
 
 Also measured, outside the timed region: the requantisation plan of config 4
-(batched moves, pages/s) and the CPU oracle on a bounded sample of the same
-workload. Prints one JSON line.
+(batched moves, pages/s), the prefill attention (the reference's 16-query
+tile at 32K with key bias, and config 5's 16K prefill in 2K chunks on the
+matrix cores), and the CPU oracle on a bounded sample of the same workload.
+Prints one JSON line.
 """
 
 from __future__ import annotations
@@ -33,6 +35,7 @@ sys.path.insert(0, str(REPO))
 
 METRIC = "mixed-tier decode-attn GB/s (% HBM peak) & µs/token @32K; requant pages/s"
 PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
 P = 32
 
 
@@ -171,6 +174,139 @@ def requant_plan(m, shape, context, seed=0, layers=None):
             "shadows_taken": cache.last_batch and len(down)}
 
 
+def timed_graph(m, stream, body, steps, warmup) -> float:
+    """Milliseconds a replay of `body`, captured once as a HIP graph on
+    `stream`, averaged over `steps` replays after `warmup`."""
+    body()
+    m.synchronize()
+    graph = m.Graph(stream)
+    with graph.capture():
+        body()
+    for _ in range(warmup):
+        graph.launch()
+    stream.synchronize()
+    timer = m.Timer(stream)
+    timer.start()
+    for _ in range(steps):
+        graph.launch()
+    timer.stop()
+    stream.synchronize()
+    return timer.elapsed_ms() / steps
+
+
+def prefill_tile(m, shape, cache, alloc, host_rows, layers, context, stream, steps, warmup):
+    """The reference's prefill-tile measurement (benchmark.jsonl:3292-3296:
+    16 queries at the end of a 32K context, key bias on, one launch a
+    layer) on the config-3 cache: microseconds a launch, and parity of
+    layer 0 against the oracle."""
+    from oracle import attention as att
+    d = m.device
+    heads, hd, kv = shape.heads, shape.head_dim, shape.kv_heads
+    n = 16
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((layers, n, heads, hd)).astype(np.float16)
+    bias = (3 * rng.standard_normal((layers, kv, hd))).astype(np.float16)
+    rope = d.RopeTable(hd, shape.rope_theta)
+    rope.cover(context)
+    qs = [m.upload_fp16(q[l].astype(np.float32)) for l in range(layers)]
+    bs = [m.upload_fp16(bias[l].astype(np.float32)) for l in range(layers)]
+    ks = [m.upload_fp16(host_rows[l][0][-n:].astype(np.float32)) for l in range(layers)]
+    vs = [m.upload_fp16(host_rows[l][1][-n:].astype(np.float32)) for l in range(layers)]
+    outs = [d.empty(n * heads * hd) for _ in range(layers)]
+    partials = d.empty_f32(d.attention_partials(hd))
+
+    def body():
+        for l in range(layers):
+            cache.attention(l, qs[l], bs[l], rope, outs[l], n, context, heads, kv, hd, ks[l],
+                            vs[l], None, partials)
+
+    ms = timed_graph(m, stream, body, steps, warmup)
+    sealed = (context - 1) // P
+    pages = [alloc.read(0, i) for i in range(sealed)]
+    tiers = [int(alloc.locate(0, i)[0]) for i in range(sealed)]
+    k, v = host_rows[0]
+    want, bound = att.causal_chunk(q[0].astype(np.float64), pages, tiers, k, v, kv, hd, P,
+                                   bias[0].astype(np.float64), shape.rope_theta, with_bound=True)
+    check_gate(outs[0].to_numpy().reshape(n, heads, hd), want, bound, "prefill tile layer 0")
+    return {"us_per_launch": round(ms * 1e3 / layers, 2),
+            "ms_per_token_all_layers": round(ms * shape.layers / layers, 4),
+            "queries": n, "context": context, "key_bias": True,
+            "reference_us_per_launch_rtx4050": [6160.9, 7132.3],
+            "note": "config-3 cache (tiers 20/30/40/10 %), one launch a layer, HIP graph of "
+                    f"{layers} launches; MFMA chunk kernel with split-K + combine"}
+
+
+def prefill_chunks(m, stream, steps, warmup, seed=5):
+    """Config 5's prefill attention: Llama-3.2-1B shape, 16K positions in 2K
+    chunks over pages born at 30/40/30 % FP16/INT8/INT4 (seeded importance);
+    each chunk's 2048 queries attend the pages before their own at their
+    tiers and their own at FP16. One layer's 8 chunk launches, timed as a
+    graph; TFLOP/s of the causal attention's algorithmic work
+    4 * heads * head_dim * (keys each query sees), against the dense fp16
+    MFMA peak."""
+    from microinfer import workloads as w
+    from oracle import attention as att
+    d = m.device
+    shape = w.LLAMA_1B
+    heads, hd, kv = shape.heads, shape.head_dim, shape.kv_heads
+    context, chunk = 16384, 2048
+    pages = context // P
+    tier_map = w.tier_map(seed, 1, pages, w.MIX_CONFIG5)
+    sizes = [d.page_bytes(P, shape.kv_width)] + [
+        m.quantised_page_layout(t, kv, hd, P)["page_bytes"] for t in (1, 2, 3)]
+    alloc = m.PagedKVCache(sizes, [pages + 8] * 4)
+    cache = d.KVPages(alloc, 1, P, kv, hd, m.Tier.FP16, d.Halves.Both, tier_map, True)
+    rng = np.random.default_rng(seed)
+    k, v = w.kv_rows(rng, context, shape, w.outlier_channels(rng, shape.kv_width))
+    cache.reserve(context)
+    cache.store(0, m.upload_fp16(k.astype(np.float32)), m.upload_fp16(v.astype(np.float32)), 0,
+                context)
+    q = rng.standard_normal((context, heads, hd)).astype(np.float16)
+    qs, ks, vs, outs = [], [], [], []
+    for c in range(context // chunk):
+        rows = slice(c * chunk, (c + 1) * chunk)
+        qs.append(m.upload_fp16(q[rows].astype(np.float32)))
+        ks.append(m.upload_fp16(k[rows].astype(np.float32)))
+        vs.append(m.upload_fp16(v[rows].astype(np.float32)))
+        outs.append(d.empty(chunk * heads * hd))
+    partials = d.empty_f32(d.attention_partials(hd))
+
+    def body():
+        for c in range(context // chunk):
+            cache.attention(0, qs[c], None, None, outs[c], chunk, (c + 1) * chunk, heads, kv, hd,
+                            ks[c], vs[c], None, partials)
+
+    ms = timed_graph(m, stream, body, steps, warmup)
+    flop = 4.0 * heads * hd * context * (context + 1) / 2
+    tflops = flop / (ms * 1e-3) / 1e12
+    # Parity: the last 64 queries of the last chunk against the oracle.
+    n = 64
+    sealed = (context - 1) // P
+    pp = [alloc.read(0, i) for i in range(sealed)]
+    tiers = [int(alloc.locate(0, i)[0]) for i in range(sealed)]
+    want, bound = att.causal_chunk(q[-n:].astype(np.float64), pp, tiers, k, v, kv, hd, P,
+                                   with_bound=True)
+    got = outs[-1].to_numpy().reshape(chunk, heads, hd)[-n:]
+    check_gate(got, want, bound, "prefill chunk 7, last 64 queries")
+    return {"ms_per_layer": round(ms, 4), "ms_all_layers": round(ms * shape.layers, 3),
+            "tflops": round(tflops, 1),
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                         "algorithmic_flop_per_layer": flop},
+            "config": "llama-3.2-1b 32q/8kv/hd64, 16K in 2K chunks, tiers FP16/INT8/INT4 30/40/30 %"}
+
+
+def check_gate(got, want, bound, what) -> None:
+    """The reference's error gate (tests/ulp_gate.py, tests/test_attention.py:
+    58-115) held to 1e-3: relative error floored at fp16's least normal and
+    where the fp32 error bound spends the budget; mean under 2^-11."""
+    from oracle import attention as att
+    floor = np.maximum(att.FP16_MIN_NORMAL, bound / 1e-3)
+    err = np.abs(got - want) / np.maximum(np.abs(want), floor)
+    if err.max() >= 1e-3 or err.mean() >= 2.0**-11:
+        raise AssertionError(f"{what}: off the oracle: max {err.max():.3g}, mean {err.mean():.3g}")
+
+
 def copy_peak(m, page=32768, count=32768, reps=10) -> float:
     """The achieved HBM rate of a plain device copy (1 GiB read + 1 GiB
     written a launch, the batched page-copy kernel), GB/s of read + write."""
@@ -209,6 +345,7 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=None, help="fewer layers, for a quick look")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-requant", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--traffic-reference", action="store_true",
                     help="only copy 128 MiB with the page-copy kernel (4096 pages of 32 KiB): "
                          "the known-size launch HBM byte counters are scaled by")
@@ -318,17 +455,18 @@ def main() -> int:
         q = qs[layer].raw().reshape(1, heads, hd)
         want, _, bound = att.causal_decode(q, pages, tiers, k[sealed * P:], v[sealed * P:],
                                            shape.kv_heads, hd, P, with_bound=True)
-        # The reference's error gate (tests/ulp_gate.py, tests/test_attention.py:58-115)
-        # held to 1e-3: relative error floored at fp16's least normal and where the
-        # fp32 error bound spends the budget.
-        floor = np.maximum(att.FP16_MIN_NORMAL, bound / 1e-3)
         for name, got in (("per-layer", outs[layer].to_numpy().reshape(1, heads, hd)),
                           ("one-launch", got_all[layer])):
-            err = np.abs(got - want) / np.maximum(np.abs(want), floor)
-            if err.max() >= 1e-3 or err.mean() >= 2.0**-11:
-                raise AssertionError(f"layer {layer}: the {name} output is off the oracle: "
-                                     f"max {err.max():.3g}, mean {err.mean():.3g}")
+            check_gate(got, want, bound, f"layer {layer}: the {name} output")
     log("parity of both timed paths: ok")
+
+    prefill = None
+    if not args.no_prefill:
+        prefill = {"tile": prefill_tile(m, shape, cache, alloc, host_rows, layers, context,
+                                        stream, args.steps, args.warmup),
+                   "chunks": prefill_chunks(m, stream, max(args.steps // 5, 3),
+                                            max(args.warmup // 5, 1))}
+        log(f"prefill: {prefill}")
 
     requant = None
     if not args.no_requant:
@@ -377,6 +515,7 @@ def main() -> int:
                                           "launch, not the per-layer decode order"},
         "cpu_baseline": cpu,
         "requant": requant,
+        "prefill": prefill,
     }
     print(json.dumps(result), flush=True)
     return 0

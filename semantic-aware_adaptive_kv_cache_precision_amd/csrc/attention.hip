@@ -615,15 +615,6 @@ namespace mi
 
   bool launch_decode_fast(const KVSource &kv, const AttentionArgs &a, hipStream_t stream);
 
-  void launch_attention_combine(const float *partials, std::uint16_t *out, int seq_q, int heads,
-                                int head_dim, int splits, hipStream_t stream)
-  {
-    hipLaunchKernelGGL(combine_kernel, dim3(seq_q * heads), dim3(kCombineThreads),
-                       splits * sizeof(float), stream, partials, out, seq_q, heads, head_dim,
-                       splits, 0, nullptr, 0, 0);
-    hip_check(hipGetLastError(), "attention combine kernel launch");
-  }
-
   void launch_attention(const KVSource &kv, const AttentionArgs &a, hipStream_t stream)
   {
     check_grouping(a.heads, a.kv_heads);

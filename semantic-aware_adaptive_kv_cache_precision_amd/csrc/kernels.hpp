@@ -125,10 +125,6 @@ namespace mi
   int device_multiprocessors();
 
   void launch_attention(const KVSource &kv, const AttentionArgs &a, hipStream_t stream);
-  // Folds split-K runs' partials, (m natural-log, l, o[hd]) a (run, query,
-  // head) slot, into fp16 outputs (attention.hip's combine, no mass).
-  void launch_attention_combine(const float *partials, std::uint16_t *out, int seq_q, int heads,
-                                int head_dim, int splits, hipStream_t stream);
 
   // The matrix-core chunk path (prefill.hip): any number of queries, no mass,
   // head_dim 64 or 128, 32-key pages (or a contiguous cache), 16-byte aligned

@@ -7,7 +7,8 @@
 // own at the tier the page table records, dequantised exactly as
 // dequantise_page does, and its own page at FP16 from the open page and the
 // chunk's rows; an unread page is skipped; the key bias is completed as
-// k + RoPE(k_bias, j); online softmax; split-K runs folded by the combine.
+// k + RoPE(k_bias, j); online softmax; split-K runs of whole pages folded by
+// a combine.
 //
 // Work decomposition. A workgroup takes one KV head, `qb` consecutive queries
 // and, when the keys are split, one run of whole pages. Its rows are the
@@ -61,7 +62,6 @@ namespace mi
     constexpr int kVS = kP + 8;         // V^T row stride in halves (80 B: no bank conflicts)
     constexpr float kPScale = 16384.0f; // probabilities are held x2^14 for PV
     constexpr float kPUnscale = 1.0f / 16384.0f;
-    constexpr float kLn2 = 0.693147180559945309f;
     constexpr int kMaxWaves = 8;
     constexpr int kMinThreads = 256; // a workgroup stages with at least this many threads
 
@@ -138,9 +138,36 @@ namespace mi
 
     // Fetches one (key t, chunk c) of the item (page p, version) for KV head
     // kvh: global loads only; what it needs to dequantise comes with it.
+    // The page-table entry of an item: the sealed page's address and tier
+    // (or an FP16 page's address); loaded two items ahead of its data.
+    struct Entry
+    {
+      unsigned long long page;
+      int tier;
+    };
+
+    __device__ inline Entry entry_of(const KVSource &kv, int p, int version, int p_end)
+    {
+      Entry e{0, kFP16};
+      if (p >= p_end)
+      {
+        return e;
+      }
+      if (kv.layout == Layout::kCausal && version == kSealed)
+      {
+        e.page = kv.pages[p];
+        e.tier = kv.tiers[p];
+      }
+      else if (kv.layout == Layout::kPaged)
+      {
+        e.page = kv.pages[p];
+      }
+      return e;
+    }
+
     template <int HD>
-    __device__ inline void fetch(const PrefillArgs &a, int p, int version, int kvh, int t, int c,
-                                 Fetched &f)
+    __device__ inline void fetch(const PrefillArgs &a, int p, int version, const Entry &entry,
+                                 int kvh, int t, int c, Fetched &f)
     {
       const KVSource &kv = a.kv;
       const std::size_t row = static_cast<std::size_t>(a.kv_heads) * HD;
@@ -151,8 +178,8 @@ namespace mi
       const std::uint16_t *v_row = nullptr;
       if (kv.layout == Layout::kCausal && version == kSealed)
       {
-        const int tier = kv.tiers[p];
-        const auto *page = reinterpret_cast<const std::uint8_t *>(kv.pages[p]);
+        const int tier = entry.tier;
+        const auto *page = reinterpret_cast<const std::uint8_t *>(entry.page);
         if (tier == kFP16)
         {
           const auto *h = reinterpret_cast<const std::uint16_t *>(page);
@@ -208,7 +235,7 @@ namespace mi
           break;
         case Layout::kPaged:
         {
-          const auto *h = reinterpret_cast<const std::uint16_t *>(kv.pages[p]);
+          const auto *h = reinterpret_cast<const std::uint16_t *>(entry.page);
           k_row = h + t * row;
           v_row = h + (kP + t) * row;
           break;
@@ -298,29 +325,41 @@ namespace mi
       }
     }
 
-    // RoPE of the key bias at position j for channels d0..d0+7 (reference:
-    // attention.cu:104-116): d < hd/2 pairs with d + hd/2.
+    // The cos/sin pairs of position j for channels d0..d0+7 (the rope table
+    // holds {cos, sin} per (position, j < hd/2)).
     template <int HD>
-    __device__ inline void rotated_bias8(const std::uint16_t *bias, const float *rope, int j,
-                                         int d0, float rb[8])
+    __device__ inline void fetch_rope(const float *rope, int j, int d0, f32x4 cs[4])
     {
       constexpr int half = HD / 2;
       const int j0 = d0 < half ? d0 : d0 - half;
-      const float *cs = rope + 2 * (static_cast<std::size_t>(j) * half + j0);
+      const auto *src =
+          reinterpret_cast<const f32x4 *>(rope + 2 * (static_cast<std::size_t>(j) * half + j0));
+      for (int i = 0; i < 4; ++i)
+      {
+        cs[i] = src[i];
+      }
+    }
+
+    // RoPE of the key bias at one position for channels d0..d0+7 (reference:
+    // attention.cu:104-116): channel d < hd/2 pairs with d + hd/2. b_first
+    // holds bias[j0 .. j0+7] and b_second bias[j0+hd/2 .. +7], j0 the pair index.
+    __device__ inline void rotated_bias8(const u32x4 &b_first, const u32x4 &b_second,
+                                         const f32x4 cs[4], bool first_half, float rb[8])
+    {
       for (int e = 0; e < 8; ++e)
       {
-        const float c = cs[2 * e];
-        const float s = cs[2 * e + 1];
-        const float b1 = h2f(bias[j0 + e]);
-        const float b2 = h2f(bias[j0 + e + half]);
-        rb[e] = d0 < half ? b1 * c - b2 * s : b2 * c + b1 * s;
+        const float c = cs[e / 2][2 * (e % 2)];
+        const float s = cs[e / 2][2 * (e % 2) + 1];
+        const float b1 = h2f(half_of(b_first, e));
+        const float b2 = h2f(half_of(b_second, e));
+        rb[e] = first_half ? b1 * c - b2 * s : b2 * c + b1 * s;
       }
     }
 
     // Writes a fetch into a stage: K (hi, and lo with a bias) row t, and V^T.
     template <int HD, bool kBias>
-    __device__ inline void commit(const PrefillArgs &a, const Fetched &f, int kvh, int j, int t,
-                                  int c, std::uint16_t *stage)
+    __device__ inline void commit(const Fetched &f, const f32x4 cs[4], const u32x4 &b_first,
+                                  const u32x4 &b_second, int t, int c, std::uint16_t *stage)
     {
       constexpr int KS = Geometry<HD>::kKS;
       std::uint16_t k[8], v[8];
@@ -334,7 +373,7 @@ namespace mi
         if (f.tier >= 0)
         {
           float rb[8];
-          rotated_bias8<HD>(a.k_bias + static_cast<std::size_t>(kvh) * HD, a.rope, j, 8 * c, rb);
+          rotated_bias8(b_first, b_second, cs, 8 * c < HD / 2, rb);
           for (int e = 0; e < 8; ++e)
           {
             const float x = h2f(k[e]) + rb[e];
@@ -379,37 +418,27 @@ namespace mi
       }
     }
 
-    // The pages a workgroup visits, in order, as (page, version) items.
-    struct Walk
+    // The (page, version) items a workgroup visits, in order: a page before
+    // every row's own page once, sealed; a page in the rows' own-page range
+    // [o_lo, o_hi] sealed (when a row is past it) and then at FP16. Without
+    // a cache that seals, every page once.
+    __device__ inline int first_version(int p, bool causal, int o_hi)
     {
-      int p;
-      int version;
-      int p_end;
-      int o_lo;
-      int o_hi;
-      bool causal;
+      return causal && p < o_hi ? kSealed : kOwn;
+    }
 
-      __device__ bool done() const { return p >= p_end; }
-
-      __device__ void start(int p_begin)
+    __device__ inline void advance(int &p, int &version, bool causal, int o_lo, int o_hi)
+    {
+      if (version == kSealed && p >= o_lo)
       {
-        p = p_begin;
-        version = causal && p < o_hi ? kSealed : kOwn;
+        version = kOwn;
       }
-
-      __device__ void next()
+      else
       {
-        if (version == kSealed && p >= o_lo)
-        {
-          version = kOwn;
-        }
-        else
-        {
-          ++p;
-          version = causal && p < o_hi ? kSealed : kOwn;
-        }
+        ++p;
+        version = first_version(p, causal, o_hi);
       }
-    };
+    }
 
     template <int HD, int TPW, bool kBias>
     __global__ void __launch_bounds__(kMaxWaves * 64)
@@ -476,67 +505,113 @@ namespace mi
       }
 
       // The pages this workgroup visits.
-      const int x_lo = shift + q_first;
-      const int x_hi = shift + q_last;
-      Walk walk;
-      walk.causal = causal;
-      walk.o_lo = x_lo / kP;
-      walk.o_hi = x_hi / kP;
+      const int o_lo = (shift + q_first) / kP;
+      const int o_hi = (shift + q_last) / kP;
       const int p_begin = split * a.pages_per_split;
-      walk.p_end = min(p_begin + a.pages_per_split, x_hi / kP + 1);
-      walk.start(p_begin);
+      const int p_end = min(p_begin + a.pages_per_split, o_hi + 1);
 
-      // Stage the first item.
+      // Staging items run key-fastest: item = key + 32 * chunk. A wave then
+      // stores V^T rows of two chunks for all 32 keys at once, 32 distinct
+      // LDS dwords a store, where key-major order put several chunks on one
+      // bank. A thread's items keep their channel chunks from page to page,
+      // so its bias channels are loaded once.
+      u32x4 b_first[kFetch];
+      u32x4 b_second[kFetch];
+      for (int u = 0; u < kFetch; ++u)
+      {
+        b_first[u] = u32x4{0, 0, 0, 0};
+        b_second[u] = u32x4{0, 0, 0, 0};
+        const int item = threadIdx.x + u * threads;
+        if constexpr (kBias)
+        {
+          if (item < kItems)
+          {
+            const int d0 = 8 * (item / kP);
+            const int j0 = d0 < HD / 2 ? d0 : d0 - HD / 2;
+            const std::uint16_t *b = a.k_bias + static_cast<std::size_t>(kvh) * HD;
+            b_first[u] = *reinterpret_cast<const u32x4 *>(b + j0);
+            b_second[u] = *reinterpret_cast<const u32x4 *>(b + j0 + HD / 2);
+          }
+        }
+      }
+
       Fetched f[kFetch];
-      const auto fetch_item = [&](const Walk &w) {
+      f32x4 cs[kFetch][4];
+      const auto fetch_item = [&](int p, int version, const Entry &entry) {
         for (int u = 0; u < kFetch; ++u)
         {
           const int item = threadIdx.x + u * threads;
           if (item < kItems)
           {
-            fetch<HD>(a, w.p, w.version, kvh, item / kChunks, item % kChunks, f[u]);
+            const int t = item % kP;
+            const int c = item / kP;
+            fetch<HD>(a, p, version, entry, kvh, t, c, f[u]);
+            if constexpr (kBias)
+            {
+              if (p * kP + t < a.seq_k)
+              {
+                fetch_rope<HD>(a.rope, p * kP + t, 8 * c, cs[u]);
+              }
+            }
           }
         }
       };
-      const auto commit_item = [&](const Walk &w, std::uint16_t *stage) {
+      const auto commit_item = [&](std::uint16_t *stage) {
         for (int u = 0; u < kFetch; ++u)
         {
           const int item = threadIdx.x + u * threads;
           if (item < kItems)
           {
-            const int t = item / kChunks;
-            commit<HD, kBias>(a, f[u], kvh, w.p * kP + t, t, item % kChunks, stage);
+            commit<HD, kBias>(f[u], cs[u], b_first[u], b_second[u], item % kP, item / kP, stage);
           }
         }
       };
       // Whether an item has anything to read: an unread sealed page has not.
-      const auto readable = [&](const Walk &w) {
-        return !(causal && w.version == kSealed && a.kv.tiers[w.p] == kUnreadPage);
+      const auto readable = [&](int version, const Entry &entry) {
+        return !(causal && version == kSealed && entry.tier == kUnreadPage);
       };
 
+      // The item being computed, the next (being fetched) and the one after
+      // (its table entry in flight).
+      int p = p_begin;
+      int version = first_version(p, causal, o_hi);
+      Entry entry = entry_of(a.kv, p, version, p_end);
+      int p1 = p, v1 = version;
+      advance(p1, v1, causal, o_lo, o_hi);
+      Entry e1 = entry_of(a.kv, p1, v1, p_end);
+      int p2 = p1, v2 = v1;
+      advance(p2, v2, causal, o_lo, o_hi);
+      Entry e2 = entry_of(a.kv, p2, v2, p_end);
       int buf = 0;
-      if (!walk.done() && readable(walk))
+      if (p < p_end && readable(version, entry))
       {
-        fetch_item(walk);
-        commit_item(walk, smem);
+        fetch_item(p, version, entry);
+        commit_item(smem);
       }
       __syncthreads();
 
-      while (!walk.done())
+      while (p < p_end)
       {
-        Walk next = walk;
-        next.next();
-        const bool has_next = !next.done() && readable(next);
+        int p3 = p2, v3 = v2;
+        advance(p3, v3, causal, o_lo, o_hi);
+        const Entry e3 = entry_of(a.kv, p3, v3, p_end);
+        const bool has_next = p1 < p_end && readable(v1, e1);
         if (has_next)
         {
-          fetch_item(next);
+          fetch_item(p1, v1, e1);
         }
-        if (computes && readable(walk))
+        if (computes && readable(version, entry))
         {
           const std::uint16_t *stage = smem + buf * kStage;
           const std::uint16_t *k_hi = stage;
           const std::uint16_t *k_lo = stage + kP * KS;
           const std::uint16_t *vt = stage + (kBias ? 2 : 1) * kP * KS;
+          // Whether every row of the workgroup sees all 32 keys: a sealed page
+          // before every row's own page, or (no sealing) a page wholly before
+          // the first query. Rows past the chunk's end see them too; their
+          // outputs are never stored.
+          const bool full = causal ? version == kSealed && p < o_lo
+                                   : p * kP + kP - 1 <= shift + q_first;
           // Each row's last visible key position on this item (-1: none).
           int limit[TPW];
           for (int tt = 0; tt < TPW; ++tt)
@@ -545,13 +620,13 @@ namespace mi
             {
               limit[tt] = pos[tt];
             }
-            else if (walk.version == kSealed)
+            else if (version == kSealed)
             {
-              limit[tt] = walk.p < own[tt] ? 0x7fffffff : -1;
+              limit[tt] = p < own[tt] ? 0x7fffffff : -1;
             }
             else
             {
-              limit[tt] = walk.p == own[tt] ? pos[tt] : -1;
+              limit[tt] = p == own[tt] ? pos[tt] : -1;
             }
           }
           // S^T = K . Q^T, two 16-key tiles.
@@ -591,9 +666,9 @@ namespace mi
             {
               for (int i = 0; i < 4; ++i)
               {
-                const int j = walk.p * kP + key_of(kt, g, i);
+                const int j = p * kP + key_of(kt, g, i);
                 const float x = s[tt][kt][i] * a.scale2;
-                const float v = j <= limit[tt] ? x : -INFINITY;
+                const float v = full || j <= limit[tt] ? x : -INFINITY;
                 sc[4 * kt + i] = v;
                 top = fmaxf(top, v);
               }
@@ -615,7 +690,9 @@ namespace mi
               p_lo[tt][e] = static_cast<_Float16>(ps - static_cast<float>(h));
             }
             l[tt] = l[tt] * keep + sum;
-            if (keep != 1.0f)
+            // Most pages leave every row's maximum where it was: rescale only
+            // when some lane's moved.
+            if (__any(keep != 1.0f))
             {
               for (int dt = 0; dt < HD / 16; ++dt)
               {
@@ -637,11 +714,19 @@ namespace mi
         }
         if (has_next)
         {
-          commit_item(next, smem + (buf ^ 1) * kStage);
+          commit_item(smem + (buf ^ 1) * kStage);
         }
         __syncthreads();
         buf ^= 1;
-        walk = next;
+        p = p1;
+        version = v1;
+        entry = e1;
+        p1 = p2;
+        v1 = v2;
+        e1 = e2;
+        p2 = p3;
+        v2 = v3;
+        e2 = e3;
       }
 
       // Each row's sum over its four lanes; then the output or the run's slot.
@@ -674,7 +759,7 @@ namespace mi
                                           a.heads + head[tt]) * (HD + 2);
           if (g == 0)
           {
-            slot[0] = m[tt] == -INFINITY ? -INFINITY : m[tt] * kLn2;
+            slot[0] = m[tt]; // base 2, -inf for a run that saw no key
             slot[1] = total;
           }
           for (int dt = 0; dt < HD / 16; ++dt)
@@ -688,10 +773,82 @@ namespace mi
       }
     }
 
+    // Folds the runs of one (query, head) row: weights 2^(m_s - max m) (a
+    // run that saw no key has m = -inf and weighs 0), out = sum(w o) /
+    // sum(w l). kCombineThreads / HD groups of HD threads, a thread a channel,
+    // share the runs; their sums meet in LDS. Runs' slots are (run, query,
+    // head) apart, run_stride floats.
+    constexpr int kCombineThreads = 1024;
+
+    template <int HD>
+    __global__ void __launch_bounds__(kCombineThreads)
+        prefill_combine_kernel(const float *__restrict__ partials, std::uint16_t *__restrict__ out,
+                               std::size_t run_stride, int splits)
+    {
+      constexpr int kGroups = kCombineThreads / HD;
+      __shared__ float s_top[kCombineThreads / 64];
+      __shared__ float s_acc[kGroups][HD];
+      __shared__ float s_l[kGroups];
+      const float *row = partials + static_cast<std::size_t>(blockIdx.x) * (HD + 2);
+      float top = -INFINITY;
+      for (int s = threadIdx.x; s < splits; s += kCombineThreads)
+      {
+        top = fmaxf(top, row[s * run_stride]);
+      }
+      for (int off = 32; off > 0; off >>= 1)
+      {
+        top = fmaxf(top, __shfl_xor(top, off));
+      }
+      if (threadIdx.x % 64 == 0)
+      {
+        s_top[threadIdx.x / 64] = top;
+      }
+      __syncthreads();
+      top = s_top[0];
+      for (int w = 1; w < kCombineThreads / 64; ++w)
+      {
+        top = fmaxf(top, s_top[w]);
+      }
+      const int group = threadIdx.x / HD;
+      const int d = threadIdx.x % HD;
+      float l = 0.0f;
+      float acc = 0.0f;
+#pragma unroll 4
+      for (int s = group; s < splits; s += kGroups)
+      {
+        const float *slot = row + s * run_stride;
+        const float w = exp2_fast(slot[0] - top);
+        l += slot[1] * w;
+        acc += slot[2 + d] * w;
+      }
+      s_acc[group][d] = acc;
+      if (d == 0)
+      {
+        s_l[group] = l;
+      }
+      __syncthreads();
+      if (group == 0)
+      {
+        float sum = 0.0f;
+        float total = 0.0f;
+        for (int g = 0; g < kGroups; ++g)
+        {
+          sum += s_acc[g][d];
+          total += s_l[g];
+        }
+        out[static_cast<std::size_t>(blockIdx.x) * HD + d] =
+            __half_as_ushort(__float2half_rn(sum / total));
+      }
+    }
+
     bool aligned16(const void *p) { return (reinterpret_cast<std::uintptr_t>(p) & 15) == 0; }
 
+    // Launches the kernel for `args` (pages_per_split and partials still to
+    // set): the keys split into runs of whole pages when the attention
+    // workspace is given and the query blocks alone would not fill every
+    // workgroup slot the kernel's occupancy allows, then a combine.
     template <int HD, int TPW, bool kBias>
-    void run(const PrefillArgs &args, dim3 grid, int waves, hipStream_t stream)
+    void run(PrefillArgs args, float *partials, int qblocks, int waves, hipStream_t stream)
     {
       const std::size_t lds = 2 * stage_halves<HD, kBias>() * sizeof(std::uint16_t);
       auto kernel = prefill_kernel<HD, TPW, kBias>;
@@ -702,22 +859,47 @@ namespace mi
                                       static_cast<int>(lds)),
                   "hipFuncSetAttribute prefill LDS");
       }
-      hipLaunchKernelGGL(kernel, grid, dim3(64 * waves), lds, stream, args);
+      const int pages = (args.seq_k + kP - 1) / kP;
+      int splits = 1;
+      if (partials != nullptr)
+      {
+        int resident = 0;
+        hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kernel, 64 * waves, lds),
+                  "hipOccupancyMaxActiveBlocksPerMultiprocessor prefill");
+        const long blocks = static_cast<long>(qblocks) * args.kv_heads;
+        const long target = static_cast<long>(std::max(resident, 1)) * device_multiprocessors();
+        const long cap = static_cast<long>(attention_partials_floats(HD) / (HD + 2)) /
+                         (static_cast<long>(args.seq_q) * args.heads);
+        splits = static_cast<int>(
+            std::max<long>(1, std::min<long>({target / blocks, pages / 2, cap})));
+      }
+      args.pages_per_split = (pages + splits - 1) / splits;
+      splits = (pages + args.pages_per_split - 1) / args.pages_per_split;
+      args.partials = splits > 1 ? partials : nullptr;
+      hipLaunchKernelGGL(kernel, dim3(qblocks, args.kv_heads, splits), dim3(64 * waves), lds,
+                         stream, args);
+      hip_check(hipGetLastError(), "prefill kernel launch");
+      if (splits > 1)
+      {
+        const std::size_t run_stride = static_cast<std::size_t>(args.seq_q) * args.heads * (HD + 2);
+        hipLaunchKernelGGL(prefill_combine_kernel<HD>, dim3(args.seq_q * args.heads),
+                           dim3(kCombineThreads), 0, stream, partials, args.out, run_stride,
+                           splits);
+        hip_check(hipGetLastError(), "prefill combine kernel launch");
+      }
     }
 
-    template <int HD>
-    void dispatch(const PrefillArgs &args, dim3 grid, int waves, int tpw, bool bias,
+    template <int HD, int TPW>
+    void dispatch(const PrefillArgs &args, float *partials, int qblocks, int waves, bool bias,
                   hipStream_t stream)
     {
       if (bias)
       {
-        tpw == 2 ? run<HD, 2, true>(args, grid, waves, stream)
-                 : run<HD, 1, true>(args, grid, waves, stream);
+        run<HD, TPW, true>(args, partials, qblocks, waves, stream);
       }
       else
       {
-        tpw == 2 ? run<HD, 2, false>(args, grid, waves, stream)
-                 : run<HD, 1, false>(args, grid, waves, stream);
+        run<HD, TPW, false>(args, partials, qblocks, waves, stream);
       }
     }
 
@@ -771,44 +953,35 @@ namespace mi
     args.heads = a.heads;
     args.kv_heads = a.kv_heads;
     args.group = group;
-    args.qb = std::max(1, std::min(a.seq_q, std::max(1, 128 / group)));
+    // Rows a workgroup: up to 128 (eight tiles), 256 at head_dim 64 for a
+    // long chunk (eight waves of two tiles), so each staged page feeds more
+    // matrix work.
+    const int row_target = hd == 64 && a.seq_q >= 256 ? 256 : 128;
+    args.qb = std::max(1, std::min(a.seq_q, std::max(1, row_target / group)));
     args.rows = args.qb * group;
     args.scale2 = 1.4426950408889634f / std::sqrt(static_cast<float>(hd));
     const int tiles = (args.rows + 15) / 16;
-    const int tpw = tiles >= 4 ? 2 : 1;
+    // Two tiles a wave share each K and V operand read; at head_dim 128 the
+    // second tile's accumulators do not fit the registers.
+    const int tpw = hd == 64 && tiles >= 4 ? 2 : 1;
     const int waves = std::max((tiles + tpw - 1) / tpw, kMinThreads / 64);
     if (waves > kMaxWaves)
     {
       throw InvalidArgument("prefill: " + std::to_string(tiles) + " row tiles exceed a workgroup");
     }
     const int qblocks = (a.seq_q + args.qb - 1) / args.qb;
-    const int pages = (a.seq_k + kP - 1) / kP;
-    int splits = 1;
-    if (a.partials != nullptr)
+    const bool bias = a.k_bias != nullptr;
+    if (hd == 128)
     {
-      const long blocks = static_cast<long>(qblocks) * a.kv_heads;
-      const long target = 2L * device_multiprocessors();
-      const long cap = static_cast<long>(attention_partials_floats(hd) / (hd + 2)) /
-                       (static_cast<long>(a.seq_q) * a.heads);
-      const long want = std::min<long>({(target + blocks - 1) / blocks, pages / 4, cap});
-      splits = static_cast<int>(std::max<long>(1, want));
+      dispatch<128, 1>(args, a.partials, qblocks, waves, bias, stream);
     }
-    args.pages_per_split = (pages + splits - 1) / splits;
-    splits = (pages + args.pages_per_split - 1) / args.pages_per_split;
-    args.partials = splits > 1 ? a.partials : nullptr;
-    const dim3 grid(qblocks, a.kv_heads, splits);
-    if (hd == 64)
+    else if (tpw == 2)
     {
-      dispatch<64>(args, grid, waves, tpw, a.k_bias != nullptr, stream);
+      dispatch<64, 2>(args, a.partials, qblocks, waves, bias, stream);
     }
     else
     {
-      dispatch<128>(args, grid, waves, tpw, a.k_bias != nullptr, stream);
-    }
-    hip_check(hipGetLastError(), "prefill kernel launch");
-    if (splits > 1)
-    {
-      launch_attention_combine(a.partials, a.out, a.seq_q, a.heads, hd, splits, stream);
+      dispatch<64, 1>(args, a.partials, qblocks, waves, bias, stream);
     }
   }
 
