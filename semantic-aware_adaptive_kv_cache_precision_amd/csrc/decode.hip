@@ -10,40 +10,36 @@
 // head's softmax, the EWMA folded with every operation rounded once.
 //
 // Work layout (MI355X-first):
-//   - a wave64 owns one 32-token page of a *pack* of NP KV heads, NP chosen
-//     so that the pack's query heads (NP x group) fill the 16 columns of a
-//     16x16x32 f16 MFMA as far as they go: each page's softmax and its
-//     bookkeeping are paid once for the pack, not once a KV head;
-//   - q.K^T: the page's keys are the MFMA's rows. Lane group g (lane / 16)
-//     holds the contiguous channels [g W'/4, (g+1) W'/4) of the pack's
-//     W' = NP hd channels of two key rows, so its codes arrive as whole
-//     16-byte (or 8- or 4-byte) global loads straight into registers. A lane
-//     group's channels belong to one KV head, so q enters as a block-diagonal
-//     operand: zero where a column's head is not that KV head's;
+//   - a wave64 owns one 32-token page of one KV head, for every query head of
+//     that KV head's group (up to 16): the page is read from HBM once. Lane
+//     group g (lane / 16) holds the contiguous channels [g hd/4, (g+1) hd/4)
+//     of rows r and 16 + r (r = lane % 16), so each row's codes are one
+//     16-byte global load at INT4 (two at INT8, one 8-byte load at INT2);
 //   - codes are dequantised in registers with packed fp16 arithmetic: bytes
 //     spliced into the fp16 1024 + code by v_perm, 1024 subtracted, then one
-//     fp16 fma with the scale and zero. The reference forms code * scale +
-//     zero in fp32 and rounds that to fp16; rounding the exact value once to
-//     fp16 differs from it only where the fp32 value lands on an fp16 tie,
-//     by one fp16 ulp;
-//   - P.V needs V with the keys along each lane's eight MFMA operands: V
-//     goes global -> LDS by direct DMA (global_load_lds), laid out so that
-//     gfx950's transposing LDS reads (ds_read_b64_tr_b16 / _b8 / _b4) hand
-//     every lane eight consecutive keys of one channel, each read instruction
-//     covering one contiguous 512-byte run (no bank conflicts). INT8 and INT4
-//     codes are transposed as codes and dequantised after, with each key's
-//     value scale and zero; INT2 (no 2-bit transpose exists) is dequantised
-//     in rows and written to LDS as fp16 first;
-//   - scores are kept in base-2 units (scale * log2 e folded in), so the
-//     softmax weights are single exp2 instructions; P is split into an fp16
-//     high and low part, two MFMAs, keeping ~22 bits of P;
-//   - a wave walks a contiguous run of pages of one (layer, pack) with one
-//     page in flight: the next page's K codes (to registers), metadata and V
-//     (to LDS) are requested before the current page's P.V is computed;
-//   - a workgroup of 8 waves owns a contiguous page range of one (layer,
-//     pack) and folds its waves into one partial (m, l, o) per head in LDS;
-//     the combine kernel folds the partials, and turns each page's
-//     (max, sum) into its mass and the layer's scores.
+//     fp16 fma with the page's scale and zero. The reference forms
+//     code * scale + zero in fp32 and rounds that to fp16; rounding the exact
+//     value once to fp16 differs from it only where the fp32 value lands on
+//     an fp16 tie, by one fp16 ulp;
+//   - a page's key scales and zeros are read once per wave into LDS and from
+//     there 32 channels at a time, not held by all 16 lanes that share them;
+//   - q.K^T is a 16x16x32 f16 MFMA a 32-channel step, the page's keys as M
+//     and the group's heads as N (q and the keys are exact in fp16, the
+//     products in fp32); scores are kept in base-2 units (scale * log2 e
+//     folded in), so the softmax weights are single exp2 instructions;
+//   - V is transposed in registers by an MFMA against a 0/1 selection
+//     matrix (exact), which puts each lane's keys on the K axis of P.V; P is
+//     split into an fp16 high and low part, two MFMAs, keeping ~22 bits of P;
+//   - each tier has its own straight-line path (keys dequantised and
+//     multiplied a step at a time, FP16 values loaded after q.K^T), so that
+//     no path holds a whole page twice;
+//   - lane % 16 is a head throughout: its scores, softmax state and output
+//     live in the same lanes, so only the max/sum over the 4 lane groups
+//     crosses lanes;
+//   - a workgroup of 8 waves covers 8 consecutive pages of one KV head of one
+//     layer and writes one partial (m, l, o); the combine kernel folds the
+//     partials, and turns each page's (max, sum) into its mass and the
+//     layer's scores.
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -61,23 +57,18 @@ namespace mi
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
     typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-    typedef short i16x4 __attribute__((ext_vector_type(4)));
-    typedef int i32x2 __attribute__((ext_vector_type(2)));
-    // Global-address-space views: loads through them are global_load_*.
+    // Global-address-space views: loads through them are global_load_*
+    // with the base in scalar registers where uniform, not flat loads.
     typedef const __attribute__((address_space(1))) u32x4 *g_u32x4;
     typedef const __attribute__((address_space(1))) u32x2 *g_u32x2;
     typedef const __attribute__((address_space(1))) unsigned *g_u32;
-    typedef __attribute__((address_space(3))) void *lds_void;
-    typedef __attribute__((address_space(3))) i16x4 *lds_i16x4;
-    typedef __attribute__((address_space(3))) i32x2 *lds_i32x2;
-    typedef const __attribute__((address_space(1))) void *global_void;
+    typedef const __attribute__((address_space(1))) unsigned short *g_u16;
 
     constexpr int kWaves = 8;
     constexpr int kThreads = 64 * kWaves;
     constexpr int kPageTokens = 32;
     constexpr int kMaxGroup = 16;
     constexpr int kMaxHeads = 64;
-    constexpr int kMaxKvHeads = 16;
     constexpr int kOwnPage = 0xFE; // the query's own page: open page + chunk rows
     constexpr unsigned kMagic = 0x64646464u; // the high byte of fp16 1024, four times
 
@@ -113,10 +104,19 @@ namespace mi
       int kv_heads;
       int group;
       int pages;
-      int splits;   // workgroups a (layer, pack): blockIdx.x
-      float scale;  // 1/sqrt(hd) * log2 e: scores in base-2 units
-      float *partials;   // [launch layer][kv_heads][splits][group][kSlotHead + hd]
-      float *page_stats; // [launch layer][heads][pages][2]: each page's max and sum
+      int pages_per_wave;
+      int splits;
+      float scale; // 1/sqrt(hd) * log2 e: scores in base-2 units
+      // Streaming launches: the (layer, KV head, page) units split into
+      // stream_waves equal contiguous ranges, one a wave; a group's splits are
+      // the waves whose ranges meet it. 0: fixed splits of pages_per_wave * 8.
+      long long stream_units;
+      int stream_waves;
+      float *partials;   // [launch layer][kv_heads][splits][group][hd]: each split's output
+      float *split_ml;   // [launch layer][kv_heads][group][splits][2]: each split's max and
+                         // sum, a head's splits side by side so that they read coalesced
+      float *page_stats; // [launch layer][kv_heads][pages][group][2]: each page's max and
+                         // sum, a page's heads side by side so that one store writes them
     };
 
     __device__ inline half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
@@ -134,7 +134,6 @@ namespace mi
 
     // A partial slot: m, l, then padding to 128 bytes, then the HD outputs,
     // so that each 32-channel chunk of o is one aligned 128-byte line.
-    constexpr int kSlotHead = 32;
 
     __device__ inline f32x4 mfma(half8 a, half8 b, f32x4 c)
     {
@@ -193,19 +192,6 @@ namespace mi
       return __builtin_bit_cast(half8, out);
     }
 
-    // Eight INT4 codes of one word (nibble t the t-th) in the order
-    // (0, 4, 1, 5, 2, 6, 3, 7): one mask-and-merge a pair, no reordering.
-    // s2/z2 pair the scales the same way.
-    __device__ inline half8 dequant_int4_interleaved(unsigned w, u32x4 s2, u32x4 z2)
-    {
-      u32x4 out;
-      out[0] = dq2((w & 0x000F000Fu) | 0x64006400u, s2[0], z2[0]);
-      out[1] = dq2(((w >> 4) & 0x000F000Fu) | 0x64006400u, s2[1], z2[1]);
-      out[2] = dq2(((w >> 8) & 0x000F000Fu) | 0x64006400u, s2[2], z2[2]);
-      out[3] = dq2(((w >> 12) & 0x000F000Fu) | 0x64006400u, s2[3], z2[3]);
-      return __builtin_bit_cast(half8, out);
-    }
-
     // Loads `Bytes` bytes (4, 8 or a multiple of 16, aligned to that) from
     // global memory into words.
     template <int Bytes>
@@ -236,110 +222,27 @@ namespace mi
       }
     }
 
-    // Direct global-to-LDS copies (global_load_lds): lane l's 16 (or 4)
-    // bytes land at block + 16 l (4 l); `block` must be wave-uniform.
-    __device__ inline void dma16(const void *src, void *block)
+    // One FP16 row's run of the lane's channels: HD/32 steps of 8.
+    template <int HD>
+    __device__ inline void load_fp16_run(half8 *dst, const std::uint16_t *run)
     {
-      __builtin_amdgcn_global_load_lds((global_void)src, (lds_void)block, 16, 0, 0);
-    }
-    __device__ inline void dma4(const void *src, void *block)
-    {
-      __builtin_amdgcn_global_load_lds((global_void)src, (lds_void)block, 4, 0, 0);
-    }
-    // s_waitcnt vmcnt(0): every load, to registers or into LDS, has landed.
-    __device__ inline void wait_copies()
-    {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-    // s_waitcnt lgkmcnt(0): every LDS access has completed, so the slot may
-    // be overwritten.
-    __device__ inline void wait_reads()
-    {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-    // Orders this wave's LDS writes before its later LDS reads (LDS
-    // operations of one wave are performed in order; this keeps the
-    // compiler from moving them).
-    __device__ inline void lds_order()
-    {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int s = 0; s < HD / 32; ++s)
+      {
+        dst[s] = as_half8(*((g_u32x4)(run + 8 * s)));
+      }
     }
 
-    // The lane index, opaque to the compiler: address arithmetic derived from
-    // it inside the page loop stays there instead of being hoisted out and
-    // held in registers across the loop, one set per tier.
-    __device__ inline int opaque(int v)
+    // The channel of o[2 s + h][i] in lane group g: P.V's M index m = 4 g + i
+    // reads channel 8 s + m % 8 of the run of lane group 2 h + m / 8.
+    template <int HD>
+    __device__ inline int out_channel(int s, int h, int g, int i)
     {
-      asm volatile("" : "+v"(v));
-      return v;
+      const int m = 4 * g + i;
+      return (2 * h + m / 8) * (HD / 4) + 8 * s + m % 8;
     }
 
-    // Global loads from a wave-uniform base plus a 32-bit per-lane offset
-    // (the scalar-base form of global_load).
-    template <int Bytes>
-    __device__ inline void load_at(unsigned *w, const std::uint8_t *base, unsigned offset)
-    {
-      load_words<Bytes>(w, base + offset);
-    }
-
-    __device__ inline u32x2 tr16(const std::uint8_t *p)
-    {
-      return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(p)));
-    }
-    __device__ inline u32x2 tr8(const std::uint8_t *p)
-    {
-      return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2)(p)));
-    }
-    __device__ inline u32x2 tr4(const std::uint8_t *p)
-    {
-      return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2)(p)));
-    }
-
-    // Sizes of one (HD, NP) instantiation. W' = NP * HD channels a page row
-    // of the pack.
-    template <int HD, int NP>
-    struct Cfg
-    {
-      static constexpr int kWp = NP * HD;
-      static constexpr int kRun = kWp / 4;         // channels a lane group holds of a row
-      static constexpr int kSteps = kRun / 8;      // q.K^T steps of 32 channels
-      static constexpr int kCB = HD / 16;          // 16-channel output blocks
-      static constexpr int kVBytes = NP * HD * 64; // V as fp16: 32 rows of W' halves
-      static constexpr int kKMeta = 4 * NP * HD;   // key scales, then key zeros, of the pack
-      static constexpr int kRaw = NP * HD / 4;     // words of a lane's two FP16 key rows
-      static constexpr int kVt = NP * HD / 4;      // words of a lane's transposed FP16 V
-    };
-
-    // The key row behind MFMA row m (0..15) of key block kb. C's rows 4g..4g+3
-    // of both blocks then hold keys 8g..8g+7 in the order P.V reads them:
-    // natural, or (0, 4, 1, 5, 2, 6, 3, 7) for an INT4 page, whose values
-    // dequantise in that order.
-    template <bool Interleaved>
-    __device__ inline int key_of(int m, int kb)
-    {
-      const int i = m & 3;
-      const int j = Interleaved ? (i & 1) * 4 + (i >> 1) + 2 * kb : 4 * kb + i;
-      return 8 * (m >> 2) + j;
-    }
-
-    // Where key t sits in the FP16 V image: the 16 keys of one half h
-    // ((t / 4) % 2) together, so a transposing read of one half is one run.
-    __device__ inline int fp16_image_row(int t)
-    {
-      return 16 * ((t >> 2) & 1) + 4 * (t >> 3) + (t & 3);
-    }
-    __device__ inline int fp16_image_key(int row)
-    {
-      return 8 * ((row >> 2) & 3) + 4 * (row >> 4) + (row & 3);
-    }
-
-    // The running softmax of one wave over its pages, for the lane's column.
+    // The running softmax of one wave over its pages, for the lane's head.
     template <int HD>
     struct Running
     {
@@ -351,13 +254,14 @@ namespace mi
     // Everything one page needs beside its bytes.
     struct PageCtx
     {
+      int r;
       int g;
-      bool live;    // the lane's column is one of the pack's heads
+      int group;
       int last;     // the page's last valid row
-      bool partial; // rows past `last` exist on this page (natural key order)
+      bool partial; // rows past `last` exist on this page
       bool first;   // the wave's first page: it starts the running softmax
       float scale;
-      float *stat;  // this page's (max, sum) slot for the lane's head
+      float *stat;  // this page's (max, sum) slot for head r
     };
 
     // Scores (base-2 units) from the two 16-key accumulators, masked past
@@ -382,7 +286,7 @@ namespace mi
 #pragma unroll
         for (int e = 0; e < 8; ++e)
         {
-          if (8 * c.g + e > c.last)
+          if ((e / 4) * 16 + 4 * c.g + e % 4 > c.last)
           {
             sc[e] = -INFINITY;
           }
@@ -407,10 +311,9 @@ namespace mi
       }
       l_page += __shfl_xor(l_page, 16);
       l_page += __shfl_xor(l_page, 32);
-      if (c.g == 0 && c.live)
+      if (c.g == 0 && c.r < c.group)
       {
-        c.stat[0] = m_page;
-        c.stat[1] = l_page;
+        *reinterpret_cast<float2 *>(c.stat) = make_float2(m_page, l_page);
       }
       float f_page = 1.0f;
       if (c.first)
@@ -447,831 +350,1053 @@ namespace mi
       }
     }
 
-    // The rows one unit (a page of a pack) is read from.
-    struct Rows
+    // P.V for one 32-channel step s: V^T by selection (two MFMAs a 16-channel
+    // half), then the high and low parts of P.
+    template <int HD>
+    __device__ inline void pv_step(Running<HD> &run, int s, half8 v0, half8 v1, int r, int g,
+                                   half8 p_hi, half8 p_lo)
     {
-      const std::uint8_t *page;     // sealed page (any tier)
-      const std::uint16_t *open;    // own page: rows before t_start
-      const std::uint16_t *chunk_k; // own page: rows from t_start
-      const std::uint16_t *chunk_v;
-      int t_start;
-      int last;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+      {
+        half8 sel;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+        {
+          sel[e] = (8 * g + e == r + 16 * h) ? static_cast<_Float16>(1.0f)
+                                             : static_cast<_Float16>(0.0f);
+        }
+        const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4 t0 = mfma(v0, sel, zero);
+        const f32x4 t1 = mfma(v1, sel, zero);
+        half8 vt;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+          vt[i] = static_cast<_Float16>(t0[i]);
+          vt[4 + i] = static_cast<_Float16>(t1[i]);
+        }
+        run.o[2 * s + h] = mfma(vt, p_hi, run.o[2 * s + h]);
+        run.o[2 * s + h] = mfma(vt, p_lo, run.o[2 * s + h]);
+      }
+    }
+
+    // The per-lane codes and value metadata of one quantised page: rows r
+    // and 16 + r, the lane's run of channels.
+    template <int HD, int Bits>
+    struct QuantRaw
+    {
+      static constexpr int kRowWords = (HD / 4) * Bits / 8 / 4;
+      unsigned kc[2][kRowWords];
+      unsigned vc[2][kRowWords];
+      unsigned vs[2];
+      unsigned vz[2];
     };
 
-    // Key row t of an FP16 unit (a sealed page, or the own page: the open page
-    // before t_start, the chunk from there; rows past `last` read row 0).
-    __device__ inline const std::uint16_t *key_row(const Rows &u, int tier, int t, std::size_t W)
+    // q.K^T, softmax and P.V of a quantised page from its raw codes. `ks` and
+    // `kz` point at the KV head's key scales and key zeros (HD halves each)
+    // in LDS, read 32 channels at a time.
+    template <int HD, int Bits>
+    __device__ inline void quantised_compute(Running<HD> &run, const PageCtx &c, const half8 *qb,
+                                             const QuantRaw<HD, Bits> &raw, const unsigned *ks,
+                                             const unsigned *kz)
     {
-      if (tier != kOwnPage)
-      {
-        return reinterpret_cast<const std::uint16_t *>(u.page) + static_cast<std::size_t>(t) * W;
-      }
-      const int tt = t <= u.last ? t : 0;
-      return tt < u.t_start ? u.open + static_cast<std::size_t>(tt) * W
-                            : u.chunk_k + static_cast<std::size_t>(tt - u.t_start) * W;
-    }
-    __device__ inline const std::uint16_t *value_row(const Rows &u, int tier, int t, std::size_t W)
-    {
-      if (tier != kOwnPage)
-      {
-        return reinterpret_cast<const std::uint16_t *>(u.page) +
-               static_cast<std::size_t>(kPageTokens + t) * W;
-      }
-      const int tt = t <= u.last ? t : 0;
-      return tt < u.t_start ? u.open + static_cast<std::size_t>(kPageTokens + tt) * W
-                            : u.chunk_v + static_cast<std::size_t>(tt - u.t_start) * W;
-    }
-
-    // The per-wave LDS of one instantiation: V image, key metadata, value
-    // metadata (all KV heads' value scales then zeros).
-    template <int HD, int NP>
-    struct Slot
-    {
-      std::uint8_t *v;
-      std::uint8_t *kmeta;
-      std::uint8_t *vmeta;
-    };
-
-    // The pack's value scales and zeros: for each of the 32 keys, the
-    // dwords holding the pack's NP halves (one dword when NP is 1 or 2).
-    template <int NP>
-    constexpr int value_meta_dwords() { return NP > 2 ? NP / 2 : 1; }
-
-    template <int HD, int NP>
-    __host__ __device__ constexpr int slot_bytes()
-    {
-      return Cfg<HD, NP>::kVBytes + Cfg<HD, NP>::kKMeta + 256 * value_meta_dwords<NP>();
-    }
-
-    // Requests the LDS part of unit `u` at `tier`: the pack's key metadata
-    // and every value scale and zero to the slot's metadata, V to the slot's
-    // image (INT8, INT4, FP16). No registers are held while these fly.
-    template <int HD, int NP>
-    __device__ inline void issue_lds(const DecodeArgs &a, const Rows &u, int tier, int kp,
-                                     const Slot<HD, NP> &slot, int lane)
-    {
-      using C = Cfg<HD, NP>;
-      const std::size_t W = static_cast<std::size_t>(a.kv_heads) * HD;
-      const std::size_t pack0 = static_cast<std::size_t>(kp) * C::kWp; // pack's first channel
-      if (tier == kFP16 || tier == kOwnPage)
-      {
-        // V image: chunk q = 64 d + lane is (c8, k, row) with row = q % 32.
-        const int row = lane & 31;
-        const int t = fp16_image_key(row);
-        if (tier == kFP16)
-        {
-          const unsigned off =
-              static_cast<unsigned>(((kPageTokens + t) * W + pack0) * 2);
+      constexpr int S = HD / 32;
+      constexpr int kRun = HD / 4;
+      const int r = c.r, g = c.g;
+      f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-          for (int d = 0; d < C::kVBytes / 1024; ++d)
+      for (int s = 0; s < S; ++s)
+      {
+        const u32x4 s2 = *reinterpret_cast<const u32x4 *>(ks + (g * kRun + 8 * s) / 2);
+        const u32x4 z2 = *reinterpret_cast<const u32x4 *>(kz + (g * kRun + 8 * s) / 2);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+        {
+          unsigned w0, w1 = 0;
+          if constexpr (Bits == 8)
           {
-            const int idx = 2 * d + (lane >> 5); // c8 * NP + k
-            const int k = idx % NP, c8 = idx / NP;
-            dma16(u.page + off + (k * HD + 8 * c8) * 2, slot.v + 1024 * d);
+            w0 = raw.kc[kb][2 * s];
+            w1 = raw.kc[kb][2 * s + 1];
           }
-          return;
-        }
-        const std::uint16_t *vrow = value_row(u, tier, t, W) + pack0;
-#pragma unroll
-        for (int d = 0; d < C::kVBytes / 1024; ++d)
-        {
-          const int idx = 2 * d + (lane >> 5); // c8 * NP + k
-          const int k = idx % NP, c8 = idx / NP;
-          dma16(vrow + k * HD + 8 * c8, slot.v + 1024 * d);
-        }
-        return;
-      }
-      const auto quantised = [&](auto bits_tag) {
-        constexpr int Bits = decltype(bits_tag)::value;
-        const PageLayout &L = a.lay[Bits == 8 ? kINT8 : Bits == 4 ? kINT4 : kINT2];
-        const std::uint8_t *p = u.page;
-        if constexpr (Bits != 2)
-        {
-          // V codes: chunk q = 64 d + lane is 16 bytes of row q % 32 at chunk
-          // index q / 32 = (c * NP + k), c a 16-byte column of the row.
-          constexpr int kChunkChannels = 128 / Bits;
-          const int t = lane & 31;
-          const unsigned vrow = static_cast<unsigned>(L.value_codes + (t * W + pack0) * Bits / 8);
-#pragma unroll
-          for (int d = 0; d < C::kWp * 32 * Bits / 8 / 1024; ++d)
+          else if constexpr (Bits == 4)
           {
-            const int idx = 2 * d + (lane >> 5);
-            const int k = idx % NP, c = idx / NP;
-            dma16(p + vrow + (k * HD + kChunkChannels * c) * Bits / 8, slot.v + 1024 * d);
+            w0 = raw.kc[kb][s];
           }
-        }
-        // Key scales then key zeros of the pack: 2 * W' bytes each.
-        constexpr int kMetaLanes = C::kKMeta / 16;
-#pragma unroll
-        for (int d = 0; d < (kMetaLanes + 63) / 64; ++d)
-        {
-          const int ml = 64 * d + lane;
-          if (ml < kMetaLanes)
+          else
           {
-            const int half = ml / (kMetaLanes / 2);
-            const unsigned region = static_cast<unsigned>(half == 0 ? L.key_scales : L.key_zeros);
-            dma16(p + region + static_cast<unsigned>(2 * pack0 + 16 * (ml % (kMetaLanes / 2))),
-                  slot.kmeta + 1024 * d);
+            w0 = raw.kc[kb][s / 2] >> (16 * (s & 1));
           }
+          acc[kb] = mfma(dequant_step<Bits>(w0, w1, s2, z2), qb[s], acc[kb]);
         }
-        // The pack's value scales then zeros: dword q = 64 d + lane is
-        // (region, key t, j) with j < D, the pack's halves of key t.
-        constexpr int D = value_meta_dwords<NP>();
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-        {
-          const int q = 64 * d + lane;
-          const int region = q / (32 * D), t = (q / D) % 32, j = q % D;
-          const int half = t * a.kv_heads + kp * NP; // the pack's first half of key t
-          const unsigned region_at =
-              static_cast<unsigned>(region == 0 ? L.value_scales : L.value_zeros);
-          dma4(p + region_at + static_cast<unsigned>(4 * (half / 2 + j)), slot.vmeta + 256 * d);
-        }
-      };
-      switch (tier)
-      {
-      case kINT8:
-        quantised(std::integral_constant<int, 8>{});
-        break;
-      case kINT4:
-        quantised(std::integral_constant<int, 4>{});
-        break;
-      case kINT2:
-        quantised(std::integral_constant<int, 2>{});
-        break;
-      default:
-        break;
       }
-    }
-
-    // The register part of a sealed unit: the lane's two key rows (and, at
-    // INT2, its two value rows) as eight 16-byte blocks, kraw slot kb * 4 + q
-    // for row kb. Every tier issues the same eight loads into the same
-    // registers, only the offsets differ: FP16 rows are 64 bytes (q = 0..3);
-    // INT8 rows 32 (q = 0, 1, then again); INT4 rows 16 (q = 0, then again);
-    // INT2 key and value rows 8 bytes each, in the 16-byte blocks holding
-    // them (q = 0 keys, q = 1 values, then again). The repeats hit the cache;
-    // one instruction sequence means the loads land in fixed registers with
-    // nothing to merge between tiers.
-    template <int HD, int NP>
-    __device__ inline void issue_regs(const DecodeArgs &a, const std::uint8_t *page, int tier,
-                                      int kp, unsigned *kraw, int lane)
-    {
-      using C = Cfg<HD, NP>;
-      static_assert(C::kRun == 32, "a lane group holds 32 channels of a row");
-      const int r = lane & 15, g = lane >> 4;
-      const unsigned W = static_cast<unsigned>(a.kv_heads * HD);
-      const unsigned gc = static_cast<unsigned>(kp * C::kWp + g * C::kRun);
-      const int bits = tier == kINT8 ? 8 : tier == kINT4 ? 4 : tier == kINT2 ? 2 : 16;
-      const unsigned vcodes = static_cast<unsigned>(a.lay[kINT2].value_codes);
+      half8 p_hi, p_lo;
+      softmax_page<HD>(acc, c, run, p_hi, p_lo);
+      // Values: one scale and zero a row (token) of this KV head.
+      u32x4 sv[2], zv[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
       {
-        const int t = tier == kINT4 ? key_of<true>(r, kb) : key_of<false>(r, kb);
-        const unsigned key_at = (t * W + gc) * bits / 8; // key codes start the page
-        const unsigned value_at = vcodes + (key_of<false>(r, kb) * W + gc) * 2 / 8;
-        // Offsets without branches: block q of the row is 16 q (FP16),
-        // 16 (q & 1) (INT8), 0 (INT4); INT2 takes keys at even q, values at
-        // odd, each in its aligned block.
-        const unsigned stride = bits >= 8 ? 16u : 0u;
-        const unsigned qmask = bits == 16 ? 3u : 1u;
+        const unsigned sp = raw.vs[kb] | (raw.vs[kb] << 16), zp = raw.vz[kb] | (raw.vz[kb] << 16);
+        sv[kb] = u32x4{sp, sp, sp, sp};
+        zv[kb] = u32x4{zp, zp, zp, zp};
+      }
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+      for (int s = 0; s < S; ++s)
+      {
+        half8 v[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
         {
-          const unsigned wide = key_at + stride * (static_cast<unsigned>(q) & qmask);
-          const unsigned narrow = ((q & 1) != 0 ? value_at : key_at) & ~15u;
-          load_at<16>(kraw + 4 * (kb * 4 + q), page, bits == 2 ? narrow : wide);
+          unsigned w0, w1 = 0;
+          if constexpr (Bits == 8)
+          {
+            w0 = raw.vc[kb][2 * s];
+            w1 = raw.vc[kb][2 * s + 1];
+          }
+          else if constexpr (Bits == 4)
+          {
+            w0 = raw.vc[kb][s];
+          }
+          else
+          {
+            w0 = raw.vc[kb][s / 2] >> (16 * (s & 1));
+          }
+          v[kb] = dequant_step<Bits>(w0, w1, sv[kb], zv[kb]);
         }
+        pv_step<HD>(run, s, v[0], v[1], r, g, p_hi, p_lo);
       }
     }
 
-    // The own page's key rows, FP16, as sealed FP16 rows sit in kraw: rows
-    // before t_start from the open page, from t_start on from the chunk;
-    // rows past the last key read row 0 (their scores are masked).
-    template <int HD, int NP>
-    __device__ inline void issue_regs_own(const DecodeArgs &a, const Rows &u, int kp,
-                                          unsigned *kraw, int lane)
+    // A page at INT8/INT4/INT2, read from global memory. `meta` is this
+    // wave's 4 * HD bytes of LDS: the key scales and zeros pass through it.
+    template <int HD, int Bits>
+    __device__ inline void quantised_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
+                                          const std::uint8_t *page, const PageLayout &L,
+                                          std::size_t W, int kvh, int kv_heads, int lane,
+                                          unsigned *meta)
     {
-      using C = Cfg<HD, NP>;
-      const int r = lane & 15, g = lane >> 4;
-      const std::size_t W = static_cast<std::size_t>(a.kv_heads) * HD;
-      const std::size_t gc = static_cast<std::size_t>(kp) * C::kWp + g * C::kRun;
+      using Raw = QuantRaw<HD, Bits>;
+      constexpr int kRun = HD / 4;
+      constexpr int kRowBytes = Raw::kRowWords * 4;
+      constexpr int kMetaLanes = HD / 4; // 8 bytes (4 channels) a lane, a region
+      const int r = c.r, g = c.g;
+      const std::size_t ch0 = static_cast<std::size_t>(kvh) * HD + g * kRun;
+      // Every load first: codes of both rows, the key scales and zeros (two
+      // regions, a lane's 8 bytes each), the rows' value scales and zeros.
+      Raw raw;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
       {
-        load_words<2 * C::kRun>(kraw + kb * 16, key_row(u, kOwnPage, key_of<false>(r, kb), W) + gc);
+        const std::size_t at = (static_cast<std::size_t>(kb * 16 + r) * W + ch0) * Bits / 8;
+        load_words<kRowBytes>(raw.kc[kb], page + L.key_codes + at);
+        load_words<kRowBytes>(raw.vc[kb], page + L.value_codes + at);
       }
+      u32x2 km = {0u, 0u};
+      const bool meta_lane = lane < 2 * kMetaLanes;
+      if (meta_lane)
+      {
+        const std::size_t region = lane < kMetaLanes ? L.key_scales : L.key_zeros;
+        km = *((g_u32x2)(page + region + 2 * static_cast<std::size_t>(kvh) * HD +
+                         8 * (lane % kMetaLanes)));
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+      {
+        const std::size_t grp = static_cast<std::size_t>(kb * 16 + r) * kv_heads + kvh;
+        raw.vs[kb] = *((g_u16)(page + L.value_scales + 2 * grp));
+        raw.vz[kb] = *((g_u16)(page + L.value_zeros + 2 * grp));
+      }
+      // The key scales and zeros through LDS: [scales HD halves][zeros HD].
+      // LDS operations of one wave complete in order; the fences keep the
+      // compiler from moving the reads above the write.
+      if (meta_lane)
+      {
+        *reinterpret_cast<u32x2 *>(meta + 2 * lane) = km;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      quantised_compute<HD, Bits>(run, c, qb, raw, meta, meta + HD / 2);
     }
 
-    // q.K^T of a unit: acc[kb] = the scores of C rows (keys key_of(., kb)),
-    // the keys read from kraw's slots (see issue_regs).
-    template <int HD, int NP, int Bits>
-    __device__ inline void unit_scores(f32x4 (&acc)[2], const unsigned *kraw, const half8 *qb,
-                                       const std::uint8_t *kmeta, int g)
+    // q.K^T of an FP16 page's two 16-row blocks.
+    template <int HD>
+    __device__ inline void fp16_scores(f32x4 (&acc)[2], const half8 (&k)[2][HD / 32],
+                                       const half8 *qb)
     {
-      using C = Cfg<HD, NP>;
       acc[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       acc[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if constexpr (Bits == 16)
+#pragma unroll
+      for (int s = 0; s < HD / 32; ++s)
       {
-#pragma unroll
-        for (int s = 0; s < C::kSteps; ++s)
-        {
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-          {
-            const unsigned *w = kraw + 4 * (kb * 4 + s);
-            acc[kb] = mfma(as_half8(u32x4{w[0], w[1], w[2], w[3]}), qb[s], acc[kb]);
-          }
-        }
-      }
-      else
-      {
-        const auto *ks = reinterpret_cast<const u32x4 *>(kmeta) + g * (C::kRun / 8);
-        const auto *kz = reinterpret_cast<const u32x4 *>(kmeta + 2 * C::kWp) + g * (C::kRun / 8);
-        // INT2: an odd lane group's 8 bytes are its block's upper half; picked
-        // by masking values, never by indexing, so kraw stays in registers.
-        const unsigned upper = (g & 1) != 0 ? 0xFFFFFFFFu : 0u;
-#pragma unroll
-        for (int s = 0; s < C::kSteps; ++s)
-        {
-          const u32x4 s2 = ks[s];
-          const u32x4 z2 = kz[s];
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-          {
-            unsigned w0, w1 = 0;
-            if constexpr (Bits == 8)
-            {
-              const unsigned *w = kraw + 4 * (kb * 4 + s / 2) + 2 * (s & 1);
-              w0 = w[0];
-              w1 = w[1];
-            }
-            else if constexpr (Bits == 4)
-            {
-              w0 = kraw[4 * (kb * 4) + s];
-            }
-            else
-            {
-              const unsigned *w = kraw + 4 * (kb * 4);
-              const unsigned lo = w[s / 2], hi = w[2 + s / 2];
-              w0 = (lo ^ ((lo ^ hi) & upper)) >> (16 * (s & 1));
-            }
-            acc[kb] = mfma(dequant_step<Bits>(w0, w1, s2, z2), qb[s], acc[kb]);
-          }
-        }
+        acc[0] = mfma(k[0][s], qb[s], acc[0]);
+        acc[1] = mfma(k[1][s], qb[s], acc[1]);
       }
     }
 
-    // Value scale (region 0) or zero (region 1) of key t, KV head k of the
-    // pack, from the slot's value metadata, as fp16 bits.
-    template <int NP>
-    __device__ inline unsigned value_meta(const std::uint8_t *vmeta, int region, int t, int k,
-                                          int kp, int kv_heads)
+    // P.V of an FP16 page. Rows past the last key may hold anything: their
+    // scores are masked, and their values zeroed so that a non-finite one
+    // cannot reach P.V.
+    template <int HD>
+    __device__ inline void fp16_values(Running<HD> &run, const PageCtx &c, half8 (&v)[2][HD / 32],
+                                       half8 p_hi, half8 p_lo)
     {
-      constexpr int D = value_meta_dwords<NP>();
-      const int half = NP == 1 ? ((t * kv_heads + kp) & 1) : (k & 1);
-      const auto *w = reinterpret_cast<const unsigned *>(vmeta) + (region * 32 + t) * D +
-                      (NP == 1 ? 0 : k / 2);
-      return (*w >> (16 * half)) & 0xFFFFu;
-    }
-
-    // Value scales (or zeros) of keys 8g .. 8g+7 of the pack's KV head k, as
-    // four packed pairs: natural (t, t+1), or (t, t+4) for INT4's order. The
-    // keys' dwords are read together, the halves paired by byte permutes.
-    template <int NP, bool Interleaved>
-    __device__ inline u32x4 value_pairs(const std::uint8_t *vmeta, int region, int g, int k,
-                                        int kp, int kv_heads)
-    {
-      constexpr int D = value_meta_dwords<NP>();
-      // The dword of key 8g + j holding KV head k: j * D + k / 2.
-      const auto *base = reinterpret_cast<const unsigned *>(vmeta) + (region * 32 + 8 * g) * D;
-      unsigned w[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
+      constexpr int S = HD / 32;
+      if (c.partial)
       {
-        w[j] = base[j * D + (NP == 1 ? 0 : k / 2)];
-      }
-      u32x4 out;
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-      {
-        const int j0 = Interleaved ? u : 2 * u;
-        const int j1 = j0 + (Interleaved ? 4 : 1);
-        const int h0 = NP == 1 ? (((8 * g + j0) * kv_heads + kp) & 1) : (k & 1);
-        const int h1 = NP == 1 ? (((8 * g + j1) * kv_heads + kp) & 1) : (k & 1);
-        const unsigned sel = static_cast<unsigned>(2 * h0) |
-                             (static_cast<unsigned>(2 * h0 + 1) << 8) |
-                             (static_cast<unsigned>(4 + 2 * h1) << 16) |
-                             (static_cast<unsigned>(5 + 2 * h1) << 24);
-        out[u] = __builtin_amdgcn_perm(w[j1], w[j0], sel);
-      }
-      return out;
-    }
-
-    // INT2 values: the lane's two value rows dequantised in registers and
-    // written to the slot's FP16 image, for the same transposing reads as an
-    // FP16 page.
-    template <int HD, int NP>
-    __device__ inline void int2_values_to_image(const unsigned *kraw, const Slot<HD, NP> &slot,
-                                                int kp, int kv_heads, int lane)
-    {
-      using C = Cfg<HD, NP>;
-      const int r = lane & 15, g = lane >> 4;
-      const int k = g * C::kRun / HD;                // KV head within the pack
-      const int c0 = (g * C::kRun) % HD;             // first channel within it
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-      {
-        const int t = key_of<false>(r, kb);
-        const unsigned s = value_meta<NP>(slot.vmeta, 0, t, k, kp, kv_heads);
-        const unsigned z = value_meta<NP>(slot.vmeta, 1, t, k, kp, kv_heads);
-        const unsigned sp = s | (s << 16), zp = z | (z << 16);
-        const u32x4 s2 = {sp, sp, sp, sp}, z2 = {zp, zp, zp, zp};
-        const unsigned *vc = kraw + 4 * (kb * 4 + 1);
-        const unsigned upper = (g & 1) != 0 ? 0xFFFFFFFFu : 0u; // see unit_scores
-        const int row = fp16_image_row(t);
-#pragma unroll
-        for (int s8 = 0; s8 < C::kRun / 8; ++s8)
+        for (int kb = 0; kb < 2; ++kb)
         {
-          const unsigned lo = vc[s8 / 2], hi = vc[2 + s8 / 2];
-          const half8 v = dequant_step<2>((lo ^ ((lo ^ hi) & upper)) >> (16 * (s8 & 1)), 0u, s2, z2);
-          const int c8 = c0 / 8 + s8;
-          *reinterpret_cast<half8 *>(slot.v + 16 * ((c8 * NP + k) * 32 + row)) = v;
-        }
-      }
-    }
-
-    // P.V of a unit, V read transposed out of the slot block by block: per
-    // 16-channel block and KV head k of the pack, eight keys of one channel
-    // a lane (FP16 and INT2 from the fp16 image, two 4-key reads; INT8 one
-    // 8-code read; INT4 one 16-code read serving two (block, k) pairs),
-    // dequantised with each key's value scale and zero, times that head's
-    // P (zero in other heads' columns), high and low parts.
-    template <int HD, int NP, int Bits>
-    __device__ inline void unit_pv(Running<HD> &run, const Slot<HD, NP> &slot,
-                                   const half8 (&b_hi)[NP], const half8 (&b_lo)[NP], int kp,
-                                   int kv_heads, int lane, const PageCtx &c)
-    {
-      using C = Cfg<HD, NP>;
-      const int g = lane >> 4, s = lane & 15;
-      if constexpr (Bits == 16 || Bits == 2)
-      {
-        const std::uint8_t *base =
-            slot.v + 16 * (((s & 3) >> 1) * NP * 32 + 4 * g + (s >> 2)) + 8 * (s & 1);
-        // A partial page (a cache that does not seal: its last page) may hold
-        // anything past its last key: those values are zeroed, so that a
-        // non-finite one cannot reach P.V through a zero weight.
-        unsigned keep = 0xFFu;
-        if (c.partial)
-        {
-          const int valid = c.last + 1 - 8 * g; // keys 8g .. 8g+7 of this lane
-          keep = valid <= 0 ? 0u : valid >= 8 ? 0xFFu : (1u << valid) - 1u;
-        }
-#pragma unroll
-        for (int cb = 0; cb < C::kCB; ++cb)
-        {
-#pragma unroll
-          for (int k = 0; k < NP; ++k)
-          {
-            const std::uint8_t *p = base + 16 * (2 * cb * NP + k) * 32;
-            const u32x2 x0 = tr16(p);
-            const u32x2 x1 = tr16(p + 16 * 16);
-            u32x4 w = {x0.x, x0.y, x1.x, x1.y};
-            if (c.partial)
-            {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-              {
-                const unsigned lo = (keep >> (2 * e)) & 1u ? 0x0000FFFFu : 0u;
-                const unsigned hi = (keep >> (2 * e + 1)) & 1u ? 0xFFFF0000u : 0u;
-                w[e] &= lo | hi;
-              }
-            }
-            const half8 v = as_half8(w);
-            run.o[cb] = mfma(v, b_hi[k], run.o[cb]);
-            run.o[cb] = mfma(v, b_lo[k], run.o[cb]);
-          }
-        }
-      }
-      else
-      {
-        u32x4 vs[NP], vz[NP];
-#pragma unroll
-        for (int k = 0; k < NP; ++k)
-        {
-          vs[k] = value_pairs<NP, Bits == 4>(slot.vmeta, 0, g, k, kp, kv_heads);
-          vz[k] = value_pairs<NP, Bits == 4>(slot.vmeta, 1, g, k, kp, kv_heads);
-        }
-        if constexpr (Bits == 8)
-        {
-#pragma unroll
-          for (int cb = 0; cb < C::kCB; ++cb)
+          if (kb * 16 + c.r > c.last)
           {
 #pragma unroll
-            for (int k = 0; k < NP; ++k)
+            for (int s = 0; s < S; ++s)
             {
-              const u32x2 x = tr8(slot.v + 512 * (cb * NP + k) + 8 * lane);
-              const half8 v = dequant_step<8>(x.x, x.y, vs[k], vz[k]);
-              run.o[cb] = mfma(v, b_hi[k], run.o[cb]);
-              run.o[cb] = mfma(v, b_lo[k], run.o[cb]);
-            }
-          }
-        }
-        else
-        {
-          // Read rho: source lanes s < 8 carry pair 2 rho, s >= 8 pair
-          // 2 rho + 1 (pair = cb * NP + k); source lane s reads key 8 g + s % 8.
-#pragma unroll
-          for (int rho = 0; rho < NP * C::kCB / 2; ++rho)
-          {
-            const int mine = 2 * rho + (s >> 3);
-            const int mcb = mine / NP, mk = mine % NP;
-            const u32x2 x = tr4(slot.v + 16 * (((mcb >> 1) * NP + mk) * 32 + 8 * g + (s & 7)) +
-                                8 * (mcb & 1));
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-            {
-              const int pair = 2 * rho + h;
-              const int cb = pair / NP, k = pair % NP;
-              const half8 v = dequant_int4_interleaved(h == 0 ? x.x : x.y, vs[k], vz[k]);
-              run.o[cb] = mfma(v, b_hi[k], run.o[cb]);
-              run.o[cb] = mfma(v, b_lo[k], run.o[cb]);
+              v[kb][s] = as_half8(u32x4{0u, 0u, 0u, 0u});
             }
           }
         }
       }
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+      {
+        pv_step<HD>(run, s, v[0][s], v[1][s], c.r, c.g, p_hi, p_lo);
+      }
     }
 
-    template <int HD, int NP>
-    __device__ inline Slot<HD, NP> slot_in(std::uint8_t *buffer, int wave)
+    // A page of FP16 rows from global memory: keys at k0/k1 (rows r and
+    // 16 + r, the lane's run), values at v0/v1, all requested at once so that
+    // the page costs one trip to memory.
+    template <int HD>
+    __device__ inline void fp16_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
+                                     const std::uint16_t *k0, const std::uint16_t *k1,
+                                     const std::uint16_t *v0, const std::uint16_t *v1)
     {
-      Slot<HD, NP> slot;
-      slot.v = buffer + wave * slot_bytes<HD, NP>();
-      slot.kmeta = slot.v + Cfg<HD, NP>::kVBytes;
-      slot.vmeta = slot.kmeta + Cfg<HD, NP>::kKMeta;
-      return slot;
+      constexpr int S = HD / 32;
+      half8 k[2][S], v[2][S];
+      load_fp16_run<HD>(k[0], k0);
+      load_fp16_run<HD>(k[1], k1);
+      load_fp16_run<HD>(v[0], v0);
+      load_fp16_run<HD>(v[1], v1);
+      f32x4 acc[2];
+      fp16_scores<HD>(acc, k, qb);
+      half8 p_hi, p_lo;
+      softmax_page<HD>(acc, c, run, p_hi, p_lo);
+      fp16_values<HD>(run, c, v, p_hi, p_lo);
     }
 
-    template <int HD, int NP>
+    template <int HD>
     __global__ void __launch_bounds__(kThreads) decode_pages_kernel(DecodeArgs a)
     {
-      using C = Cfg<HD, NP>;
+      constexpr int S = HD / 32;  // K steps of q.K^T
+      constexpr int DB = HD / 16; // 16-channel blocks of the output
+      constexpr int kRun = HD / 4;
       constexpr int kRow = HD + 4;
-      // Two LDS buffers a wave: the unit being computed reads one while the
-      // next unit's V and metadata land in the other. Two distinct arrays, so
-      // that the compiler sees the copies into one cannot alias reads of the
-      // other and adds no waits for them.
-      __shared__ __attribute__((aligned(16))) std::uint8_t buf_a[kWaves * slot_bytes<HD, NP>()];
-      __shared__ __attribute__((aligned(16))) std::uint8_t buf_b[kWaves * slot_bytes<HD, NP>()];
+      extern __shared__ float lds[];
 
       const int lane = threadIdx.x & 63;
-      // The wave index, and all that follows from it (pages, tiers, page
-      // addresses), is uniform across the wave: said so, the tier switch is
-      // scalar branching and only one tier's registers are live at a time.
+      // Uniform across the wave, as are its pages: their tiers and addresses
+      // are scalar loads.
       const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
       const int r = lane & 15;
       const int g = lane >> 4;
       const int split = blockIdx.x;
-      const int kp = blockIdx.y;
+      const int kvh = blockIdx.y;
       const int li = blockIdx.z;
       const int layer = a.first_layer + li;
       const int G = a.group;
-      const int n_live = NP * G;
-      const bool live = r < n_live;
-      const int kn = live ? r / G : NP; // the column's KV head within the pack
-      const Slot<HD, NP> sa = slot_in<HD, NP>(buf_a, wave);
-      const Slot<HD, NP> sb = slot_in<HD, NP>(buf_b, wave);
+      const std::size_t W = static_cast<std::size_t>(a.kv_heads) * HD;
+      const std::size_t run0 = static_cast<std::size_t>(kvh) * HD + g * kRun;
+      // LDS: each wave's key metadata, then the epilogue's per-wave state.
+      unsigned *meta = reinterpret_cast<unsigned *>(lds) + wave * HD;
+      float *s_m = lds + kWaves * HD;
+      float *s_l = s_m + kWaves * G;
+      float *s_w = s_l + kWaves * G; // kWaves * G weights, then G maxima
+      float *s_o = s_w + kWaves * G + G;
 
       const unsigned long long *table = a.table + layer * a.table_stride;
       const std::uint8_t *tiers = a.tiers != nullptr ? a.tiers + layer * a.table_stride : nullptr;
       const int own = a.causal ? (a.seq_k - 1) / kPageTokens : -1;
-      // The workgroup's pages, then this wave's share of them.
-      const int wg0 = static_cast<int>(static_cast<long long>(split) * a.pages / a.splits);
-      const int wg1 = static_cast<int>(static_cast<long long>(split + 1) * a.pages / a.splits);
-      const int p0 = wg0 + (wg1 - wg0) * wave / kWaves;
-      const int p1 = wg0 + (wg1 - wg0) * (wave + 1) / kWaves;
+      const int p0 = (split * kWaves + wave) * a.pages_per_wave;
+      const std::uint16_t *q_row = a.q + li * a.q_stride +
+                                   static_cast<std::size_t>(kvh * G + (r < G ? r : 0)) * HD +
+                                   g * kRun;
       float *stats = a.page_stats + static_cast<std::size_t>(li) * a.heads * a.pages * 2;
-      const int head = kp * n_live + (live ? r : 0);
-
-      // q of the lane's column, block-diagonal: zero unless the lane group's
-      // channels are the column's KV head's.
-      half8 qb[C::kSteps];
-      {
-        const int kg = g * NP / 4; // the lane group's KV head within the pack
-        const std::uint16_t *q_row = a.q + li * a.q_stride + static_cast<std::size_t>(head) * HD +
-                                     (g * C::kRun) % HD;
-        unsigned qw[C::kRun / 2];
-        load_words<2 * C::kRun>(qw, q_row);
-#pragma unroll
-        for (int s = 0; s < C::kSteps; ++s)
-        {
-          qb[s] = (live && kg == kn)
-                      ? as_half8(u32x4{qw[4 * s], qw[4 * s + 1], qw[4 * s + 2], qw[4 * s + 3]})
-                      : as_half8(u32x4{0u, 0u, 0u, 0u});
-        }
-      }
 
       Running<HD> run;
       run.m = -INFINITY;
       run.l = 0.0f;
 #pragma unroll
-      for (int cb = 0; cb < C::kCB; ++cb)
+      for (int db = 0; db < DB; ++db)
       {
-        run.o[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        run.o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       }
 
+      // q of head r, the lane's run of channels. Columns past the group
+      // repeat the group's first head: their scores and outputs stay in
+      // their own columns and are never stored.
+      half8 qb[S];
+      load_fp16_run<HD>(qb, q_row);
+
+      // Where the tiers and addresses are read from: q (always readable)
+      // stands in for a table that has no entries.
+      const auto *tier_base = a.causal ? tiers : reinterpret_cast<const std::uint8_t *>(a.q);
+      const auto *page_base =
+          !a.causal || own > 0 ? table : reinterpret_cast<const unsigned long long *>(a.q);
+      // The open page's rows, asked for with q, not after the tier.
       const auto *open = a.open_table != nullptr
                              ? reinterpret_cast<const std::uint16_t *>(a.open_table[layer])
                              : a.open;
-      const auto own_rows = [&](int p) {
-        Rows u;
-        u.page = nullptr;
-        u.open = open;
-        u.chunk_k = a.chunk_k + li * a.chunk_stride;
-        u.chunk_v = a.chunk_v + li * a.chunk_stride;
-        u.t_start = a.start - p * kPageTokens;
-        u.last = a.seq_k - 1 - p * kPageTokens;
-        return u;
-      };
-      // Sealed pages of this wave: [p0, q1); the own page, if this wave's,
-      // after them. Their tiers and addresses are read once, a lane a page,
-      // 64 pages at a time, and taken out of the lanes as the loop goes.
-      const int q1 = a.causal ? min(p1, own) : p1;
-      unsigned long long my_addr = 0;
-      int my_tier = kUnreadPage;
-      const auto preload = [&](int from) {
-        const int pl = from + lane;
-        my_tier = kUnreadPage;
-        my_addr = 0;
-        if (pl < q1)
-        {
-          my_tier = a.causal ? static_cast<int>(tiers[pl]) : static_cast<int>(kFP16);
-          if (my_tier != kUnreadPage)
-          {
-            my_addr = table[pl];
-          }
-        }
-      };
-      const auto tier_at = [&](int p) {
-        return p < q1 ? __builtin_amdgcn_readlane(my_tier, (p - p0) & 63) : kUnreadPage;
-      };
-      const auto page_at = [&](int p) {
-        const int i = (p - p0) & 63;
-        return reinterpret_cast<const std::uint8_t *>(
-            (static_cast<unsigned long long>(
-                 __builtin_amdgcn_readlane(static_cast<unsigned>(my_addr >> 32), i))
-             << 32) |
-            static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<unsigned>(my_addr), i)));
-      };
-
-      unsigned kraw[C::kRaw];
       bool first = true;
-      // A readable stand-in for a next unit that does not exist: the key
-      // loads read the start of the decode workspace (at least 4 MiB; an
-      // FP16 unit's offsets stay below 64 W bytes, 32 KiB at most) and
-      // nothing uses what they return.
-      const auto *stand_in = reinterpret_cast<const std::uint8_t *>(a.partials);
-      const auto masks = [&](const half8 &p_hi, const half8 &p_lo, half8 (&b_hi)[NP],
-                             half8 (&b_lo)[NP]) {
-        // Each KV head of the pack multiplies its own heads' P only.
-#pragma unroll
-        for (int k = 0; k < NP; ++k)
+      for (int i = 0; i < a.pages_per_wave; ++i)
+      {
+        const int p = p0 + i;
+        if (p >= a.pages)
         {
-          b_hi[k] = kn == k ? p_hi : as_half8(u32x4{0u, 0u, 0u, 0u});
-          b_lo[k] = kn == k ? p_lo : as_half8(u32x4{0u, 0u, 0u, 0u});
+          break;
         }
-      };
-      const auto context = [&](int p) {
+        // The page's tier and address are requested together, with no
+        // branch between them, so that both are one trip to memory.
+        const bool sealed = !a.causal || p < own;
+        const int tier_raw = __builtin_amdgcn_readfirstlane(tier_base[a.causal && p < own ? p : 0]);
+        const unsigned long long page_raw = page_base[sealed ? p : 0];
+        const int tier = !a.causal ? static_cast<int>(kFP16) : (p < own ? tier_raw : kOwnPage);
+        const auto *page = reinterpret_cast<const std::uint8_t *>(sealed ? page_raw : 0ull);
         PageCtx c;
+        c.r = r;
         c.g = g;
-        c.live = live;
+        c.group = G;
         c.last = a.seq_k - 1 - p * kPageTokens;
         c.partial = c.last < kPageTokens - 1;
         c.first = first;
         c.scale = a.scale;
-        c.stat = stats + (static_cast<std::size_t>(head) * a.pages + p) * 2;
-        return c;
-      };
-      const auto unread = [&](int p) {
-        if (g == 0 && live)
-        {
-          float *stat = stats + (static_cast<std::size_t>(head) * a.pages + p) * 2;
-          stat[0] = -INFINITY;
-          stat[1] = 0.0f;
-        }
-      };
-      // One sealed unit: page p at `tier`, its V and metadata in x, its key
-      // rows in kraw. The next sealed unit (page p + 1 at next_tier, at
-      // next_page) is requested into y and kraw as soon as this unit's keys
-      // are used, to fly while this unit's softmax and P.V are computed. The
-      // key rows are requested from one place, whatever the tiers, so that
-      // kraw's registers are the same on every path (with no next unit, a
-      // page of the q rows stands in and is never read).
-      const auto step = [&](int p, int tier, int next_tier, const std::uint8_t *next_page,
-                            const Slot<HD, NP> &x, const Slot<HD, NP> &y) {
-        const int ln = opaque(lane);
-        f32x4 acc[2];
-        // Every path waits here, so that no load is in flight into kraw when
-        // the next unit's loads reuse its registers.
-        wait_copies();
-        if (tier != kUnreadPage)
-        {
-          switch (tier)
-          {
-          case kINT8:
-            unit_scores<HD, NP, 8>(acc, kraw, qb, x.kmeta, ln >> 4);
-            break;
-          case kINT4:
-            unit_scores<HD, NP, 4>(acc, kraw, qb, x.kmeta, ln >> 4);
-            break;
-          case kINT2:
-            unit_scores<HD, NP, 2>(acc, kraw, qb, x.kmeta, ln >> 4);
-            int2_values_to_image<HD, NP>(kraw, x, kp, a.kv_heads, ln);
-            lds_order();
-            break;
-          default:
-            unit_scores<HD, NP, 16>(acc, kraw, qb, x.kmeta, ln >> 4);
-            break;
-          }
-        }
-        const bool has_next = next_tier != kUnreadPage;
-        if (has_next)
-        {
-          Rows u{};
-          u.page = next_page;
-          issue_lds<HD, NP>(a, u, next_tier, kp, y, ln);
-        }
-        issue_regs<HD, NP>(a, has_next ? next_page : stand_in, has_next ? next_tier : kFP16, kp,
-                           kraw, ln);
+        c.stat = stats + ((static_cast<std::size_t>(kvh) * a.pages + p) * G + r) * 2;
         if (tier == kUnreadPage)
         {
-          unread(p);
-          return;
+          if (g == 0 && r < G)
+          {
+            *reinterpret_cast<float2 *>(c.stat) = make_float2(-INFINITY, 0.0f);
+          }
+          continue;
         }
-        const PageCtx c = context(p);
-        half8 p_hi, p_lo;
-        softmax_page<HD>(acc, c, run, p_hi, p_lo);
-        half8 b_hi[NP], b_lo[NP];
-        masks(p_hi, p_lo, b_hi, b_lo);
         switch (tier)
         {
         case kINT8:
-          unit_pv<HD, NP, 8>(run, x, b_hi, b_lo, kp, a.kv_heads, ln, c);
+          quantised_page<HD, 8>(run, c, qb, page, a.lay[kINT8], W, kvh, a.kv_heads, lane, meta);
           break;
         case kINT4:
-          unit_pv<HD, NP, 4>(run, x, b_hi, b_lo, kp, a.kv_heads, ln, c);
+          quantised_page<HD, 4>(run, c, qb, page, a.lay[kINT4], W, kvh, a.kv_heads, lane, meta);
           break;
         case kINT2:
-          unit_pv<HD, NP, 2>(run, x, b_hi, b_lo, kp, a.kv_heads, ln, c);
+          quantised_page<HD, 2>(run, c, qb, page, a.lay[kINT2], W, kvh, a.kv_heads, lane, meta);
           break;
+        case kOwnPage:
+        {
+          // Rows before `start` from the open page, the rest from the chunk;
+          // rows past the last key read row 0 (masked).
+          const int t_start = a.start - p * kPageTokens;
+          const std::uint16_t *ck = a.chunk_k + li * a.chunk_stride;
+          const std::uint16_t *cv = a.chunk_v + li * a.chunk_stride;
+          const std::uint16_t *rk[2], *rv[2];
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+          {
+            const int t = kb * 16 + r;
+            const int tt = t <= c.last ? t : 0;
+            if (tt < t_start)
+            {
+              rk[kb] = open + static_cast<std::size_t>(tt) * W + run0;
+              rv[kb] = open + static_cast<std::size_t>(kPageTokens + tt) * W + run0;
+            }
+            else
+            {
+              rk[kb] = ck + static_cast<std::size_t>(tt - t_start) * W + run0;
+              rv[kb] = cv + static_cast<std::size_t>(tt - t_start) * W + run0;
+            }
+          }
+          fp16_page<HD>(run, c, qb, rk[0], rk[1], rv[0], rv[1]);
+          break;
+        }
         default:
-          unit_pv<HD, NP, 16>(run, x, b_hi, b_lo, kp, a.kv_heads, ln, c);
+        {
+          const auto *h = reinterpret_cast<const std::uint16_t *>(page);
+          fp16_page<HD>(run, c, qb, h + static_cast<std::size_t>(r) * W + run0,
+                        h + static_cast<std::size_t>(16 + r) * W + run0,
+                        h + static_cast<std::size_t>(kPageTokens + r) * W + run0,
+                        h + static_cast<std::size_t>(kPageTokens + 16 + r) * W + run0);
           break;
         }
-        first = false;
-      };
-
-      preload(p0);
-      int tier = tier_at(p0);
-      {
-        const bool has = tier != kUnreadPage;
-        Rows u{};
-        u.page = has ? page_at(p0) : stand_in;
-        if (has)
-        {
-          issue_lds<HD, NP>(a, u, tier, kp, sa, lane);
         }
-        issue_regs<HD, NP>(a, u.page, has ? tier : kFP16, kp, kraw, lane);
-      }
-      for (int p = p0; p < q1; p += 2)
-      {
-        // Every 64 pages the next 64 pages' tiers and addresses; the page
-        // that starts the block was read with the block before.
-        int t1 = kUnreadPage;
-        const std::uint8_t *a1 = nullptr;
-        if (p + 1 < q1)
-        {
-          if (((p + 1 - p0) & 63) == 0)
-          {
-            preload(p + 1);
-          }
-          t1 = tier_at(p + 1);
-          a1 = page_at(p + 1);
-        }
-        step(p, tier, t1, a1, sa, sb);
-        if (p + 1 >= q1)
-        {
-          break;
-        }
-        int t2 = kUnreadPage;
-        const std::uint8_t *a2 = nullptr;
-        if (p + 2 < q1)
-        {
-          if (((p + 2 - p0) & 63) == 0)
-          {
-            preload(p + 2);
-          }
-          t2 = tier_at(p + 2);
-          a2 = page_at(p + 2);
-        }
-        step(p + 1, t1, t2, a2, sb, sa);
-        tier = t2;
-      }
-      if (a.causal && own >= p0 && own < p1)
-      {
-        // The query's own page, FP16 from the open page and the chunk rows:
-        // the last page, after the sealed ones (all of whose loads are done).
-        const Rows u = own_rows(own);
-        issue_lds<HD, NP>(a, u, kOwnPage, kp, sa, lane);
-        issue_regs_own<HD, NP>(a, u, kp, kraw, lane);
-        const PageCtx c = context(own);
-        wait_copies();
-        f32x4 acc[2];
-        unit_scores<HD, NP, 16>(acc, kraw, qb, sa.kmeta, g);
-        half8 p_hi, p_lo;
-        softmax_page<HD>(acc, c, run, p_hi, p_lo);
-        half8 b_hi[NP], b_lo[NP];
-        masks(p_hi, p_lo, b_hi, b_lo);
-        unit_pv<HD, NP, 16>(run, sa, b_hi, b_lo, kp, a.kv_heads, lane, c);
         first = false;
       }
-      wait_reads();
 
-      // The workgroup's waves into one partial: each wave's state to LDS
-      // (buffer a is free once every wave is past its loop), then each
-      // (wave, column)'s weight at the columns' common max, once.
-      __syncthreads();
-      auto *lf = reinterpret_cast<float *>(buf_a);
-      float *s_m = lf;
-      float *s_l = s_m + kWaves * 16;
-      float *s_w = s_l + kWaves * 16; // kWaves * 16 weights, then 16 maxima
-      float *s_o = s_w + kWaves * 16 + 16;
-      static_assert((3 * kWaves * 16 + 16 + kWaves * 16 * kRow) * 4 <=
-                        kWaves * slot_bytes<HD, NP>(),
-                    "the epilogue's state fits buffer a");
-      if (g == 0)
+      // The workgroup's waves into one partial: each wave's state to LDS,
+      // then each (wave, head)'s weight at the heads' common max, once.
+      if (r < G)
       {
-        s_m[wave * 16 + r] = first ? -INFINITY : run.m;
-        s_l[wave * 16 + r] = first ? 0.0f : run.l;
-      }
-#pragma unroll
-      for (int cb = 0; cb < C::kCB; ++cb)
-      {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
+        if (g == 0)
         {
-          s_o[(wave * 16 + r) * kRow + 16 * cb + 4 * g + i] =
-              first ? 0.0f : run.o[cb][i] * kPUnscale;
+          s_m[wave * G + r] = run.m;
+          s_l[wave * G + r] = run.l;
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+        {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+          {
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2)
+            {
+              s_o[(wave * G + r) * kRow + out_channel<HD>(s, h, g, i2)] =
+                  run.o[2 * s + h][i2] * kPUnscale;
+            }
+          }
         }
       }
       __syncthreads();
-      if (threadIdx.x < kWaves * 16)
+      if (threadIdx.x < kWaves * G)
       {
-        const int h = threadIdx.x % 16;
+        const int h = threadIdx.x % G;
         float top = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
         {
-          top = fmaxf(top, s_m[w * 16 + h]);
+          top = fmaxf(top, s_m[w * G + h]);
         }
         const float from = top == -INFINITY ? 0.0f : top;
         s_w[threadIdx.x] = exp2_fast(s_m[threadIdx.x] - from);
-        if (threadIdx.x < 16)
+        if (threadIdx.x < G)
         {
-          s_w[kWaves * 16 + h] = top;
+          s_w[kWaves * G + h] = top;
         }
       }
       __syncthreads();
-      for (int idx = threadIdx.x; idx < n_live * (HD + 2); idx += kThreads)
+      float *part = a.partials +
+                    ((static_cast<std::size_t>(li) * a.kv_heads + kvh) * a.splits + split) * G * HD;
+      float *ml = a.split_ml + (static_cast<std::size_t>(li) * a.kv_heads + kvh) * G * a.splits * 2;
+      for (int idx = threadIdx.x; idx < G * (HD + 2); idx += kThreads)
       {
         const int h = idx / (HD + 2);
         const int col = idx % (HD + 2);
-        float acc = s_w[kWaves * 16 + h];
+        float acc = s_w[kWaves * G + h];
         if (col != 0)
         {
           acc = 0.0f;
 #pragma unroll
           for (int w = 0; w < kWaves; ++w)
           {
-            const float v = col == 1 ? s_l[w * 16 + h] : s_o[(w * 16 + h) * kRow + col - 2];
-            acc += v * s_w[w * 16 + h];
+            const float v = col == 1 ? s_l[w * G + h] : s_o[(w * G + h) * kRow + col - 2];
+            acc += v * s_w[w * G + h];
           }
         }
-        const int kvh = kp * NP + h / G;
-        float *part = a.partials +
-                      (((static_cast<std::size_t>(li) * a.kv_heads + kvh) * a.splits + split) * G +
-                       h % G) *
-                          (kSlotHead + HD);
-        part[col < 2 ? col : kSlotHead + col - 2] = acc;
+        if (col < 2)
+        {
+          ml[(static_cast<std::size_t>(h) * a.splits + split) * 2 + col] = acc;
+        }
+        else
+        {
+          part[h * HD + col - 2] = acc;
+        }
       }
     }
 
+    // LDS of decode_pages_kernel, bytes.
+    std::size_t pages_kernel_lds(int group, int hd)
+    {
+      return (static_cast<std::size_t>(kWaves) * hd + 3 * kWaves * group + group +
+              static_cast<std::size_t>(kWaves) * group * (hd + 4)) *
+             sizeof(float);
+    }
+
+    // ---- the streaming kernel: several layers in one launch ----------------
+
+    typedef __attribute__((address_space(3))) void *lds_void;
+    // Word 3 of a raw buffer descriptor on gfx9-family parts (gfx950).
+    constexpr int kBufferWord3 = 0x00020000;
+    typedef const __attribute__((address_space(1))) void *global_void;
+
+    // Direct global-to-LDS copies (global_load_lds): lane l's 16 (or 4)
+    // bytes land at block + 16 l (4 l); `block` must be wave-uniform.
+    __device__ inline void dma16(const void *src, void *block)
+    {
+      __builtin_amdgcn_global_load_lds((global_void)src, (lds_void)block, 16, 0, 0);
+    }
+    __device__ inline void dma4(const void *src, void *block)
+    {
+      __builtin_amdgcn_global_load_lds((global_void)src, (lds_void)block, 4, 0, 0);
+    }
+    // s_waitcnt vmcnt(0): every copy into LDS has landed.
+    __device__ inline void wait_copies()
+    {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // s_waitcnt lgkmcnt(0): every LDS read has returned, so its slot may be
+    // overwritten.
+    __device__ inline void wait_reads()
+    {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    __device__ inline u32x4 lds16(const void *block, int lane)
+    {
+      return *reinterpret_cast<const u32x4 *>(static_cast<const std::uint8_t *>(block) + 16 * lane);
+    }
+    __device__ inline unsigned lds4(const void *block, int lane)
+    {
+      return *reinterpret_cast<const unsigned *>(static_cast<const std::uint8_t *>(block) + 4 * lane);
+    }
+
+    // Where a quantised page's pieces sit in a wave's LDS slot. Codes go in
+    // 1 KiB blocks of 16 bytes a lane when a lane's row run is a multiple of
+    // 16 bytes, else in 256-byte blocks of 4 bytes a lane; both in the order
+    // the lanes read them. Then the KV head's key scales, key zeros (a
+    // 256-byte block each) and the page's value scales and zeros.
+    template <int HD, int Bits>
+    struct SlotLayout
+    {
+      static constexpr int kRowWords = QuantRaw<HD, Bits>::kRowWords;
+      static constexpr bool kWide = kRowWords % 4 == 0;
+      static constexpr int kBlocksARow = kWide ? kRowWords / 4 : kRowWords;
+      static constexpr int kBlock = kWide ? 1024 : 256;
+      static constexpr int kCodes = 4 * kBlocksARow * kBlock; // K rows r, 16+r; V rows
+      static constexpr int kKeyScales = kCodes;
+      static constexpr int kKeyZeros = kCodes + 256;
+      static constexpr int kValueMeta = kCodes + 512;
+    };
+
+    // The bytes of one (page, KV head) unit a wave's slot must hold, and the
+    // slot's size: an FP16 unit (4 rows of the lane's run, 16 bytes a lane a
+    // step) is the largest.
+    template <int HD>
+    constexpr int stream_slot_bytes()
+    {
+      return 4 * (HD / 32) * 1024;
+    }
+
+    struct Unit
+    {
+      int li;   // layer within the launch
+      int kvh;
+      int page;
+    };
+
+    __device__ inline Unit unit_of(long long u, int kv_heads, int pages)
+    {
+      const long long group = u / pages;
+      return {static_cast<int>(group / kv_heads), static_cast<int>(group % kv_heads),
+              static_cast<int>(u - group * pages)};
+    }
+
+    // Range of wave w: units [w U / W, (w+1) U / W).
+    __host__ __device__ inline long long range_start(long long w, long long units, int waves)
+    {
+      return w * units / waves;
+    }
+
+    // The wave whose range holds unit x.
+    __host__ __device__ inline int wave_of(long long x, long long units, int waves)
+    {
+      long long w = x * waves / units;
+      while (w + 1 < waves && range_start(w + 1, units, waves) <= x)
+      {
+        ++w;
+      }
+      while (w > 0 && range_start(w, units, waves) > x)
+      {
+        --w;
+      }
+      return static_cast<int>(w);
+    }
+
+    // Splits of (layer li, KV head kvh): fixed, or the streaming waves that
+    // meet its pages; and the split a streaming wave writes for it.
+    __host__ __device__ inline int group_splits(const DecodeArgs &a, int li, int kvh)
+    {
+      if (a.stream_waves == 0)
+      {
+        return a.splits;
+      }
+      const long long base = (static_cast<long long>(li) * a.kv_heads + kvh) * a.pages;
+      return wave_of(base + a.pages - 1, a.stream_units, a.stream_waves) -
+             wave_of(base, a.stream_units, a.stream_waves) + 1;
+    }
+
+    // Issues the copies of unit `u` (address `page`, tier `tier`) into `slot`.
+    template <int HD>
+    __device__ inline void stream_copy(const DecodeArgs &a, const Unit &u, const std::uint8_t *page,
+                                       int tier, std::uint8_t *slot, int lane)
+    {
+      constexpr int S = HD / 32;
+      constexpr int kRun = HD / 4;
+      const int r = lane & 15, g = lane >> 4;
+      const std::size_t W = static_cast<std::size_t>(a.kv_heads) * HD;
+      const std::size_t run0 = static_cast<std::size_t>(u.kvh) * HD + g * kRun;
+      const auto quantised = [&](auto bits_tag) {
+        constexpr int Bits = decltype(bits_tag)::value;
+        using SL = SlotLayout<HD, Bits>;
+        const PageLayout &L = a.lay[Bits == 8 ? kINT8 : Bits == 4 ? kINT4 : kINT2];
+        // One buffer over the page (reads past it return zeros); each lane's
+        // row offset once, the regions and rows as scalar offsets, the steps
+        // as immediates.
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<std::uint8_t *>(page), 0, static_cast<int>(L.page_bytes), kBufferWord3);
+        const int lane_row = static_cast<int>((r * W + run0) * Bits / 8);
+        const int row16 = static_cast<int>(16 * W * Bits / 8);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) // keys, values
+        {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+          {
+            const int region =
+                static_cast<int>(half == 0 ? L.key_codes : L.value_codes) + kb * row16;
+#pragma unroll
+            for (int i = 0; i < SL::kBlocksARow; ++i)
+            {
+              std::uint8_t *block = slot + ((half * 2 + kb) * SL::kBlocksARow + i) * SL::kBlock;
+              if constexpr (SL::kWide)
+              {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)block, 16, lane_row,
+                                                         region + 16 * i, 0, 0);
+              }
+              else
+              {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)block, 4, lane_row,
+                                                         region + 4 * i, 0, 0);
+              }
+            }
+          }
+        }
+        // Key scales and zeros of this KV head: HD halves each, 4 bytes a lane.
+        const int meta_off = 4 * (lane % (HD / 2));
+        const int kvh_meta = 2 * u.kvh * HD;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)(slot + SL::kKeyScales), 4, meta_off,
+                                                 static_cast<int>(L.key_scales) + kvh_meta, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)(slot + SL::kKeyZeros), 4, meta_off,
+                                                 static_cast<int>(L.key_zeros) + kvh_meta, 0, 0);
+        // Value scales then value zeros, all KV heads: 64 * kv bytes each,
+        // contiguous in the page (zeros follow scales).
+        const int words = 16 * a.kv_heads;
+        for (int b = 0; b < (2 * words + 63) / 64; ++b)
+        {
+          const int w = b * 64 + lane;
+          const int wc = w < 2 * words ? w : 2 * words - 1;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)(slot + SL::kValueMeta + 256 * b),
+                                                   4, 4 * wc, static_cast<int>(L.value_scales),
+                                                   0, 0);
+        }
+      };
+      if (tier != kOwnPage && tier >= kINT8 && tier <= kINT2)
+      {
+        switch (tier)
+        {
+        case kINT8:
+          quantised(std::integral_constant<int, 8>{});
+          break;
+        case kINT4:
+          quantised(std::integral_constant<int, 4>{});
+          break;
+        default:
+          quantised(std::integral_constant<int, 2>{});
+          break;
+        }
+        return;
+      }
+      if (tier != kOwnPage)
+      {
+        // FP16 rows: keys r, 16+r then values r, 16+r, the lane's run, a
+        // 16-byte step at a time, through one buffer over the page.
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<std::uint8_t *>(page), 0, static_cast<int>(4 * kPageTokens * W),
+            kBufferWord3);
+        const int lane_row = static_cast<int>((r * W + run0) * 2);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+          const int row = static_cast<int>(((j / 2) * kPageTokens + (j % 2) * 16) * W * 2);
+#pragma unroll
+          for (int st = 0; st < S; ++st)
+          {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)(slot + (j * S + st) * 1024), 16,
+                                                     lane_row, row + 16 * st, 0, 0);
+          }
+        }
+        return;
+      }
+      // The own page: rows before `start` from the open page, the rest from
+      // the chunk; rows past the last key read row 0.
+      const int layer = a.first_layer + u.li;
+      const auto *open = a.open_table != nullptr
+                             ? reinterpret_cast<const std::uint16_t *>(a.open_table[layer])
+                             : a.open;
+      const int last = a.seq_k - 1 - u.page * kPageTokens;
+      const int t_start = a.start - u.page * kPageTokens;
+      const std::uint16_t *ck = a.chunk_k + u.li * a.chunk_stride;
+      const std::uint16_t *cv = a.chunk_v + u.li * a.chunk_stride;
+      const std::uint16_t *rows[4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+      {
+        const int t = kb * 16 + r;
+        const int tt = t <= last ? t : 0;
+        if (tt < t_start)
+        {
+          rows[kb] = open + static_cast<std::size_t>(tt) * W + run0;
+          rows[2 + kb] = open + static_cast<std::size_t>(kPageTokens + tt) * W + run0;
+        }
+        else
+        {
+          rows[kb] = ck + static_cast<std::size_t>(tt - t_start) * W + run0;
+          rows[2 + kb] = cv + static_cast<std::size_t>(tt - t_start) * W + run0;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+      {
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+        {
+          dma16(rows[j] + 8 * st, slot + (j * S + st) * 1024);
+        }
+      }
+    }
+
+    // Reads a quantised unit's codes and value metadata from the slot.
+    template <int HD, int Bits>
+    __device__ inline void stream_read_quantised(QuantRaw<HD, Bits> &raw, const std::uint8_t *slot,
+                                                 int lane, int kvh, int kv_heads)
+    {
+      using SL = SlotLayout<HD, Bits>;
+      const int r = lane & 15;
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+      {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+        {
+          unsigned *dst = half == 0 ? raw.kc[kb] : raw.vc[kb];
+#pragma unroll
+          for (int i = 0; i < SL::kBlocksARow; ++i)
+          {
+            const std::uint8_t *block =
+                slot + ((half * 2 + kb) * SL::kBlocksARow + i) * SL::kBlock;
+            if constexpr (SL::kWide)
+            {
+              const u32x4 v = lds16(block, lane);
+              dst[4 * i + 0] = v.x;
+              dst[4 * i + 1] = v.y;
+              dst[4 * i + 2] = v.z;
+              dst[4 * i + 3] = v.w;
+            }
+            else
+            {
+              dst[i] = lds4(block, lane);
+            }
+          }
+        }
+      }
+      const auto *vmeta = reinterpret_cast<const std::uint16_t *>(slot + SL::kValueMeta);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+      {
+        const int grp = (kb * 16 + r) * kv_heads + kvh;
+        raw.vs[kb] = vmeta[grp];
+        raw.vz[kb] = vmeta[32 * kv_heads + grp];
+      }
+    }
+
+    // Writes a wave's running softmax as the partial of its group's split.
+    template <int HD>
+    __device__ inline void stream_flush(const DecodeArgs &a, const Running<HD> &run, int li, int kvh,
+                                        int split, int r, int g)
+    {
+      const int G = a.group;
+      if (r >= G)
+      {
+        return;
+      }
+      float *part = a.partials +
+                    (((static_cast<std::size_t>(li) * a.kv_heads + kvh) * a.splits + split) * G + r) * HD;
+      if (g == 0)
+      {
+        *reinterpret_cast<float2 *>(
+            a.split_ml +
+            (((static_cast<std::size_t>(li) * a.kv_heads + kvh) * G + r) * a.splits + split) * 2) =
+            make_float2(run.m, run.l);
+      }
+#pragma unroll
+      for (int s = 0; s < HD / 32; ++s)
+      {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+        {
+          *reinterpret_cast<f32x4 *>(part + out_channel<HD>(s, h, g, 0)) =
+              run.o[2 * s + h] * kPUnscale;
+        }
+      }
+    }
+
+    // A quantised unit from the slot: codes and value metadata to registers,
+    // the key scales and zeros to the wave's metadata area (out of the
+    // slot), then `next` (which reuses the slot), then the arithmetic.
+    template <int HD, int Bits, typename Next>
+    __device__ inline void stream_quantised(Running<HD> &run, const PageCtx &c, const half8 *qb,
+                                            const std::uint8_t *slot, std::uint8_t *meta,
+                                            int lane, int kvh, int kv_heads, const Next &next)
+    {
+      using SL = SlotLayout<HD, Bits>;
+      QuantRaw<HD, Bits> raw;
+      stream_read_quantised<HD, Bits>(raw, slot, lane, kvh, kv_heads);
+      const u32x2 km = *reinterpret_cast<const u32x2 *>(slot + SL::kKeyScales + 8 * lane);
+      *reinterpret_cast<u32x2 *>(meta + 8 * lane) = km;
+      next();
+      quantised_compute<HD, Bits>(run, c, qb, raw, reinterpret_cast<const unsigned *>(meta),
+                                  reinterpret_cast<const unsigned *>(meta + 256));
+    }
+
+    // Each wave takes an equal contiguous range of (layer, KV head, page)
+    // units (at most 64, and at most two groups) and walks it with one unit
+    // in flight: the next unit's bytes are copied into the wave's LDS slot by
+    // global_load_lds while the current one, already in registers, is
+    // computed. A wave writes one partial per group it touches.
+    template <int HD>
+    __global__ void __launch_bounds__(kThreads) decode_stream_kernel(DecodeArgs a)
+    {
+      constexpr int S = HD / 32;
+      constexpr int DB = HD / 16;
+      constexpr int kRun = HD / 4;
+      extern __shared__ float lds[];
+      const int lane = threadIdx.x & 63;
+      const int wave = threadIdx.x >> 6;
+      const int r = lane & 15;
+      const int g = lane >> 4;
+      const int G = a.group;
+      const int gw = blockIdx.x * kWaves + wave;
+      if (gw >= a.stream_waves)
+      {
+        return;
+      }
+      const long long u0 = range_start(gw, a.stream_units, a.stream_waves);
+      const long long u1 = range_start(gw + 1, a.stream_units, a.stream_waves);
+      const int n = static_cast<int>(u1 - u0);
+      if (n <= 0)
+      {
+        return;
+      }
+      std::uint8_t *slot = reinterpret_cast<std::uint8_t *>(lds) + wave * stream_slot_bytes<HD>();
+      std::uint8_t *meta =
+          reinterpret_cast<std::uint8_t *>(lds) + kWaves * stream_slot_bytes<HD>() + wave * 512;
+      const int own = a.causal ? (a.seq_k - 1) / kPageTokens : -1;
+
+      // Every unit's address and tier, a lane a unit, read once.
+      unsigned long long my_addr = 0;
+      int my_tier = kFP16;
+      if (lane < n)
+      {
+        const Unit u = unit_of(u0 + lane, a.kv_heads, a.pages);
+        const long long at = static_cast<long long>(a.first_layer + u.li) * a.table_stride + u.page;
+        if (a.causal)
+        {
+          my_tier = u.page < own ? static_cast<int>(a.tiers[at]) : kOwnPage;
+        }
+        if (my_tier != kUnreadPage && my_tier != kOwnPage)
+        {
+          my_addr = a.table[at];
+        }
+      }
+      const auto addr_of = [&](int i) {
+        return reinterpret_cast<const std::uint8_t *>(
+            (static_cast<unsigned long long>(__builtin_amdgcn_readlane(
+                 static_cast<unsigned>(my_addr >> 32), i))
+             << 32) |
+            static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<unsigned>(my_addr), i)));
+      };
+      const auto tier_of = [&](int i) { return __builtin_amdgcn_readlane(my_tier, i); };
+
+      Running<HD> run;
+      run.m = -INFINITY;
+      run.l = 0.0f;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+      {
+        run.o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      half8 qb[S];
+      int seg_group = -1;
+      bool first = true;
+
+      {
+        const int t = tier_of(0);
+        if (t != kUnreadPage)
+        {
+          stream_copy<HD>(a, unit_of(u0, a.kv_heads, a.pages), addr_of(0), t, slot, lane);
+        }
+      }
+      Unit u = unit_of(u0, a.kv_heads, a.pages);
+      for (int i = 0; i < n; ++i)
+      {
+        if (i > 0)
+        {
+          // The next unit: the next page, or the next group's first.
+          if (++u.page == a.pages)
+          {
+            u.page = 0;
+            if (++u.kvh == a.kv_heads)
+            {
+              u.kvh = 0;
+              ++u.li;
+            }
+          }
+        }
+        const int group = u.li * a.kv_heads + u.kvh;
+        if (group != seg_group)
+        {
+          seg_group = group;
+          first = true;
+          const std::uint16_t *q_row =
+              a.q + u.li * a.q_stride + static_cast<std::size_t>(u.kvh * G + (r < G ? r : 0)) * HD +
+              g * kRun;
+          load_fp16_run<HD>(qb, q_row);
+          if (r >= G)
+          {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+            {
+              qb[s] = as_half8(u32x4{0u, 0u, 0u, 0u});
+            }
+          }
+        }
+        const int tier = tier_of(i);
+        PageCtx c;
+        c.r = r;
+        c.g = g;
+        c.group = G;
+        c.last = a.seq_k - 1 - u.page * kPageTokens;
+        c.partial = c.last < kPageTokens - 1;
+        c.first = first;
+        c.scale = a.scale;
+        c.stat = a.page_stats +
+                 (((static_cast<std::size_t>(u.li) * a.kv_heads + u.kvh) * a.pages + u.page) * G + r) *
+                     2;
+        // The next unit's copies go out as soon as this one is out of LDS.
+        const auto next = [&]() {
+          wait_reads();
+          if (i + 1 < n)
+          {
+            const int t = tier_of(i + 1);
+            if (t != kUnreadPage)
+            {
+              Unit v = u;
+              if (++v.page == a.pages)
+              {
+                v.page = 0;
+                if (++v.kvh == a.kv_heads)
+                {
+                  v.kvh = 0;
+                  ++v.li;
+                }
+              }
+              stream_copy<HD>(a, v, addr_of(i + 1), t, slot, lane);
+            }
+          }
+        };
+        wait_copies();
+        switch (tier)
+        {
+        case kUnreadPage:
+          next();
+          if (g == 0 && r < G)
+          {
+            *reinterpret_cast<float2 *>(c.stat) = make_float2(-INFINITY, 0.0f);
+          }
+          break;
+        case kINT8:
+          stream_quantised<HD, 8>(run, c, qb, slot, meta, lane, u.kvh, a.kv_heads, next);
+          first = false;
+          break;
+        case kINT4:
+          stream_quantised<HD, 4>(run, c, qb, slot, meta, lane, u.kvh, a.kv_heads, next);
+          first = false;
+          break;
+        case kINT2:
+          stream_quantised<HD, 2>(run, c, qb, slot, meta, lane, u.kvh, a.kv_heads, next);
+          first = false;
+          break;
+        default:
+        {
+          half8 k[2][S], v[2][S];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+          {
+#pragma unroll
+            for (int st = 0; st < S; ++st)
+            {
+              const half8 x = as_half8(lds16(slot + (j * S + st) * 1024, lane));
+              if (j < 2)
+              {
+                k[j][st] = x;
+              }
+              else
+              {
+                v[j - 2][st] = x;
+              }
+            }
+          }
+          next();
+          f32x4 acc[2];
+          fp16_scores<HD>(acc, k, qb);
+          half8 p_hi, p_lo;
+          softmax_page<HD>(acc, c, run, p_hi, p_lo);
+          fp16_values<HD>(run, c, v, p_hi, p_lo);
+          first = false;
+          break;
+        }
+        }
+        // The group's last unit in this wave's range: its partial.
+        const bool group_ends = i + 1 == n || u.page + 1 == a.pages;
+        if (group_ends)
+        {
+          const long long base = static_cast<long long>(group) * a.pages;
+          const int split = gw - wave_of(base, a.stream_units, a.stream_waves);
+          if (first)
+          {
+            // Every unit of the segment was unread: an empty partial.
+            run.m = -INFINITY;
+            run.l = 0.0f;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+            {
+              run.o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+          }
+          stream_flush<HD>(a, run, u.li, u.kvh, split, r, g);
+          run.m = -INFINITY;
+          run.l = 0.0f;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+          {
+            run.o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          }
+        }
+      }
+    }
+
+    // LDS of decode_stream_kernel, bytes: a slot and a metadata area a wave.
+    template <int HD>
+    constexpr std::size_t stream_kernel_lds()
+    {
+      return static_cast<std::size_t>(kWaves) * (stream_slot_bytes<HD>() + 512);
+    }
+
     constexpr int kCombineThreads = 256;
-    constexpr int kCombineDims = 32;
-    constexpr int kSplitLanes = kCombineThreads / kCombineDims; // 8
-    constexpr int kLoadsAhead = 16; // split rows a thread loads before using any
-    constexpr int kHeadsAPass = 16;
+    constexpr int kQuads = 16;                                // 4-channel quads a block
+    constexpr int kSplitRows = kCombineThreads / kQuads;      // splits read side by side
+    constexpr int kSplitsAhead = 8;                           // a thread's loads before any use
 
     // Folds (m, l) into a running (max, sum), both softmax partials in base 2.
     __device__ inline void fold_partial(float &top, float &sum, float m, float l)
@@ -1314,200 +1439,241 @@ namespace mi
       return v;
     }
 
-    // Blocks x < heads * HD/32: one head's 32 output channels; 32 threads
-    // read a split's 32 channels (coalesced), 8 splits at a time, each thread
-    // issuing the loads of its next 16 splits before it uses any, since the
-    // partials come from other XCDs' writes, a far round trip away. Blocks
-    // past that: 256 pages' masses and the layer's scores
+    // The same over the whole wave, as a uniform value: the four rows'
+    // results read out of lanes 0, 16, 32 and 48 (no LDS round trip).
+    __device__ inline float lane_value(float v, int lane)
+    {
+      return __builtin_bit_cast(float,
+                                __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+    }
+    __device__ inline float wave_max(float v)
+    {
+      v = row16_max(v);
+      return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)),
+                   fmaxf(lane_value(v, 32), lane_value(v, 48)));
+    }
+    __device__ inline float wave_sum(float v)
+    {
+      v = row16_sum(v);
+      return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+    }
+
+    // Blocks x < heads * HD/64: 64 output channels of one head. A split's
+    // 64 channels are 16 threads' float4 loads (coalesced), 16 splits side
+    // by side, and every thread issues the loads of its next 8 splits before
+    // it uses any: the partials come from other XCDs' writes, a far round
+    // trip away, so the block's whole read is one trip. Indices past the
+    // last split are clamped to it and weighted zero, so no load is
+    // conditional. Blocks past that: 256 pages' masses and the layer's scores
     // (importance_scores.cu:31-50: heads summed in order, every operation
     // rounded once). blockIdx.y is the launch's layer.
-    template <int HD>
+    template <int HD, bool Streamed>
     __global__ void __launch_bounds__(kCombineThreads) decode_combine_kernel(DecodeArgs a)
     {
-      __shared__ float s_red[kCombineThreads / 64];
-      __shared__ float s_acc[kSplitLanes][kCombineDims + 1];
-      __shared__ float s_l[kSplitLanes];
-      __shared__ float s_top[kMaxHeads];
-      __shared__ float s_sum[kMaxHeads];
+      // Fixed splits unless the streaming kernel wrote the partials: the
+      // per-layer form carries none of the streaming geometry's code.
+      const auto splits_of = [&](int li, int kvh) {
+        return Streamed ? group_splits(a, li, kvh) : a.splits;
+      };
+      constexpr int kBlocksAHead = HD / (4 * kQuads);
+      __shared__ f32x4 s_o[kSplitRows][kQuads];
+      __shared__ float s_m[kSplitRows];
+      __shared__ float s_l[kSplitRows];
+      __shared__ float s_share[kMaxHeads][64];
       const int G = a.group;
       const int li = blockIdx.y;
       const int t = threadIdx.x;
-      const int splits = a.splits;
-      const auto slot = [&](int h, int s) {
+      // Head h's split outputs (split s at s * split_stride) and its splits'
+      // (max, sum) pairs, side by side.
+      const auto head_out = [&](int h) {
         return a.partials +
-               (((static_cast<std::size_t>(li) * a.kv_heads + h / G) * splits + s) * G + h % G) *
-                   (kSlotHead + HD);
+               ((static_cast<std::size_t>(li) * a.kv_heads + h / G) * a.splits * G + h % G) * HD;
       };
-      constexpr int kChunks = HD / kCombineDims;
-      if (static_cast<int>(blockIdx.x) < a.heads * kChunks)
+      const auto head_ml = [&](int h) {
+        return reinterpret_cast<const float2 *>(a.split_ml) +
+               (static_cast<std::size_t>(li) * a.heads + h) * a.splits;
+      };
+      const std::size_t split_stride = static_cast<std::size_t>(G) * HD;
+      if (static_cast<int>(blockIdx.x) < a.heads * kBlocksAHead)
       {
-        const int h = blockIdx.x / kChunks;
-        const int d0 = (blockIdx.x % kChunks) * kCombineDims;
-        const int c = t % kCombineDims;
-        const int j = t / kCombineDims;
-        // This thread's running max, output channel and sum over its splits.
-        float top = -INFINITY, acc = 0.0f, l = 0.0f;
-        for (int s0 = j; s0 < splits; s0 += kSplitLanes * kLoadsAhead)
-        {
-          float mv[kLoadsAhead], lv[kLoadsAhead], ov[kLoadsAhead];
+        const int h = blockIdx.x / kBlocksAHead;
+        const int c0 = (blockIdx.x % kBlocksAHead) * 4 * kQuads;
+        const int quad = t % kQuads;
+        const int row = t / kQuads;
+        const int splits = splits_of(li, h / G);
+        const float *base = head_out(h);
+        const float2 *mls = head_ml(h);
+        float top = -INFINITY, l = 0.0f;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        const auto fold_from = [&](int s0) {
+          float mv[kSplitsAhead], lv[kSplitsAhead];
+          f32x4 ov[kSplitsAhead];
 #pragma unroll
-          for (int i = 0; i < kLoadsAhead; ++i)
+          for (int i = 0; i < kSplitsAhead; ++i)
           {
-            const int s = s0 + i * kSplitLanes;
-            mv[i] = -INFINITY;
-            lv[i] = 0.0f;
-            ov[i] = 0.0f;
-            if (s < splits)
-            {
-              const float *p = slot(h, s);
-              mv[i] = p[0];
-              lv[i] = p[1];
-              ov[i] = p[kSlotHead + d0 + c];
-            }
+            const int s = min(s0 + i * kSplitRows, splits - 1);
+            const float2 ml = mls[s];
+            mv[i] = ml.x;
+            lv[i] = ml.y;
+            ov[i] = *reinterpret_cast<const f32x4 *>(base + s * split_stride + c0 + 4 * quad);
           }
           float next = top;
 #pragma unroll
-          for (int i = 0; i < kLoadsAhead; ++i)
+          for (int i = 0; i < kSplitsAhead; ++i)
           {
-            next = fmaxf(next, mv[i]);
+            if (s0 + i * kSplitRows < splits)
+            {
+              next = fmaxf(next, mv[i]);
+            }
           }
           const float from = next == -INFINITY ? 0.0f : next;
           const float keep = exp2_fast(top - from);
           acc *= keep;
           l *= keep;
 #pragma unroll
-          for (int i = 0; i < kLoadsAhead; ++i)
+          for (int i = 0; i < kSplitsAhead; ++i)
           {
-            const float w = exp2_fast(mv[i] - from);
+            const float w = s0 + i * kSplitRows < splits ? exp2_fast(mv[i] - from) : 0.0f;
             acc += ov[i] * w;
             l += lv[i] * w;
           }
           top = next;
-        }
-        // Across the block: the common max, then every thread's share at it.
-        const float all = block_reduce<true>(top, s_red);
-        const float from = all == -INFINITY ? 0.0f : all;
-        const float keep = exp2_fast(top - from);
-        s_acc[j][c] = acc * keep;
-        if (c == 0)
+        };
+        // The first kSplitRows * kSplitsAhead splits outside the loop, so
+        // that their loads are not held behind a loop head's wait.
+        fold_from(row);
+        for (int s0 = row + kSplitRows * kSplitsAhead; s0 < splits;
+             s0 += kSplitRows * kSplitsAhead)
         {
-          s_l[j] = l * keep;
+          fold_from(s0);
+        }
+        // The rows into one: every row's share at the rows' common max.
+        s_o[row][quad] = acc;
+        if (quad == 0)
+        {
+          s_m[row] = top;
+          s_l[row] = l;
         }
         __syncthreads();
-        if (t < kCombineDims)
+        if (t < kQuads)
         {
-          float sum = 0.0f, total = 0.0f;
+          float all = -INFINITY;
 #pragma unroll
-          for (int u = 0; u < kSplitLanes; ++u)
+          for (int u = 0; u < kSplitRows; ++u)
           {
-            sum += s_acc[u][t];
-            total += s_l[u];
+            all = fmaxf(all, s_m[u]);
           }
-          a.out[li * a.out_stride + static_cast<std::size_t>(h) * HD + d0 + t] =
-              __half_as_ushort(__float2half(sum / total));
+          const float from = all == -INFINITY ? 0.0f : all;
+          f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+          float total = 0.0f;
+#pragma unroll
+          for (int u = 0; u < kSplitRows; ++u)
+          {
+            const float w = exp2_fast(s_m[u] - from);
+            sum += s_o[u][t] * w;
+            total += s_l[u] * w;
+          }
+          unsigned short hv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+          {
+            hv[i] = __half_as_ushort(__float2half(sum[i] / total));
+          }
+          std::uint16_t *dst =
+              a.out + li * a.out_stride + static_cast<std::size_t>(h) * HD + c0 + 4 * t;
+          if (reinterpret_cast<std::uintptr_t>(dst) % 8 == 0)
+          {
+            *reinterpret_cast<u32x2 *>(dst) = u32x2{hv[0] | (static_cast<unsigned>(hv[1]) << 16),
+                                                    hv[2] | (static_cast<unsigned>(hv[3]) << 16)};
+          }
+          else
+          {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+              dst[i] = hv[i];
+            }
+          }
         }
         return;
       }
-      // This block's page: its (max, sum) of the first kHeadsAPass heads and
-      // its old score are loaded now, while the head totals are formed.
-      const int page = (blockIdx.x - a.heads * kChunks) * kCombineThreads + t;
+      // A mass block: 64 pages, a wave a head at a time (heads w, w + 4, ...):
+      // the wave requests its heads' split pairs (one coalesced 512-byte read
+      // each) and the pages' (max, sum) together, forms each head's total,
+      // and leaves each page's share in LDS; then wave 0 sums a page's shares
+      // in head order and folds the score.
+      const int lane = t & 63;
+      const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+      constexpr int kWavesC = kCombineThreads / 64;
+      constexpr int kHeadsAWave = kMaxHeads / kWavesC;
+      const int page = (blockIdx.x - a.heads * kBlocksAHead) * 64 + lane;
       const bool has_page = page < a.pages;
+      const int pg = has_page ? page : a.pages - 1; // clamped: loads, never stores
       const float *stats = a.page_stats + static_cast<std::size_t>(li) * a.heads * a.pages * 2;
       float *scores = a.scores != nullptr ? a.scores + li * a.scores_stride : nullptr;
-      const float old = has_page && scores != nullptr ? scores[page] : 0.0f;
-      float2 st0[kHeadsAPass];
+      float *mass = a.mass != nullptr ? a.mass + li * a.mass_stride : nullptr;
+      const float old = scores != nullptr && wave == 0 ? scores[pg] : 0.0f;
+      for (int j0 = 0; j0 < kHeadsAWave && wave + kWavesC * j0 < a.heads; j0 += 4)
+      {
+        float2 st[4], ml[4][2];
+        int splits[4];
 #pragma unroll
-      for (int i = 0; i < kHeadsAPass; ++i)
-      {
-        if (has_page && i < a.heads)
+        for (int j = 0; j < 4; ++j)
         {
-          st0[i] = *reinterpret_cast<const float2 *>(
-              stats + (static_cast<std::size_t>(i) * a.pages + page) * 2);
-        }
-      }
-      // Every head's whole max and sum: a 16-lane row a head, each lane
-      // folding every 16th split (its loads issued ahead), then the row
-      // reduced with DPP moves.
-      const int q = t & 15;
-      for (int h0 = 0; h0 < a.heads; h0 += kCombineThreads / 16)
-      {
-        const int h = h0 + t / 16;
-        float top = -INFINITY, sum = 0.0f;
-        if (h < a.heads)
-        {
-          for (int s0 = q; s0 < splits; s0 += 16 * kLoadsAhead)
+          const int h = min(wave + kWavesC * (j0 + j), a.heads - 1);
+          splits[j] = splits_of(li, h / G);
+          st[j] = *reinterpret_cast<const float2 *>(
+              stats + ((static_cast<std::size_t>(h / G) * a.pages + pg) * G + h % G) * 2);
+          const float2 *mls = head_ml(h);
+#pragma unroll
+          for (int k = 0; k < 2; ++k)
           {
-            float mv[kLoadsAhead], lv[kLoadsAhead];
-#pragma unroll
-            for (int i = 0; i < kLoadsAhead; ++i)
-            {
-              const int s = s0 + 16 * i;
-              mv[i] = -INFINITY;
-              lv[i] = 0.0f;
-              if (s < splits)
-              {
-                const float2 ml = *reinterpret_cast<const float2 *>(slot(h, s));
-                mv[i] = ml.x;
-                lv[i] = ml.y;
-              }
-            }
-#pragma unroll
-            for (int i = 0; i < kLoadsAhead; ++i)
-            {
-              fold_partial(top, sum, mv[i], lv[i]);
-            }
+            ml[j][k] = mls[min(lane + 64 * k, splits[j] - 1)];
           }
         }
-        const float all = row16_max(top);
-        const float from = all == -INFINITY ? 0.0f : all;
-        const float total = row16_sum(sum * exp2_fast(top - from));
-        if (q == 0 && h < a.heads)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
         {
-          s_top[h] = from;
-          s_sum[h] = total;
+          const int h = wave + kWavesC * (j0 + j);
+          if (h >= a.heads)
+          {
+            break;
+          }
+          float top = -INFINITY, sum = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 2; ++k)
+          {
+            if (lane + 64 * k < splits[j])
+            {
+              fold_partial(top, sum, ml[j][k].x, ml[j][k].y);
+            }
+          }
+          // More than 128 splits only when several layers share a launch.
+          const float2 *mls = head_ml(h);
+          for (int sp = lane + 128; sp < splits[j]; sp += 64)
+          {
+            const float2 v = mls[sp];
+            fold_partial(top, sum, v.x, v.y);
+          }
+          const float all = wave_max(top);
+          const float from = all == -INFINITY ? 0.0f : all;
+          const float whole = wave_sum(sum * exp2_fast(top - from));
+          const float share = st[j].y * exp2_fast(st[j].x - from) / whole;
+          s_share[h][lane] = share;
+          if (mass != nullptr && has_page)
+          {
+            mass[static_cast<std::size_t>(h) * a.pages + page] = share;
+          }
         }
       }
       __syncthreads();
-      if (!has_page)
+      if (wave == 0 && has_page && scores != nullptr)
       {
-        return;
-      }
-      float *mass = a.mass != nullptr ? a.mass + li * a.mass_stride : nullptr;
-      float total = 0.0f;
-      for (int h0 = 0; h0 < a.heads; h0 += kHeadsAPass)
-      {
-        // The page's (max, sum) of kHeadsAPass heads, loaded together.
-        float2 st[kHeadsAPass];
-#pragma unroll
-        for (int i = 0; i < kHeadsAPass; ++i)
+        float total = 0.0f;
+        for (int h = 0; h < a.heads; ++h)
         {
-          if (h0 == 0)
-          {
-            st[i] = st0[i];
-          }
-          else if (h0 + i < a.heads)
-          {
-            st[i] = *reinterpret_cast<const float2 *>(
-                stats + (static_cast<std::size_t>(h0 + i) * a.pages + page) * 2);
-          }
+          total = __fadd_rn(total, s_share[h][lane]);
         }
-#pragma unroll
-        for (int i = 0; i < kHeadsAPass; ++i)
-        {
-          const int h = h0 + i;
-          if (h < a.heads)
-          {
-            const float share = st[i].y * exp2_fast(st[i].x - s_top[h]) / s_sum[h];
-            if (mass != nullptr)
-            {
-              mass[static_cast<std::size_t>(h) * a.pages + page] = share;
-            }
-            total = __fadd_rn(total, share);
-          }
-        }
-      }
-      if (scores != nullptr)
-      {
         const float observed = __fdiv_rn(total, static_cast<float>(a.heads));
         scores[page] = isnan(old) ? observed
                                   : __fadd_rn(__fmul_rn(a.alpha, observed),
@@ -1545,14 +1711,8 @@ namespace mi
   {
     if (a.seq_q != 1 || a.k_bias != nullptr || kv.layout == Layout::kContiguous ||
         kv.page_tokens != kPageTokens || (a.head_dim != 64 && a.head_dim != 128) ||
-        a.kv_heads <= 0 || a.kv_heads > kMaxKvHeads || a.heads % a.kv_heads != 0 ||
-        a.heads / a.kv_heads > kMaxGroup || a.heads > kMaxHeads || a.seq_k <= 0)
-    {
-      return false;
-    }
-    // A wave's pack is 128 channels: one KV head at head_dim 128; two at 64,
-    // whose query heads must then fit the MFMA's 16 columns together.
-    if (a.head_dim == 64 && (a.kv_heads % 2 != 0 || 2 * (a.heads / a.kv_heads) > kMaxGroup))
+        a.kv_heads <= 0 || a.heads % a.kv_heads != 0 || a.heads / a.kv_heads > kMaxGroup ||
+        a.heads > kMaxHeads || a.seq_k <= 0)
     {
       return false;
     }
@@ -1567,14 +1727,14 @@ namespace mi
       if (kv.layout == Layout::kCausal && kv.may_be_at[t])
       {
         const PageLayout L = page_layout(t, kPageTokens, a.kv_heads, a.head_dim);
-        if ((L.key_scales | L.key_zeros | L.value_codes | L.value_scales | L.page_bytes) % 16 != 0)
+        if ((L.key_scales | L.key_zeros | L.value_codes | L.page_bytes) % 16 != 0)
         {
           return false;
         }
       }
     }
     const int pages = (a.seq_k + kPageTokens - 1) / kPageTokens;
-    return pages <= 65535 * kWaves;
+    return (pages + kWaves - 1) / kWaves <= 65535;
   }
 
   void launch_decode_layers(const KVSource &kv, const AttentionArgs &a, const DecodeLayers &ls,
@@ -1621,47 +1781,90 @@ namespace mi
     d.pages = pages;
     // Scores in base-2 units: the softmax weights are exp2 of them.
     d.scale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(a.head_dim)));
-    // A pack is 128 channels of a row: one KV head at head_dim 128, two at 64.
-    const int cus = device_multiprocessors();
-    const int wave_pages = (pages + kWaves - 1) / kWaves; // workgroups a group could have
-    const int np = 128 / a.head_dim;
-    const int packs = a.kv_heads / np;
-    const long long groups = static_cast<long long>(ls.layers) * packs;
-    if (!ls.split)
+    // One layer: a page a wave, so a launch has a wave for every page of
+    // every KV head (or, unsplit, one workgroup a KV head). Several layers:
+    // the streaming kernel, equal ranges of units a wave.
+    const bool streaming = ls.split && ls.layers > 1;
+    int stream_blocks = 0;
+    if (streaming)
     {
-      d.splits = 1; // no partials given: one workgroup a (layer, pack)
+      const long long units = static_cast<long long>(ls.layers) * a.kv_heads * pages;
+      const int per_cu = 1; // 2 waves a SIMD (registers); LDS holds a slot a wave
+      long long waves = static_cast<long long>(device_multiprocessors()) * per_cu * kWaves;
+      waves = std::max(waves, (units + 63) / 64); // at most 64 units a wave
+      waves = std::min(waves, units);             // no wave without a unit
+      d.stream_units = units;
+      d.stream_waves = static_cast<int>(waves);
+      stream_blocks = static_cast<int>((waves + kWaves - 1) / kWaves);
+      d.pages_per_wave = 0;
+      d.splits = 1;
+      for (int li = 0; li < ls.layers; ++li)
+      {
+        for (int kvh = 0; kvh < a.kv_heads; ++kvh)
+        {
+          d.splits = std::max(d.splits, group_splits(d, li, kvh));
+        }
+      }
+    }
+    else if (ls.split)
+    {
+      d.pages_per_wave = 1;
+      d.splits = (pages + kWaves - 1) / kWaves;
     }
     else
     {
-      // Workgroups a group: the compute units shared out, at most a page a wave.
-      const long long share = std::max<long long>(1, cus / groups);
-      d.splits = static_cast<int>(std::min<long long>(share, wave_pages));
+      d.pages_per_wave = (pages + kWaves - 1) / kWaves;
+      d.splits = 1;
     }
-    const std::size_t part = static_cast<std::size_t>(ls.layers) * a.kv_heads * d.splits * group *
-                             (kSlotHead + a.head_dim);
+    const std::size_t part =
+        static_cast<std::size_t>(ls.layers) * a.kv_heads * d.splits * group * a.head_dim;
+    const std::size_t ml = static_cast<std::size_t>(ls.layers) * a.kv_heads * group * d.splits * 2;
     const std::size_t stats = static_cast<std::size_t>(ls.layers) * a.heads * pages * 2;
-    float *ws = decode_workspace(part + stats);
+    float *ws = decode_workspace(part + ml + stats);
     d.partials = ws;
-    d.page_stats = ws + part;
-    const int mass_blocks = (a.mass != nullptr || a.scores != nullptr)
-                                ? (pages + kCombineThreads - 1) / kCombineThreads
-                                : 0;
-    const auto run = [&](auto pages_kernel, auto combine_kernel, int hd) {
-      hipLaunchKernelGGL(pages_kernel, dim3(d.splits, packs, ls.layers), dim3(kThreads), 0,
-                         stream, d);
-      hip_check(hipGetLastError(), "decode pages kernel launch");
-      hipLaunchKernelGGL(combine_kernel,
-                         dim3(a.heads * (hd / kCombineDims) + mass_blocks, ls.layers),
+    d.split_ml = ws + part;
+    d.page_stats = ws + part + ml;
+    const int mass_blocks = (a.mass != nullptr || a.scores != nullptr) ? (pages + 63) / 64 : 0;
+    const auto run = [&](auto pages_kernel, auto stream_kernel, auto combine_kernel,
+                         auto combine_streamed, int hd, std::size_t stream_lds) {
+      if (stream_blocks > 0)
+      {
+        hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(stream_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(stream_lds)),
+                  "hipFuncSetAttribute decode stream LDS");
+        hipLaunchKernelGGL(stream_kernel, dim3(stream_blocks), dim3(kThreads), stream_lds, stream,
+                           d);
+        hip_check(hipGetLastError(), "decode stream kernel launch");
+      }
+      else
+      {
+        const std::size_t lds = pages_kernel_lds(group, hd);
+        if (lds > 64 * 1024)
+        {
+          hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(pages_kernel),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds)),
+                    "hipFuncSetAttribute decode LDS");
+        }
+        hipLaunchKernelGGL(pages_kernel, dim3(d.splits, a.kv_heads, ls.layers), dim3(kThreads),
+                           lds, stream, d);
+        hip_check(hipGetLastError(), "decode pages kernel launch");
+      }
+      hipLaunchKernelGGL(stream_blocks > 0 ? combine_streamed : combine_kernel,
+                         dim3(a.heads * (hd / (4 * kQuads)) + mass_blocks, ls.layers),
                          dim3(kCombineThreads), 0, stream, d);
       hip_check(hipGetLastError(), "decode combine kernel launch");
     };
     if (a.head_dim == 128)
     {
-      run(decode_pages_kernel<128, 1>, decode_combine_kernel<128>, 128);
+      run(decode_pages_kernel<128>, decode_stream_kernel<128>, decode_combine_kernel<128, false>,
+          decode_combine_kernel<128, true>, 128, stream_kernel_lds<128>());
     }
     else
     {
-      run(decode_pages_kernel<64, 2>, decode_combine_kernel<64>, 64);
+      run(decode_pages_kernel<64>, decode_stream_kernel<64>, decode_combine_kernel<64, false>,
+          decode_combine_kernel<64, true>, 64, stream_kernel_lds<64>());
     }
   }
 
