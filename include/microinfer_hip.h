@@ -243,6 +243,11 @@ int mi_cache_mapped_bytes(mi_cache *cache, int tier, size_t *out);
 int mi_cache_keep_spare_granules(mi_cache *cache, int tier, size_t granules);
 int mi_cache_spare_granules(mi_cache *cache, int tier, size_t *out);
 int mi_cache_granule_bytes(mi_cache *cache, size_t *out);
+/* Granules a range gives up are unmapped and released by a thread of the
+ * cache's own, after the call that gave them up has returned (the reference
+ * releases them inside that call, paged_kv_cache.cu). This waits until every
+ * one is back with the driver. No counterpart in the reference. */
+int mi_cache_drain_releases(mi_cache *cache);
 /* Test hook (no counterpart in the reference; the reference forces the
  * same paths by exhausting VRAM): the next n granule maps fail as out of
  * memory. */

@@ -136,9 +136,101 @@ namespace mi
 
   PagedKVCache::~PagedKVCache() { release_everything(); }
 
+  void PagedKVCache::retire(char *at, hipMemGenericAllocationHandle_t handle)
+  {
+    {
+      std::lock_guard<std::mutex> lock(release_mutex_);
+      retired_.push_back(Retired{at, handle});
+    }
+    if (!releaser_.joinable())
+    {
+      releaser_ = std::thread([this] { release_loop(); });
+    }
+    release_wake_.notify_one();
+  }
+
+  void PagedKVCache::release_loop()
+  {
+    const hipError_t set = hipSetDevice(device_);
+    std::unique_lock<std::mutex> lock(release_mutex_);
+    for (;;)
+    {
+      release_wake_.wait(lock, [this] { return release_stop_ || !retired_.empty(); });
+      if (retired_.empty())
+      {
+        return; // stopping, and nothing left
+      }
+      const Retired g = retired_.front();
+      releasing_ = g.at;
+      retired_.pop_front();
+      lock.unlock();
+      hipError_t e = set;
+      if (e == hipSuccess)
+      {
+        e = hipMemUnmap(g.at, granule_);
+      }
+      const hipError_t released = hipMemRelease(g.handle);
+      if (e == hipSuccess)
+      {
+        e = released;
+      }
+      lock.lock();
+      releasing_ = nullptr;
+      if (e != hipSuccess && release_error_.empty())
+      {
+        release_error_ = std::string("releasing a granule: ") + hipGetErrorString(e);
+      }
+      release_done_.notify_all();
+    }
+  }
+
+  // Waits until the granule at `at` (or, for nullptr, every granule) given
+  // up earlier is back with the driver, so that its address can be mapped
+  // again; raises a failure of the release thread.
+  void PagedKVCache::wait_for_release(const char *at)
+  {
+    std::unique_lock<std::mutex> lock(release_mutex_);
+    const auto pending = [&] {
+      if (at == nullptr)
+      {
+        return !retired_.empty() || releasing_ != nullptr;
+      }
+      if (releasing_ == at)
+      {
+        return true;
+      }
+      for (const Retired &g : retired_)
+      {
+        if (g.at == at)
+        {
+          return true;
+        }
+      }
+      return false;
+    };
+    release_done_.wait(lock, [&] { return !pending(); });
+    if (!release_error_.empty())
+    {
+      const std::string error = release_error_;
+      release_error_.clear();
+      throw DeviceError(error);
+    }
+  }
+
+  void PagedKVCache::drain_releases() { wait_for_release(nullptr); }
+
   void PagedKVCache::release_everything() noexcept
   {
     (void)hipDeviceSynchronize();
+    if (releaser_.joinable())
+    {
+      {
+        std::lock_guard<std::mutex> lock(release_mutex_);
+        release_stop_ = true;
+      }
+      release_wake_.notify_one();
+      releaser_.join();
+    }
     for (Range &r : ranges_)
     {
       while (!r.granules.empty())
@@ -413,8 +505,18 @@ namespace mi
       throw OutOfMemory("hipMemCreate: out of memory (injected by the test hook)");
     }
     char *at = r.base + r.granules.size() * granule_;
+    // The address may be one a release still holds.
+    wait_for_release(at);
     hipMemGenericAllocationHandle_t handle;
-    hip_check(hipMemCreate(&handle, granule_, &prop_, 0), "hipMemCreate");
+    hipError_t created = hipMemCreate(&handle, granule_, &prop_, 0);
+    if (created == hipErrorOutOfMemory || created == hipErrorMemoryAllocation)
+    {
+      // Memory the release thread has yet to give back may be what is short.
+      (void)hipGetLastError();
+      drain_releases();
+      created = hipMemCreate(&handle, granule_, &prop_, 0);
+    }
+    hip_check(created, "hipMemCreate");
     const hipError_t mapped = hipMemMap(at, granule_, 0, handle, 0);
     if (mapped != hipSuccess)
     {
@@ -456,8 +558,7 @@ namespace mi
     while (r.granules.size() > kept)
     {
       const std::size_t last = r.granules.size() - 1;
-      hip_check(hipMemUnmap(r.base + last * granule_, granule_), "hipMemUnmap");
-      hip_check(hipMemRelease(r.granules.back()), "hipMemRelease");
+      retire(r.base + last * granule_, r.granules.back());
       r.granules.pop_back();
     }
   }

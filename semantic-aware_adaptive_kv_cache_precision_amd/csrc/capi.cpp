@@ -849,6 +849,11 @@ int mi_cache_granule_bytes(mi_cache *c, size_t *out)
   return guarded([&] { *out = c->impl.granule(); });
 }
 
+int mi_cache_drain_releases(mi_cache *c)
+{
+  return guarded([&] { c->impl.drain_releases(); });
+}
+
 int mi_debug_fail_next_granules(int n)
 {
   return guarded([&] { mi::fail_next_granules(n); });

@@ -12,10 +12,14 @@
 #include "kernels.hpp"
 
 #include <array>
+#include <condition_variable>
+#include <deque>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <optional>
 #include <set>
+#include <thread>
 #include <utility>
 #include <vector>
 
@@ -97,6 +101,8 @@ namespace mi
     std::size_t spare_granules(int tier) const { return ranges_.at(tier).spare; }
     std::size_t granule() const { return granule_; }
     std::uint64_t generation() const { return generation_; }
+    // Waits until every granule given up so far is back with the driver.
+    void drain_releases();
     // Valid until the next allocator operation: for the cache's own launches.
     char *address(PageKey key, std::size_t bytes) const;
 
@@ -111,11 +117,22 @@ namespace mi
       std::vector<hipMemGenericAllocationHandle_t> granules;
       std::size_t spare = 0;
     };
+    // A granule given up by a range: unmapped and released by the release
+    // thread, off the caller's path (each unmap costs the driver a fraction
+    // of a millisecond, and a batch can give up hundreds).
+    struct Retired
+    {
+      char *at;
+      hipMemGenericAllocationHandle_t handle;
+    };
     static void check_tier(int tier);
     void fit_granules(Range &r, bool map_spares);
     void map_granule(Range &r);
     void roll_back(Range &r);
     void release_everything() noexcept;
+    void retire(char *at, hipMemGenericAllocationHandle_t handle);
+    void wait_for_release(const char *at);
+    void release_loop();
 
     std::uint64_t generation_ = 0;
     int device_ = 0;
@@ -123,6 +140,14 @@ namespace mi
     std::size_t granule_ = 0;
     std::array<Range, kTierCount> ranges_;
     std::map<PageKey, PageLocation> table_;
+    std::mutex release_mutex_;
+    std::condition_variable release_wake_; // the release thread: work or stop
+    std::condition_variable release_done_; // waiters: a granule was released
+    std::deque<Retired> retired_;          // oldest first
+    const char *releasing_ = nullptr;      // the granule the thread is releasing
+    bool release_stop_ = false;
+    std::string release_error_;            // the first failure, raised to the next waiter
+    std::thread releaser_;
   };
 
   // FP16 shadows of downgraded pages in pinned host memory mapped for the

@@ -116,6 +116,7 @@ SIGNATURES = {
     "mi_cache_reserved_bytes": ((_vp, _i, _szp), C.c_int),
     "mi_cache_mapped_bytes": ((_vp, _i, _szp), C.c_int),
     "mi_cache_keep_spare_granules": ((_vp, _i, _sz), C.c_int),
+    "mi_cache_drain_releases": ((_vp,), C.c_int),
     "mi_cache_spare_granules": ((_vp, _i, _szp), C.c_int),
     "mi_cache_granule_bytes": ((_vp, _szp), C.c_int),
     "mi_debug_fail_next_granules": ((_i,), C.c_int),
@@ -869,6 +870,12 @@ class PagedKVCache:
 
     def spare_granules(self, tier) -> int:
         return self._get(lib.mi_cache_spare_granules, tier)
+
+    def drain_releases(self) -> None:
+        """Waits until every granule the ranges gave up is unmapped and back
+        with the driver (a thread of the cache's releases them after the call
+        that gave them up returns)."""
+        _check(lib.mi_cache_drain_releases(self._h))
 
     @property
     def granule_bytes(self) -> int:

@@ -117,6 +117,30 @@ def test_spare_granules_are_kept_mapped_beyond_the_tail():
     assert alloc.mapped_bytes(2) == 2 * granule
 
 
+def test_given_up_granules_are_mapped_again_once_released():
+    """Granules a range gives up go back to the driver on the cache's release
+    thread; mapping the same addresses again waits for them, and the pages
+    written there read back whole."""
+    m = mi()
+    granule = m.granule_bytes()
+    page = granule // 4
+    alloc = m.PagedKVCache([page] * 4, [64, 64, 64, 64])
+    rng = np.random.default_rng(7)
+    for round_ in range(3):
+        data = {}
+        for i in range(32):
+            alloc.allocate(round_, i, 1)
+            data[i] = rng.integers(0, 256, page, dtype=np.uint8)
+            alloc.write(round_, i, data[i])
+        assert alloc.mapped_bytes(1) == 8 * granule
+        for i in range(32):
+            assert np.array_equal(alloc.read(round_, i), data[i])
+        alloc.free_pages([(round_, i) for i in range(32)])
+        assert alloc.mapped_bytes(1) == 0
+    alloc.drain_releases()
+    assert alloc.mapped_bytes(1) == 0
+
+
 def test_footprint_at_32k_is_the_reference_measurement():
     """experiments/logs/benchmark.jsonl:48-51: a 28-layer Qwen2.5-1.5B cache
     reserved for 32K positions maps exactly the reference's measured bytes at
