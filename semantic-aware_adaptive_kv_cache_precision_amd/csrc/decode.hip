@@ -43,6 +43,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "lane_ops.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -298,8 +299,7 @@ namespace mi
       {
         m_page = fmaxf(m_page, sc[e]);
       }
-      m_page = fmaxf(m_page, __shfl_xor(m_page, 16));
-      m_page = fmaxf(m_page, __shfl_xor(m_page, 32));
+      m_page = lane_max32(lane_max16(m_page));
       const float m_from = m_page == -INFINITY ? 0.0f : m_page;
       float pv[8];
       float l_page = 0.0f;
@@ -309,8 +309,7 @@ namespace mi
         pv[e] = exp2_fast(sc[e] - m_from);
         l_page += pv[e];
       }
-      l_page += __shfl_xor(l_page, 16);
-      l_page += __shfl_xor(l_page, 32);
+      l_page = lane_sum32(lane_sum16(l_page));
       if (c.g == 0 && c.r < c.group)
       {
         *reinterpret_cast<float2 *>(c.stat) = make_float2(m_page, l_page);

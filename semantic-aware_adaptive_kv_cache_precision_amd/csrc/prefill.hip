@@ -45,6 +45,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "lane_ops.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -673,8 +674,7 @@ namespace mi
                 top = fmaxf(top, v);
               }
             }
-            top = fmaxf(top, __shfl_xor(top, 16));
-            top = fmaxf(top, __shfl_xor(top, 32));
+            top = lane_max32(lane_max16(top));
             const float m_new = fmaxf(m[tt], top);
             const float from = m_new == -INFINITY ? 0.0f : m_new;
             const float keep = exp2_fast(m[tt] - from);
@@ -733,8 +733,7 @@ namespace mi
       for (int tt = 0; tt < TPW; ++tt)
       {
         float total = l[tt];
-        total += __shfl_xor(total, 16);
-        total += __shfl_xor(total, 32);
+        total = lane_sum32(lane_sum16(total));
         if (pos[tt] < 0)
         {
           continue;
