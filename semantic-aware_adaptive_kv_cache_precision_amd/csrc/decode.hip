@@ -113,6 +113,13 @@ namespace mi
       // the waves whose ranges meet it. 0: fixed splits of pages_per_wave * 8.
       long long stream_units;
       int stream_waves;
+      // The next layer's page table, read ahead by the combine's last
+      // kWarmBlocks blocks (one an XCD): a byte of tier and 8 of address a
+      // page.
+      const unsigned long long *warm_table;
+      const std::uint8_t *warm_tiers;
+      int warm_count;
+      int mass_blocks;
       float *partials;   // [launch layer][kv_heads][splits][group][hd]: each split's output
       float *split_ml;   // [launch layer][kv_heads][group][splits][2]: each split's max and
                          // sum, a head's splits side by side so that they read coalesced
@@ -1393,6 +1400,7 @@ namespace mi
     }
 
     constexpr int kCombineThreads = 256;
+    constexpr int kWarmBlocks = 8; // one an XCD
     constexpr int kQuads = 16;                                // 4-channel quads a block
     constexpr int kSplitRows = kCombineThreads / kQuads;      // splits read side by side
     constexpr int kSplitsAhead = 8;                           // a thread's loads before any use
@@ -1593,6 +1601,22 @@ namespace mi
               dst[i] = hv[i];
             }
           }
+        }
+        return;
+      }
+      if (static_cast<int>(blockIdx.x) >= a.heads * kBlocksAHead + a.mass_blocks)
+      {
+        // A warm block: the next layer's tiers and page addresses through
+        // this XCD's caches (workgroups go to the XCDs in turn, so the
+        // kWarmBlocks consecutive blocks cover them all).
+        unsigned fold = 0;
+        for (int i = t; i < a.warm_count; i += kCombineThreads)
+        {
+          fold ^= a.warm_tiers[i] ^ static_cast<unsigned>(a.warm_table[i]);
+        }
+        if (fold == 0x9E3779B9u && a.warm_count < 0) // never: keeps the reads
+        {
+          a.scores[0] = 0.0f;
         }
         return;
       }
@@ -1824,6 +1848,11 @@ namespace mi
     d.split_ml = ws + part;
     d.page_stats = ws + part + ml;
     const int mass_blocks = (a.mass != nullptr || a.scores != nullptr) ? (pages + 63) / 64 : 0;
+    d.mass_blocks = mass_blocks;
+    const bool warm = kv.warm_pages != nullptr && ls.layers == 1;
+    d.warm_table = warm ? kv.warm_pages : nullptr;
+    d.warm_tiers = warm ? kv.warm_tiers : nullptr;
+    d.warm_count = warm ? kv.warm_count : 0;
     const auto run = [&](auto pages_kernel, auto stream_kernel, auto combine_kernel,
                          auto combine_streamed, int hd, std::size_t stream_lds) {
       if (stream_blocks > 0)
@@ -1851,7 +1880,8 @@ namespace mi
         hip_check(hipGetLastError(), "decode pages kernel launch");
       }
       hipLaunchKernelGGL(stream_blocks > 0 ? combine_streamed : combine_kernel,
-                         dim3(a.heads * (hd / (4 * kQuads)) + mass_blocks, ls.layers),
+                         dim3(a.heads * (hd / (4 * kQuads)) + mass_blocks + (warm ? kWarmBlocks : 0),
+                              ls.layers),
                          dim3(kCombineThreads), 0, stream, d);
       hip_check(hipGetLastError(), "decode combine kernel launch");
     };

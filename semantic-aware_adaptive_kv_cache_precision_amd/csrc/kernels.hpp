@@ -94,6 +94,13 @@ namespace mi
     int start;
     // Which tiers a page may be at: a layout is formed for each.
     bool may_be_at[kTierCount];
+    // Decode of one layer: the next layer's page table (its first warm_count
+    // entries), which the launch reads ahead once its own work is done, so
+    // that the next layer's first trip to memory finds it in cache. Null:
+    // none.
+    const unsigned long long *warm_pages;
+    const std::uint8_t *warm_tiers;
+    int warm_count;
   };
 
   struct AttentionArgs

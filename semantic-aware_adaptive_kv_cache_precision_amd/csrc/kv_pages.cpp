@@ -1080,6 +1080,14 @@ namespace mi
     {
       kv.may_be_at[t] = may_be_at_[t];
     }
+    if (seq_q == 1 && layer + 1 < layers_)
+    {
+      // A decode step visits the layers in order.
+      const LayerTable next = resolve(layer + 1);
+      kv.warm_pages = next.pages;
+      kv.warm_tiers = next.tiers;
+      kv.warm_count = (seq_k + page_tokens_ - 1) / page_tokens_;
+    }
     launch_attention(kv, a, runtime_stream());
   }
 
