@@ -113,6 +113,12 @@ namespace mi
       // the waves whose ranges meet it. 0: fixed splits of pages_per_wave * 8.
       long long stream_units;
       int stream_waves;
+      // The key bias (one layer's, kv_heads x hd fp16), the RoPE table
+      // ({cos, sin} per position and angle, fp32) and its first page's
+      // angles as fp16 high and low parts ([row][hi | lo][hd]); null: no bias.
+      const std::uint16_t *k_bias;
+      const float *rope;
+      const std::uint16_t *rope_angles;
       // The next layer's page table, read ahead by the combine's last
       // kWarmBlocks blocks (one an XCD): a byte of tier and 8 of address a
       // page.
@@ -272,6 +278,47 @@ namespace mi
       float *stat;  // this page's (max, sum) slot for head r
     };
 
+    // The key bias as a term of the scores. With k + RoPE(b, t) for the keys
+    // (attention.cu:104-116: channel j < hd/2 pairs with j' = j + hd/2),
+    // q.RoPE(b, t) = sum over angles j of A_j cos(w_j t) + B_j sin(w_j t),
+    // A_j = q_j b_j + q_j' b_j', B_j = q_j' b_j - q_j b_j'. For the rows
+    // t = t0 + u of a page, RoPE(b, t) = RoPE(RoPE(b, t0), u): with the bias
+    // turned to the page's first row, b(t0) = RoPE(b, t0), the term is
+    // [cos | sin](w u) against [A | B] of b(t0), the same for every page but
+    // for A and B. That product runs on the matrix cores in the q.K layout,
+    // both operands split into fp16 high and low parts (hi.hi + hi.lo + lo.hi)
+    // for fp32 accuracy, its left operand the 32 rows of [cos | sin](w u):
+    // 16 KB that a workgroup copies to its LDS once, where [cos | sin](w t) of
+    // every position would be as many bytes as the keys.
+    template <int HD>
+    struct KeyBias
+    {
+      float b, b2;               // lane i's bias b_i, b_i' (i = lane % (HD/2))
+      float2 turn;               // cos, sin of angle i at the page's first row
+      const std::uint16_t *rows; // the angle rows in LDS, kAngleRowPitch<HD> apart
+      float *lds;                // the wave's 2 HD floats of LDS
+      int lane;
+    };
+
+    // Halves between angle rows in LDS ([hi | lo], padded by 16 bytes so that
+    // the 16 rows one read asks for fall in different banks).
+    template <int HD>
+    constexpr int kAngleRowPitch = 2 * HD + 8;
+
+    // The workgroup's copy of the angle rows [u][hi | lo][HD] (u < 32).
+    template <int HD>
+    __device__ inline void copy_angle_rows(std::uint16_t *rows, const std::uint16_t *angles)
+    {
+      constexpr int kChunks = 32 * 2 * HD / 8; // 16 bytes each
+      constexpr int kRowChunks = 2 * HD / 8;
+      for (int k = threadIdx.x; k < kChunks; k += kThreads)
+      {
+        const u32x4 v = *((g_u32x4)(angles + 8 * k));
+        *reinterpret_cast<u32x4 *>(rows + (k / kRowChunks) * kAngleRowPitch<HD> +
+                                   8 * (k % kRowChunks)) = v;
+      }
+    }
+
     // Scores (base-2 units) from the two 16-key accumulators, masked past
     // the last key; the page's max and sum over the lane group, its stats,
     // and the running softmax merged; returns P (hi, lo) for P.V.
@@ -399,13 +446,87 @@ namespace mi
       unsigned vz[2];
     };
 
+    // Adds the key bias's term to a page's scores. The wave turns
+    // the bias to the page's first row through its LDS (lane i: angle i), as
+    // [b_j | b_j'] and [-b_j' | b_j], so that lane (g, r) forms A (g < 2) or
+    // B (g >= 2) of head r as q_j y_j + q_j' y_j' from the first or second
+    // copy, over its run of angles j = (g % 2) kRun + 8 s + e, with q_j and
+    // q_j' from lanes l and l ^ 32.
+    template <int HD>
+    __device__ inline void key_bias_scores(f32x4 (&acc)[2], const KeyBias<HD> &b,
+                                           const half8 *qb, int r, int g)
+    {
+      constexpr int S = HD / 32;
+      constexpr int kRun = HD / 4;
+      constexpr int kHalf = HD / 2;
+      // b(t0): b_j cos - b_j' sin, b_j' cos + b_j sin.
+      const float turned = b.b * b.turn.x - b.b2 * b.turn.y;
+      const float turned2 = b.b2 * b.turn.x + b.b * b.turn.y;
+      if (b.lane < kHalf)
+      {
+        b.lds[b.lane] = turned;
+        b.lds[kHalf + b.lane] = turned2;
+        b.lds[HD + b.lane] = -turned2;
+        b.lds[HD + kHalf + b.lane] = turned;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float *y = b.lds + (g < 2 ? 0 : HD) + (g & 1) * kRun;
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+      {
+        const float4 *t1 = reinterpret_cast<const float4 *>(y + 8 * s);
+        const float4 *t2 = reinterpret_cast<const float4 *>(y + kHalf + 8 * s);
+        const float4 y1a = t1[0], y1b = t1[1], y2a = t2[0], y2b = t2[1];
+        const float y1[8] = {y1a.x, y1a.y, y1a.z, y1a.w, y1b.x, y1b.y, y1b.z, y1b.w};
+        const float y2[8] = {y2a.x, y2a.y, y2a.z, y2a.w, y2b.x, y2b.y, y2b.z, y2b.w};
+        // q_j (the lower lane's) and q_j' (the upper lane's) of the pair.
+        const u32x4 own = __builtin_bit_cast(u32x4, qb[s]);
+        u32x4 qlo, qhi;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+        {
+          // (A vector element is copied out before its bits are recast:
+          // the compiler recasts the vector's first element otherwise.)
+          const unsigned word = own[w];
+          float lo, hi;
+          lane_pair32(__uint_as_float(word), lo, hi);
+          qlo[w] = __float_as_uint(lo);
+          qhi[w] = __float_as_uint(hi);
+        }
+        const half8 q1 = as_half8(qlo), q2 = as_half8(qhi);
+        half8 ab_hi, ab_lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+        {
+          const float ab = static_cast<float>(q1[e]) * y1[e] + static_cast<float>(q2[e]) * y2[e];
+          const _Float16 hi = static_cast<_Float16>(ab);
+          ab_hi[e] = hi;
+          ab_lo[e] = static_cast<_Float16>(ab - static_cast<float>(hi));
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+        {
+          const std::uint16_t *row =
+              b.rows + (16 * kb + r) * kAngleRowPitch<HD> + g * kRun + 8 * s;
+          const half8 e_hi = as_half8(*reinterpret_cast<const u32x4 *>(row));
+          const half8 e_lo = as_half8(*reinterpret_cast<const u32x4 *>(row + HD));
+          acc[kb] = mfma(e_hi, ab_hi, acc[kb]);
+          acc[kb] = mfma(e_hi, ab_lo, acc[kb]);
+          acc[kb] = mfma(e_lo, ab_hi, acc[kb]);
+        }
+      }
+    }
+
     // q.K^T, softmax and P.V of a quantised page from its raw codes. `ks` and
     // `kz` point at the KV head's key scales and key zeros (HD halves each)
     // in LDS, read 32 channels at a time.
-    template <int HD, int Bits>
+    template <int HD, int Bits, bool kBias = false>
     __device__ inline void quantised_compute(Running<HD> &run, const PageCtx &c, const half8 *qb,
                                              const QuantRaw<HD, Bits> &raw, const unsigned *ks,
-                                             const unsigned *kz)
+                                             const unsigned *kz,
+                                             const KeyBias<HD> *bias = nullptr)
     {
       constexpr int S = HD / 32;
       constexpr int kRun = HD / 4;
@@ -435,6 +556,10 @@ namespace mi
           }
           acc[kb] = mfma(dequant_step<Bits>(w0, w1, s2, z2), qb[s], acc[kb]);
         }
+      }
+      if constexpr (kBias)
+      {
+        key_bias_scores<HD>(acc, *bias, qb, r, g);
       }
       half8 p_hi, p_lo;
       softmax_page<HD>(acc, c, run, p_hi, p_lo);
@@ -476,11 +601,11 @@ namespace mi
 
     // A page at INT8/INT4/INT2, read from global memory. `meta` is this
     // wave's 4 * HD bytes of LDS: the key scales and zeros pass through it.
-    template <int HD, int Bits>
+    template <int HD, int Bits, bool kBias = false>
     __device__ inline void quantised_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
                                           const std::uint8_t *page, const PageLayout &L,
                                           std::size_t W, int kvh, int kv_heads, int lane,
-                                          unsigned *meta)
+                                          unsigned *meta, const KeyBias<HD> *bias = nullptr)
     {
       using Raw = QuantRaw<HD, Bits>;
       constexpr int kRun = HD / 4;
@@ -523,16 +648,14 @@ namespace mi
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      quantised_compute<HD, Bits>(run, c, qb, raw, meta, meta + HD / 2);
+      quantised_compute<HD, Bits, kBias>(run, c, qb, raw, meta, meta + HD / 2, bias);
     }
 
-    // q.K^T of an FP16 page's two 16-row blocks.
+    // q.K^T of an FP16 page's two 16-row blocks, added to acc.
     template <int HD>
     __device__ inline void fp16_scores(f32x4 (&acc)[2], const half8 (&k)[2][HD / 32],
                                        const half8 *qb)
     {
-      acc[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      acc[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < HD / 32; ++s)
       {
@@ -574,10 +697,11 @@ namespace mi
     // A page of FP16 rows from global memory: keys at k0/k1 (rows r and
     // 16 + r, the lane's run), values at v0/v1, all requested at once so that
     // the page costs one trip to memory.
-    template <int HD>
+    template <int HD, bool kBias = false>
     __device__ inline void fp16_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
                                      const std::uint16_t *k0, const std::uint16_t *k1,
-                                     const std::uint16_t *v0, const std::uint16_t *v1)
+                                     const std::uint16_t *v0, const std::uint16_t *v1,
+                                     const KeyBias<HD> *bias = nullptr)
     {
       constexpr int S = HD / 32;
       half8 k[2][S], v[2][S];
@@ -585,14 +709,18 @@ namespace mi
       load_fp16_run<HD>(k[1], k1);
       load_fp16_run<HD>(v[0], v0);
       load_fp16_run<HD>(v[1], v1);
-      f32x4 acc[2];
+      f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
       fp16_scores<HD>(acc, k, qb);
+      if constexpr (kBias)
+      {
+        key_bias_scores<HD>(acc, *bias, qb, c.r, c.g);
+      }
       half8 p_hi, p_lo;
       softmax_page<HD>(acc, c, run, p_hi, p_lo);
       fp16_values<HD>(run, c, v, p_hi, p_lo);
     }
 
-    template <int HD>
+    template <int HD, bool kBias>
     __global__ void __launch_bounds__(kThreads) decode_pages_kernel(DecodeArgs a)
     {
       constexpr int S = HD / 32;  // K steps of q.K^T
@@ -614,9 +742,10 @@ namespace mi
       const int G = a.group;
       const std::size_t W = static_cast<std::size_t>(a.kv_heads) * HD;
       const std::size_t run0 = static_cast<std::size_t>(kvh) * HD + g * kRun;
-      // LDS: each wave's key metadata, then the epilogue's per-wave state.
-      unsigned *meta = reinterpret_cast<unsigned *>(lds) + wave * HD;
-      float *s_m = lds + kWaves * HD;
+      // LDS: each wave's key metadata and turned key bias, then the
+      // epilogue's per-wave state.
+      unsigned *meta = reinterpret_cast<unsigned *>(lds) + wave * 3 * HD;
+      float *s_m = lds + kWaves * 3 * HD;
       float *s_l = s_m + kWaves * G;
       float *s_w = s_l + kWaves * G; // kWaves * G weights, then G maxima
       float *s_o = s_w + kWaves * G + G;
@@ -644,6 +773,20 @@ namespace mi
       // their own columns and are never stored.
       half8 qb[S];
       load_fp16_run<HD>(qb, q_row);
+
+      // The key bias: lane i holds b_i and b_i' of this KV head; the
+      // workgroup's angle rows follow the epilogue's LDS.
+      float bias_b = 0.0f, bias_b2 = 0.0f;
+      auto *angle_rows = reinterpret_cast<std::uint16_t *>(s_o + kWaves * G * kRow);
+      if constexpr (kBias)
+      {
+        copy_angle_rows<HD>(angle_rows, a.rope_angles);
+        __syncthreads();
+        const int i = lane % (HD / 2);
+        const std::uint16_t *bh = a.k_bias + static_cast<std::size_t>(kvh) * HD;
+        bias_b = static_cast<float>(__builtin_bit_cast(_Float16, bh[i]));
+        bias_b2 = static_cast<float>(__builtin_bit_cast(_Float16, bh[HD / 2 + i]));
+      }
 
       // Where the tiers and addresses are read from: q (always readable)
       // stands in for a table that has no entries.
@@ -678,6 +821,19 @@ namespace mi
         c.first = first;
         c.scale = a.scale;
         c.stat = stats + ((static_cast<std::size_t>(kvh) * a.pages + p) * G + r) * 2;
+        KeyBias<HD> bias;
+        if constexpr (kBias)
+        {
+          bias.b = bias_b;
+          bias.b2 = bias_b2;
+          bias.lds = reinterpret_cast<float *>(meta + HD);
+          bias.lane = lane;
+          // cos and sin of the lane's angle at the page's first row.
+          bias.turn = *reinterpret_cast<const float2 *>(
+              a.rope + 2 * (static_cast<std::size_t>(p) * kPageTokens * (HD / 2) + lane % (HD / 2)));
+          bias.rows = angle_rows;
+        }
+        const KeyBias<HD> *page_bias = &bias;
         if (tier == kUnreadPage)
         {
           if (g == 0 && r < G)
@@ -689,13 +845,16 @@ namespace mi
         switch (tier)
         {
         case kINT8:
-          quantised_page<HD, 8>(run, c, qb, page, a.lay[kINT8], W, kvh, a.kv_heads, lane, meta);
+          quantised_page<HD, 8, kBias>(run, c, qb, page, a.lay[kINT8], W, kvh, a.kv_heads,
+                                         lane, meta, page_bias);
           break;
         case kINT4:
-          quantised_page<HD, 4>(run, c, qb, page, a.lay[kINT4], W, kvh, a.kv_heads, lane, meta);
+          quantised_page<HD, 4, kBias>(run, c, qb, page, a.lay[kINT4], W, kvh, a.kv_heads,
+                                         lane, meta, page_bias);
           break;
         case kINT2:
-          quantised_page<HD, 2>(run, c, qb, page, a.lay[kINT2], W, kvh, a.kv_heads, lane, meta);
+          quantised_page<HD, 2, kBias>(run, c, qb, page, a.lay[kINT2], W, kvh, a.kv_heads,
+                                         lane, meta, page_bias);
           break;
         case kOwnPage:
         {
@@ -721,16 +880,16 @@ namespace mi
               rv[kb] = cv + static_cast<std::size_t>(tt - t_start) * W + run0;
             }
           }
-          fp16_page<HD>(run, c, qb, rk[0], rk[1], rv[0], rv[1]);
+          fp16_page<HD, kBias>(run, c, qb, rk[0], rk[1], rv[0], rv[1], page_bias);
           break;
         }
         default:
         {
           const auto *h = reinterpret_cast<const std::uint16_t *>(page);
-          fp16_page<HD>(run, c, qb, h + static_cast<std::size_t>(r) * W + run0,
+          fp16_page<HD, kBias>(run, c, qb, h + static_cast<std::size_t>(r) * W + run0,
                         h + static_cast<std::size_t>(16 + r) * W + run0,
                         h + static_cast<std::size_t>(kPageTokens + r) * W + run0,
-                        h + static_cast<std::size_t>(kPageTokens + 16 + r) * W + run0);
+                        h + static_cast<std::size_t>(kPageTokens + 16 + r) * W + run0, page_bias);
           break;
         }
         }
@@ -809,11 +968,13 @@ namespace mi
     }
 
     // LDS of decode_pages_kernel, bytes.
-    std::size_t pages_kernel_lds(int group, int hd)
+    std::size_t pages_kernel_lds(int group, int hd, bool bias)
     {
-      return (static_cast<std::size_t>(kWaves) * hd + 3 * kWaves * group + group +
+      const std::size_t angle_rows = bias ? 32 * (2 * hd + 8) * sizeof(std::uint16_t) : 0;
+      return (static_cast<std::size_t>(kWaves) * 3 * hd + 3 * kWaves * group + group +
               static_cast<std::size_t>(kWaves) * group * (hd + 4)) *
-             sizeof(float);
+                 sizeof(float) +
+             angle_rows;
     }
 
     // ---- the streaming kernel: several layers in one launch ----------------
@@ -1354,7 +1515,7 @@ namespace mi
             }
           }
           next();
-          f32x4 acc[2];
+          f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
           fp16_scores<HD>(acc, k, qb);
           half8 p_hi, p_lo;
           softmax_page<HD>(acc, c, run, p_hi, p_lo);
@@ -1732,10 +1893,17 @@ namespace mi
 
   bool decode_fast_applies(const KVSource &kv, const AttentionArgs &a)
   {
-    if (a.seq_q != 1 || a.k_bias != nullptr || kv.layout == Layout::kContiguous ||
+    if (a.seq_q != 1 || kv.layout == Layout::kContiguous ||
         kv.page_tokens != kPageTokens || (a.head_dim != 64 && a.head_dim != 128) ||
         a.kv_heads <= 0 || a.heads % a.kv_heads != 0 || a.heads / a.kv_heads > kMaxGroup ||
         a.heads > kMaxHeads || a.seq_k <= 0)
+    {
+      return false;
+    }
+    // The key bias: with the table over every key position and its first
+    // page's angles.
+    if (a.k_bias != nullptr && (a.rope == nullptr || a.rope_angles == nullptr ||
+                                a.rope_positions < a.seq_k || !aligned16(a.rope_angles)))
     {
       return false;
     }
@@ -1795,6 +1963,14 @@ namespace mi
     d.scores = a.scores;
     d.scores_stride = ls.scores_stride;
     d.alpha = a.alpha;
+    // The key bias, one layer's, on the one-layer launch only.
+    if (a.k_bias != nullptr && (ls.layers != 1 || a.rope == nullptr || a.rope_angles == nullptr))
+    {
+      throw InvalidArgument("decode: the key bias needs one layer and the RoPE table's angles");
+    }
+    d.k_bias = a.k_bias;
+    d.rope = a.k_bias != nullptr ? a.rope : nullptr;
+    d.rope_angles = a.k_bias != nullptr ? a.rope_angles : nullptr;
     d.start = kv.start;
     d.causal = kv.layout == Layout::kCausal;
     d.seq_k = a.seq_k;
@@ -1867,7 +2043,7 @@ namespace mi
       }
       else
       {
-        const std::size_t lds = pages_kernel_lds(group, hd);
+        const std::size_t lds = pages_kernel_lds(group, hd, d.k_bias != nullptr);
         if (lds > 64 * 1024)
         {
           hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(pages_kernel),
@@ -1887,13 +2063,29 @@ namespace mi
     };
     if (a.head_dim == 128)
     {
-      run(decode_pages_kernel<128>, decode_stream_kernel<128>, decode_combine_kernel<128, false>,
-          decode_combine_kernel<128, true>, 128, stream_kernel_lds<128>());
+      if (d.k_bias != nullptr)
+      {
+        run(decode_pages_kernel<128, true>, decode_stream_kernel<128>,
+            decode_combine_kernel<128, false>, decode_combine_kernel<128, true>, 128,
+            stream_kernel_lds<128>());
+      }
+      else
+      {
+        run(decode_pages_kernel<128, false>, decode_stream_kernel<128>,
+            decode_combine_kernel<128, false>, decode_combine_kernel<128, true>, 128,
+            stream_kernel_lds<128>());
+      }
+    }
+    else if (d.k_bias != nullptr)
+    {
+      run(decode_pages_kernel<64, true>, decode_stream_kernel<64>, decode_combine_kernel<64, false>,
+          decode_combine_kernel<64, true>, 64, stream_kernel_lds<64>());
     }
     else
     {
-      run(decode_pages_kernel<64>, decode_stream_kernel<64>, decode_combine_kernel<64, false>,
-          decode_combine_kernel<64, true>, 64, stream_kernel_lds<64>());
+      run(decode_pages_kernel<64, false>, decode_stream_kernel<64>,
+          decode_combine_kernel<64, false>, decode_combine_kernel<64, true>, 64,
+          stream_kernel_lds<64>());
     }
   }
 

@@ -38,6 +38,10 @@ namespace mi
   // ---- pointwise (pointwise.hip) --------------------------------------------------
   void launch_rope(const void *x, const std::int32_t *positions, void *out, int seq, int heads,
                    int head_dim, double theta, hipStream_t stream);
+  // fp16 high and low parts of a RoPE table's cos (channels < head_dim/2)
+  // and sin (the rest) per position: [position][hi | lo][head_dim].
+  void launch_rope_angles(const float *table, std::uint16_t *angles, int positions, int head_dim,
+                          hipStream_t stream);
   void launch_rope_table(float *table, int positions, int head_dim, double theta,
                          hipStream_t stream);
   void launch_rmsnorm(const void *x, bool x_is_f32, const void *weight, void *out, int rows,
@@ -110,6 +114,10 @@ namespace mi
     const std::uint16_t *k_bias; // (kv_heads, hd) fp16 or null
     const float *rope;        // {cos, sin} per (position, j < hd/2), fp32; with k_bias
     int rope_positions;
+    // The first 32 positions' angles as fp16 high and low parts
+    // ([position][hi | lo][hd]), when the caller has them (a RopeTable's):
+    // the decode fast path takes the key bias only with these.
+    const std::uint16_t *rope_angles;
     int seq_q;
     int seq_k;
     int heads;

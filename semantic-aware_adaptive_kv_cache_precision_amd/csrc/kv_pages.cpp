@@ -217,11 +217,16 @@ namespace mi
     {
       return;
     }
-    const int grown = count > 2 * positions_ ? count : 2 * positions_;
+    const int grown = std::max({count, 2 * positions_, kAngleRows});
     auto table = std::make_unique<DeviceBuffer>(static_cast<std::size_t>(grown) * head_dim_ *
                                                 sizeof(float));
     launch_rope_table(table->as<float>(), grown, head_dim_, theta_, runtime_stream());
+    auto angles = std::make_unique<DeviceBuffer>(static_cast<std::size_t>(kAngleRows) * head_dim_ *
+                                                 2 * sizeof(std::uint16_t));
+    launch_rope_angles(table->as<const float>(), angles->as<std::uint16_t>(), kAngleRows,
+                       head_dim_, runtime_stream());
     table_ = std::move(table);
+    angles_ = std::move(angles);
     positions_ = grown;
   }
 
@@ -1042,6 +1047,7 @@ namespace mi
     a.k_bias = static_cast<const std::uint16_t *>(k_bias);
     a.rope = k_bias != nullptr ? rope->data() : nullptr;
     a.rope_positions = k_bias != nullptr ? rope->positions() : 0;
+    a.rope_angles = k_bias != nullptr ? rope->angles() : nullptr;
     a.seq_q = seq_q;
     a.seq_k = seq_k;
     a.heads = heads;

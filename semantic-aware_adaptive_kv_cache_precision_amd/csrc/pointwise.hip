@@ -63,6 +63,29 @@ namespace mi
       }
     }
 
+    // The table's angles as fp16 high and low parts, a row a position:
+    // channel c < half holds cos of angle c, channel c >= half sin of angle
+    // c - half; high parts (head_dim halves), then low parts (the fp32 value
+    // less the high part, rounded again). hi + lo carries the fp32 value to
+    // within 2^-22 of it, for matrix-core products that need fp32 accuracy.
+    __global__ void rope_angles_kernel(const float *__restrict__ table,
+                                       std::uint16_t *__restrict__ angles, int half, int head_dim,
+                                       std::size_t count)
+    {
+      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+           i < count; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+      {
+        const std::size_t t = i / head_dim;
+        const int c = static_cast<int>(i % head_dim);
+        const int j = c < half ? c : c - half;
+        const float value = table[2 * (t * half + j) + (c < half ? 0 : 1)];
+        const __half hi = __float2half_rn(value);
+        const __half lo = __float2half_rn(value - __half2float(hi));
+        angles[2 * t * head_dim + c] = __half_as_ushort(hi);
+        angles[(2 * t + 1) * head_dim + c] = __half_as_ushort(lo);
+      }
+    }
+
     __device__ inline float widen(const std::uint16_t *x, std::size_t i)
     {
       return h2f(x[i]);
@@ -165,6 +188,19 @@ namespace mi
     hipLaunchKernelGGL(rope_table_kernel, dim3(grid_for(entries, 256)), dim3(256), 0, stream,
                        table, head_dim / 2, head_dim, theta, entries);
     hip_check(hipGetLastError(), "rope table kernel launch");
+  }
+
+  void launch_rope_angles(const float *table, std::uint16_t *angles, int positions, int head_dim,
+                          hipStream_t stream)
+  {
+    const std::size_t count = static_cast<std::size_t>(positions) * head_dim;
+    if (count == 0)
+    {
+      return;
+    }
+    hipLaunchKernelGGL(rope_angles_kernel, dim3(grid_for(count, 256)), dim3(256), 0, stream, table,
+                       angles, head_dim / 2, head_dim, count);
+    hip_check(hipGetLastError(), "rope angles kernel launch");
   }
 
   void launch_rmsnorm(const void *x, bool x_is_f32, const void *weight, void *out, int rows,

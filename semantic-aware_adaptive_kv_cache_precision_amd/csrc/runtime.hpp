@@ -221,6 +221,15 @@ namespace mi
     RopeTable(int head_dim, double theta);
     void cover(int count);
     const float *data() const { return table_ ? table_->as<const float>() : nullptr; }
+    // The angles of the first kAngleRows positions (a decode page's rows)
+    // as fp16 high and low parts, for the decode kernel's key bias:
+    // [position][hi | lo][head_dim], cos then sin. The table always covers
+    // that many positions.
+    static constexpr int kAngleRows = 32;
+    const std::uint16_t *angles() const
+    {
+      return angles_ ? angles_->as<const std::uint16_t>() : nullptr;
+    }
     int positions() const { return positions_; }
     int head_dim() const { return head_dim_; }
     double theta() const { return theta_; }
@@ -231,6 +240,7 @@ namespace mi
     double theta_;
     int positions_ = 0;
     std::unique_ptr<DeviceBuffer> table_;
+    std::unique_ptr<DeviceBuffer> angles_;
   };
 
   // The page_index of a layer's two open pages, of a move's staging page, of
