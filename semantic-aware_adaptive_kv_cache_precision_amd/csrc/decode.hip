@@ -519,19 +519,19 @@ namespace mi
       }
     }
 
-    // q.K^T, softmax and P.V of a quantised page from its raw codes. `ks` and
-    // `kz` point at the KV head's key scales and key zeros (HD halves each)
-    // in LDS, read 32 channels at a time.
-    template <int HD, int Bits, bool kBias = false>
+    // q.K^T, softmax and P.V of a quantised page from its raw codes, the
+    // scores starting from `start`. `ks` and `kz` point at the KV head's key
+    // scales and key zeros (HD halves each) in LDS, read 32 channels at a
+    // time.
+    template <int HD, int Bits>
     __device__ inline void quantised_compute(Running<HD> &run, const PageCtx &c, const half8 *qb,
                                              const QuantRaw<HD, Bits> &raw, const unsigned *ks,
-                                             const unsigned *kz,
-                                             const KeyBias<HD> *bias = nullptr)
+                                             const unsigned *kz, const f32x4 (&start)[2])
     {
       constexpr int S = HD / 32;
       constexpr int kRun = HD / 4;
       const int r = c.r, g = c.g;
-      f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+      f32x4 acc[2] = {start[0], start[1]};
 #pragma unroll
       for (int s = 0; s < S; ++s)
       {
@@ -556,10 +556,6 @@ namespace mi
           }
           acc[kb] = mfma(dequant_step<Bits>(w0, w1, s2, z2), qb[s], acc[kb]);
         }
-      }
-      if constexpr (kBias)
-      {
-        key_bias_scores<HD>(acc, *bias, qb, r, g);
       }
       half8 p_hi, p_lo;
       softmax_page<HD>(acc, c, run, p_hi, p_lo);
@@ -638,6 +634,12 @@ namespace mi
         raw.vs[kb] = *((g_u16)(page + L.value_scales + 2 * grp));
         raw.vz[kb] = *((g_u16)(page + L.value_zeros + 2 * grp));
       }
+      // The key bias's scores while the codes are on their way.
+      f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+      if constexpr (kBias)
+      {
+        key_bias_scores<HD>(acc, *bias, qb, r, g);
+      }
       // The key scales and zeros through LDS: [scales HD halves][zeros HD].
       // LDS operations of one wave complete in order; the fences keep the
       // compiler from moving the reads above the write.
@@ -648,7 +650,7 @@ namespace mi
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      quantised_compute<HD, Bits, kBias>(run, c, qb, raw, meta, meta + HD / 2, bias);
+      quantised_compute<HD, Bits>(run, c, qb, raw, meta, meta + HD / 2, acc);
     }
 
     // q.K^T of an FP16 page's two 16-row blocks, added to acc.
@@ -710,11 +712,12 @@ namespace mi
       load_fp16_run<HD>(v[0], v0);
       load_fp16_run<HD>(v[1], v1);
       f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-      fp16_scores<HD>(acc, k, qb);
+      // The key bias's scores while the keys are on their way.
       if constexpr (kBias)
       {
         key_bias_scores<HD>(acc, *bias, qb, c.r, c.g);
       }
+      fp16_scores<HD>(acc, k, qb);
       half8 p_hi, p_lo;
       softmax_page<HD>(acc, c, run, p_hi, p_lo);
       fp16_values<HD>(run, c, v, p_hi, p_lo);
@@ -1322,8 +1325,9 @@ namespace mi
       const u32x2 km = *reinterpret_cast<const u32x2 *>(slot + SL::kKeyScales + 8 * lane);
       *reinterpret_cast<u32x2 *>(meta + 8 * lane) = km;
       next();
+      const f32x4 zero[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
       quantised_compute<HD, Bits>(run, c, qb, raw, reinterpret_cast<const unsigned *>(meta),
-                                  reinterpret_cast<const unsigned *>(meta + 256));
+                                  reinterpret_cast<const unsigned *>(meta + 256), zero);
     }
 
     // Each wave takes an equal contiguous range of (layer, KV head, page)
