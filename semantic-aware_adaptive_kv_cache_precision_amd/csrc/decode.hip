@@ -792,8 +792,10 @@ namespace mi
       }
 
       // Where the tiers and addresses are read from: q (always readable)
-      // stands in for a table that has no entries.
-      const auto *tier_base = a.causal ? tiers : reinterpret_cast<const std::uint8_t *>(a.q);
+      // stands in for a table that has no entries (a causal cache with no
+      // page sealed yet has no tables at all: both pointers are null).
+      const auto *tier_base =
+          a.causal && own > 0 ? tiers : reinterpret_cast<const std::uint8_t *>(a.q);
       const auto *page_base =
           !a.causal || own > 0 ? table : reinterpret_cast<const unsigned long long *>(a.q);
       // The open page's rows, asked for with q, not after the tier.

@@ -159,7 +159,9 @@ def test_decode_over_mixed_tiers_is_the_oracle():
              (16, (14, 2, 64), 16 * 20 + 5, False), (48, (12, 2, 128), 48 * 7 + 20, False),
              (32, (32, 8, 64), 32 * 33, False), (32, (12, 2, 128), 32 * 300 + 31, False),
              (32, (12, 2, 128), 32 * 9 + 7, True), (32, (12, 2, 128), 32 * 300 + 31, True),
-             (32, (32, 8, 64), 32 * 33, True)]
+             (32, (32, 8, 64), 32 * 33, True), (32, (14, 2, 64), 20, False),
+             (32, (14, 2, 64), 20, True),
+             (32, (12, 2, 128), 32 * 2 + 1, True), (32, (12, 2, 128), 32, True)]
     each(cases, check)
 
 
