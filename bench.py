@@ -2,7 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
-The step: one decode step's attention over every layer
+The step (the headline workload, config 3): one decode step's attention over every layer
 of a Qwen2.5-1.5B-shaped cache at 32K positions -- 28 layers, 12 query / 2 KV
 heads, head_dim 128, 32-token pages born at seeded-importance tiers 20%
 FP16, 30% INT8, 40% INT4, 10% INT2 -- with each layer's per-page attention

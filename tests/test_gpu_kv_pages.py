@@ -444,7 +444,7 @@ def test_an_evicted_page_reads_as_a_masked_one_to_the_bit():
 
 
 def test_full_size_config3_layer_against_the_oracle():
-    """BASELINE config 3 at its full size on one layer: 32K positions of
+    """Config 3 (the headline workload) at its full size on one layer: 32K positions of
     Qwen2.5-1.5B shape, tiers 20/30/40/10 by seeded importance, built by
     storing all rows (pages sealed at birth tier in batched launches), then
     one decode with the fused mass and EWMA, against the float64 oracle."""
