@@ -69,11 +69,12 @@ def chunk_case(heads, kv, hd, seq, seq_q, seed, bias, split, unread=()):
 
 def test_a_chunk_reads_earlier_pages_at_their_tiers_and_its_own_at_fp16():
     """Chunks that begin mid-page and cross pages, a one-page chunk, a chunk
-    that is the whole prompt; every shape; the key bias on and off."""
+    that is the whole prompt, a prompt shorter than a page (no page sealed:
+    the cache has no page tables); every shape; the key bias on and off."""
     cases = []
     for i, (heads, kv, hd) in enumerate(SHAPES):
         for seq, seq_q in ((P * 9 + 7, 75), (P * 4, P), (P * 3 + 5, P * 3 + 5), (P * 20 + 1, 16),
-                           (P * 6 + 31, 130)):
+                           (P * 6 + 31, 130), (20, 20)):
             for bias in (False, True):
                 cases.append((heads, kv, hd, seq, seq_q, 100 * i + seq_q, bias))
     each(cases, lambda h, kv, hd, seq, sq, seed, bias: chunk_case(h, kv, hd, seq, sq, seed, bias,
