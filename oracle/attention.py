@@ -69,7 +69,8 @@ def attention64(q, k, v, k_bias=None, theta: float = 0.0, unread=None, positions
     if positions is None:
         positions = np.arange(seq_q) + (seq_k - seq_q)
     kk, vv = expand_kv(heads, k), expand_kv(heads, v)
-    scores = np.einsum("qhd,khd->hqk", q, kk) / np.sqrt(hd)
+    # Batched over heads: (h, q, d) @ (h, d, k), float64 throughout.
+    scores = np.matmul(q.transpose(1, 0, 2), kk.transpose(1, 2, 0)) / np.sqrt(hd)
     masked = np.arange(seq_k)[None, :] > np.asarray(positions)[:, None]
     if unread is not None:
         masked = masked | np.asarray(unread, bool)[None, :]
@@ -77,7 +78,7 @@ def attention64(q, k, v, k_bias=None, theta: float = 0.0, unread=None, positions
     top = scores.max(axis=-1, keepdims=True)
     p = np.exp(scores - top)
     p /= p.sum(axis=-1, keepdims=True)
-    out = np.einsum("hqk,khd->qhd", p, vv)
+    out = np.matmul(p, vv.transpose(1, 0, 2)).transpose(1, 0, 2)
     return out, p
 
 
@@ -106,8 +107,9 @@ def attention_bound(q, k, v, weights, k_bias=None, theta: float = 0.0, unread=No
         positions = np.arange(seq_q) + (seq_k - seq_q)
     positions = np.asarray(positions)
     kk, vv = expand_kv(heads, k), expand_kv(heads, v)
-    terms = np.einsum("hqk,khd->qhd", weights, np.abs(vv))
-    score_terms = np.einsum("qhd,khd->hqk", np.abs(q), np.abs(kk)) / np.sqrt(hd)
+    terms = np.matmul(weights, np.abs(vv).transpose(1, 0, 2)).transpose(1, 0, 2)
+    score_terms = np.matmul(np.abs(q).transpose(1, 0, 2),
+                            np.abs(kk).transpose(1, 2, 0)) / np.sqrt(hd)
     masked = np.arange(seq_k)[None, :] > positions[:, None]
     if unread is not None:
         masked = masked | np.asarray(unread, bool)[None, :]

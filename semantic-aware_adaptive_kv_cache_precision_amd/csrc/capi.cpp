@@ -62,7 +62,7 @@ namespace
     catch (const mi::Full &e) { return fail(MI_ERR_FULL, e.what()); }
     catch (const mi::DeviceError &e) { return fail(MI_ERR_DEVICE, e.what()); }
     catch (const std::bad_alloc &) { return fail(MI_ERR_OUT_OF_MEMORY, "host allocation failed"); }
-    catch (const std::out_of_range &e) { return fail(MI_ERR_NOT_FOUND, e.what()); }
+    catch (const std::out_of_range &e) { return fail(MI_ERR_RANGE, e.what()); }
     catch (const std::exception &e) { return fail(MI_ERR_LOGIC, e.what()); }
     catch (...) { return fail(MI_ERR_LOGIC, "unknown error"); }
   }

@@ -475,3 +475,161 @@ def test_full_size_config3_layer_against_the_oracle():
     assert_mass_close(mass, want_mass, "config3 mass")
     np.testing.assert_array_equal(scores.download()[0],
                                   ewma.host_ewma([(0, mass.astype(np.float32))], 1, seq // P)[0])
+
+
+def test_chained_store_and_decode_steps_across_a_seal_at_llama_shape():
+    """Forty-four decode steps at the Llama-3.2-1B shape (32 q / 8 KV heads,
+    head_dim 64), each storing its row and then attending, crossing a seal
+    (the own page's 32nd row arrives, the page is quantised at its birth tier,
+    the next open page takes over) over a 30/40/30 FP16/INT8/INT4 cache:
+    every step's output and masses against the float64 causal view of the
+    cache as it then is, and the scores folded on every step equal, to the
+    bit, the oracle's fold of the kernel's masses."""
+    from microinfer import workloads as w
+    m = mi()
+    d = m.device
+    P, shape = 32, w.LLAMA_1B
+    heads, kv, hd = shape.heads, shape.kv_heads, shape.head_dim
+    rng = np.random.default_rng(17)
+    seq0, steps = P * 20 + 10, 44                 # 650 -> 694: seals page 20 at 672
+    total = seq0 + steps
+    k, v = normal(rng, total, kv, hd), normal(rng, total, kv, hd)
+    k[:, :, rng.choice(hd, 2, replace=False)] *= 10
+    k = fp16_exact(k)
+    tmap = w.tier_map(0, LAYERS, total // P + 1, w.MIX_CONFIG5)
+    alloc, cache = pages_for(P, kv, hd, 0, tier_map=tmap, always_seal=True)
+    max_pages = total // P + 1
+    scores = d.ImportanceScores(LAYERS, max_pages)
+    store_in_runs(cache, 0, k[:seq0], v[:seq0], [seq0])
+    folded = []
+    for t in range(seq0, total):
+        cache.reserve(t + 1)
+        cache.store(0, put(k[t:t + 1]), put(v[t:t + 1]), t, 1)
+        q = normal(rng, 1, heads, hd)
+        announce("chained llama step", t)
+        got, mass = run_decode(m, cache, k[:t + 1], v[:t + 1], q, heads, kv, hd, scores=scores)
+        folded.append((0, mass.astype(np.float32)))
+        want, want_mass, bound = oracle_decode(alloc, P, kv, hd, k[:t + 1], v[:t + 1], q)
+        assert_attention_close(got, want, f"step {t}", bound)
+        assert_mass_close(mass, want_mass, f"step {t} mass")
+        np.testing.assert_allclose(mass.sum(1), 1.0, atol=1e-5)
+    # The page sealed during the run holds quantise_page of its rows.
+    sealed = seq0 // P
+    assert total // P > sealed
+    tier = int(alloc.locate(0, sealed)[0])
+    assert tier == tmap[0][sealed]
+    kp = k[sealed * P:(sealed + 1) * P].astype(np.float16)
+    vp = v[sealed * P:(sealed + 1) * P].astype(np.float16)
+    want_page = quant.fp16_page(kp, vp) if tier == 0 else quant.quantise_page(kp, vp, tier, P)
+    np.testing.assert_array_equal(alloc.read(0, sealed), want_page)
+    np.testing.assert_array_equal(scores.download(), ewma.host_ewma(folded, LAYERS, max_pages))
+
+
+def test_decode_after_pages_move_reads_them_where_they_now_are():
+    """tests/test_kv_pages.py:112-150 and tests/test_quantised_pages.py:
+    202-224: the cache's page tables are resolved by a first decode; then
+    pages move under it three ways: a batched move (new slots at new tiers),
+    an eviction whose free moves a tier's tail page into the hole, and a
+    free of someone else's page that moves one of the cache's own pages. The
+    slot each moved page left is then taken by another page and filled with
+    NaN, so that a stale table cannot read the old bytes back by luck. Every
+    decode after each change, the per-layer call and the one-launch form,
+    meets the float64 oracle over the cache as it then is."""
+    m = mi()
+    d = m.device
+    P, heads, kv, hd = 32, 12, 2, 128
+    rng = np.random.default_rng(31)
+    seq = P * 24 + 5
+    k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+    tmap = [[(1, 0, 2, 0, 3)[i % 5] for i in range(seq // P + 1)] for _ in range(LAYERS)]
+    alloc, cache = pages_for(P, kv, hd, 0, tier_map=tmap, always_seal=True)
+    cache.reserve(P)
+    # Someone else's pages, between the cache's own at every tier.
+    for t in range(4):
+        alloc.allocate(90 + t, 0, t)
+    store_in_runs(cache, 0, k, v, [seq - 1, 1])
+    store_in_runs(cache, 1, k, v, [seq - 1, 1])
+    q = normal(rng, 1, heads, hd)
+    own = (seq - 1) // P
+    pages = own + 1
+
+    def oracle_now():
+        """The float64 view of layer 0 as the cache now holds it: an evicted
+        page unread."""
+        tiers_now = cache.page_tiers()[0]
+        raw, tiers = [], []
+        for p in range(own):
+            if tiers_now[p] == 4:
+                raw.append(None)
+                tiers.append(quant.UNREAD)
+            else:
+                raw.append(alloc.read(0, p))
+                tiers.append(int(alloc.locate(0, p)[0]))
+        return att.causal_decode(q, raw, tiers, k[own * P:], v[own * P:], kv, hd, P,
+                                 with_bound=True)
+
+    def decode_both(what):
+        announce("moved pages decode", what)
+        got, mass = run_decode(m, cache, k, v, q, heads, kv, hd)
+        want, want_mass, bound = oracle_now()
+        assert_attention_close(got, want, what, bound)
+        assert_mass_close(mass, want_mass, what + " mass")
+        # The one-launch form over both layers reads the same tables.
+        q2 = np.concatenate([q, q])
+        out = d.empty(2 * heads * hd)
+        mass2 = d.empty_f32(2 * heads * pages)
+        cache.attention_layers(0, 2, put(q2), out, seq, heads, kv, hd,
+                               put(np.concatenate([k[-1:], k[-1:]])),
+                               put(np.concatenate([v[-1:], v[-1:]])), mass2)
+        both = out.to_numpy().reshape(2, heads, hd)
+        assert_attention_close(both[:1], want, what + " one launch", bound)
+        return got
+
+    def poison_slot(tier, slot):
+        """Another page takes the slot a moved page left and fills it with
+        NaN (FP16) or 0xFF bytes."""
+        key = (70 + len(poisoned), 0)
+        alloc.allocate(*key, tier)
+        assert alloc.locate(*key) == (tier, slot), (alloc.locate(*key), tier, slot)
+        nbytes = alloc.page_bytes(tier)
+        junk = (np.full(nbytes // 2, np.nan, np.float16).view(np.uint8) if tier == 0
+                else np.full(nbytes, 0xFF, np.uint8))
+        alloc.write(*key, junk)
+        poisoned.append(key)
+
+    poisoned = []
+    first = decode_both("before")
+
+    # 1. A foreign free: the tier's tail (one of the cache's pages) moves
+    # into the freed slot; the slot it left is poisoned.
+    for t in range(4):
+        tail = alloc.pages(t)[-1]
+        assert tail[0] < LAYERS, "the tail should be one of the cache's pages"
+        tail_slot = alloc.locate(*tail)[1]
+        alloc.free(90 + t, 0)
+        assert alloc.locate(*tail)[1] < tail_slot
+        poison_slot(t, tail_slot)
+    np.testing.assert_array_equal(decode_both("after a foreign free"), first)
+
+    # 2. A batched move: FP16 pages down, an INT8 page up from its shadow
+    # after a first downgrade; the slots the old pages held are reused.
+    fp16_pages = [p for p in range(own) if tmap[0][p] == 0][:6]
+    plan = [(0, fp16_pages[0], 2), (0, fp16_pages[1], 3), (0, fp16_pages[2], 1),
+            (1, fp16_pages[3], 2), (0, fp16_pages[4], 3)]
+    cache.move_pages(plan)
+    for layer, page, tier in plan:
+        assert cache.page_tier(layer, page) == tier
+    decode_both("after a batched move")
+    cache.move_pages([(0, fp16_pages[0], 0), (0, fp16_pages[1], 1)])
+    decode_both("after a restore")
+
+    # 3. An eviction whose free swaps the tier's tail into the hole.
+    victim = next(p for p in range(own) if tmap[0][p] == 2 and cache.page_tier(0, p) == 2)
+    tier = int(alloc.locate(0, victim)[0])
+    tail = alloc.pages(tier)[-1]
+    tail_slot = alloc.locate(*tail)[1]
+    cache.evict(0, victim)
+    if tail != (0, victim):
+        assert alloc.locate(*tail)[1] < tail_slot
+    poison_slot(tier, tail_slot)
+    decode_both("after an eviction")

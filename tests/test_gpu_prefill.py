@@ -125,3 +125,49 @@ def test_fp16_page_table_and_contiguous_rows():
             out = d.empty(q.size)
             d.attention(put(q), put(k), put(v), None, None, out, seq_q, seq, heads, kv, hd, part)
             assert_attention_close(out.to_numpy().reshape(q.shape), want, "contiguous", bound)
+
+
+def test_config5_chunk_at_full_size():
+    """Config 5's prefill chunk at its full size: the Llama-3.2-1B shape
+    (32 q / 8 KV heads, head_dim 64), a 2,048-query chunk ending at position
+    16,384 over a cache of 30/40/30 FP16/INT8/INT4 pages (tiers by seeded
+    importance), split across the attention workspace. 256 queries, eight
+    runs of 32 spread over the chunk so that each run is one own page's
+    queries, are held to the float64 oracle; every output is finite."""
+    from microinfer import workloads as w
+    m = mi()
+    d = m.device
+    shape = w.LLAMA_1B
+    heads, kv, hd = shape.heads, shape.kv_heads, shape.head_dim
+    seq, seq_q = 16384, 2048
+    rng = np.random.default_rng(5)
+    k, v = w.kv_rows(rng, seq, shape, w.outlier_channels(rng, shape.kv_width))
+    k, v = k.astype(np.float32), v.astype(np.float32)
+    tmap = w.tier_map(0, LAYERS, seq // P, w.MIX_CONFIG5)
+    alloc, cache = pages_for(P, kv, hd, 0, tier_map=tmap, always_seal=True,
+                             capacity=seq // P * LAYERS + 8)
+    start = store_in_runs(cache, 1, k, v, [seq - seq_q, seq_q])
+    assert start == seq - seq_q
+    counts = np.bincount([int(alloc.locate(1, p)[0]) for p in range(seq // P)], minlength=4)
+    assert list(counts) == [153, 205, 154, 0], counts
+    q = normal(rng, seq_q, heads, hd)
+    out = d.empty(seq_q * heads * hd)
+    part = d.empty_f32(d.attention_partials(hd))
+    announce("config5 chunk", seq, seq_q)
+    cache.attention(1, put(q), None, None, out, seq_q, seq, heads, kv, hd, put(k[start:]),
+                    put(v[start:]), None, part)
+    got = out.to_numpy().reshape(seq_q, heads, hd)
+    assert np.isfinite(got).all()
+    pages, tiers = sealed_pages(alloc, 1, (seq - 1) // P)
+    # Own pages sampled across the chunk: its first, last and six between.
+    own_pages = np.linspace(start // P, (seq - 1) // P, 8).astype(int)
+    checked = 0
+    for own in own_pages:
+        end = min((own + 1) * P, seq)      # the run's last position + 1
+        first = own * P
+        rows = slice(first - start, end - start)
+        want, bound = att.causal_chunk(q[rows], pages, tiers, k[:end], v[:end], kv, hd, P,
+                                       with_bound=True)
+        assert_attention_close(got[rows], want, f"config5 own page {own}", bound)
+        checked += end - first
+    assert checked >= 256
