@@ -138,6 +138,10 @@ namespace
     a.scores = scores;
     a.alpha = alpha;
     a.partials = partials;
+    // The header's contract: a partials buffer holds
+    // mi_attention_partials_floats(head_dim) floats.
+    a.partials_floats = partials != nullptr && head_dim > 0 ? mi::attention_partials_floats(head_dim)
+                                                            : 0;
     if (seq_q < 0 || seq_k < 0 || seq_q > seq_k)
     {
       throw mi::InvalidArgument("seq_q " + std::to_string(seq_q) + " exceeds seq_k " +

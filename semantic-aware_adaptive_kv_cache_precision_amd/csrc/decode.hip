@@ -47,6 +47,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <map>
+#include <mutex>
 #include <vector>
 
 namespace mi
@@ -1781,10 +1783,9 @@ namespace mi
         {
           fold ^= a.warm_tiers[i] ^ static_cast<unsigned>(a.warm_table[i]);
         }
-        if (fold == 0x9E3779B9u && a.warm_count < 0) // never: keeps the reads
-        {
-          a.scores[0] = 0.0f;
-        }
+        // The reads are for their side effect on the caches: an empty asm
+        // that takes the folded value keeps the compiler from dropping them.
+        asm volatile("" ::"v"(fold));
         return;
       }
       // A mass block: 64 pages, a wave a head at a time (heads w, w + 4, ...):
@@ -1871,31 +1872,53 @@ namespace mi
       }
     }
 
-    // The decode workspace: partials and page statistics. Grown on demand and
-    // never freed before the process ends, so an address a captured graph
-    // holds stays valid.
-    float *decode_workspace(std::size_t floats)
+    // Where a launch's scratch comes from: the caller's workspace source,
+    // else the caller's partials buffer when it is known to be large enough,
+    // else the stream's library buffer.
+    float *decode_scratch(const AttentionArgs &a, std::size_t floats, hipStream_t stream)
     {
-      static float *buffer = nullptr;
-      static std::size_t held = 0;
-      static std::vector<float *> retired;
-      if (floats > held)
+      if (a.workspace != nullptr)
       {
-        if (buffer != nullptr)
-        {
-          retired.push_back(buffer);
-        }
-        const std::size_t grown = std::max<std::size_t>(floats, 1 << 20);
-        hip_check(hipMalloc(reinterpret_cast<void **>(&buffer), grown * sizeof(float)),
-                  "hipMalloc decode workspace");
-        held = grown;
+        return a.workspace->floats(floats);
       }
-      return buffer;
+      if (a.partials != nullptr && a.partials_floats >= floats)
+      {
+        return a.partials;
+      }
+      return stream_workspace(stream, floats);
     }
 
     bool aligned16(const void *p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 
   } // namespace
+
+  float *stream_workspace(hipStream_t stream, std::size_t count)
+  {
+    struct Held
+    {
+      float *buffer = nullptr;
+      std::size_t count = 0;
+    };
+    static std::mutex lock;
+    static std::map<hipStream_t, Held> held;
+    static std::vector<float *> retired; // kept: a captured graph may hold one
+    std::lock_guard<std::mutex> guard(lock);
+    Held &h = held[stream];
+    if (count > h.count)
+    {
+      if (h.buffer != nullptr)
+      {
+        retired.push_back(h.buffer);
+      }
+      const std::size_t grown = std::max<std::size_t>(count, 1 << 20);
+      float *buffer = nullptr;
+      hip_check(hipMalloc(reinterpret_cast<void **>(&buffer), grown * sizeof(float)),
+                "hipMalloc decode workspace");
+      h.buffer = buffer;
+      h.count = grown;
+    }
+    return h.buffer;
+  }
 
   bool decode_fast_applies(const KVSource &kv, const AttentionArgs &a)
   {
@@ -2025,7 +2048,7 @@ namespace mi
         static_cast<std::size_t>(ls.layers) * a.kv_heads * d.splits * group * a.head_dim;
     const std::size_t ml = static_cast<std::size_t>(ls.layers) * a.kv_heads * group * d.splits * 2;
     const std::size_t stats = static_cast<std::size_t>(ls.layers) * a.heads * pages * 2;
-    float *ws = decode_workspace(part + ml + stats);
+    float *ws = decode_scratch(a, part + ml + stats, stream);
     d.partials = ws;
     d.split_ml = ws + part;
     d.page_stats = ws + part + ml;

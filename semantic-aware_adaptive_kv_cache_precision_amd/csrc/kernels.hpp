@@ -107,6 +107,25 @@ namespace mi
     int warm_count;
   };
 
+  // Device scratch a launch needs beside its inputs and outputs (the decode
+  // path's split partials and page statistics): `count` floats on the
+  // stream the launch goes on, valid until the next request of the same
+  // source. An owner (a KVPages, the allocation-free entry point's static
+  // array) gives its own; a launch without one takes the caller's partials
+  // buffer when it is large enough, else a library buffer of the stream's.
+  struct WorkspaceSource
+  {
+    virtual float *floats(std::size_t count) = 0;
+
+  protected:
+    ~WorkspaceSource() = default;
+  };
+  // The library's scratch for launches on `stream`: one buffer a stream,
+  // grown on demand and never freed before the process ends (an address a
+  // captured graph holds stays valid). Launches on different streams never
+  // share one; launches on one stream are ordered by it.
+  float *stream_workspace(hipStream_t stream, std::size_t count);
+
   struct AttentionArgs
   {
     const std::uint16_t *q;   // (seq_q, heads, hd) fp16
@@ -127,6 +146,8 @@ namespace mi
     float *scores;            // this layer's importance scores or null; decode only
     float alpha;
     float *partials;          // attention_partials_floats(hd) or null: no split
+    std::size_t partials_floats; // its size, when the caller knows it (0: unknown)
+    WorkspaceSource *workspace;  // the decode path's scratch, or null (see above)
   };
 
   // How a launch given partials splits its keys: runs and keys a run.

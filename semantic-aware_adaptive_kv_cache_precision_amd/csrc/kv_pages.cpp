@@ -1057,6 +1057,7 @@ namespace mi
     a.scores = scores;
     a.alpha = alpha;
     a.partials = partials;
+    a.workspace = &workspace_;
     if (!seals_)
     {
       kv.layout = Layout::kPaged;
@@ -1092,7 +1093,8 @@ namespace mi
       const LayerTable next = resolve(layer + 1);
       kv.warm_pages = next.pages;
       kv.warm_tiers = next.tiers;
-      kv.warm_count = (seq_k + page_tokens_ - 1) / page_tokens_;
+      // The next layer's sealed pages only: the table holds pages_ entries.
+      kv.warm_count = std::min((seq_k - 1) / page_tokens_, pages_);
     }
     launch_attention(kv, a, runtime_stream());
   }
@@ -1166,6 +1168,7 @@ namespace mi
     a.mass = mass;
     a.scores = scores;
     a.alpha = alpha;
+    a.workspace = &workspace_;
     const LayerTable base = resolve(0);
     kv.pages = base.pages;
     if (seals_)

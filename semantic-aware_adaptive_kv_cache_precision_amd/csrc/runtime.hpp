@@ -64,6 +64,31 @@ namespace mi
   // device: never assumed.
   std::size_t granule_bytes();
 
+  // A workspace of one owner's: a device buffer grown on demand. A buffer it
+  // outgrows is kept until the owner goes, so that an address a captured
+  // graph holds stays valid as long as the owner does.
+  class OwnedWorkspace final : public WorkspaceSource
+  {
+  public:
+    float *floats(std::size_t count) override
+    {
+      if (current_ == nullptr || current_->bytes() < count * sizeof(float))
+      {
+        if (current_ != nullptr)
+        {
+          outgrown_.push_back(std::move(current_));
+        }
+        current_ = std::make_unique<DeviceBuffer>(std::max<std::size_t>(count, 1 << 16) *
+                                                  sizeof(float));
+      }
+      return current_->as<float>();
+    }
+
+  private:
+    std::unique_ptr<DeviceBuffer> current_;
+    std::vector<std::unique_ptr<DeviceBuffer>> outgrown_;
+  };
+
   struct PageLocation
   {
     int tier;
@@ -399,6 +424,8 @@ namespace mi
     std::vector<unsigned long long> open_uploaded_;
     // Address tables for batched launches, grown as needed.
     std::unique_ptr<DeviceBuffer> batch_table_;
+    // The decode path's split partials and page statistics: this cache's own.
+    OwnedWorkspace workspace_;
   };
 
   // The stream every launch of the runtime goes on, per host thread: the
