@@ -164,6 +164,26 @@ int mi_attention_paged_causal(const void *q, const unsigned long long *sealed,
                               float *mass, float *scores, float alpha, float *partials,
                               void *stream);
 
+/* No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). mi_attention_paged_causal's one-query decode (seq_q 1, no key
+ * bias, split across pages) that allocates nothing: its scratch (split
+ * partials and page statistics) is a static device array of 8 MiB that each
+ * GPU holds until the process ends, instead of library memory. The caller
+ * passes every input and output. Only what the decode fast path takes is
+ * accepted (32-token pages, head_dim 64 or 128, at most 16 query heads a KV
+ * head, 16-byte aligned q, open page and rows); anything else, or a decode
+ * whose scratch would exceed 8 MiB (about 290K positions at Qwen2.5-1.5B's
+ * shape), fails with MI_ERR_INVALID. Nothing in the scratch needs clearing:
+ * every split and page writes its slot before the combine reads it. Every
+ * call on one GPU shares that GPU's array, so calls that overlap on one GPU
+ * (different streams, or threads) race; calls on one stream are ordered. */
+int mi_attention_paged_causal_noalloc(const void *q, const unsigned long long *sealed,
+                                      const uint8_t *tiers, int may_be_at_mask, const void *open,
+                                      const void *chunk_k, const void *chunk_v, int page_tokens,
+                                      void *out, int seq_k, int heads, int kv_heads, int head_dim,
+                                      float *mass, float *scores, float alpha, void *stream);
+
 /* ---- pages, rows and scores ----------------------------------------------
  * reference: page_copy.cu:41-70, kv_pages.cu:47-60, importance_scores.cu:18-50. */
 int mi_copy_pages(const void *const *from, void *const *to, size_t bytes, int count, void *stream);

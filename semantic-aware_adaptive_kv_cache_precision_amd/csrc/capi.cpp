@@ -6,6 +6,7 @@
 #include "runtime.hpp"
 
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -73,6 +74,59 @@ namespace
   {
     return s != nullptr ? static_cast<hipStream_t>(s) : mi::runtime_stream();
   }
+
+  // ---- the allocation-free decode's scratch -------------------------------
+  // A static device array: each GPU the library runs on holds its own copy,
+  // at its own address, until the process ends. Host code never passes the
+  // array's name to a kernel (on the host it is a stand-in, not a device
+  // address): it looks up, once per device with that device current, the
+  // address hipGetSymbolAddress gives, and passes that.
+  constexpr std::size_t kNoAllocScratchBytes = std::size_t{8} << 20;
+  constexpr std::size_t kNoAllocScratchFloats = kNoAllocScratchBytes / sizeof(float);
+  constexpr int kMaxDevices = 64;
+  static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+  float *scratch_on_current_device()
+  {
+    static std::once_flag once[kMaxDevices];
+    static float *address[kMaxDevices] = {};
+    int device = 0;
+    mi::hip_check(hipGetDevice(&device), "hipGetDevice");
+    if (device < 0 || device >= kMaxDevices)
+    {
+      throw mi::InvalidArgument("device " + std::to_string(device) + " is beyond the " +
+                                std::to_string(kMaxDevices) + " the scratch table holds");
+    }
+    std::call_once(once[device], [device] {
+      void *p = nullptr;
+      mi::hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                    "hipGetSymbolAddress of the decode scratch");
+      address[device] = static_cast<float *>(p);
+    });
+    if (address[device] == nullptr)
+    {
+      throw mi::DeviceError("the decode scratch has no address on device " +
+                            std::to_string(device));
+    }
+    return address[device];
+  }
+
+  // Hands the launch the static scratch, and refuses a need beyond it.
+  struct StaticScratch final : mi::WorkspaceSource
+  {
+    float *base;
+    float *floats(std::size_t count) override
+    {
+      if (count > kNoAllocScratchFloats)
+      {
+        throw mi::InvalidArgument(
+            "this decode needs " + std::to_string(count * sizeof(float)) +
+            " bytes of scratch; the allocation-free entry point holds " +
+            std::to_string(kNoAllocScratchBytes) + " (fewer pages or heads fit)");
+      }
+      return base;
+    }
+  };
 
   void need(const void *p, const char *what)
   {
@@ -526,6 +580,45 @@ int mi_attention_paged_causal(const void *q, const unsigned long long *sealed,
       }
     }
     mi::launch_attention(kv, a, as_stream(stream));
+  });
+}
+
+int mi_attention_paged_causal_noalloc(const void *q, const unsigned long long *sealed,
+                                      const uint8_t *tiers, int may_be_at_mask, const void *open,
+                                      const void *chunk_k, const void *chunk_v, int page_tokens,
+                                      void *out, int seq_k, int heads, int kv_heads, int head_dim,
+                                      float *mass, float *scores, float alpha, void *stream)
+{
+  return guarded([&] {
+    mi::AttentionArgs a{};
+    fill_args(a, q, nullptr, nullptr, 0, out, 1, seq_k, heads, kv_heads, head_dim, mass, scores,
+              alpha, nullptr);
+    mi::KVSource kv{};
+    kv.layout = mi::Layout::kCausal;
+    kv.pages = sealed;
+    kv.tiers = tiers;
+    kv.open = static_cast<const std::uint16_t *>(open);
+    kv.chunk_k = static_cast<const std::uint16_t *>(chunk_k);
+    kv.chunk_v = static_cast<const std::uint16_t *>(chunk_v);
+    kv.page_tokens = page_tokens;
+    kv.start = seq_k - 1;
+    for (int t = 0; t < mi::kTierCount; ++t)
+    {
+      kv.may_be_at[t] = (may_be_at_mask >> t) & 1;
+    }
+    if (!mi::decode_fast_applies(kv, a))
+    {
+      throw mi::InvalidArgument(
+          "the allocation-free decode takes one query over 32-token pages at head_dim 64 or 128, "
+          "at most 16 query heads a KV head, with 16-byte aligned q, open page and rows");
+    }
+    StaticScratch ws;
+    ws.base = scratch_on_current_device();
+    a.workspace = &ws;
+    mi::DecodeLayers one{};
+    one.split = true;
+    one.layers = 1;
+    mi::launch_decode_layers(kv, a, one, as_stream(stream));
   });
 }
 

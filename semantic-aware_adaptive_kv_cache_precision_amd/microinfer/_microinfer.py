@@ -83,6 +83,8 @@ SIGNATURES = {
                            C.c_int),
     "mi_attention_paged_causal": ((_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _i,
                                    _i, _i, _i, _i, _vp, _vp, _f, _vp, _vp), C.c_int),
+    "mi_attention_paged_causal_noalloc": ((_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i,
+                                           _i, _i, _vp, _vp, _f, _vp), C.c_int),
     "mi_copy_pages": ((_vp, _vp, _sz, _i, _vp), C.c_int),
     "mi_store_pages": ((_vp, _vp, _vp, _i, _sz, _i, _i, _vp), C.c_int),
     "mi_fill_f32": ((_vp, _sz, _f, _vp), C.c_int),
