@@ -19,6 +19,92 @@ namespace mi
   void launch_dequantise_page(const void *page, void *keys, void *values, int tier,
                               int page_tokens, int kv_heads, int head_dim, hipStream_t stream);
 
+  // ---- page jobs by reference (page_jobs.hip) -----------------------------------
+  // A page's place as 32 bits: the space that holds it (bits 29-31) and its
+  // index there. Spaces 0-3 are the allocator's four tier ranges (the index
+  // a slot), space 4 the FP16 shadows in pinned host memory (the index a
+  // shadow number). Kernels turn a reference into an address themselves, so
+  // a batch sends 8 bytes a page pair to the device, not two addresses.
+  constexpr int kShadowSpace = 4;
+  constexpr unsigned kRefIndexBits = 29;
+  constexpr std::uint32_t kRefIndexMask = (1u << kRefIndexBits) - 1;
+  __host__ __device__ constexpr std::uint32_t page_ref(int space, std::uint32_t index)
+  {
+    return (static_cast<std::uint32_t>(space) << kRefIndexBits) | index;
+  }
+
+  // Where the spaces are: each tier range's base and page size (fixed for an
+  // allocator's life), and the device table of the shadows' mapped addresses.
+  struct PageSpaces
+  {
+    unsigned long long base[kTierCount];
+    unsigned long long bytes[kTierCount];
+    const unsigned long long *shadows; // shadow number -> device address
+    unsigned long long shadow_bytes;   // an FP16 page
+  };
+
+  struct RefPair
+  {
+    std::uint32_t from;
+    std::uint32_t to;
+  };
+
+  // Copies pair i's page from `from` to `to`: the destination space's page
+  // size (an FP16 page when either side is a shadow). No copy may read
+  // what another writes.
+  void launch_copy_refs(const RefPair *pairs, int count, const PageSpaces &spaces,
+                        hipStream_t stream);
+  // Quantises pair i's FP16 page (a slot of the FP16 range, or a shadow) to
+  // `tier` into its destination slot. head_dim 64 or 128, 32-token pages and
+  // kv_heads * head_dim >= 128 take the register quantiser (a lane a task of
+  // 64 elements, nothing staged); any other shape the LDS one.
+  void launch_requant_refs(const RefPair *pairs, int count, int tier, const PageSpaces &spaces,
+                           int page_tokens, int kv_heads, int head_dim, hipStream_t stream);
+
+  // A job on one page's rows, as a cache's store makes them. A page's keys
+  // are rows of kv_heads * head_dim fp16; rows [0, split) come from k_lo /
+  // v_lo (an open page's), rows [split, P) from k_hi / v_hi (the rows the
+  // store brought), row t at k_hi + (t - split) * width.
+  enum class RowJobKind : int
+  {
+    kQuantise = 0,  // seal at `tier` into the page at dst
+    kCopy = 1,      // seal at FP16: the rows as they are
+    kRoundKeys = 2, // the diagnostic Halves: keys through `tier` and back, values as they are
+    kRoundValues = 3,
+    kFill = 4,      // rows [0, rows) of k_hi / v_hi to rows [dst_row, dst_row + rows) of an
+                    // open page at dst
+  };
+  struct RowJob
+  {
+    const std::uint16_t *k_lo;
+    const std::uint16_t *v_lo;
+    const std::uint16_t *k_hi;
+    const std::uint16_t *v_hi;
+    std::uint8_t *dst;
+    int split;
+    int kind;
+    int tier;
+    int rows;
+    int dst_row;
+    int pad;
+  };
+  constexpr int kRowJobsALaunch = 24;
+  // The jobs of one store, every kind in one launch (in launches of
+  // kRowJobsALaunch, passed by value: a decode step's store sends nothing
+  // ahead of its launch).
+  void launch_row_jobs(const RowJob *jobs, int count, int page_tokens, int kv_heads, int head_dim,
+                       hipStream_t stream);
+
+  // Page table edits: entry `index` of the address and tier arrays set.
+  struct TableEdit
+  {
+    unsigned long long address;
+    std::uint32_t index;
+    std::uint32_t tier;
+  };
+  void launch_table_edits(const TableEdit *edits, int count, unsigned long long *addresses,
+                          std::uint8_t *tiers, hipStream_t stream);
+
   // ---- pages and scores (pages.hip) ----------------------------------------------
   // from[i] -> to[i], `bytes` each, `count` pages, one launch; tables on the
   // device. No copy may read what another writes.

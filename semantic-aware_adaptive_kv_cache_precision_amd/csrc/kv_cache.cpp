@@ -1,0 +1,996 @@
+// KVPages, the cache manager: pages reserved per layer, rows stored and
+// sealed, decode and chunk attention over the page tables, tier moves.
+//
+// Contract (reference: src/core_kernels/kv_pages.h and kv_pages.cu): a page
+// is born at its tier (the tier map's, else the cache's) and sealed when its
+// last row arrives; a cache that seals keeps each layer's partial page in
+// one of two FP16 open pages; a page at tier T always holds quantise_page of
+// its FP16 rows at T, and a page back at FP16 its FP16 shadow; a batch of
+// moves leaves every byte, tier and shadow as the same moves one at a time;
+// a refused call changes nothing.
+//
+// How it is done here (this build's own design):
+//   - page tables: the device copy is edited, not rebuilt. The allocator
+//     reports each page whose slot changes (PlacementObserver); the cache
+//     sets that entry in a host mirror and marks it, and the next launch
+//     that reads the tables first sends the marked entries (one small copy
+//     and a scatter launch, or the whole table when that is smaller);
+//   - a store is one launch: every page it seals (quantised at its birth
+//     tier from the open page's rows and the rows just brought, or copied at
+//     FP16) and the rows it leaves in an open page, as row jobs passed by
+//     value;
+//   - a batch of moves sends the device 8 bytes a page pair: 32-bit
+//     references to a tier slot or a shadow number, from which the kernels
+//     form addresses; shadows out, restores, one quantise launch per target
+//     tier, then the allocator's compaction, all queued on one stream with
+//     one wait at the end; the single-page downgrade and upgrade are a batch
+//     of one.
+
+#include "runtime.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+
+namespace mi
+{
+  namespace
+  {
+    using Clock = std::chrono::steady_clock;
+
+    double since(Clock::time_point t)
+    {
+      return std::chrono::duration<double>(Clock::now() - t).count();
+    }
+  } // namespace
+
+  // ---- PageTable --------------------------------------------------------------------
+
+  void PageTable::ensure(int pages)
+  {
+    if (pages <= stride_)
+    {
+      return;
+    }
+    const int grown = std::max(pages, 2 * stride_);
+    std::vector<unsigned long long> address(static_cast<std::size_t>(layers_) * grown, 0);
+    std::vector<std::uint8_t> tier(address.size(), kUnreadPage);
+    for (int l = 0; l < layers_; ++l)
+    {
+      std::copy_n(address_.begin() + static_cast<std::ptrdiff_t>(l) * stride_, stride_,
+                  address.begin() + static_cast<std::ptrdiff_t>(l) * grown);
+      std::copy_n(tier_.begin() + static_cast<std::ptrdiff_t>(l) * stride_, stride_,
+                  tier.begin() + static_cast<std::ptrdiff_t>(l) * grown);
+    }
+    address_.swap(address);
+    tier_.swap(tier);
+    stride_ = grown;
+    dirty_.assign(address_.size(), 0);
+    marked_.clear();
+    // The device copy is made anew, whole (the old one may still be read by
+    // a queued launch: its free waits for the device).
+    device_.reset();
+    device_ = std::make_unique<DeviceBuffer>(address_.size() * (sizeof(unsigned long long) + 1));
+    whole_ = true;
+  }
+
+  void PageTable::set(int layer, int page, unsigned long long address, std::uint8_t tier)
+  {
+    const std::size_t at = static_cast<std::size_t>(layer) * stride_ + page;
+    address_[at] = address;
+    tier_[at] = tier;
+    if (!whole_ && !dirty_[at])
+    {
+      dirty_[at] = 1;
+      marked_.push_back(static_cast<std::uint32_t>(at));
+    }
+  }
+
+  void PageTable::commit(hipStream_t stream)
+  {
+    if (device_ == nullptr)
+    {
+      return;
+    }
+    const std::size_t n = address_.size();
+    // An edit is 16 bytes and a launch; the whole table 9 bytes an entry.
+    if (!whole_ && marked_.size() * 16 > n * 9)
+    {
+      whole_ = true;
+    }
+    if (whole_)
+    {
+      hip_check(hipMemcpyAsync(device_->raw(), address_.data(), n * sizeof(unsigned long long),
+                               hipMemcpyHostToDevice, stream),
+                "hipMemcpyAsync page addresses");
+      hip_check(hipMemcpyAsync(device_->as<unsigned long long>() + n, tier_.data(), n,
+                               hipMemcpyHostToDevice, stream),
+                "hipMemcpyAsync page tiers");
+      whole_ = false;
+    }
+    else if (!marked_.empty())
+    {
+      std::vector<TableEdit> edits;
+      edits.reserve(marked_.size());
+      for (const std::uint32_t at : marked_)
+      {
+        edits.push_back({address_[at], at, tier_[at]});
+      }
+      launch_table_edits(edit_upload_.send(edits, stream), static_cast<int>(edits.size()),
+                         device_->as<unsigned long long>(),
+                         reinterpret_cast<std::uint8_t *>(device_->as<unsigned long long>() + n),
+                         stream);
+    }
+    for (const std::uint32_t at : marked_)
+    {
+      dirty_[at] = 0;
+    }
+    marked_.clear();
+  }
+
+  // ---- KVPages: set-up --------------------------------------------------------------
+
+  bool KVPages::seals_for(int tier, const TierMap &tier_map, bool always_seal)
+  {
+    // Only a cache all of whose pages stay FP16 can leave its last page in
+    // the page table, partly written.
+    if (always_seal || tier != kFP16)
+    {
+      return true;
+    }
+    return std::any_of(tier_map.begin(), tier_map.end(), [tier](const std::vector<int> &row) {
+      return std::any_of(row.begin(), row.end(), [tier](int t) { return t != tier; });
+    });
+  }
+
+  KVPages::KVPages(PagedKVCache &allocator, int layers, int page_tokens, int kv_heads,
+                   int head_dim, int tier, Halves halves, TierMap tier_map, bool always_seal)
+      : allocator_(allocator), layers_(layers), page_tokens_(page_tokens), kv_heads_(kv_heads),
+        head_dim_(head_dim), kv_width_(static_cast<std::size_t>(std::max(kv_heads, 0)) *
+                                       std::max(head_dim, 0)),
+        tier_(tier), halves_(halves),
+        storage_tier_(tier != kFP16 && halves != Halves::kBoth ? kFP16 : tier),
+        tier_map_(std::move(tier_map)), shadows_(fp16_page_bytes(std::max(page_tokens, 0), kv_width_)),
+        table_(std::max(layers, 0))
+  {
+    if (layers <= 0 || page_tokens <= 0 || kv_heads <= 0 || head_dim <= 0)
+    {
+      throw InvalidArgument("layers, page_tokens, kv_heads and head_dim must be positive");
+    }
+    if (tier < 0 || tier >= kTierCount)
+    {
+      throw InvalidArgument("tier " + std::to_string(tier) + " is not one of the four");
+    }
+    if (tier == kFP16 && halves != Halves::kBoth)
+    {
+      throw InvalidArgument("only a quantised tier can quantise one half of a page");
+    }
+    if (!tier_map_.empty() && static_cast<int>(tier_map_.size()) != layers)
+    {
+      throw InvalidArgument("a tier map needs a row for every layer: " +
+                            std::to_string(tier_map_.size()) + " rows for " +
+                            std::to_string(layers) + " layers");
+    }
+    if (!tier_map_.empty() && halves != Halves::kBoth)
+    {
+      throw InvalidArgument("a diagnostic Halves rounds every page at the cache's one tier, and "
+                            "takes no tier map");
+    }
+    may_be_at_[storage_tier_] = true;
+    for (const auto &row : tier_map_)
+    {
+      for (const int t : row)
+      {
+        if (t < 0 || t >= kTierCount)
+        {
+          throw InvalidArgument("a tier map names tier " + std::to_string(t) +
+                                ", not one of the four");
+        }
+        may_be_at_[t] = true;
+        mixed_ = mixed_ || t != tier;
+      }
+    }
+    seals_ = seals_for(tier, tier_map_, always_seal);
+    page_bytes_ = bytes_at(storage_tier_);
+    for (int t = 0; t < kTierCount; ++t)
+    {
+      if (may_be_at_[t])
+      {
+        require_page_size(t, "a page of positions");
+      }
+    }
+    if (seals_)
+    {
+      require_page_size(kFP16, "an open page");
+    }
+    if (halves != Halves::kBoth)
+    {
+      // The diagnostic's round trip needs the tier's layout.
+      page_layout(tier, page_tokens, kv_heads, head_dim);
+    }
+    current_open_.assign(layers, 0);
+    attend_open_.assign(layers, 0);
+    sealed_.assign(layers, 0);
+    open_address_.assign(2 * static_cast<std::size_t>(layers), 0);
+    allocator_.watch(this);
+  }
+
+  KVPages::~KVPages()
+  {
+    allocator_.unwatch(this);
+    try
+    {
+      // Newest first, so that each free takes its tier's last page.
+      for (int page = pages_ - 1; page >= 0; --page)
+      {
+        for (int layer = layers_ - 1; layer >= 0; --layer)
+        {
+          if (!evicted({layer, page}))
+          {
+            allocator_.free({layer, page});
+          }
+        }
+      }
+      if (open_pages_)
+      {
+        for (int k = 1; k >= 0; --k)
+        {
+          for (int layer = layers_ - 1; layer >= 0; --layer)
+          {
+            allocator_.free({layer, kOpenPages[k]});
+          }
+        }
+      }
+    }
+    catch (...)
+    {
+    }
+  }
+
+  void KVPages::require_layer(int layer) const
+  {
+    if (layer < 0 || layer >= layers_)
+    {
+      throw OutOfRange("layer " + std::to_string(layer) + " of " + std::to_string(layers_));
+    }
+  }
+
+  std::size_t KVPages::bytes_at(int tier) const
+  {
+    return page_bytes_at(tier, page_tokens_, kv_heads_, head_dim_);
+  }
+
+  void KVPages::require_page_size(int tier, const char *what) const
+  {
+    const std::size_t needed = bytes_at(tier);
+    if (allocator_.page_bytes(tier) != needed)
+    {
+      throw InvalidArgument(std::string("the allocator's ") + tier_name(tier) + " pages hold " +
+                            std::to_string(allocator_.page_bytes(tier)) + " bytes; " + what +
+                            " of " + std::to_string(page_tokens_) + " positions at " +
+                            std::to_string(kv_width_) + " elements needs " +
+                            std::to_string(needed));
+    }
+  }
+
+  int KVPages::birth_tier(int layer, int page) const
+  {
+    if (layer >= 0 && layer < static_cast<int>(tier_map_.size()) && page >= 0 &&
+        page < static_cast<int>(tier_map_[layer].size()))
+    {
+      return tier_map_[layer][page];
+    }
+    return storage_tier_;
+  }
+
+  std::string KVPages::page_name(PageKey key)
+  {
+    return "page " + std::to_string(key.page) + " of layer " + std::to_string(key.layer);
+  }
+
+  // ---- the tables follow the allocator ------------------------------------------------
+
+  void KVPages::placed(PageKey key, int tier, std::size_t slot)
+  {
+    if (key.layer < 0 || key.layer >= layers_)
+    {
+      return;
+    }
+    const auto address =
+        reinterpret_cast<unsigned long long>(allocator_.address_of({tier, slot}));
+    if (key.page == kOpenPages[0] || key.page == kOpenPages[1])
+    {
+      open_address_[2 * static_cast<std::size_t>(key.layer) + (key.page == kOpenPages[0] ? 0 : 1)] =
+          address;
+      return;
+    }
+    if (key.page >= 0 && key.page < table_.stride())
+    {
+      const bool unread = flag(key, kMasked) || flag(key, kEvicted);
+      table_.set(key.layer, key.page, address,
+                 unread ? kUnreadPage : static_cast<std::uint8_t>(tier));
+    }
+  }
+
+  void KVPages::removed(PageKey key)
+  {
+    if (key.layer >= 0 && key.layer < layers_ && key.page >= 0 && key.page < table_.stride())
+    {
+      table_.set(key.layer, key.page, 0, kUnreadPage);
+    }
+  }
+
+  void KVPages::set_flag(PageKey key, std::uint8_t bit)
+  {
+    flags_[static_cast<std::size_t>(key.layer) * flag_stride_ + key.page] |= bit;
+  }
+
+  void KVPages::grow(int pages)
+  {
+    if (pages > flag_stride_)
+    {
+      const int grown = std::max(pages, 2 * flag_stride_);
+      std::vector<std::uint8_t> flags(static_cast<std::size_t>(layers_) * grown, 0);
+      for (int l = 0; l < layers_; ++l)
+      {
+        std::copy_n(flags_.begin() + static_cast<std::ptrdiff_t>(l) * flag_stride_, flag_stride_,
+                    flags.begin() + static_cast<std::ptrdiff_t>(l) * grown);
+      }
+      flags_.swap(flags);
+      flag_stride_ = grown;
+    }
+    const int old_stride = table_.stride();
+    table_.ensure(pages);
+    if (table_.stride() != old_stride)
+    {
+      // A new table: every page held so far written into it.
+      for (int l = 0; l < layers_; ++l)
+      {
+        for (int p = 0; p < pages_; ++p)
+        {
+          refresh_entry(l, p);
+        }
+      }
+    }
+  }
+
+  void KVPages::refresh_entry(int layer, int page)
+  {
+    const PageKey key{layer, page};
+    if (!allocator_.contains(key))
+    {
+      table_.set(layer, page, 0, kUnreadPage);
+      return;
+    }
+    const PageLocation at = allocator_.locate(key);
+    table_.set(layer, page, reinterpret_cast<unsigned long long>(allocator_.address_of(at)),
+               masked(key) ? kUnreadPage : static_cast<std::uint8_t>(at.tier));
+  }
+
+  void KVPages::sync_tables(hipStream_t stream) { table_.commit(stream); }
+
+  // ---- reserve and store ---------------------------------------------------------------
+
+  void KVPages::reserve(int tokens)
+  {
+    const int needed = seals_ ? tokens / page_tokens_ : (tokens + page_tokens_ - 1) / page_tokens_;
+    // Table room first, so the allocator's reports land in it.
+    grow(std::max(needed, pages_));
+    // Open pages (all of the first, then all of the second), then each new
+    // page of positions for every layer, at its birth tier; the pages of one
+    // tier are allocated in this order in one call.
+    std::vector<PageKey> taken;
+    try
+    {
+      if (seals_ && !open_pages_ && tokens > 0)
+      {
+        std::vector<PageKey> open;
+        for (const int page : kOpenPages)
+        {
+          for (int layer = 0; layer < layers_; ++layer)
+          {
+            open.push_back({layer, page});
+          }
+        }
+        allocator_.allocate_run(open, kFP16);
+        taken.insert(taken.end(), open.begin(), open.end());
+      }
+      std::array<std::vector<PageKey>, kTierCount> runs;
+      for (int page = pages_; page < needed; ++page)
+      {
+        for (int layer = 0; layer < layers_; ++layer)
+        {
+          runs[birth_tier(layer, page)].push_back({layer, page});
+        }
+      }
+      for (int t = 0; t < kTierCount; ++t)
+      {
+        allocator_.allocate_run(runs[t], t);
+        taken.insert(taken.end(), runs[t].begin(), runs[t].end());
+      }
+    }
+    catch (...)
+    {
+      // Every page taken is its tier's latest: giving them back moves none.
+      allocator_.free_pages(taken);
+      throw;
+    }
+    if (seals_ && tokens > 0)
+    {
+      open_pages_ = true;
+    }
+    pages_ = std::max(needed, pages_);
+  }
+
+  void KVPages::store(int layer, const void *keys, const void *values, int start, int n)
+  {
+    if (start < 0 || n < 0 || start + n > capacity_tokens())
+    {
+      throw OutOfRange("positions [" + std::to_string(start) + ", " + std::to_string(start + n) +
+                       ") are not all on pages; " + std::to_string(capacity_tokens()) +
+                       " positions are reserved");
+    }
+    require_layer(layer);
+    if (n == 0)
+    {
+      return;
+    }
+    const hipStream_t stream = runtime_stream();
+    if (seals_)
+    {
+      store_sealed(layer, static_cast<const std::uint16_t *>(keys),
+                   static_cast<const std::uint16_t *>(values), start, n);
+      return;
+    }
+    sync_tables(stream);
+    launch_store_pages(keys, values, table_.addresses() + static_cast<std::size_t>(layer) * table_.stride(),
+                       page_tokens_, kv_width_, start, n, stream);
+  }
+
+  void KVPages::store_sealed(int layer, const std::uint16_t *keys, const std::uint16_t *values,
+                             int start, int n)
+  {
+    const std::size_t W = kv_width_;
+    const std::size_t half = static_cast<std::size_t>(page_tokens_) * W;
+    const int cur = current_open_[layer];
+    attend_open_[layer] = cur;
+    const int first_span = start / page_tokens_;
+    const int end = start + n;
+    std::vector<RowJob> jobs;
+    for (int span = first_span; span * page_tokens_ < end; ++span)
+    {
+      const int span_start = span * page_tokens_;
+      const int a = std::max(start, span_start);
+      const int b = std::min(end, span_start + page_tokens_);
+      const std::uint16_t *k_rows = keys + static_cast<std::size_t>(a - start) * W;
+      const std::uint16_t *v_rows = values + static_cast<std::size_t>(a - start) * W;
+      RowJob j{};
+      if (b == span_start + page_tokens_)
+      {
+        // The page's last row is here: it is sealed from the rows the open
+        // page holds before `a` and the rows brought from `a` on.
+        const PageKey key{layer, span};
+        const PageLocation at = allocator_.locate(key);
+        const std::uint16_t *open = open_page(layer, cur);
+        j.k_lo = open;
+        j.v_lo = open + half;
+        j.k_hi = k_rows;
+        j.v_hi = v_rows;
+        j.split = a - span_start;
+        j.dst = reinterpret_cast<std::uint8_t *>(allocator_.address_of(at));
+        j.tier = halves_ != Halves::kBoth ? tier_ : at.tier;
+        if (halves_ == Halves::kKeys)
+        {
+          j.kind = static_cast<int>(RowJobKind::kRoundKeys);
+        }
+        else if (halves_ == Halves::kValues)
+        {
+          j.kind = static_cast<int>(RowJobKind::kRoundValues);
+        }
+        else
+        {
+          j.kind = static_cast<int>(at.tier == kFP16 ? RowJobKind::kCopy : RowJobKind::kQuantise);
+        }
+        sealed_[layer] = std::max(sealed_[layer], span + 1);
+      }
+      else
+      {
+        // A partial page: its rows wait in an open page, the current one if
+        // the page was begun before this store, else the other.
+        const int which = span == first_span ? cur : 1 - cur;
+        j.kind = static_cast<int>(RowJobKind::kFill);
+        j.k_lo = j.k_hi = k_rows;
+        j.v_lo = j.v_hi = v_rows;
+        j.split = 0;
+        j.rows = b - a;
+        j.dst_row = a - span_start;
+        j.dst = reinterpret_cast<std::uint8_t *>(open_page(layer, which));
+        j.tier = kFP16;
+        current_open_[layer] = which;
+      }
+      jobs.push_back(j);
+    }
+    launch_row_jobs(jobs.data(), static_cast<int>(jobs.size()), page_tokens_, kv_heads_,
+                    head_dim_, runtime_stream());
+  }
+
+  // ---- evict, mask ---------------------------------------------------------------------
+
+  PageKey KVPages::require_movable(int layer, int page, const char *verb) const
+  {
+    if (!seals_)
+    {
+      throw InvalidArgument(std::string("only a cache that seals can ") + verb +
+                            " a page: in one that does not, every page is FP16 and its last is "
+                            "still being written");
+    }
+    if (halves_ != Halves::kBoth)
+    {
+      throw InvalidArgument(std::string("a diagnostic Halves stores every page at FP16 by its "
+                                        "definition; none can ") +
+                            verb);
+    }
+    require_layer(layer);
+    if (page < 0 || page >= pages_)
+    {
+      throw InvalidArgument(page_name({layer, page}) +
+                            " is not a page of positions this cache holds; only one of those moves");
+    }
+    if (page >= sealed_[layer])
+    {
+      throw InvalidArgument(page_name({layer, page}) +
+                            " is not sealed: its positions are reserved, not all stored");
+    }
+    return {layer, page};
+  }
+
+  PageKey KVPages::require_held(int layer, int page, const char *verb) const
+  {
+    const PageKey key = require_movable(layer, page, verb);
+    if (evicted(key))
+    {
+      throw InvalidArgument(page_name(key) + " is evicted: its positions are gone, and nothing can " +
+                            verb + " it");
+    }
+    return key;
+  }
+
+  void KVPages::evict(int layer, int page)
+  {
+    const PageKey key = require_held(layer, page, "evict");
+    if (masked(key))
+    {
+      throw InvalidArgument(page_name(key) +
+                            " is masked, the reference an eviction is measured against; evict "
+                            "another cache's page");
+    }
+    set_flag(key, kEvicted);
+    allocator_.free(key); // its entry turns unread as the allocator reports it gone
+  }
+
+  void KVPages::mask(int layer, int page)
+  {
+    const PageKey key = require_held(layer, page, "mask");
+    set_flag(key, kMasked);
+    refresh_entry(layer, page);
+  }
+
+  // ---- tier moves ----------------------------------------------------------------------
+
+  void KVPages::downgrade(int layer, int page, int target)
+  {
+    const PageKey key = require_held(layer, page, "downgrade");
+    if (target < 0 || target >= kTierCount)
+    {
+      throw InvalidArgument("tier " + std::to_string(target) + " is not one of the four");
+    }
+    const int current = page_tier(key);
+    if (!is_lower(target, current))
+    {
+      throw InvalidArgument(page_name(key) + " is at " + tier_name(current) +
+                            "; a downgrade is to a lower tier, and " + tier_name(target) +
+                            " is not");
+    }
+    if (current != kFP16 && !shadows_.contains(key))
+    {
+      throw InvalidArgument(page_name(key) + " was born at " + tier_name(current) +
+                            " and has no FP16 shadow to quantise from; only a page sealed at "
+                            "FP16 downgrades");
+    }
+    require_page_size(target, "a page of positions");
+    hip_check(hipStreamSynchronize(runtime_stream()), "hipStreamSynchronize before a move");
+    const Clock::time_point began = Clock::now();
+    double shadow_seconds = 0.0;
+    run_moves({key}, {current}, {target}, &shadow_seconds);
+    last_move_ = MoveRecord{key, current, target, bytes_at(current), bytes_at(target),
+                            since(began), shadow_seconds};
+  }
+
+  void KVPages::upgrade(int layer, int page, int target)
+  {
+    const PageKey key = require_held(layer, page, "upgrade");
+    if (target < 0 || target >= kTierCount)
+    {
+      throw InvalidArgument("tier " + std::to_string(target) + " is not one of the four");
+    }
+    const int current = page_tier(key);
+    if (!is_lower(current, target))
+    {
+      throw InvalidArgument(page_name(key) + " is at " + tier_name(current) +
+                            "; an upgrade is to a higher tier, and " + tier_name(target) +
+                            " is not");
+    }
+    if (!shadows_.contains(key))
+    {
+      throw InvalidArgument(page_name(key) + " was born at " + tier_name(current) +
+                            " and has no FP16 shadow to restore it from");
+    }
+    require_page_size(target, "a page of positions");
+    hip_check(hipStreamSynchronize(runtime_stream()), "hipStreamSynchronize before a move");
+    const Clock::time_point began = Clock::now();
+    double shadow_seconds = 0.0;
+    run_moves({key}, {current}, {target}, &shadow_seconds);
+    last_move_ = MoveRecord{key, current, target, bytes_at(current), bytes_at(target),
+                            since(began), shadow_seconds};
+  }
+
+  void KVPages::move_pages(const std::vector<PageMove> &moves)
+  {
+    std::vector<PageKey> keys;
+    std::vector<int> from, targets;
+    std::vector<std::uint64_t> named;
+    keys.reserve(moves.size());
+    for (const PageMove &m : moves)
+    {
+      const PageKey key = require_held(m.key.layer, m.key.page, "move");
+      named.push_back(pack(key));
+      if (m.target < 0 || m.target >= kTierCount)
+      {
+        throw InvalidArgument("tier " + std::to_string(m.target) + " is not one of the four");
+      }
+      const int now = page_tier(key);
+      if (now == m.target)
+      {
+        throw InvalidArgument(page_name(key) + " is already at " + tier_name(now));
+      }
+      if (now != kFP16 && !shadows_.contains(key))
+      {
+        throw InvalidArgument(page_name(key) + " was born at " + tier_name(now) +
+                              " and has no FP16 shadow to move from; only a page sealed at FP16 "
+                              "moves");
+      }
+      require_page_size(m.target, "a page of positions");
+      keys.push_back(key);
+      from.push_back(now);
+      targets.push_back(m.target);
+    }
+    std::sort(named.begin(), named.end());
+    const auto dup = std::adjacent_find(named.begin(), named.end());
+    if (dup != named.end())
+    {
+      throw InvalidArgument(page_name(unpack(*dup)) +
+                            " is named twice in one batch; a batch moves a page once, to the "
+                            "tier it ends at");
+    }
+    hip_check(hipStreamSynchronize(runtime_stream()), "hipStreamSynchronize before a batch");
+    const Clock::time_point began = Clock::now();
+    const std::size_t shadows_before = shadows_.count();
+    if (!keys.empty())
+    {
+      run_moves(keys, from, targets, nullptr);
+    }
+    last_batch_ = BatchRecord{keys.size(), shadows_.count() - shadows_before, since(began)};
+  }
+
+  void KVPages::run_moves(const std::vector<PageKey> &keys, const std::vector<int> &from,
+                          const std::vector<int> &targets, double *shadow_seconds)
+  {
+    const hipStream_t stream = runtime_stream();
+    const std::size_t n = keys.size();
+    // 1. Every new page under a staging key of its own, a tier's pages in
+    // one allocator call; and pinned room for the shadows first downgrades
+    // take. A failure here gives back what was taken and changes nothing.
+    std::vector<PageKey> staged(n);
+    std::array<std::vector<PageKey>, kTierCount> runs;
+    for (std::size_t i = 0; i < n; ++i)
+    {
+      staged[i] = {keys[i].layer, kBatchStagingPage - static_cast<int>(i)};
+      runs[targets[i]].push_back(staged[i]);
+    }
+    std::vector<PageKey> taken;
+    std::size_t first_downgrades = 0;
+    for (std::size_t i = 0; i < n; ++i)
+    {
+      first_downgrades += from[i] == kFP16 && !shadows_.contains(keys[i]);
+    }
+    try
+    {
+      for (int t = 0; t < kTierCount; ++t)
+      {
+        allocator_.allocate_run(runs[t], t);
+        taken.insert(taken.end(), runs[t].begin(), runs[t].end());
+      }
+      shadows_.reserve(first_downgrades);
+    }
+    catch (...)
+    {
+      allocator_.free_pages(taken);
+      throw;
+    }
+
+    // 2. The device's work, by page reference: shadows out, restores in, one
+    // quantise launch per target tier, each reading pages before any is
+    // freed.
+    std::vector<RefPair> shadows_out, restores;
+    std::array<std::vector<RefPair>, kTierCount> requant;
+    bool touches_shadow = false;
+    for (std::size_t i = 0; i < n; ++i)
+    {
+      const std::uint32_t to = allocator_.ref_of(staged[i]);
+      std::uint32_t rows;
+      if (from[i] == kFP16)
+      {
+        rows = allocator_.ref_of(keys[i]);
+        if (!shadows_.contains(keys[i]))
+        {
+          shadows_out.push_back({rows, page_ref(kShadowSpace, shadows_.add(keys[i]))});
+        }
+      }
+      else
+      {
+        rows = page_ref(kShadowSpace, shadows_.number(keys[i]));
+        touches_shadow = true;
+      }
+      if (targets[i] == kFP16)
+      {
+        restores.push_back({rows, to});
+      }
+      else
+      {
+        requant[targets[i]].push_back({rows, to});
+      }
+    }
+    touches_shadow = touches_shadow || !shadows_out.empty();
+    std::vector<RefPair> all;
+    all.reserve(2 * n);
+    all.insert(all.end(), shadows_out.begin(), shadows_out.end());
+    all.insert(all.end(), restores.begin(), restores.end());
+    for (const auto &r : requant)
+    {
+      all.insert(all.end(), r.begin(), r.end());
+    }
+    PageSpaces spaces = allocator_.spaces();
+    spaces.shadows = shadows_.device_table(stream);
+    const Clock::time_point device_began = Clock::now();
+    const RefPair *on_device = pairs_upload_.send(all, stream);
+    std::size_t at = 0;
+    launch_copy_refs(on_device + at, static_cast<int>(shadows_out.size()), spaces, stream);
+    at += shadows_out.size();
+    launch_copy_refs(on_device + at, static_cast<int>(restores.size()), spaces, stream);
+    at += restores.size();
+    for (int t = kINT8; t <= kINT2; ++t)
+    {
+      launch_requant_refs(on_device + at, static_cast<int>(requant[t].size()), t, spaces,
+                          page_tokens_, kv_heads_, head_dim_, stream);
+      at += requant[t].size();
+    }
+    if (shadow_seconds != nullptr)
+    {
+      // A single move reports what its shadow's trip over the host link
+      // took: the device work that reads or writes the shadow.
+      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize after a move's copies");
+      *shadow_seconds = touches_shadow ? since(device_began) : 0.0;
+    }
+
+    // 3. The page table names the new pages; the old ones go together.
+    std::vector<std::pair<PageKey, PageKey>> pairs(n);
+    for (std::size_t i = 0; i < n; ++i)
+    {
+      pairs[i] = {keys[i], staged[i]};
+      may_be_at_[targets[i]] = true;
+    }
+    allocator_.replace_pages(pairs);
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize after a batch");
+  }
+
+  // ---- attention ---------------------------------------------------------------------
+
+  const unsigned long long *KVPages::open_table(hipStream_t stream)
+  {
+    std::vector<unsigned long long> now(static_cast<std::size_t>(layers_));
+    for (int l = 0; l < layers_; ++l)
+    {
+      now[l] = open_address_[2 * static_cast<std::size_t>(l) + attend_open_[l]];
+    }
+    if (open_table_ == nullptr)
+    {
+      open_table_ = std::make_unique<DeviceBuffer>(now.size() * sizeof(unsigned long long));
+    }
+    if (now != open_uploaded_)
+    {
+      hip_check(hipMemcpyAsync(open_table_->raw(), now.data(), now.size() * sizeof(unsigned long long),
+                               hipMemcpyHostToDevice, stream),
+                "hipMemcpyAsync open-page table");
+      open_uploaded_ = now;
+    }
+    return open_table_->as<const unsigned long long>();
+  }
+
+  void KVPages::attention(int layer, const void *q, const void *k_bias, const RopeTable *rope,
+                          void *out, int seq_q, int seq_k, int heads, int kv_heads, int head_dim,
+                          const void *keys, const void *values, float *mass, float *scores,
+                          float alpha, float *partials)
+  {
+    if (static_cast<std::size_t>(kv_heads) * head_dim != kv_width_)
+    {
+      throw InvalidArgument("kv_heads * head_dim is " + std::to_string(kv_heads * head_dim) +
+                            "; this cache holds " + std::to_string(kv_width_) + " per token");
+    }
+    if (seq_k < 0 || seq_k > capacity_tokens())
+    {
+      throw OutOfRange("seq_k " + std::to_string(seq_k) + " exceeds the " +
+                       std::to_string(capacity_tokens()) + " positions on pages");
+    }
+    require_layer(layer);
+    if (seq_q <= 0)
+    {
+      return;
+    }
+    if (k_bias != nullptr && (rope == nullptr || rope->head_dim() != head_dim))
+    {
+      throw InvalidArgument("a key bias needs a RoPE table for head_dim " +
+                            std::to_string(head_dim) + " covering " + std::to_string(seq_k) +
+                            " positions");
+    }
+    const hipStream_t stream = runtime_stream();
+    AttentionArgs a{};
+    a.q = static_cast<const std::uint16_t *>(q);
+    a.out = static_cast<std::uint16_t *>(out);
+    a.k_bias = static_cast<const std::uint16_t *>(k_bias);
+    a.rope = k_bias != nullptr ? rope->data() : nullptr;
+    a.rope_positions = k_bias != nullptr ? rope->positions() : 0;
+    a.rope_angles = k_bias != nullptr ? rope->angles() : nullptr;
+    a.seq_q = seq_q;
+    a.seq_k = seq_k;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.mass = mass;
+    a.scores = scores;
+    a.alpha = alpha;
+    a.partials = partials;
+    a.partials_floats = partials != nullptr ? attention_partials_floats(head_dim) : 0;
+    a.workspace = &workspace_;
+    KVSource kv{};
+    kv.page_tokens = page_tokens_;
+    const std::size_t row = static_cast<std::size_t>(layer) * table_.stride();
+    if (!seals_)
+    {
+      sync_tables(stream);
+      kv.layout = Layout::kPaged;
+      kv.pages = pages_ > 0 ? table_.addresses() + row : nullptr;
+      kv.may_be_at[kFP16] = true;
+      launch_attention(kv, a, stream);
+      return;
+    }
+    if (keys == nullptr || values == nullptr)
+    {
+      throw InvalidArgument("attention at a quantised tier reads each query's own page from the "
+                            "rows the queries stored; pass them");
+    }
+    if (!open_pages_)
+    {
+      throw LogicError("attention before any position was reserved");
+    }
+    sync_tables(stream);
+    kv.layout = Layout::kCausal;
+    kv.pages = pages_ > 0 ? table_.addresses() + row : nullptr;
+    kv.tiers = pages_ > 0 ? table_.tiers() + row : nullptr;
+    kv.open = open_page(layer, attend_open_[layer]);
+    kv.chunk_k = static_cast<const std::uint16_t *>(keys);
+    kv.chunk_v = static_cast<const std::uint16_t *>(values);
+    kv.start = seq_k - seq_q;
+    std::copy(may_be_at_.begin(), may_be_at_.end(), kv.may_be_at);
+    if (seq_q == 1 && layer + 1 < layers_ && pages_ > 0)
+    {
+      // A decode step visits the layers in order: the next layer's sealed
+      // entries are read ahead into the caches.
+      const std::size_t next = row + table_.stride();
+      kv.warm_pages = table_.addresses() + next;
+      kv.warm_tiers = table_.tiers() + next;
+      kv.warm_count = std::min((seq_k - 1) / page_tokens_, pages_);
+    }
+    launch_attention(kv, a, stream);
+  }
+
+  void KVPages::attention_layers(int first_layer, int layers, const void *q, long long q_stride,
+                                 void *out, long long out_stride, int seq_k, int heads,
+                                 int kv_heads, int head_dim, const void *keys, const void *values,
+                                 long long kv_stride, float *mass, long long mass_stride,
+                                 float *scores, long long scores_stride, float alpha)
+  {
+    if (layers < 0 || first_layer < 0 || first_layer + layers > layers_)
+    {
+      throw OutOfRange("layers [" + std::to_string(first_layer) + ", " +
+                       std::to_string(first_layer + layers) + ") are not all in this cache's " +
+                       std::to_string(layers_));
+    }
+    if (layers == 0)
+    {
+      return;
+    }
+    if (static_cast<std::size_t>(kv_heads) * head_dim != kv_width_)
+    {
+      throw InvalidArgument("kv_heads * head_dim is " + std::to_string(kv_heads * head_dim) +
+                            "; this cache holds " + std::to_string(kv_width_) + " per token");
+    }
+    if (seq_k <= 0 || seq_k > capacity_tokens())
+    {
+      throw OutOfRange("seq_k " + std::to_string(seq_k) + " is not within the " +
+                       std::to_string(capacity_tokens()) + " positions on pages");
+    }
+    if (seals_ && (keys == nullptr || values == nullptr))
+    {
+      throw InvalidArgument("attention at a quantised tier reads each query's own page from the "
+                            "rows the queries stored; pass them");
+    }
+    if (seals_ && !open_pages_)
+    {
+      throw LogicError("attention before any position was reserved");
+    }
+    const hipStream_t stream = runtime_stream();
+    sync_tables(stream);
+    AttentionArgs a{};
+    a.q = static_cast<const std::uint16_t *>(q);
+    a.out = static_cast<std::uint16_t *>(out);
+    a.seq_q = 1;
+    a.seq_k = seq_k;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.mass = mass;
+    a.scores = scores;
+    a.alpha = alpha;
+    a.workspace = &workspace_;
+    KVSource kv{};
+    kv.page_tokens = page_tokens_;
+    kv.pages = pages_ > 0 ? table_.addresses() : nullptr;
+    if (seals_)
+    {
+      kv.layout = Layout::kCausal;
+      kv.tiers = pages_ > 0 ? table_.tiers() : nullptr;
+      kv.open = open_page(first_layer, attend_open_[first_layer]);
+      kv.chunk_k = static_cast<const std::uint16_t *>(keys);
+      kv.chunk_v = static_cast<const std::uint16_t *>(values);
+      kv.start = seq_k - 1;
+      std::copy(may_be_at_.begin(), may_be_at_.end(), kv.may_be_at);
+    }
+    else
+    {
+      kv.layout = Layout::kPaged;
+      kv.may_be_at[kFP16] = true;
+    }
+    if (!decode_fast_applies(kv, a))
+    {
+      throw InvalidArgument("attention over several layers in one launch takes one query per "
+                            "head, 32-token pages, head_dim 64 or 128 and at most 16 query heads "
+                            "per KV head, 16-byte aligned; got head_dim " +
+                            std::to_string(head_dim) + ", " + std::to_string(heads) + "/" +
+                            std::to_string(kv_heads) + " heads, " + std::to_string(page_tokens_) +
+                            "-token pages");
+    }
+    DecodeLayers ls{};
+    ls.split = true;
+    ls.first_layer = first_layer;
+    ls.layers = layers;
+    ls.table_stride = table_.stride();
+    ls.open_table = seals_ ? open_table(stream) : nullptr;
+    ls.q_stride = q_stride;
+    ls.chunk_stride = kv_stride;
+    ls.out_stride = out_stride;
+    ls.mass_stride = mass_stride;
+    ls.scores_stride = scores_stride;
+    launch_decode_layers(kv, a, ls, stream);
+  }
+
+} // namespace mi

@@ -1,11 +1,15 @@
-// The cache runtime on the host: the per-tier VMM page allocator, the pinned
+// The cache runtime on the host: the per-tier page allocator, the pinned
 // FP16 shadow store, the importance scores, the RoPE table, and KVPages, the
-// cache manager that seals, attends, and moves pages between tiers.
+// cache manager that stores, seals, attends and moves pages between tiers.
 //
-// Semantics follow the reference's classes of the same names
-// (src/core_kernels/paged_kv_cache.{h,cu}, shadow_store.{h,cu},
-// importance_scores.{h,cu}, rope_table.{h,cu}, kv_pages.{h,cu}); the device
-// side is HIP on one MI355X, every launch on one stream.
+// The classes keep the reference's names and observable behaviour
+// (src/core_kernels/paged_kv_cache.h, shadow_store.h, importance_scores.h,
+// rope_table.h, kv_pages.h): slot order, error classes and messages, what a
+// page holds after every operation. How they drive the device is this
+// build's own: page tables kept current by edits the allocator reports as
+// pages move, batches named by 32-bit page references that the kernels turn
+// into addresses, granules released off the caller's path once the device
+// has passed their last use, and one launch for all of a store's seals.
 #pragma once
 
 #include "common.hpp"
@@ -14,12 +18,11 @@
 #include <array>
 #include <condition_variable>
 #include <deque>
-#include <map>
 #include <memory>
 #include <mutex>
 #include <optional>
-#include <set>
 #include <thread>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -36,6 +39,18 @@ namespace mi
     }
     bool operator==(const PageKey &o) const { return layer == o.layer && page == o.page; }
   };
+
+  // A key as one 64-bit word, for hashing and packed arrays.
+  inline std::uint64_t pack(PageKey k)
+  {
+    return (static_cast<std::uint64_t>(static_cast<std::uint32_t>(k.layer)) << 32) |
+           static_cast<std::uint32_t>(k.page);
+  }
+  inline PageKey unpack(std::uint64_t w)
+  {
+    return {static_cast<int>(static_cast<std::uint32_t>(w >> 32)),
+            static_cast<int>(static_cast<std::uint32_t>(w))};
+  }
 
   std::string describe(PageKey key);
 
@@ -56,13 +71,20 @@ namespace mi
     std::size_t bytes_ = 0;
   };
 
-  // Test hook: the next `n` granule maps fail as if the device were out of
-  // memory, so rollback paths are exercised without exhausting real VRAM.
-  void fail_next_granules(int n);
+  // Host data sent to a device buffer on a stream, the buffer grown as
+  // needed (a grown buffer's old one is freed after the device is idle).
+  class UploadBuffer
+  {
+  public:
+    template <typename T> const T *send(const std::vector<T> &host, hipStream_t stream)
+    {
+      return static_cast<const T *>(send_bytes(host.data(), host.size() * sizeof(T), stream));
+    }
+    const void *send_bytes(const void *host, std::size_t bytes, hipStream_t stream);
 
-  // The driver's allocation granularity for device memory on the current
-  // device: never assumed.
-  std::size_t granule_bytes();
+  private:
+    std::unique_ptr<DeviceBuffer> buffer_;
+  };
 
   // A workspace of one owner's: a device buffer grown on demand. A buffer it
   // outgrows is kept until the owner goes, so that an address a captured
@@ -89,17 +111,40 @@ namespace mi
     std::vector<std::unique_ptr<DeviceBuffer>> outgrown_;
   };
 
+  // Test hook: the next `n` granule maps fail as if the device were out of
+  // memory, so rollback paths are exercised without exhausting real VRAM.
+  void fail_next_granules(int n);
+
+  // The granule the allocator maps and releases tier ranges in, on the
+  // current device: the driver's recommended granularity, at least 2 MiB.
+  std::size_t granule_bytes();
+
   struct PageLocation
   {
     int tier;
     std::size_t slot;
   };
 
+  // Told of every page whose place changes: a KVPages keeps its device page
+  // tables current from these, instead of rebuilding them.
+  class PlacementObserver
+  {
+  public:
+    virtual void placed(PageKey key, int tier, std::size_t slot) = 0;
+    virtual void removed(PageKey key) = 0;
+
+  protected:
+    ~PlacementObserver() = default;
+  };
+
+  class GranuleReleaser;
+
   // ADR-0007's allocator (reference: paged_kv_cache.h:88-227): one reserved
   // virtual range per tier, pages packed from slot 0 with no holes, physical
-  // granules mapped only as far as the packed pages reach and unmapped and
-  // released as the tail retracts. Freeing a page moves its tier's tail page
-  // into the vacated slot. A page's address is never handed out.
+  // granules mapped only as far as the packed pages reach and given back as
+  // the tail retracts. A free moves the tier's tail page into the hole; a
+  // batched free fills the holes below the kept count with the pages above
+  // it, in slot order. A page's address is never handed out.
   class PagedKVCache
   {
   public:
@@ -110,6 +155,9 @@ namespace mi
     PagedKVCache &operator=(const PagedKVCache &) = delete;
 
     void allocate(PageKey key, int tier);
+    // Every key at `tier`, in order, mapping the granules they need once;
+    // all or none.
+    void allocate_run(const std::vector<PageKey> &keys, int tier);
     void free(PageKey key);
     void free_pages(const std::vector<PageKey> &keys);
     void replace(PageKey key, PageKey staged);
@@ -117,11 +165,14 @@ namespace mi
     void write(PageKey key, const void *host, std::size_t bytes);
     void read(PageKey key, void *host, std::size_t bytes) const;
     PageLocation locate(PageKey key) const;
-    bool contains(PageKey key) const { return table_.count(key) != 0; }
-    const std::vector<PageKey> &pages(int tier) const { return ranges_.at(tier).slots; }
+    bool contains(PageKey key) const { return where_.count(pack(key)) != 0; }
+    std::vector<PageKey> pages(int tier) const;
     std::size_t page_bytes(int tier) const { return ranges_.at(tier).page_bytes; }
     std::size_t reserved_bytes(int tier) const { return ranges_.at(tier).reserved; }
-    std::size_t mapped_bytes(int tier) const { return ranges_.at(tier).granules.size() * granule_; }
+    std::size_t mapped_bytes(int tier) const
+    {
+      return ranges_.at(tier).granules.size() * granule_;
+    }
     void keep_spare_granules(int tier, std::size_t granules);
     std::size_t spare_granules(int tier) const { return ranges_.at(tier).spare; }
     std::size_t granule() const { return granule_; }
@@ -130,6 +181,17 @@ namespace mi
     void drain_releases();
     // Valid until the next allocator operation: for the cache's own launches.
     char *address(PageKey key, std::size_t bytes) const;
+    char *address_of(PageLocation at) const
+    {
+      const Range &r = ranges_[at.tier];
+      return r.base + at.slot * r.page_bytes;
+    }
+    // The kernels' view of the four ranges (bases and page sizes), and a
+    // page's 32-bit reference.
+    PageSpaces spaces() const;
+    std::uint32_t ref_of(PageKey key) const;
+    void watch(PlacementObserver *o) { observers_.push_back(o); }
+    void unwatch(PlacementObserver *o);
 
   private:
     struct Range
@@ -138,46 +200,43 @@ namespace mi
       std::size_t reserved = 0;
       std::size_t page_bytes = 0;
       std::size_t capacity = 0;
-      std::vector<PageKey> slots;
+      std::vector<std::uint64_t> owners; // slot -> packed key
       std::vector<hipMemGenericAllocationHandle_t> granules;
       std::size_t spare = 0;
     };
-    // A granule given up by a range: unmapped and released by the release
-    // thread, off the caller's path (each unmap costs the driver a fraction
-    // of a millisecond, and a batch can give up hundreds).
-    struct Retired
-    {
-      char *at;
-      hipMemGenericAllocationHandle_t handle;
-    };
     static void check_tier(int tier);
-    void fit_granules(Range &r, bool map_spares);
-    void map_granule(Range &r);
-    void roll_back(Range &r);
-    void release_everything() noexcept;
-    void retire(char *at, hipMemGenericAllocationHandle_t handle);
-    void wait_for_release(const char *at);
-    void release_loop();
+    // The location word kept per key: tier in the top byte, slot below.
+    static std::uint64_t loc_word(int tier, std::size_t slot)
+    {
+      return (static_cast<std::uint64_t>(tier) << 56) | slot;
+    }
+    static PageLocation loc_of(std::uint64_t w)
+    {
+      return {static_cast<int>(w >> 56), static_cast<std::size_t>(w & ((1ull << 56) - 1))};
+    }
+    void release_keys(const std::vector<PageKey> &keys);
+    void fit(Range &r, bool map_spares);
+    void map_one(Range &r);
+    void tell_placed(std::uint64_t key, int tier, std::size_t slot);
+    void tell_removed(std::uint64_t key);
 
     std::uint64_t generation_ = 0;
     int device_ = 0;
     hipMemAllocationProp prop_{};
     std::size_t granule_ = 0;
     std::array<Range, kTierCount> ranges_;
-    std::map<PageKey, PageLocation> table_;
-    std::mutex release_mutex_;
-    std::condition_variable release_wake_; // the release thread: work or stop
-    std::condition_variable release_done_; // waiters: a granule was released
-    std::deque<Retired> retired_;          // oldest first
-    const char *releasing_ = nullptr;      // the granule the thread is releasing
-    bool release_stop_ = false;
-    std::string release_error_;            // the first failure, raised to the next waiter
-    std::thread releaser_;
+    std::unordered_map<std::uint64_t, std::uint64_t> where_; // packed key -> loc word
+    std::vector<PlacementObserver *> observers_;
+    std::unique_ptr<GranuleReleaser> releaser_;
+    UploadBuffer moves_upload_;
   };
 
   // FP16 shadows of downgraded pages in pinned host memory mapped for the
-  // device, packed into allocations of about 2 MiB (reference:
-  // shadow_store.h:11-86). Only ever added; freed with the store.
+  // device (reference: shadow_store.h:11-86): packed into pinned blocks of
+  // about 2 MiB, or of any size pinned ahead (reserve), numbered in the
+  // order they are taken. A device table gives each number's mapped address,
+  // so kernels read and write shadows by number. Only ever added; freed with
+  // the store.
   class ShadowStore
   {
   public:
@@ -187,18 +246,23 @@ namespace mi
     ShadowStore(const ShadowStore &) = delete;
     ShadowStore &operator=(const ShadowStore &) = delete;
 
+    // One device page copied into a new shadow (synchronously).
     void take(PageKey key, const void *device_page, hipStream_t stream);
+    // Pinned room for `count` more shadows, made now.
     void reserve(std::size_t count);
-    std::uint8_t *add(PageKey key);           // device address to write the shadow at
-    bool contains(PageKey key) const { return shadows_.count(key) != 0; }
+    // A new shadow's number, its room pinned already or now.
+    std::uint32_t add(PageKey key);
+    bool contains(PageKey key) const { return number_.count(pack(key)) != 0; }
+    std::uint32_t number(PageKey key) const;
     const std::uint8_t *shadow(PageKey key) const;
-    const std::uint8_t *device_shadow(PageKey key) const;
     std::size_t page_bytes() const { return page_bytes_; }
-    std::size_t count() const { return shadows_.size(); }
-    std::size_t bytes() const { return capacity_ * page_bytes_; }
+    std::size_t count() const { return host_.size(); }
+    std::size_t bytes() const { return pinned_pages_ * page_bytes_; }
+    // The device table of every shadow's mapped address, current on `stream`.
+    const unsigned long long *device_table(hipStream_t stream);
 
   private:
-    struct Allocation
+    struct Block
     {
       std::uint8_t *host;
       std::uint8_t *device;
@@ -206,11 +270,15 @@ namespace mi
       std::size_t used;
     };
     std::size_t page_bytes_;
-    std::size_t per_allocation_;
-    std::vector<Allocation> allocations_;
-    std::size_t capacity_ = 0;
-    std::map<const std::uint8_t *, std::size_t> by_address_;
-    std::map<PageKey, std::uint8_t *> shadows_;
+    std::vector<Block> blocks_;
+    std::size_t pinned_pages_ = 0;
+    std::size_t cursor_ = 0; // the first block with room
+    std::unordered_map<std::uint64_t, std::uint32_t> number_;
+    std::vector<std::uint8_t *> host_;       // by number
+    std::vector<unsigned long long> device_; // by number
+    std::size_t sent_ = 0;                   // entries already in the device table
+    std::unique_ptr<DeviceBuffer> table_;
+    std::vector<std::unique_ptr<DeviceBuffer>> outgrown_;
   };
 
   // The per-(layer, page) EWMA of attention mass (reference:
@@ -309,8 +377,45 @@ namespace mi
     double seconds;
   };
 
+  // Every layer's page addresses and tiers on the device, [layer][stride]
+  // each, with a host copy. Entries change one at a time as the allocator
+  // reports pages moving; commit() sends the changed entries (or the whole
+  // table, if that is less) before the next launch that reads it.
+  class PageTable
+  {
+  public:
+    explicit PageTable(int layers) : layers_(layers) {}
+    int stride() const { return stride_; }
+    // Room for `pages` a layer; a new stride starts every entry unread.
+    void ensure(int pages);
+    void set(int layer, int page, unsigned long long address, std::uint8_t tier);
+    void commit(hipStream_t stream);
+    const unsigned long long *addresses() const
+    {
+      return device_ ? device_->as<const unsigned long long>() : nullptr;
+    }
+    const std::uint8_t *tiers() const
+    {
+      return device_ ? reinterpret_cast<const std::uint8_t *>(
+                           device_->as<const unsigned long long>() + entries())
+                     : nullptr;
+    }
+
+  private:
+    std::size_t entries() const { return static_cast<std::size_t>(layers_) * stride_; }
+    int layers_;
+    int stride_ = 0;
+    std::vector<unsigned long long> address_;
+    std::vector<std::uint8_t> tier_;
+    std::vector<std::uint8_t> dirty_;    // an entry changed since the last commit
+    std::vector<std::uint32_t> marked_;  // those entries, once each
+    bool whole_ = false;
+    std::unique_ptr<DeviceBuffer> device_;
+    UploadBuffer edit_upload_;
+  };
+
   // The engine's KV cache on pages (reference: kv_pages.h:66-412).
-  class KVPages
+  class KVPages final : private PlacementObserver
   {
   public:
     static bool seals_for(int tier, const TierMap &tier_map, bool always_seal);
@@ -339,9 +444,13 @@ namespace mi
     void move_pages(const std::vector<PageMove> &moves);
     void evict(int layer, int page);
     void mask(int layer, int page);
+    // Pins host memory for `pages` more FP16 shadows now, so that first
+    // downgrades later take none of their time pinning (ADR-0015's "pinning
+    // ahead of need"). No counterpart in the reference.
+    void pin_shadows(std::size_t pages) { shadows_.reserve(pages); }
 
-    bool evicted(PageKey key) const { return evicted_.count(key) != 0; }
-    bool masked(PageKey key) const { return masked_.count(key) != 0; }
+    bool evicted(PageKey key) const { return flag(key, kEvicted); }
+    bool masked(PageKey key) const { return flag(key, kMasked); }
     int page_tier(PageKey key) const { return allocator_.locate(key).tier; }
     const ShadowStore &shadows() const { return shadows_; }
     const std::optional<MoveRecord> &last_move() const { return last_move_; }
@@ -361,33 +470,43 @@ namespace mi
     int kv_heads() const { return kv_heads_; }
     int head_dim() const { return head_dim_; }
 
-    // The device table of one layer, resolved now: page addresses, then tiers.
-    struct LayerTable
-    {
-      const unsigned long long *pages;
-      const std::uint8_t *tiers;
-    };
-    LayerTable resolve(int layer);
-
   private:
-    struct Seal
+    static constexpr std::uint8_t kEvicted = 1;
+    static constexpr std::uint8_t kMasked = 2;
+
+    // PlacementObserver: the allocator moved or dropped one of its pages.
+    void placed(PageKey key, int tier, std::size_t slot) override;
+    void removed(PageKey key) override;
+
+    bool flag(PageKey key, std::uint8_t bit) const
     {
-      int span;
-      const std::uint16_t *keys;
-      const std::uint16_t *values;
-    };
-    void seal_batch(int layer, const std::vector<Seal> &seals);
+      if (key.layer < 0 || key.layer >= layers_ || key.page < 0 || key.page >= pages_)
+      {
+        return false;
+      }
+      return (flags_[static_cast<std::size_t>(key.layer) * flag_stride_ + key.page] & bit) != 0;
+    }
+    void set_flag(PageKey key, std::uint8_t bit);
+    void grow(int pages); // flags and table room for `pages` a layer
+    void refresh_entry(int layer, int page);
+    void sync_tables(hipStream_t stream);
+
     void store_sealed(int layer, const std::uint16_t *keys, const std::uint16_t *values, int start,
                       int n);
     PageKey require_movable(int layer, int page, const char *verb) const;
     PageKey require_held(int layer, int page, const char *verb) const;
-    void move(PageKey key, int current, int target);
+    // The tier moves of a batch: validated already, every page held.
+    void run_moves(const std::vector<PageKey> &keys, const std::vector<int> &from,
+                   const std::vector<int> &targets, double *shadow_seconds);
     void require_layer(int layer) const;
     std::size_t bytes_at(int tier) const;
     void require_page_size(int tier, const char *what) const;
-    std::uint16_t *open_page(int layer, int which);
+    std::uint16_t *open_page(int layer, int which) const
+    {
+      return reinterpret_cast<std::uint16_t *>(open_address_[2 * layer + which]);
+    }
     // Every layer's open page as the next attention reads it, on the device.
-    const unsigned long long *open_table();
+    const unsigned long long *open_table(hipStream_t stream);
     static std::string page_name(PageKey key);
 
     PagedKVCache &allocator_;
@@ -409,21 +528,16 @@ namespace mi
     std::vector<int> current_open_;
     std::vector<int> attend_open_;
     std::vector<int> sealed_;
+    std::vector<unsigned long long> open_address_; // [layer][2]
+    std::vector<std::uint8_t> flags_;              // [layer][flag_stride_]
+    int flag_stride_ = 0;
     ShadowStore shadows_;
-    std::set<PageKey> evicted_;
-    std::set<PageKey> masked_;
     std::optional<MoveRecord> last_move_;
     std::optional<BatchRecord> last_batch_;
-    std::unique_ptr<DeviceBuffer> scratch_page_;
-    std::unique_ptr<DeviceBuffer> scratch_halves_;
-    std::unique_ptr<DeviceBuffer> tables_;
-    int table_stride_ = 0;
-    int resolved_pages_ = -1;
-    std::uint64_t resolved_generation_ = 0;
+    PageTable table_;
     std::unique_ptr<DeviceBuffer> open_table_;
     std::vector<unsigned long long> open_uploaded_;
-    // Address tables for batched launches, grown as needed.
-    std::unique_ptr<DeviceBuffer> batch_table_;
+    UploadBuffer pairs_upload_;
     // The decode path's split partials and page statistics: this cache's own.
     OwnedWorkspace workspace_;
   };
