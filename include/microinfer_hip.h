@@ -66,6 +66,10 @@ const char *mi_build_info(void);
  * paged_kv_cache.cu:46-60 (allocation_granularity). */
 int mi_device_count(int *count);
 int mi_device_name(char *out, size_t capacity);
+/* The current device's PCI bus id ("dddd:bb:dd.f"), by which a management
+ * library (amdsmi) finds the same GPU. No counterpart in the reference, whose
+ * NVML reader takes device 0 (nvml.py:80-84). */
+int mi_device_pci_bus_id(char *out, size_t capacity);
 int mi_runtime_version(int *version);
 /* reference: device.cu:10-17 cuda_driver_version (renamed: the HIP driver's). */
 int mi_driver_version(int *version);
@@ -338,6 +342,12 @@ int mi_kv_downgrade(mi_kv_pages *kv, int layer, int page, int target);
 int mi_kv_upgrade(mi_kv_pages *kv, int layer, int page, int target);
 /* triples: n (layer, page, target tier), 3n ints. */
 int mi_kv_move_pages(mi_kv_pages *kv, const int *triples, size_t n);
+/* Pins host memory for `pages` more FP16 shadows now, so that first
+ * downgrades later pin nothing on their own path. No counterpart in the
+ * reference, whose shadows are pinned as they are taken; its ADR-0015
+ * (:202-208) names pinning ahead of need as the remedy for a first
+ * downgrade's cost. shadow_bytes counts what is pinned. */
+int mi_kv_pin_shadows(mi_kv_pages *kv, size_t pages);
 int mi_kv_evict(mi_kv_pages *kv, int layer, int page);
 int mi_kv_mask(mi_kv_pages *kv, int layer, int page);
 int mi_kv_page_tier(mi_kv_pages *kv, int layer, int page, int *tier);

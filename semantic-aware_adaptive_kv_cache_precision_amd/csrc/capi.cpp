@@ -229,12 +229,27 @@ int mi_device_name(char *out, size_t capacity)
     mi::hip_check(hipGetDevice(&device), "hipGetDevice");
     hipDeviceProp_t prop{};
     mi::hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
-    std::string name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    // Some runtimes leave the marketing name empty: the architecture then
+    // names the device.
+    const std::string arch = prop.gcnArchName;
+    const std::string base = prop.name[0] != '\0' ? std::string(prop.name)
+                                                  : "AMD GPU " + arch.substr(0, arch.find(':'));
+    const std::string name = base + " (" + arch + ")";
     std::strncpy(out, name.c_str(), capacity);
     if (capacity > 0)
     {
       out[capacity - 1] = '\0';
     }
+  });
+}
+
+int mi_device_pci_bus_id(char *out, size_t capacity)
+{
+  return guarded([&] {
+    int device = 0;
+    mi::hip_check(hipGetDevice(&device), "hipGetDevice");
+    mi::hip_check(hipDeviceGetPCIBusId(out, static_cast<int>(capacity), device),
+                  "hipDeviceGetPCIBusId");
   });
 }
 
@@ -1179,6 +1194,11 @@ int mi_kv_move_pages(mi_kv_pages *kv, const int *triples, size_t n)
     }
     kv->impl.move_pages(moves);
   });
+}
+
+int mi_kv_pin_shadows(mi_kv_pages *kv, size_t pages)
+{
+  return guarded([&] { kv->impl.pin_shadows(pages); });
 }
 
 int mi_kv_evict(mi_kv_pages *kv, int layer, int page)

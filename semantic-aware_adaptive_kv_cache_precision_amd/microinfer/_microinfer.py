@@ -59,7 +59,8 @@ def _sig(name, *args, restype=C.c_int):
 SIGNATURES = {
     "mi_last_error": ((), C.c_char_p), "mi_build_info": ((), C.c_char_p),
     "mi_device_count": ((_ip,), C.c_int), "mi_device_name": ((C.c_char_p, _sz), C.c_int),
-    "mi_runtime_version": ((_ip,), C.c_int), "mi_memory_info": ((_szp, _szp), C.c_int),
+    "mi_runtime_version": ((_ip,), C.c_int),
+    "mi_device_pci_bus_id": ((C.c_char_p, _sz), C.c_int), "mi_memory_info": ((_szp, _szp), C.c_int),
     "mi_granule_bytes": ((_szp,), C.c_int), "mi_malloc": ((C.POINTER(_vp), _sz), C.c_int),
     "mi_free": ((_vp,), C.c_int), "mi_memcpy": ((_vp, _vp, _sz, _i), C.c_int),
     "mi_memset": ((_vp, _i, _sz), C.c_int), "mi_synchronize": ((), C.c_int),
@@ -152,6 +153,7 @@ SIGNATURES = {
     "mi_kv_downgrade": ((_vp, _i, _i, _i), C.c_int),
     "mi_kv_upgrade": ((_vp, _i, _i, _i), C.c_int),
     "mi_kv_move_pages": ((_vp, _ip, _sz), C.c_int),
+    "mi_kv_pin_shadows": ((_vp, _sz), C.c_int),
     "mi_kv_evict": ((_vp, _i, _i), C.c_int),
     "mi_kv_mask": ((_vp, _i, _i), C.c_int),
     "mi_kv_page_tier": ((_vp, _i, _i, _ip), C.c_int),
@@ -313,6 +315,13 @@ class DeviceArena:
 def device_name() -> str:
     buf = C.create_string_buffer(256)
     _check(lib.mi_device_name(buf, 256))
+    return buf.value.decode()
+
+
+def device_pci_bus_id() -> str:
+    """The current device's PCI bus id, as amdsmi names GPUs."""
+    buf = C.create_string_buffer(64)
+    _check(lib.mi_device_pci_bus_id(buf, 64))
     return buf.value.decode()
 
 
@@ -1055,6 +1064,11 @@ class KVPages:
         moves = list(moves)
         flat = [int(x) for layer, page, tier in moves for x in (layer, page, _tier(tier))]
         _check(lib.mi_kv_move_pages(self._h, _int_array(flat), len(moves)))
+
+    def pin_shadows(self, pages: int) -> None:
+        """Pins host memory for `pages` more FP16 shadows now (beyond the
+        reference: its shadows are pinned as they are taken)."""
+        _check(lib.mi_kv_pin_shadows(self._h, pages))
 
     def evict(self, layer: int, page: int) -> None:
         _check(lib.mi_kv_evict(self._h, layer, page))

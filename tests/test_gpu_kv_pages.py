@@ -633,3 +633,41 @@ def test_decode_after_pages_move_reads_them_where_they_now_are():
         assert alloc.locate(*tail)[1] < tail_slot
     poison_slot(tier, tail_slot)
     decode_both("after an eviction")
+
+
+def test_the_halves_diagnostic_rounds_one_half_through_its_tier():
+    """A diagnostic Halves cache (kv_pages.h's Halves, the reference's
+    ablation of keys against values) stores every page at FP16: the chosen
+    half as quantise_page then dequantise_page at the cache's tier gives it,
+    the other half as it came, to the bit; rows arriving one by one, in one
+    run, or in runs crossing pages; the register path (P = 32, head_dim 64
+    and 128) and the LDS path (P = 16)."""
+    m = mi()
+    d = m.device
+
+    def check(P, hd, tier, halves, runs_name):
+        kv = 2
+        rng = np.random.default_rng(P * 7 + hd + tier)
+        seq = 3 * P + 3
+        k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+        k[:, :, rng.choice(hd, 2, replace=False)] *= 10
+        k = fp16_exact(k)
+        runs = {"one": [seq], "single": [1] * seq, "ragged": [P // 2 + 1, P + 3,
+                                                              seq - (3 * P // 2 + 4)]}[runs_name]
+        sizes = page_sizes(P, kv, hd)
+        alloc = m.PagedKVCache(sizes, [64 + LAYERS * 2] * 4)
+        cache = d.KVPages(alloc, LAYERS, P, kv, hd, tier, getattr(d.Halves, halves), [], False)
+        assert cache.page_bytes == sizes[0]
+        announce("halves", P, hd, tier, halves, runs_name)
+        store_in_runs(cache, 1, k, v, runs)
+        for i in range(seq // P):
+            kp = k[i * P:(i + 1) * P].astype(np.float16)
+            vp = v[i * P:(i + 1) * P].astype(np.float16)
+            kr, vr = quant.dequantise_page(quant.quantise_page(kp, vp, tier, P), tier, kv, hd, P)
+            kr = np.asarray(kr, np.float16)
+            vr = np.asarray(vr, np.float16)
+            want = quant.fp16_page(kr if halves == "Keys" else kp, vr if halves == "Values" else vp)
+            np.testing.assert_array_equal(alloc.read(1, i), want)
+
+    each([(P, hd, t, h, r) for P, hd in ((32, 128), (32, 64), (16, 64)) for t in (1, 2, 3)
+          for h in ("Keys", "Values") for r in ("one", "single", "ragged")], check)
