@@ -21,6 +21,7 @@ Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import faulthandler
 import json
 import os
 import sys
@@ -387,6 +388,8 @@ def profiled_traffic(path=REPO / "profiles" / "decode_attention_config3_hbm_byte
 
 
 def main() -> int:
+    # A fatal signal prints every thread's Python stack: where it came from.
+    faulthandler.enable()
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)

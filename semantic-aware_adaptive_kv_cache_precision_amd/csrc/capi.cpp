@@ -6,19 +6,34 @@
 #include "runtime.hpp"
 
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <string>
 
+// A KVPages keeps its allocator alive (the reference's binding does the
+// same, bindings_device.cpp:701-718): the allocator goes when its own handle
+// and every cache on it are gone, whatever order the caller drops them in
+// (a garbage collector's order is arbitrary).
 struct mi_cache
 {
-  mi::PagedKVCache impl;
-  template <typename... A> explicit mi_cache(A &&...a) : impl(std::forward<A>(a)...) {}
+  std::shared_ptr<mi::PagedKVCache> owner;
+  mi::PagedKVCache &impl;
+  template <typename... A>
+  explicit mi_cache(A &&...a)
+      : owner(std::make_shared<mi::PagedKVCache>(std::forward<A>(a)...)), impl(*owner)
+  {
+  }
 };
 struct mi_kv_pages
 {
+  std::shared_ptr<mi::PagedKVCache> allocator; // declared first: destroyed last
   mi::KVPages impl;
-  template <typename... A> explicit mi_kv_pages(A &&...a) : impl(std::forward<A>(a)...) {}
+  template <typename... A>
+  mi_kv_pages(std::shared_ptr<mi::PagedKVCache> a, A &&...rest)
+      : allocator(std::move(a)), impl(*allocator, std::forward<A>(rest)...)
+  {
+  }
 };
 struct mi_scores
 {
@@ -377,7 +392,9 @@ int mi_stream_synchronize(void *stream)
 
 int mi_set_stream(void *stream)
 {
-  return guarded([&] { mi::set_runtime_stream(as_stream(stream)); });
+  // NULL names the null stream itself (not "the current one", as a null
+  // stream argument of a launcher does).
+  return guarded([&] { mi::set_runtime_stream(static_cast<hipStream_t>(stream)); });
 }
 
 int mi_graph_begin(void *stream)
@@ -1092,7 +1109,7 @@ int mi_kv_create(mi_cache *allocator, int layers, int page_tokens, int kv_heads,
     {
       throw mi::InvalidArgument("halves is 0 (Both), 1 (Keys) or 2 (Values)");
     }
-    *out = new mi_kv_pages(allocator->impl, layers, page_tokens, kv_heads, head_dim, tier,
+    *out = new mi_kv_pages(allocator->owner, layers, page_tokens, kv_heads, head_dim, tier,
                            static_cast<mi::Halves>(halves),
                            tier_map_of(tier_map, row_lengths, map_rows), always_seal != 0);
   });

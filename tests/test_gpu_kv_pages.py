@@ -671,3 +671,88 @@ def test_the_halves_diagnostic_rounds_one_half_through_its_tier():
 
     each([(P, hd, t, h, r) for P, hd in ((32, 128), (32, 64), (16, 64)) for t in (1, 2, 3)
           for h in ("Keys", "Values") for r in ("one", "single", "ragged")], check)
+
+
+def test_a_cache_keeps_its_allocator_alive():
+    """The allocator's handle destroyed before its cache's (a garbage
+    collector finalizes a cycle in any order): the cache still stores,
+    attends and moves pages, and the allocator goes with the cache."""
+    import weakref
+    m = mi()
+    P, heads, kv, hd = 32, 12, 2, 128
+    rng = np.random.default_rng(12)
+    seq = P * 8 + 3
+    k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+    alloc, cache = pages_for(P, kv, hd, 0, tier_map=[[2, 0] * 5] * LAYERS, always_seal=True)
+    store_in_runs(cache, 0, k, v, [seq - 1])
+    # Run the allocator handle's own finalizer now.
+    for f, info in list(weakref.finalize._registry.items()):
+        if info.args == (alloc._h,) and getattr(info.func, "__name__", "") == "mi_cache_destroy":
+            f()
+    announce("cache outliving its allocator's handle")
+    cache.reserve(seq)
+    cache.store(0, put(k[-1:]), put(v[-1:]), seq - 1, 1)
+    q = normal(rng, 1, heads, hd)
+    got, mass = run_decode(m, cache, k, v, q, heads, kv, hd)
+    own = (seq - 1) // P
+    assert np.isfinite(got).all() and mass.shape == (heads, own + 1)
+    np.testing.assert_allclose(mass.sum(1), 1.0, atol=1e-5)
+    cache.move_pages([(0, 1, 3)])
+    assert cache.page_tier(0, 1) == 3
+    del cache
+
+
+def test_after_a_capture_the_runtime_is_back_on_the_null_stream():
+    """A decode captured as a graph on a stream of the caller's, replayed,
+    then the graph and the stream destroyed: the cache's later work (frees
+    that give granules back, a store, a decode) runs on the null stream, as
+    set_stream(None) after the capture names, and meets the oracle."""
+    import weakref
+    m = mi()
+    d = m.device
+    P, heads, kv, hd = 32, 12, 2, 128
+    rng = np.random.default_rng(13)
+    seq = P * 70 + 5
+    k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+    alloc, cache = pages_for(P, kv, hd, 0, tier_map=[[1, 0, 2] * 24] * LAYERS, always_seal=True)
+    store_in_runs(cache, 0, k, v, [seq - 1, 1])
+    q = normal(rng, 1, heads, hd)
+    qd, kd, vd = put(q), put(k[-1:]), put(v[-1:])
+    out = d.empty(heads * hd)
+    part = d.empty_f32(d.attention_partials(hd))
+
+    def body():
+        cache.attention(0, qd, None, None, out, 1, seq, heads, kv, hd, kd, vd, None, part)
+
+    body()
+    m.synchronize()
+    stream = m.Stream()
+    graph = m.Graph(stream)
+    announce("capture, replay, destroy the stream")
+    with graph.capture():
+        body()
+    graph.launch()
+    stream.synchronize()
+    for obj in (graph, stream):
+        for f, info in list(weakref.finalize._registry.items()):
+            if info.weakref() is obj:
+                f()
+    # Frees (whole granules given back), then an eager decode.
+    for page in range(0, 60, 3):
+        cache.evict(0, page)
+    got, mass = run_decode(m, cache, k, v, q, heads, kv, hd)
+    m.synchronize()
+    own = (seq - 1) // P
+    tiers_now = cache.page_tiers()[0]
+    raw, tiers = [], []
+    for p in range(own):
+        if tiers_now[p] == 4:
+            raw.append(None)
+            tiers.append(quant.UNREAD)
+        else:
+            raw.append(alloc.read(0, p))
+            tiers.append(int(alloc.locate(0, p)[0]))
+    want, want_mass, bound = att.causal_decode(q, raw, tiers, k[own * P:], v[own * P:], kv, hd, P,
+                                               with_bound=True)
+    assert_attention_close(got, want, "after the stream went", bound)
+    assert_mass_close(mass, want_mass, "after the stream went")
