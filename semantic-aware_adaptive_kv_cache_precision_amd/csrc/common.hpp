@@ -202,6 +202,10 @@ namespace mi
 
   __host__ __device__ inline float half_bits_to_float(std::uint16_t h)
   {
+#if defined(__HIP_DEVICE_COMPILE__)
+    // On the device, the hardware conversion: exact, subnormals included.
+    return __half2float(__ushort_as_half(h));
+#else
     const std::uint32_t sign = static_cast<std::uint32_t>(h & 0x8000u) << 16;
     const int exp = (h >> 10) & 0x1f;
     std::uint32_t mant = h & 0x3ffu;
@@ -231,6 +235,7 @@ namespace mi
     float f;
     std::memcpy(&f, &bits, sizeof(f));
     return f;
+#endif
   }
 
   // fp16 bits to fp32 on the device: the hardware conversion, exact

@@ -78,10 +78,16 @@ namespace mi
     }
     __device__ inline void store16(std::uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
 
+    // fp16 bits to fp32 by the hardware conversion (exact, denormals kept).
+    __device__ inline float f16_bits(unsigned bits)
+    {
+      return __half2float(__ushort_as_half(static_cast<unsigned short>(bits)));
+    }
+
     __device__ inline float half_at(const uint4 &v, int c)
     {
       const unsigned w = c < 2 ? v.x : c < 4 ? v.y : c < 6 ? v.z : v.w;
-      return half_bits_to_float(static_cast<std::uint16_t>((c & 1) ? (w >> 16) : (w & 0xFFFFu)));
+      return f16_bits((c & 1) ? (w >> 16) : (w & 0xFFFFu));
     }
 
     __device__ inline unsigned half_of(float x) { return __half_as_ushort(__float2half_rn(x)); }
@@ -94,29 +100,80 @@ namespace mi
       kRaw,    // this half's rows as they are, at dst
     };
 
-    // A key task: channels [8j, 8j + 8) of rows [8g, 8g + 8). The four tasks
-    // of chunk j sit in lanes 4j .. 4j + 3 of one wave.
+    // Eight codes of one 16-byte run (eight fp16 values), packed the first
+    // lowest: 8 (INT8), 4 (INT4) or 2 (INT2) bytes.
     template <int Bits>
-    __device__ void key_task(const Rows &keys, int j, int g, int W, std::uint8_t *dst,
-                             const PageLayout &L, Emit emit, int rows_limit, int dst_row)
+    __device__ __forceinline__ unsigned long long codes8(const uint4 &v, const float (&lo)[8],
+                                                         const float (&scale)[8])
     {
-      uint4 raw[8];
+      unsigned long long packed = 0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int c = 0; c < 8; ++c)
       {
-        // A fill brings fewer rows than a page: rows past them are not read.
-        raw[i] = 8 * g + i < rows_limit ? load16(keys.row(8 * g + i) + 8 * j) : uint4{0, 0, 0, 0};
+        packed |= static_cast<unsigned long long>(
+                      quant_core::code_of<Bits>(half_at(v, c), lo[c], scale[c]))
+                  << (Bits * c);
       }
+      return packed;
+    }
+
+    template <int Bits>
+    __device__ __forceinline__ void store_codes8(std::uint8_t *at, unsigned long long packed)
+    {
+      if constexpr (Bits == 8)
+      {
+        *reinterpret_cast<uint2 *>(at) =
+            uint2{static_cast<unsigned>(packed), static_cast<unsigned>(packed >> 32)};
+      }
+      else if constexpr (Bits == 4)
+      {
+        *reinterpret_cast<unsigned *>(at) = static_cast<unsigned>(packed);
+      }
+      else
+      {
+        *reinterpret_cast<std::uint16_t *>(at) = static_cast<std::uint16_t>(packed);
+      }
+    }
+
+    // fmaf(code, scale, zero) to fp16 for eight codes, as dequantise_page.
+    template <int Bits>
+    __device__ __forceinline__ uint4 round8(const uint4 &v, const float (&lo)[8],
+                                            const float (&scale)[8])
+    {
+      unsigned h[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+      {
+        const float code =
+            static_cast<float>(quant_core::code_of<Bits>(half_at(v, c), lo[c], scale[c]));
+        h[c] = half_of(fmaf(code, scale[c], lo[c]));
+      }
+      return uint4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                   h[6] | (h[7] << 16)};
+    }
+
+    // A key task: channels [8j, 8j + 8) of rows [8g, 8g + 8). The four tasks
+    // of chunk j sit in lanes 4j .. 4j + 3 of one wave. Two passes: the
+    // ranges, with all eight rows' loads in flight at once; then the codes a
+    // row at a time, each row read again (from cache: the first pass just
+    // brought it), so that the 64 divisions never hold all eight rows.
+    template <int Bits>
+    __device__ __forceinline__ void key_task(const Rows &keys, int j, int g, int W,
+                                             std::uint8_t *dst, const PageLayout &L, Emit emit,
+                                             int rows_limit, int dst_row)
+    {
       if (emit == Emit::kRaw)
       {
         auto *out = reinterpret_cast<std::uint16_t *>(dst);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
         {
+          // A fill brings fewer rows than a page: rows past them are not read.
           const int t = 8 * g + i;
           if (t < rows_limit)
           {
-            store16(out + static_cast<std::size_t>(dst_row + t) * W + 8 * j, raw[i]);
+            store16(out + static_cast<std::size_t>(dst_row + t) * W + 8 * j,
+                    load16(keys.row(t) + 8 * j));
           }
         }
         return;
@@ -127,94 +184,83 @@ namespace mi
       {
         lo[c] = INFINITY;
         hi[c] = -INFINITY;
+      }
+      {
+        uint4 raw[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
         {
-          const float x = half_at(raw[i], c);
-          lo[c] = fminf(lo[c], x);
-          hi[c] = fmaxf(hi[c], x);
+          raw[i] = load16(keys.row(8 * g + i) + 8 * j);
         }
-        // The chunk's four row groups: lanes that differ in the low two bits.
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+          {
+            const float x = half_at(raw[i], c);
+            lo[c] = fminf(lo[c], x);
+            hi[c] = fmaxf(hi[c], x);
+          }
+        }
+      }
+      // The chunk's four row groups: lanes that differ in the low two bits.
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+      {
         lo[c] = fminf(lo[c], __shfl_xor(lo[c], 1));
         hi[c] = fmaxf(hi[c], __shfl_xor(hi[c], 1));
         lo[c] = fminf(lo[c], __shfl_xor(lo[c], 2));
         hi[c] = fmaxf(hi[c], __shfl_xor(hi[c], 2));
       }
-      std::uint16_t sbits[8], zbits[8];
       float scale[8];
+      unsigned sword[4] = {0, 0, 0, 0}, zword[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int c = 0; c < 8; ++c)
       {
-        sbits[c] = scale_bits_of(lo[c], hi[c], Bits);
-        zbits[c] = static_cast<std::uint16_t>(half_of(lo[c]));
-        scale[c] = half_bits_to_float(sbits[c]);
+        const std::uint16_t s = scale_bits_of(lo[c], hi[c], Bits);
+        scale[c] = f16_bits(s);
+        sword[c / 2] |= static_cast<unsigned>(s) << (16 * (c % 2));
+        zword[c / 2] |= half_of(lo[c]) << (16 * (c % 2));
       }
       if (emit == Emit::kCodes)
       {
         if (g == 0)
         {
-          auto *ks = reinterpret_cast<std::uint16_t *>(dst + L.key_scales) + 8 * j;
-          auto *kz = reinterpret_cast<std::uint16_t *>(dst + L.key_zeros) + 8 * j;
-          store16(ks, uint4{sbits[0] | (unsigned{sbits[1]} << 16), sbits[2] | (unsigned{sbits[3]} << 16),
-                            sbits[4] | (unsigned{sbits[5]} << 16), sbits[6] | (unsigned{sbits[7]} << 16)});
-          store16(kz, uint4{zbits[0] | (unsigned{zbits[1]} << 16), zbits[2] | (unsigned{zbits[3]} << 16),
-                            zbits[4] | (unsigned{zbits[5]} << 16), zbits[6] | (unsigned{zbits[7]} << 16)});
+          store16(reinterpret_cast<std::uint16_t *>(dst + L.key_scales) + 8 * j,
+                  uint4{sword[0], sword[1], sword[2], sword[3]});
+          store16(reinterpret_cast<std::uint16_t *>(dst + L.key_zeros) + 8 * j,
+                  uint4{zword[0], zword[1], zword[2], zword[3]});
         }
-#pragma unroll
+#pragma unroll 1
         for (int i = 0; i < 8; ++i)
         {
-          const std::size_t e = static_cast<std::size_t>(8 * g + i) * W + 8 * j; // first element
-          unsigned long long packed = 0;
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-          {
-            packed |= static_cast<unsigned long long>(
-                          quant_core::code_of<Bits>(half_at(raw[i], c), lo[c], scale[c]))
-                      << (Bits * c);
-          }
-          std::uint8_t *at = dst + L.key_codes + e * Bits / 8;
-          if constexpr (Bits == 8)
-          {
-            *reinterpret_cast<uint2 *>(at) =
-                uint2{static_cast<unsigned>(packed), static_cast<unsigned>(packed >> 32)};
-          }
-          else if constexpr (Bits == 4)
-          {
-            *reinterpret_cast<unsigned *>(at) = static_cast<unsigned>(packed);
-          }
-          else
-          {
-            *reinterpret_cast<std::uint16_t *>(at) = static_cast<std::uint16_t>(packed);
-          }
+          const int t = 8 * g + i;
+          const uint4 v = load16(keys.row(t) + 8 * j);
+          const std::size_t e = static_cast<std::size_t>(t) * W + 8 * j; // first element
+          store_codes8<Bits>(dst + L.key_codes + e * Bits / 8, codes8<Bits>(v, lo, scale));
         }
         return;
       }
-      // Round trip: each code back through fmaf(code, scale, zero) to fp16,
-      // as dequantise_page gives it.
+      // Round trip: each code back to fp16, as dequantise_page gives it.
       auto *out = reinterpret_cast<std::uint16_t *>(dst);
-#pragma unroll
+#pragma unroll 1
       for (int i = 0; i < 8; ++i)
       {
-        unsigned h[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-        {
-          const float code = static_cast<float>(
-              quant_core::code_of<Bits>(half_at(raw[i], c), lo[c], scale[c]));
-          h[c] = half_of(fmaf(code, scale[c], lo[c]));
-        }
-        store16(out + static_cast<std::size_t>(8 * g + i) * W + 8 * j,
-                uint4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                      h[6] | (h[7] << 16)});
+        const int t = 8 * g + i;
+        const uint4 v = load16(keys.row(t) + 8 * j);
+        store16(out + static_cast<std::size_t>(t) * W + 8 * j, round8<Bits>(v, lo, scale));
       }
     }
 
     // A value task: channels [64 part, 64 part + 64) of head h in row r.
-    // At head_dim 128 the group's two parts sit in adjacent lanes.
+    // At head_dim 128 the group's two parts sit in adjacent lanes. The same
+    // two passes as a key task, over the row's eight 16-byte runs.
     template <int Bits, int HD>
-    __device__ void value_task(const Rows &values, int r, int h, int part, int kv_heads, int W,
-                               std::uint8_t *dst, const PageLayout &L, Emit emit, int rows_limit,
-                               int dst_row)
+    __device__ __forceinline__ void value_task(const Rows &values, int r, int h, int part,
+                                               int kv_heads, int W, std::uint8_t *dst,
+                                               const PageLayout &L, Emit emit, int rows_limit,
+                                               int dst_row)
     {
       const int ch0 = h * HD + 64 * part;
       if (r >= rows_limit)
@@ -222,36 +268,36 @@ namespace mi
         return; // a fill's row past those it brings: nothing to read or write
       }
       const std::uint16_t *src = values.row(r) + ch0;
-      uint4 raw[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-      {
-        raw[i] = load16(src + 8 * i);
-      }
       // FP16 output rows (raw and round trip) sit in the page's second half.
       auto *out = reinterpret_cast<std::uint16_t *>(dst) + static_cast<std::size_t>(kP) * W;
       if (emit == Emit::kRaw)
       {
-        if (r < rows_limit)
-        {
 #pragma unroll
-          for (int i = 0; i < 8; ++i)
-          {
-            store16(out + static_cast<std::size_t>(dst_row + r) * W + ch0 + 8 * i, raw[i]);
-          }
+        for (int i = 0; i < 8; ++i)
+        {
+          store16(out + static_cast<std::size_t>(dst_row + r) * W + ch0 + 8 * i,
+                  load16(src + 8 * i));
         }
         return;
       }
       float lo = INFINITY, hi = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
       {
+        uint4 raw[8];
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
+        for (int i = 0; i < 8; ++i)
         {
-          const float x = half_at(raw[i], c);
-          lo = fminf(lo, x);
-          hi = fmaxf(hi, x);
+          raw[i] = load16(src + 8 * i);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+          {
+            const float x = half_at(raw[i], c);
+            lo = fminf(lo, x);
+            hi = fmaxf(hi, x);
+          }
         }
       }
       if constexpr (HD == 128)
@@ -260,62 +306,43 @@ namespace mi
         hi = fmaxf(hi, __shfl_xor(hi, 1));
       }
       const std::uint16_t sbits = scale_bits_of(lo, hi, Bits);
-      const float scale = half_bits_to_float(sbits);
-      const int group = r * kv_heads + h;
+      const float scale = f16_bits(sbits);
+      float los[8], scales[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+      {
+        los[c] = lo;
+        scales[c] = scale;
+      }
       if (emit == Emit::kCodes)
       {
         if (part == 0)
         {
+          const int group = r * kv_heads + h;
           reinterpret_cast<std::uint16_t *>(dst + L.value_scales)[group] = sbits;
           reinterpret_cast<std::uint16_t *>(dst + L.value_zeros)[group] =
               static_cast<std::uint16_t>(half_of(lo));
         }
-        // 64 codes: 16 (INT8), 8 (INT4) or 4 (INT2) words.
-        constexpr int kWords = 64 * Bits / 32;
-        constexpr int kPerWord = 32 / Bits;
-        unsigned words[kWords];
-#pragma unroll
-        for (int w = 0; w < kWords; ++w)
-        {
-          unsigned word = 0;
-#pragma unroll
-          for (int c = 0; c < kPerWord; ++c)
-          {
-            const int m = w * kPerWord + c;
-            word |= quant_core::code_of<Bits>(half_at(raw[m / 8], m % 8), lo, scale) << (Bits * c);
-          }
-          words[w] = word;
-        }
         std::uint8_t *at =
             dst + L.value_codes + (static_cast<std::size_t>(r) * W + ch0) * Bits / 8;
-#pragma unroll
-        for (int w = 0; w < kWords; w += 4)
+#pragma unroll 1
+        for (int i = 0; i < 8; ++i)
         {
-          *reinterpret_cast<uint4 *>(at + 4 * w) =
-              uint4{words[w], words[w + 1], words[w + 2], words[w + 3]};
+          store_codes8<Bits>(at + i * Bits, codes8<Bits>(load16(src + 8 * i), los, scales));
         }
         return;
       }
-#pragma unroll
+#pragma unroll 1
       for (int i = 0; i < 8; ++i)
       {
-        unsigned hv[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-        {
-          const float code =
-              static_cast<float>(quant_core::code_of<Bits>(half_at(raw[i], c), lo, scale));
-          hv[c] = half_of(fmaf(code, scale, lo));
-        }
         store16(out + static_cast<std::size_t>(r) * W + ch0 + 8 * i,
-                uint4{hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
-                      hv[6] | (hv[7] << 16)});
+                round8<Bits>(load16(src + 8 * i), los, scales));
       }
     }
 
     // Task `task` (of W) of one 32-token page: keys first, then values.
     template <int Bits, int HD>
-    __device__ void page_task(int task, const Rows &keys, const Rows &values, int kv_heads,
+    __device__ __forceinline__ void page_task(int task, const Rows &keys, const Rows &values, int kv_heads,
                               std::uint8_t *dst, const PageLayout &L, Emit key_emit,
                               Emit value_emit, int rows_limit = kP, int dst_row = 0)
     {
@@ -411,7 +438,7 @@ namespace mi
     };
 
     template <int HD>
-    __device__ void run_row_task(const RowJob &j, const PageLayout *lay, int task, int kv_heads)
+    __device__ __forceinline__ void run_row_task(const RowJob &j, const PageLayout *lay, int task, int kv_heads)
     {
       const int W = kv_heads * HD;
       const RowJobKind kind = static_cast<RowJobKind>(j.kind);
