@@ -338,6 +338,20 @@ int mi_kv_attention_layers(mi_kv_pages *kv, int first_layer, int layers, const v
                            const void *values, long long kv_stride, float *mass,
                            long long mass_stride, float *scores, long long scores_stride,
                            float alpha);
+/* Beyond the reference (which folds a layer's mass as it attends it,
+ * model.py:280-286 with importance_scores.cu:74-98): a decode step whose
+ * per-page mass is formed and folded once for every layer. Each layer's
+ * mi_kv_attention_kept (one query a head, as mi_kv_attention with seq_q 1
+ * and no mass) keeps its page statistics; mi_kv_fold_kept then writes every
+ * layer's masses (mass + layer * mass_stride, if mass is given) and folds
+ * them into the scores (scores + layer * scores_stride, if given) with
+ * `alpha`, in one launch, to the bits mi_kv_attention gives with mass and
+ * scores. Every layer must be attended, at one seq_k, between two folds. */
+int mi_kv_attention_kept(mi_kv_pages *kv, int layer, const void *q, const void *k_bias,
+                         mi_rope_table *rope, void *out, int seq_k, int heads, int kv_heads,
+                         int head_dim, const void *keys, const void *values);
+int mi_kv_fold_kept(mi_kv_pages *kv, float *mass, long long mass_stride, float *scores,
+                    long long scores_stride, float alpha);
 int mi_kv_downgrade(mi_kv_pages *kv, int layer, int page, int target);
 int mi_kv_upgrade(mi_kv_pages *kv, int layer, int page, int target);
 /* triples: n (layer, page, target tier), 3n ints. */

@@ -1190,6 +1190,31 @@ int mi_kv_attention_layers(mi_kv_pages *kv, int first_layer, int layers, const v
   });
 }
 
+int mi_kv_attention_kept(mi_kv_pages *kv, int layer, const void *q, const void *k_bias,
+                         mi_rope_table *rope, void *out, int seq_k, int heads, int kv_heads,
+                         int head_dim, const void *keys, const void *values)
+{
+  return guarded([&] {
+    need(q, "q");
+    need(out, "out");
+    const mi::RopeTable *table = rope != nullptr ? &rope->impl : nullptr;
+    if (k_bias != nullptr && (table == nullptr || table->positions() < seq_k))
+    {
+      throw mi::InvalidArgument("a key bias needs a RoPE table for head_dim " +
+                                std::to_string(head_dim) + " covering " + std::to_string(seq_k) +
+                                " positions");
+    }
+    kv->impl.attention_kept(layer, q, k_bias, table, out, seq_k, heads, kv_heads, head_dim, keys,
+                            values);
+  });
+}
+
+int mi_kv_fold_kept(mi_kv_pages *kv, float *mass, long long mass_stride, float *scores,
+                    long long scores_stride, float alpha)
+{
+  return guarded([&] { kv->impl.fold_kept(mass, mass_stride, scores, scores_stride, alpha); });
+}
+
 int mi_kv_downgrade(mi_kv_pages *kv, int layer, int page, int target)
 {
   return guarded([&] { kv->impl.downgrade(layer, page, target); });

@@ -128,6 +128,9 @@ namespace mi
       const std::uint8_t *warm_tiers;
       int warm_count;
       int mass_blocks;
+      // Added to the combine's block index: a launch of mass blocks alone
+      // (the deferred fold) starts past the output blocks.
+      int block_base;
       float *partials;   // [launch layer][kv_heads][splits][group][hd]: each split's output
       float *split_ml;   // [launch layer][kv_heads][group][splits][2]: each split's max and
                          // sum, a head's splits side by side so that they read coalesced
@@ -1659,6 +1662,7 @@ namespace mi
       const int G = a.group;
       const int li = blockIdx.y;
       const int t = threadIdx.x;
+      const int bx = static_cast<int>(blockIdx.x) + a.block_base;
       // Head h's split outputs (split s at s * split_stride) and its splits'
       // (max, sum) pairs, side by side.
       const auto head_out = [&](int h) {
@@ -1670,10 +1674,10 @@ namespace mi
                (static_cast<std::size_t>(li) * a.heads + h) * a.splits;
       };
       const std::size_t split_stride = static_cast<std::size_t>(G) * HD;
-      if (static_cast<int>(blockIdx.x) < a.heads * kBlocksAHead)
+      if (bx < a.heads * kBlocksAHead)
       {
-        const int h = blockIdx.x / kBlocksAHead;
-        const int c0 = (blockIdx.x % kBlocksAHead) * 4 * kQuads;
+        const int h = bx / kBlocksAHead;
+        const int c0 = (bx % kBlocksAHead) * 4 * kQuads;
         const int quad = t % kQuads;
         const int row = t / kQuads;
         const int splits = splits_of(li, h / G);
@@ -1773,7 +1777,7 @@ namespace mi
         }
         return;
       }
-      if (static_cast<int>(blockIdx.x) >= a.heads * kBlocksAHead + a.mass_blocks)
+      if (bx >= a.heads * kBlocksAHead + a.mass_blocks)
       {
         // A warm block: the next layer's tiers and page addresses through
         // this XCD's caches (workgroups go to the XCDs in turn, so the
@@ -1797,7 +1801,7 @@ namespace mi
       const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
       constexpr int kWavesC = kCombineThreads / 64;
       constexpr int kHeadsAWave = kMaxHeads / kWavesC;
-      const int page = (blockIdx.x - a.heads * kBlocksAHead) * 64 + lane;
+      const int page = (bx - a.heads * kBlocksAHead) * 64 + lane;
       const bool has_page = page < a.pages;
       const int pg = has_page ? page : a.pages - 1; // clamped: loads, never stores
       const float *stats = a.page_stats + static_cast<std::size_t>(li) * a.heads * a.pages * 2;
@@ -2046,12 +2050,21 @@ namespace mi
     }
     const std::size_t part =
         static_cast<std::size_t>(ls.layers) * a.kv_heads * d.splits * group * a.head_dim;
-    const std::size_t ml = static_cast<std::size_t>(ls.layers) * a.kv_heads * group * d.splits * 2;
-    const std::size_t stats = static_cast<std::size_t>(ls.layers) * a.heads * pages * 2;
+    const bool kept = ls.keep_ml != nullptr;
+    const std::size_t ml =
+        kept ? 0 : static_cast<std::size_t>(ls.layers) * a.kv_heads * group * d.splits * 2;
+    const std::size_t stats = kept ? 0 : static_cast<std::size_t>(ls.layers) * a.heads * pages * 2;
     float *ws = decode_scratch(a, part + ml + stats, stream);
     d.partials = ws;
-    d.split_ml = ws + part;
-    d.page_stats = ws + part + ml;
+    // Kept statistics (a decode whose fold comes later) go where the caller
+    // keeps them; otherwise they are scratch after the partials.
+    d.split_ml = kept ? ls.keep_ml : ws + part;
+    d.page_stats = kept ? ls.keep_stats : ws + part + ml;
+    if (kept && (a.mass != nullptr || a.scores != nullptr || ls.layers != 1 || !ls.split))
+    {
+      throw InvalidArgument("a decode that keeps its statistics for a later fold is one split "
+                            "layer with no mass or scores of its own");
+    }
     const int mass_blocks = (a.mass != nullptr || a.scores != nullptr) ? (pages + 63) / 64 : 0;
     d.mass_blocks = mass_blocks;
     const bool warm = kv.warm_pages != nullptr && ls.layers == 1;
@@ -2116,6 +2129,44 @@ namespace mi
           decode_combine_kernel<64, false>, decode_combine_kernel<64, true>, 64,
           stream_kernel_lds<64>());
     }
+  }
+
+  std::size_t decode_kept_floats(int heads, int kv_heads, int seq_k)
+  {
+    const int pages = (seq_k + kPageTokens - 1) / kPageTokens;
+    const int splits = (pages + kWaves - 1) / kWaves;
+    (void)kv_heads;
+    return static_cast<std::size_t>(heads) * splits * 2 + static_cast<std::size_t>(heads) * pages * 2;
+  }
+
+  void launch_decode_fold(const DecodeFold &f, hipStream_t stream)
+  {
+    if (f.layers <= 0)
+    {
+      return;
+    }
+    DecodeArgs d{};
+    const int pages = (f.seq_k + kPageTokens - 1) / kPageTokens;
+    d.heads = f.heads;
+    d.kv_heads = f.kv_heads;
+    d.group = f.heads / f.kv_heads;
+    d.pages = pages;
+    d.seq_k = f.seq_k;
+    d.splits = (pages + kWaves - 1) / kWaves;
+    d.split_ml = f.kept;
+    d.page_stats = f.kept + static_cast<std::size_t>(f.layers) * f.heads * d.splits * 2;
+    d.mass = f.mass;
+    d.mass_stride = f.mass_stride;
+    d.scores = f.scores;
+    d.scores_stride = f.scores_stride;
+    d.alpha = f.alpha;
+    d.mass_blocks = (pages + 63) / 64;
+    const int blocks_a_head = f.head_dim / (4 * kQuads);
+    d.block_base = f.heads * blocks_a_head;
+    const auto kernel = f.head_dim == 128 ? decode_combine_kernel<128, false>
+                                          : decode_combine_kernel<64, false>;
+    hipLaunchKernelGGL(kernel, dim3(d.mass_blocks, f.layers), dim3(kCombineThreads), 0, stream, d);
+    hip_check(hipGetLastError(), "decode fold kernel launch");
   }
 
   bool launch_decode_fast(const KVSource &kv, const AttentionArgs &a, hipStream_t stream)

@@ -23,9 +23,10 @@ namespace mi
   // A page's place as 32 bits: the space that holds it (bits 29-31) and its
   // index there. Spaces 0-3 are the allocator's four tier ranges (the index
   // a slot), space 4 the FP16 shadows in pinned host memory (the index a
-  // shadow number). Kernels turn a reference into an address themselves, so
+  // shadow number), space 5 FP16 pages staged in device memory. Kernels turn a reference into an address themselves, so
   // a batch sends 8 bytes a page pair to the device, not two addresses.
   constexpr int kShadowSpace = 4;
+  constexpr int kStagingSpace = 5; // FP16 pages staged in device memory, by index
   constexpr unsigned kRefIndexBits = 29;
   constexpr std::uint32_t kRefIndexMask = (1u << kRefIndexBits) - 1;
   __host__ __device__ constexpr std::uint32_t page_ref(int space, std::uint32_t index)
@@ -41,6 +42,7 @@ namespace mi
     unsigned long long bytes[kTierCount];
     const unsigned long long *shadows; // shadow number -> device address
     unsigned long long shadow_bytes;   // an FP16 page
+    unsigned long long staging;        // base of the staged FP16 pages, shadow_bytes apart
   };
 
   struct RefPair
@@ -274,6 +276,11 @@ namespace mi
     long long out_stride;
     long long mass_stride;
     long long scores_stride;
+    // A decode whose page statistics are kept for a later fold (one layer,
+    // split, no mass or scores of its own): its split maxima and sums and
+    // its page statistics go here, in a DecodeFold's layout for its layer.
+    float *keep_ml;
+    float *keep_stats;
   };
   // Whether the fast path takes this decode: one query, no key bias, 32-token
   // pages, head_dim 64 or 128, a group of at most 16 heads, 16-byte aligned
@@ -281,5 +288,29 @@ namespace mi
   bool decode_fast_applies(const KVSource &kv, const AttentionArgs &a);
   void launch_decode_layers(const KVSource &kv, const AttentionArgs &a, const DecodeLayers &ls,
                             hipStream_t stream);
+
+  // The fold of decodes that kept their statistics: every layer's page
+  // masses (into mass + layer * mass_stride, if given) and its importance
+  // scores (scores + layer * scores_stride, if given) in one launch, to the
+  // same bits the fused form gives. `kept` holds, for `layers` layers of one
+  // step (the same seq_k), first every layer's split maxima and sums
+  // [layer][heads][splits][2], then every layer's page statistics
+  // [layer][kv_heads][pages][group][2]; decode_kept_floats is one layer's share.
+  struct DecodeFold
+  {
+    int layers;
+    int heads;
+    int kv_heads;
+    int head_dim;
+    int seq_k;
+    float *kept;
+    float *mass;
+    long long mass_stride;
+    float *scores;
+    long long scores_stride;
+    float alpha;
+  };
+  std::size_t decode_kept_floats(int heads, int kv_heads, int seq_k);
+  void launch_decode_fold(const DecodeFold &f, hipStream_t stream);
 
 } // namespace mi

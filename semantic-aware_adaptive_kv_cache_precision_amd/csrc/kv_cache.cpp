@@ -721,7 +721,10 @@ namespace mi
     // 2. The device's work, by page reference: shadows out, restores in, one
     // quantise launch per target tier, each reading pages before any is
     // freed.
-    std::vector<RefPair> shadows_out, restores;
+    // A page quantised from its shadow is first brought to device memory in
+    // one copy (the quantiser reads its rows twice, and host memory is not
+    // cached on the device).
+    std::vector<RefPair> shadows_out, restores, restage;
     std::array<std::vector<RefPair>, kTierCount> requant;
     bool touches_shadow = false;
     for (std::size_t i = 0; i < n; ++i)
@@ -740,6 +743,12 @@ namespace mi
       {
         rows = page_ref(kShadowSpace, shadows_.number(keys[i]));
         touches_shadow = true;
+        if (targets[i] != kFP16)
+        {
+          const auto slot = static_cast<std::uint32_t>(restage.size());
+          restage.push_back({rows, page_ref(kStagingSpace, slot)});
+          rows = page_ref(kStagingSpace, slot);
+        }
       }
       if (targets[i] == kFP16)
       {
@@ -755,12 +764,20 @@ namespace mi
     all.reserve(2 * n);
     all.insert(all.end(), shadows_out.begin(), shadows_out.end());
     all.insert(all.end(), restores.begin(), restores.end());
+    all.insert(all.end(), restage.begin(), restage.end());
     for (const auto &r : requant)
     {
       all.insert(all.end(), r.begin(), r.end());
     }
     PageSpaces spaces = allocator_.spaces();
     spaces.shadows = shadows_.device_table(stream);
+    const std::size_t fp16_bytes = bytes_at(kFP16);
+    if (!restage.empty() && (staging_ == nullptr || staging_->bytes() < restage.size() * fp16_bytes))
+    {
+      staging_.reset(); // waits for launches that may read the old one
+      staging_ = std::make_unique<DeviceBuffer>(restage.size() * fp16_bytes);
+    }
+    spaces.staging = staging_ ? reinterpret_cast<unsigned long long>(staging_->raw()) : 0;
     const Clock::time_point device_began = Clock::now();
     const RefPair *on_device = pairs_upload_.send(all, stream);
     std::size_t at = 0;
@@ -768,6 +785,8 @@ namespace mi
     at += shadows_out.size();
     launch_copy_refs(on_device + at, static_cast<int>(restores.size()), spaces, stream);
     at += restores.size();
+    launch_copy_refs(on_device + at, static_cast<int>(restage.size()), spaces, stream);
+    at += restage.size();
     for (int t = kINT8; t <= kINT2; ++t)
     {
       launch_requant_refs(on_device + at, static_cast<int>(requant[t].size()), t, spaces,
@@ -901,6 +920,131 @@ namespace mi
       kv.warm_count = std::min((seq_k - 1) / page_tokens_, pages_);
     }
     launch_attention(kv, a, stream);
+  }
+
+  void KVPages::attention_kept(int layer, const void *q, const void *k_bias,
+                               const RopeTable *rope, void *out, int seq_k, int heads,
+                               int kv_heads, int head_dim, const void *keys, const void *values)
+  {
+    require_layer(layer);
+    if (static_cast<std::size_t>(kv_heads) * head_dim != kv_width_)
+    {
+      throw InvalidArgument("kv_heads * head_dim is " + std::to_string(kv_heads * head_dim) +
+                            "; this cache holds " + std::to_string(kv_width_) + " per token");
+    }
+    if (seq_k <= 0 || seq_k > capacity_tokens())
+    {
+      throw OutOfRange("seq_k " + std::to_string(seq_k) + " is not within the " +
+                       std::to_string(capacity_tokens()) + " positions on pages");
+    }
+    if (seals_ && (keys == nullptr || values == nullptr))
+    {
+      throw InvalidArgument("attention at a quantised tier reads each query's own page from the "
+                            "rows the queries stored; pass them");
+    }
+    if (seals_ && !open_pages_)
+    {
+      throw LogicError("attention before any position was reserved");
+    }
+    if (k_bias != nullptr && (rope == nullptr || rope->head_dim() != head_dim))
+    {
+      throw InvalidArgument("a key bias needs a RoPE table for head_dim " +
+                            std::to_string(head_dim) + " covering " + std::to_string(seq_k) +
+                            " positions");
+    }
+    const hipStream_t stream = runtime_stream();
+    sync_tables(stream);
+    AttentionArgs a{};
+    a.q = static_cast<const std::uint16_t *>(q);
+    a.out = static_cast<std::uint16_t *>(out);
+    a.k_bias = static_cast<const std::uint16_t *>(k_bias);
+    a.rope = k_bias != nullptr ? rope->data() : nullptr;
+    a.rope_positions = k_bias != nullptr ? rope->positions() : 0;
+    a.rope_angles = k_bias != nullptr ? rope->angles() : nullptr;
+    a.seq_q = 1;
+    a.seq_k = seq_k;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.workspace = &workspace_;
+    KVSource kv{};
+    kv.page_tokens = page_tokens_;
+    const std::size_t row = static_cast<std::size_t>(layer) * table_.stride();
+    kv.pages = pages_ > 0 ? table_.addresses() + row : nullptr;
+    if (seals_)
+    {
+      kv.layout = Layout::kCausal;
+      kv.tiers = pages_ > 0 ? table_.tiers() + row : nullptr;
+      kv.open = open_page(layer, attend_open_[layer]);
+      kv.chunk_k = static_cast<const std::uint16_t *>(keys);
+      kv.chunk_v = static_cast<const std::uint16_t *>(values);
+      kv.start = seq_k - 1;
+      std::copy(may_be_at_.begin(), may_be_at_.end(), kv.may_be_at);
+      if (layer + 1 < layers_ && pages_ > 0)
+      {
+        const std::size_t next = row + table_.stride();
+        kv.warm_pages = table_.addresses() + next;
+        kv.warm_tiers = table_.tiers() + next;
+        kv.warm_count = std::min((seq_k - 1) / page_tokens_, pages_);
+      }
+    }
+    else
+    {
+      kv.layout = Layout::kPaged;
+      kv.may_be_at[kFP16] = true;
+    }
+    if (!decode_fast_applies(kv, a))
+    {
+      throw InvalidArgument("a decode that keeps its statistics takes one query per head, "
+                            "32-token pages, head_dim 64 or 128 and at most 16 query heads per "
+                            "KV head, 16-byte aligned");
+    }
+    // A new step (or a new shape) starts a new set of kept statistics.
+    if (seq_k != kept_seq_k_ || heads != kept_heads_ || kv_heads != kept_kv_heads_ ||
+        head_dim != kept_head_dim_)
+    {
+      kept_layers_.assign(layers_, 0);
+      kept_seq_k_ = seq_k;
+      kept_heads_ = heads;
+      kept_kv_heads_ = kv_heads;
+      kept_head_dim_ = head_dim;
+    }
+    const int pages = (seq_k + page_tokens_ - 1) / page_tokens_;
+    const std::size_t per_layer = decode_kept_floats(heads, kv_heads, seq_k);
+    float *kept = kept_.floats(per_layer * layers_);
+    const std::size_t ml_floats = per_layer - static_cast<std::size_t>(heads) * pages * 2;
+    DecodeLayers ls{};
+    ls.split = true;
+    ls.layers = 1;
+    ls.keep_ml = kept + layer * ml_floats;
+    ls.keep_stats = kept + layers_ * ml_floats + static_cast<std::size_t>(layer) * heads * pages * 2;
+    launch_decode_layers(kv, a, ls, stream);
+    kept_layers_[layer] = 1;
+  }
+
+  void KVPages::fold_kept(float *mass, long long mass_stride, float *scores,
+                          long long scores_stride, float alpha)
+  {
+    if (kept_seq_k_ < 0 ||
+        std::find(kept_layers_.begin(), kept_layers_.end(), 0) != kept_layers_.end())
+    {
+      throw LogicError("a fold of kept statistics needs every layer of the step attended by "
+                       "attention_kept since the last fold");
+    }
+    DecodeFold f{};
+    f.layers = layers_;
+    f.heads = kept_heads_;
+    f.kv_heads = kept_kv_heads_;
+    f.head_dim = kept_head_dim_;
+    f.seq_k = kept_seq_k_;
+    f.kept = kept_.floats(decode_kept_floats(kept_heads_, kept_kv_heads_, kept_seq_k_) * layers_);
+    f.mass = mass;
+    f.mass_stride = mass_stride;
+    f.scores = scores;
+    f.scores_stride = scores_stride;
+    f.alpha = alpha;
+    launch_decode_fold(f, runtime_stream());
+    kept_layers_.assign(layers_, 0);
   }
 
   void KVPages::attention_layers(int first_layer, int layers, const void *q, long long q_stride,

@@ -49,13 +49,17 @@ namespace mi
       {
         return reinterpret_cast<std::uint8_t *>(s.shadows[index]);
       }
+      if (space == kStagingSpace)
+      {
+        return reinterpret_cast<std::uint8_t *>(s.staging + s.shadow_bytes * index);
+      }
       return reinterpret_cast<std::uint8_t *>(s.base[space] + s.bytes[space] * index);
     }
 
     __device__ inline unsigned long long page_size(const PageSpaces &s, std::uint32_t ref)
     {
       const std::uint32_t space = ref >> kRefIndexBits;
-      return space == kShadowSpace ? s.shadow_bytes : s.bytes[space];
+      return space >= kShadowSpace ? s.shadow_bytes : s.bytes[space];
     }
 
     // Rows [0, split) at lo, rows [split, P) at hi; `width` halves a row.

@@ -439,6 +439,17 @@ namespace mi
                           int head_dim, const void *keys, const void *values,
                           long long kv_stride, float *mass, long long mass_stride,
                           float *scores, long long scores_stride, float alpha);
+    // Beyond the reference: a decode step whose per-page mass is folded once
+    // for every layer instead of once a layer. attention_kept is one layer's
+    // decode (one query a head) keeping its page statistics; fold_kept then
+    // forms every layer's page masses and folds them into the scores in one
+    // launch, to the bits attention(..., mass, scores) gives a layer at a
+    // time. Every layer is attended, at one seq_k, between two folds.
+    void attention_kept(int layer, const void *q, const void *k_bias, const RopeTable *rope,
+                        void *out, int seq_k, int heads, int kv_heads, int head_dim,
+                        const void *keys, const void *values);
+    void fold_kept(float *mass, long long mass_stride, float *scores, long long scores_stride,
+                   float alpha);
     void downgrade(int layer, int page, int target);
     void upgrade(int layer, int page, int target);
     void move_pages(const std::vector<PageMove> &moves);
@@ -538,8 +549,19 @@ namespace mi
     std::unique_ptr<DeviceBuffer> open_table_;
     std::vector<unsigned long long> open_uploaded_;
     UploadBuffer pairs_upload_;
+    // FP16 pages brought from their shadows to device memory before they are
+    // quantised (read once over the host link, then twice from HBM).
+    std::unique_ptr<DeviceBuffer> staging_;
     // The decode path's split partials and page statistics: this cache's own.
     OwnedWorkspace workspace_;
+    // Page statistics kept for fold_kept, every layer's (decode_kept_floats
+    // a layer), and the step they belong to.
+    OwnedWorkspace kept_;
+    std::vector<char> kept_layers_;
+    int kept_seq_k_ = -1;
+    int kept_heads_ = 0;
+    int kept_kv_heads_ = 0;
+    int kept_head_dim_ = 0;
   };
 
   // The stream every launch of the runtime goes on, per host thread: the

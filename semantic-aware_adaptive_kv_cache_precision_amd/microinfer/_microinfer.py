@@ -150,6 +150,8 @@ SIGNATURES = {
                          _vp), C.c_int),
     "mi_kv_attention_layers": ((_vp, _i, _i, _vp, _ll, _vp, _ll, _i, _i, _i, _i, _vp, _vp, _ll,
                                 _vp, _ll, _vp, _ll, _f), C.c_int),
+    "mi_kv_attention_kept": ((_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp), C.c_int),
+    "mi_kv_fold_kept": ((_vp, _vp, _ll, _vp, _ll, _f), C.c_int),
     "mi_kv_downgrade": ((_vp, _i, _i, _i), C.c_int),
     "mi_kv_upgrade": ((_vp, _i, _i, _i), C.c_int),
     "mi_kv_move_pages": ((_vp, _ip, _sz), C.c_int),
@@ -1018,6 +1020,39 @@ class KVPages:
         _check(lib.mi_kv_attention_layers(self._h, first_layer, layers, qa, per_q, oa, per_q,
                                           seq_k, heads, kv_heads, head_dim, ka, va, width, ma,
                                           heads * pages, sa, stride, alpha))
+
+    def attention_kept(self, layer: int, q, k_bias, rope, out, seq_k: int, heads: int,
+                       kv_heads: int, head_dim: int, keys=None, values=None) -> None:
+        """Beyond the reference's surface: one layer's decode (one query a
+        head) keeping its page statistics for fold_kept, which forms every
+        layer's masses and folds them into the scores in one launch."""
+        per_q = heads * head_dim
+        width = kv_heads * head_dim
+        qa = _need(_span(q), per_q, "q")
+        oa = _need(_span(out), per_q, "out")
+        ba = _need(_span(k_bias), width, "k_bias") if k_bias is not None else None
+        ka = _need(_span(keys), width, "keys") if keys is not None else None
+        va = _need(_span(values), width, "values") if values is not None else None
+        _check(lib.mi_kv_attention_kept(self._h, layer, qa, ba, rope._h if rope else None, oa,
+                                        seq_k, heads, kv_heads, head_dim, ka, va))
+
+    def fold_kept(self, scores=None, mass=None, seq_k: int | None = None, heads: int = 0) -> None:
+        """Every layer's page masses (mass: (layers, heads, pages) floats,
+        if given) and their fold into `scores` (an ImportanceScores, if
+        given), for the step every layer was attended in by attention_kept."""
+        ma, mstride = None, 0
+        if mass is not None:
+            if seq_k is None or heads <= 0:
+                raise ValueError("a mass output needs the step's seq_k and heads")
+            pages = -(-seq_k // self.page_tokens)
+            if mass.numel < self.layers * heads * pages:
+                raise ValueError(f"the per-page attention mass of {self.layers} layers needs "
+                                 f"{self.layers * heads * pages} floats; got {mass.numel}")
+            ma, mstride = mass.address, heads * pages
+        sa, sstride, alpha = None, 0, 0.0
+        if scores is not None:
+            sa, sstride, alpha = scores.row(0), scores.max_pages, scores.alpha
+        _check(lib.mi_kv_fold_kept(self._h, ma, mstride, sa, sstride, alpha))
 
     def page_tier(self, layer: int, page: int) -> Tier:
         t = C.c_int()

@@ -756,3 +756,59 @@ def test_after_a_capture_the_runtime_is_back_on_the_null_stream():
                                                with_bound=True)
     assert_attention_close(got, want, "after the stream went", bound)
     assert_mass_close(mass, want_mass, "after the stream went")
+
+
+def test_a_step_folded_once_is_the_fused_step_to_the_bit():
+    """attention_kept on every layer then one fold_kept (beyond the
+    reference) against attention(..., mass, scores) a layer at a time: the
+    same output bits, the same mass bits, the same score bits, over two
+    steps (the second folding into the first's scores), mixed tiers, the
+    1.5B and Llama head shapes; and a fold with a layer missing is refused."""
+    m = mi()
+    d = m.device
+    P, L = 32, 3
+    for (heads, kv, hd), seq in (((12, 2, 128), 32 * 40 + 7), ((32, 8, 64), 32 * 21 + 30)):
+        rng = np.random.default_rng(seq)
+        cap = [4096] * 4
+        cap[0] += L * 2 + 8
+        alloc = m.PagedKVCache(page_sizes(P, kv, hd), cap)
+        tmap = [[(i * 3 + l) % 4 for i in range(seq // P + 2)] for l in range(L)]
+        cache = d.KVPages(alloc, L, P, kv, hd, 0, d.Halves.Both, tmap, True)
+        k, v = normal(rng, L, seq + 1, kv, hd), normal(rng, L, seq + 1, kv, hd)
+        pages = -(-seq // P)
+        fused_scores = d.ImportanceScores(L, pages + 1)
+        kept_scores = d.ImportanceScores(L, pages + 1)
+        part = d.empty_f32(d.attention_partials(hd))
+        for step, s in enumerate((seq - 1, seq)):
+            for l in range(L):
+                if step == 0:
+                    store_in_runs(cache, l, k[l, :s], v[l, :s], [s])
+                else:
+                    cache.reserve(s)
+                    cache.store(l, put(k[l, s - 1:s]), put(v[l, s - 1:s]), s - 1, 1)
+            npages = -(-s // P)
+            q = normal(rng, L, heads, hd)
+            kept_mass = d.empty_f32(L * heads * npages)
+            outs = []
+            announce("kept step", heads, kv, hd, s)
+            for l in range(L):
+                out = d.empty(heads * hd)
+                cache.attention_kept(l, put(q[l]), None, None, out, s, heads, kv, hd,
+                                     put(k[l, s - 1:s]), put(v[l, s - 1:s]))
+                outs.append(out)
+            cache.fold_kept(kept_scores, kept_mass, s, heads)
+            got_mass = kept_mass.to_numpy().reshape(L, heads, npages)
+            for l in range(L):
+                out, mass = d.empty(heads * hd), d.empty_f32(heads * npages)
+                cache.attention(l, put(q[l]), None, None, out, 1, s, heads, kv, hd,
+                                put(k[l, s - 1:s]), put(v[l, s - 1:s]), mass, part,
+                                scores=fused_scores)
+                np.testing.assert_array_equal(outs[l].raw(), out.raw())
+                np.testing.assert_array_equal(got_mass[l], mass.to_numpy().reshape(heads, npages))
+            np.testing.assert_array_equal(kept_scores.download(), fused_scores.download())
+        # A fold with a layer not attended since the last is refused.
+        out = d.empty(heads * hd)
+        cache.attention_kept(0, put(q[0]), None, None, out, seq, heads, kv, hd,
+                             put(k[0, seq - 1:seq]), put(v[0, seq - 1:seq]))
+        with pytest.raises(RuntimeError, match="every layer"):
+            cache.fold_kept(kept_scores)
