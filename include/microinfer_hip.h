@@ -76,6 +76,12 @@ int mi_driver_version(int *version);
 int mi_memory_info(size_t *free_bytes, size_t *total_bytes);
 int mi_granule_bytes(size_t *out);
 int mi_malloc(void **out, size_t bytes);
+/* Pinned host memory mapped for the device (the memory FP16 shadows live
+ * in): *host its host address, *device the address kernels use. For
+ * measuring the host link a batch of moves crosses. No counterpart in the
+ * reference. */
+int mi_host_alloc(void **host, void **device, size_t bytes);
+int mi_host_free(void *host);
 int mi_free(void *ptr);
 /* kind: 0 host-to-device, 1 device-to-host, 2 device-to-device. Synchronous. */
 int mi_memcpy(void *dst, const void *src, size_t bytes, int kind);

@@ -258,6 +258,34 @@ int mi_device_name(char *out, size_t capacity)
   });
 }
 
+int mi_host_alloc(void **host, void **device, size_t bytes)
+{
+  return guarded([&] {
+    need(host, "host");
+    need(device, "device");
+    *host = nullptr;
+    *device = nullptr;
+    mi::hip_check(hipHostMalloc(host, bytes, hipHostMallocMapped), "hipHostMalloc");
+    const hipError_t mapped = hipHostGetDevicePointer(device, *host, 0);
+    if (mapped != hipSuccess)
+    {
+      (void)hipHostFree(*host);
+      *host = nullptr;
+      mi::hip_check(mapped, "hipHostGetDevicePointer");
+    }
+  });
+}
+
+int mi_host_free(void *host)
+{
+  return guarded([&] {
+    if (host != nullptr)
+    {
+      mi::hip_check(hipHostFree(host), "hipHostFree");
+    }
+  });
+}
+
 int mi_device_pci_bus_id(char *out, size_t capacity)
 {
   return guarded([&] {

@@ -49,6 +49,7 @@
 #include <cmath>
 #include <map>
 #include <mutex>
+#include <numeric>
 #include <vector>
 
 namespace mi
@@ -110,11 +111,15 @@ namespace mi
       int pages_per_wave;
       int splits;
       float scale; // 1/sqrt(hd) * log2 e: scores in base-2 units
-      // Streaming launches: the (layer, KV head, page) units split into
-      // stream_waves equal contiguous ranges, one a wave; a group's splits are
-      // the waves whose ranges meet it. 0: fixed splits of pages_per_wave * 8.
+      // Streaming launches: the (layer, KV-head block, page) units split into
+      // stream_ranges equal contiguous ranges. A range is walked by
+      // stream_ways waves of one workgroup together, one KV head of the block
+      // each, so that the bytes of a page's KV heads, which share its rows'
+      // lines, are asked for at the same time on one CU. A group's splits
+      // are the ranges that meet it. 0: fixed splits of pages_per_wave * 8.
       long long stream_units;
-      int stream_waves;
+      int stream_ranges;
+      int stream_ways;
       // The key bias (one layer's, kv_heads x hd fp16), the RoPE table
       // ({cos, sin} per position and angle, fp32) and its first page's
       // angles as fp16 high and low parts ([row][hi | lo][hd]); null: no bias.
@@ -1057,16 +1062,33 @@ namespace mi
 
     struct Unit
     {
-      int li;   // layer within the launch
-      int kvh;
+      int li;    // layer within the launch
+      int block; // KV-head block: heads [block * ways, (block + 1) * ways)
       int page;
+      int kvh;   // the wave's KV head of the block
     };
 
-    __device__ inline Unit unit_of(long long u, int kv_heads, int pages)
+    __device__ inline Unit unit_of(long long u, int blocks, int pages, int ways, int way)
     {
       const long long group = u / pages;
-      return {static_cast<int>(group / kv_heads), static_cast<int>(group % kv_heads),
-              static_cast<int>(u - group * pages)};
+      const int block = static_cast<int>(group % blocks);
+      return {static_cast<int>(group / blocks), block, static_cast<int>(u - group * pages),
+              block * ways + way};
+    }
+
+    // The unit after u in a range: the next page, or the next group's first.
+    __device__ inline void next_unit(Unit &u, int blocks, int pages, int ways)
+    {
+      if (++u.page == pages)
+      {
+        u.page = 0;
+        if (++u.block == blocks)
+        {
+          u.block = 0;
+          ++u.li;
+        }
+        u.kvh = u.block * ways + u.kvh % ways;
+      }
     }
 
     // Range of wave w: units [w U / W, (w+1) U / W).
@@ -1090,17 +1112,25 @@ namespace mi
       return static_cast<int>(w);
     }
 
-    // Splits of (layer li, KV head kvh): fixed, or the streaming waves that
-    // meet its pages; and the split a streaming wave writes for it.
+    // The first unit of (layer li, KV head kvh)'s group in the streaming
+    // launch's unit order.
+    __host__ __device__ inline long long group_base(const DecodeArgs &a, int li, int kvh)
+    {
+      const int blocks = a.kv_heads / a.stream_ways;
+      return (static_cast<long long>(li) * blocks + kvh / a.stream_ways) * a.pages;
+    }
+
+    // Splits of (layer li, KV head kvh): fixed, or the streaming ranges that
+    // meet its pages.
     __host__ __device__ inline int group_splits(const DecodeArgs &a, int li, int kvh)
     {
-      if (a.stream_waves == 0)
+      if (a.stream_ranges == 0)
       {
         return a.splits;
       }
-      const long long base = (static_cast<long long>(li) * a.kv_heads + kvh) * a.pages;
-      return wave_of(base + a.pages - 1, a.stream_units, a.stream_waves) -
-             wave_of(base, a.stream_units, a.stream_waves) + 1;
+      const long long base = group_base(a, li, kvh);
+      return wave_of(base + a.pages - 1, a.stream_units, a.stream_ranges) -
+             wave_of(base, a.stream_units, a.stream_ranges) + 1;
     }
 
     // Issues the copies of unit `u` (address `page`, tier `tier`) into `slot`.
@@ -1337,11 +1367,12 @@ namespace mi
                                   reinterpret_cast<const unsigned *>(meta + 256), zero);
     }
 
-    // Each wave takes an equal contiguous range of (layer, KV head, page)
-    // units (at most 64, and at most two groups) and walks it with one unit
-    // in flight: the next unit's bytes are copied into the wave's LDS slot by
-    // global_load_lds while the current one, already in registers, is
-    // computed. A wave writes one partial per group it touches.
+    // Each range of (layer, KV-head block, page) units (at most 64 of them)
+    // is walked by `ways` waves of a workgroup, one KV head of the block
+    // each, with one unit in flight a wave: the next unit's bytes are copied
+    // into the wave's LDS slot by global_load_lds while the current one,
+    // already in registers, is computed. A wave writes one partial per group
+    // it touches.
     template <int HD>
     __global__ void __launch_bounds__(kThreads) decode_stream_kernel(DecodeArgs a)
     {
@@ -1354,13 +1385,16 @@ namespace mi
       const int r = lane & 15;
       const int g = lane >> 4;
       const int G = a.group;
-      const int gw = blockIdx.x * kWaves + wave;
-      if (gw >= a.stream_waves)
+      const int ways = a.stream_ways;
+      const int way = wave % ways;
+      const int blocks = a.kv_heads / ways;
+      const int gw = blockIdx.x * (kWaves / ways) + wave / ways; // the range
+      if (gw >= a.stream_ranges)
       {
         return;
       }
-      const long long u0 = range_start(gw, a.stream_units, a.stream_waves);
-      const long long u1 = range_start(gw + 1, a.stream_units, a.stream_waves);
+      const long long u0 = range_start(gw, a.stream_units, a.stream_ranges);
+      const long long u1 = range_start(gw + 1, a.stream_units, a.stream_ranges);
       const int n = static_cast<int>(u1 - u0);
       if (n <= 0)
       {
@@ -1376,7 +1410,7 @@ namespace mi
       int my_tier = kFP16;
       if (lane < n)
       {
-        const Unit u = unit_of(u0 + lane, a.kv_heads, a.pages);
+        const Unit u = unit_of(u0 + lane, blocks, a.pages, ways, way);
         const long long at = static_cast<long long>(a.first_layer + u.li) * a.table_stride + u.page;
         if (a.causal)
         {
@@ -1412,24 +1446,15 @@ namespace mi
         const int t = tier_of(0);
         if (t != kUnreadPage)
         {
-          stream_copy<HD>(a, unit_of(u0, a.kv_heads, a.pages), addr_of(0), t, slot, lane);
+          stream_copy<HD>(a, unit_of(u0, blocks, a.pages, ways, way), addr_of(0), t, slot, lane);
         }
       }
-      Unit u = unit_of(u0, a.kv_heads, a.pages);
+      Unit u = unit_of(u0, blocks, a.pages, ways, way);
       for (int i = 0; i < n; ++i)
       {
         if (i > 0)
         {
-          // The next unit: the next page, or the next group's first.
-          if (++u.page == a.pages)
-          {
-            u.page = 0;
-            if (++u.kvh == a.kv_heads)
-            {
-              u.kvh = 0;
-              ++u.li;
-            }
-          }
+          next_unit(u, blocks, a.pages, ways);
         }
         const int group = u.li * a.kv_heads + u.kvh;
         if (group != seg_group)
@@ -1470,15 +1495,7 @@ namespace mi
             if (t != kUnreadPage)
             {
               Unit v = u;
-              if (++v.page == a.pages)
-              {
-                v.page = 0;
-                if (++v.kvh == a.kv_heads)
-                {
-                  v.kvh = 0;
-                  ++v.li;
-                }
-              }
+              next_unit(v, blocks, a.pages, ways);
               stream_copy<HD>(a, v, addr_of(i + 1), t, slot, lane);
             }
           }
@@ -1539,8 +1556,8 @@ namespace mi
         const bool group_ends = i + 1 == n || u.page + 1 == a.pages;
         if (group_ends)
         {
-          const long long base = static_cast<long long>(group) * a.pages;
-          const int split = gw - wave_of(base, a.stream_units, a.stream_waves);
+          const int split =
+              gw - wave_of(group_base(a, u.li, u.kvh), a.stream_units, a.stream_ranges);
           if (first)
           {
             // Every unit of the segment was unread: an empty partial.
@@ -2020,14 +2037,18 @@ namespace mi
     int stream_blocks = 0;
     if (streaming)
     {
-      const long long units = static_cast<long long>(ls.layers) * a.kv_heads * pages;
+      // A range's waves: as many of the KV heads as divide a workgroup.
+      const int ways = std::gcd(a.kv_heads, kWaves);
+      const long long units = static_cast<long long>(ls.layers) * (a.kv_heads / ways) * pages;
       const int per_cu = 1; // 2 waves a SIMD (registers); LDS holds a slot a wave
-      long long waves = static_cast<long long>(device_multiprocessors()) * per_cu * kWaves;
-      waves = std::max(waves, (units + 63) / 64); // at most 64 units a wave
-      waves = std::min(waves, units);             // no wave without a unit
+      long long ranges = static_cast<long long>(device_multiprocessors()) * per_cu * kWaves / ways;
+      ranges = std::max(ranges, (units + 63) / 64); // at most 64 units a range
+      ranges = std::min(ranges, units);             // no range without a unit
       d.stream_units = units;
-      d.stream_waves = static_cast<int>(waves);
-      stream_blocks = static_cast<int>((waves + kWaves - 1) / kWaves);
+      d.stream_ranges = static_cast<int>(ranges);
+      d.stream_ways = ways;
+      const long long per_block = kWaves / ways;
+      stream_blocks = static_cast<int>((ranges + per_block - 1) / per_block);
       d.pages_per_wave = 0;
       d.splits = 1;
       for (int li = 0; li < ls.layers; ++li)

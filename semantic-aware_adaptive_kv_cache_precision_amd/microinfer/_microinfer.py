@@ -60,6 +60,8 @@ SIGNATURES = {
     "mi_last_error": ((), C.c_char_p), "mi_build_info": ((), C.c_char_p),
     "mi_device_count": ((_ip,), C.c_int), "mi_device_name": ((C.c_char_p, _sz), C.c_int),
     "mi_runtime_version": ((_ip,), C.c_int),
+    "mi_host_alloc": ((C.POINTER(_vp), C.POINTER(_vp), _sz), C.c_int),
+    "mi_host_free": ((_vp,), C.c_int),
     "mi_device_pci_bus_id": ((C.c_char_p, _sz), C.c_int), "mi_memory_info": ((_szp, _szp), C.c_int),
     "mi_granule_bytes": ((_szp,), C.c_int), "mi_malloc": ((C.POINTER(_vp), _sz), C.c_int),
     "mi_free": ((_vp,), C.c_int), "mi_memcpy": ((_vp, _vp, _sz, _i), C.c_int),
@@ -291,6 +293,18 @@ def upload_fp16(host) -> DeviceTensor:
 
 
 weight_alignment = 256
+
+
+class HostBuffer:
+    """Pinned host memory mapped for the device (beyond the reference):
+    `address` is what kernels use, `array` the host's view (uint8)."""
+
+    def __init__(self, nbytes: int):
+        h, dv = _vp(), _vp()
+        _check(lib.mi_host_alloc(C.byref(h), C.byref(dv), nbytes))
+        self._host, self.address, self.nbytes = h.value, dv.value, nbytes
+        weakref.finalize(self, lib.mi_host_free, self._host)
+        self.array = np.ctypeslib.as_array((C.c_uint8 * nbytes).from_address(self._host))
 
 
 class DeviceArena:

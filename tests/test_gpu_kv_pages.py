@@ -234,9 +234,11 @@ def test_the_fused_ewma_is_the_oracle_fold_of_the_kernel_s_masses():
 
 def test_one_launch_over_several_layers_matches_each_layer_and_the_oracle():
     """attention_layers, beyond the reference (several layers' decode queries
-    in one launch, streamed through LDS a page at a time), against each
-    layer's own split attention call and the float64 oracle, at the 1e-3 bar,
-    over mixed tiers, 1.5B / 0.5B / Llama head shapes; the scores folded over
+    in one launch, streamed through LDS a page at a time, the waves of a
+    range one KV head each: 1, 2, 4 and 8 KV heads, and 3, whose heads a
+    range's waves cannot share), against each layer's own split attention
+    call and the float64 oracle, at the 1e-3 bar, over mixed tiers, 1.5B /
+    0.5B / Llama head shapes; the scores folded over
     two steps equal, to the bit, the oracle's fold of the launch's own masses.
     Also a sub-range of layers, a cache that does not seal, and a range past
     the cache refused."""
@@ -245,6 +247,7 @@ def test_one_launch_over_several_layers_matches_each_layer_and_the_oracle():
     P, L = 32, 3
     cases = [((12, 2, 128), 32 * 9 + 7), ((12, 2, 128), 32 * 64), ((12, 2, 128), 33),
              ((14, 2, 64), 32 * 40 + 1), ((32, 8, 64), 32 * 17 + 30),
+             ((12, 4, 64), 32 * 11 + 3), ((9, 3, 128), 32 * 6 + 5), ((4, 1, 128), 32 * 5),
              ((12, 2, 128), 20)]  # no page sealed yet: the cache has no page tables
     for (heads, kv, hd), seq in cases:
         announce("layers in one launch", heads, kv, hd, seq)
