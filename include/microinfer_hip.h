@@ -358,6 +358,82 @@ int mi_kv_attention_kept(mi_kv_pages *kv, int layer, const void *q, const void *
                          int head_dim, const void *keys, const void *values);
 int mi_kv_fold_kept(mi_kv_pages *kv, float *mass, long long mass_stride, float *scores,
                     long long scores_stride, float alpha);
+/* Beyond the reference: the store and the decode of a step whose position
+ * lives in device memory, what mi_decode_step's graph launches, for callers
+ * that capture graphs of their own (the reference's KVPages.store and
+ * attention take it from the host: kv_pages.h:161-195). mi_kv_store_at
+ * stores one row (keys, values: kv_width fp16 each) at *position, read when
+ * the kernel runs, sealing the page that row completes, as mi_kv_store does
+ * for one row. mi_kv_attention_at decodes one layer (one query a head) at
+ * seq_k = *seq_k, read when the kernels run, the launch sized for max_seq_k:
+ * to the bit mi_kv_attention's with partials at that seq_k. Positions up to
+ * max_seq_k must be reserved and no page may move while they run; the cache
+ * must seal. mi_kv_stored_on_device records afterwards that every position
+ * before `end` was stored. */
+int mi_kv_store_at(mi_kv_pages *kv, int layer, const void *keys, const void *values,
+                   const int *position);
+int mi_kv_attention_at(mi_kv_pages *kv, int layer, const void *q, const void *k_bias,
+                       mi_rope_table *rope, void *out, const int *seq_k, int max_seq_k,
+                       int heads, int kv_heads, int head_dim, const void *keys,
+                       const void *values);
+int mi_kv_stored_on_device(mi_kv_pages *kv, int end);
+
+/* ---- a whole decode step as one HIP graph (beyond the reference) ---------
+ * The reference sequences a decode step from the host, a device call at a
+ * time (src/microinfer/model.py:332-403 Model.run; the greedy loop of
+ * engine.py:1180-1206). mi_decode_step captures every launch of a step --
+ * embedding, per layer RMSNorm, the q/k/v projections, RoPE, the store, the
+ * paged decode, the output projection into the fp32 residual, RMSNorm, gate
+ * and up with SwiGLU, the down projection; then the final RMSNorm, the
+ * head's logits and the greedy token -- as one graph whose kernels read the
+ * step's token, position and seq_k from device memory, so one graph serves
+ * every step of a run. Weights are fp16 device pointers, [out][in]; biases
+ * may be NULL; a key bias (on every layer or on none) is added by attention,
+ * rotated, as the reference does (ADR-0009). The cache must seal its pages
+ * and outlive the step; `scores` (may be NULL) takes each step's masses at
+ * seq_k a multiple of score_every. */
+typedef struct mi_decode_step mi_decode_step;
+typedef struct mi_model_shape {
+  int layers;
+  int hidden;
+  int intermediate;
+  int heads;
+  int kv_heads;
+  int head_dim;
+  int vocab;
+  float rms_eps;
+  double rope_theta;
+} mi_model_shape;
+typedef struct mi_layer_weights {
+  const void *input_norm;
+  const void *q_w;
+  const void *q_b;
+  const void *k_w;
+  const void *k_b;
+  const void *v_w;
+  const void *v_b;
+  const void *o_w;
+  const void *post_norm;
+  const void *gate_w;
+  const void *up_w;
+  const void *down_w;
+} mi_layer_weights;
+int mi_decode_step_create(mi_decode_step **out, mi_kv_pages *kv, const mi_model_shape *shape,
+                          const void *embed, const void *final_norm, const void *head,
+                          const mi_layer_weights *layers, mi_scores *scores, int score_every);
+int mi_decode_step_destroy(mi_decode_step *step);
+/* `steps` greedy steps, the first feeding `token` at `position` (the cache
+ * holds every position before it); the chosen tokens to `tokens` (host,
+ * `steps` of them); *device_ms (may be NULL) the replays' device time. The
+ * run reserves its pages first and records its stores after. */
+int mi_decode_step_run(mi_decode_step *step, int token, int position, int steps,
+                       int32_t *tokens, double *device_ms);
+/* The last step's logits, fp32, to host memory (count <= vocab). */
+int mi_decode_step_logits(mi_decode_step *step, float *out, size_t count);
+int mi_decode_step_launches(mi_decode_step *step, int *out);
+/* Synthetic fp16 weights made on the device: uniform in [-scale, scale)
+ * from `seed`. */
+int mi_random_half(void *out, size_t count, unsigned long long seed, float scale);
 int mi_kv_downgrade(mi_kv_pages *kv, int layer, int page, int target);
 int mi_kv_upgrade(mi_kv_pages *kv, int layer, int page, int target);
 /* triples: n (layer, page, target tier), 3n ints. */

@@ -21,8 +21,9 @@ LIBRARY = HERE / "microinfer" / "libmicroinfer_hip.so"
 ARCH = os.environ.get("MI_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["quant.hip", "page_jobs.hip", "pages.hip", "pointwise.hip", "attention.hip",
-           "decode.hip", "prefill.hip", "dense.hip", "linear.cpp", "page_allocator.cpp",
-           "shadow_store.cpp", "scores_rope.cpp", "kv_cache.cpp", "capi.cpp"]
+           "decode.hip", "prefill.hip", "dense.hip", "step.hip", "linear.cpp",
+           "page_allocator.cpp", "shadow_store.cpp", "scores_rope.cpp", "kv_cache.cpp",
+           "decode_step.cpp", "capi.cpp"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 # The dense projections call hipBLASLt.
 LIBS = [f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lhipblaslt"]

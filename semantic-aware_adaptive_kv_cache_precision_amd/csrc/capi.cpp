@@ -3,6 +3,8 @@
 
 #include "../../include/microinfer_hip.h"
 
+#include "decode_step.hpp"
+#include "kernels.hpp"
 #include "runtime.hpp"
 
 #include <cstring>
@@ -44,6 +46,11 @@ struct mi_shadows
 {
   mi::ShadowStore impl;
   explicit mi_shadows(std::size_t b) : impl(b) {}
+};
+struct mi_decode_step
+{
+  mi::DecodeStep impl;
+  template <typename... A> explicit mi_decode_step(A &&...a) : impl(std::forward<A>(a)...) {}
 };
 struct mi_rope_table
 {
@@ -1241,6 +1248,118 @@ int mi_kv_fold_kept(mi_kv_pages *kv, float *mass, long long mass_stride, float *
                     long long scores_stride, float alpha)
 {
   return guarded([&] { kv->impl.fold_kept(mass, mass_stride, scores, scores_stride, alpha); });
+}
+
+int mi_kv_store_at(mi_kv_pages *kv, int layer, const void *keys, const void *values,
+                   const int *position)
+{
+  return guarded([&] {
+    need(kv, "kv");
+    need(keys, "keys");
+    need(values, "values");
+    need(position, "position");
+    kv->impl.store_step(layer, keys, values, position);
+  });
+}
+
+int mi_kv_attention_at(mi_kv_pages *kv, int layer, const void *q, const void *k_bias,
+                       mi_rope_table *rope, void *out, const int *seq_k, int max_seq_k,
+                       int heads, int kv_heads, int head_dim, const void *keys,
+                       const void *values)
+{
+  return guarded([&] {
+    need(kv, "kv");
+    need(q, "q");
+    need(out, "out");
+    need(seq_k, "seq_k");
+    need(keys, "keys");
+    need(values, "values");
+    kv->impl.attention_step(layer, q, k_bias, rope != nullptr ? &rope->impl : nullptr, out, seq_k,
+                            max_seq_k, heads, kv_heads, head_dim, keys, values, nullptr);
+  });
+}
+
+int mi_kv_stored_on_device(mi_kv_pages *kv, int end)
+{
+  return guarded([&] {
+    need(kv, "kv");
+    kv->impl.stored_on_device(end);
+  });
+}
+
+int mi_decode_step_create(mi_decode_step **out, mi_kv_pages *kv, const mi_model_shape *shape,
+                          const void *embed, const void *final_norm, const void *head,
+                          const mi_layer_weights *layers, mi_scores *scores, int score_every)
+{
+  return guarded([&] {
+    need(out, "out");
+    need(kv, "kv");
+    need(shape, "shape");
+    need(layers, "layers");
+    *out = nullptr;
+    const mi::ModelShape sh{shape->layers,   shape->hidden,   shape->intermediate,
+                            shape->heads,    shape->kv_heads, shape->head_dim,
+                            shape->vocab,    shape->rms_eps,  shape->rope_theta};
+    if (sh.layers <= 0)
+    {
+      throw mi::InvalidArgument("a model has at least one layer");
+    }
+    const auto half = [](const void *p) { return static_cast<const std::uint16_t *>(p); };
+    mi::ModelWeights w{half(embed), half(final_norm), half(head), {}};
+    for (int l = 0; l < sh.layers; ++l)
+    {
+      const mi_layer_weights &x = layers[l];
+      w.layers.push_back({half(x.input_norm), half(x.q_w), half(x.q_b), half(x.k_w), half(x.k_b),
+                          half(x.v_w), half(x.v_b), half(x.o_w), half(x.post_norm),
+                          half(x.gate_w), half(x.up_w), half(x.down_w)});
+    }
+    *out = new mi_decode_step(kv->impl, sh, std::move(w),
+                              scores != nullptr ? &scores->impl : nullptr, score_every);
+  });
+}
+
+int mi_decode_step_destroy(mi_decode_step *step)
+{
+  return guarded([&] { delete step; });
+}
+
+int mi_decode_step_run(mi_decode_step *step, int token, int position, int steps,
+                       int32_t *tokens, double *device_ms)
+{
+  return guarded([&] {
+    need(step, "step");
+    const double ms = step->impl.run(token, position, steps, tokens);
+    if (device_ms != nullptr)
+    {
+      *device_ms = ms;
+    }
+  });
+}
+
+int mi_decode_step_logits(mi_decode_step *step, float *out, size_t count)
+{
+  return guarded([&] {
+    need(step, "step");
+    need(out, "out");
+    step->impl.logits(out, count);
+  });
+}
+
+int mi_decode_step_launches(mi_decode_step *step, int *out)
+{
+  return guarded([&] {
+    need(step, "step");
+    need(out, "out");
+    *out = step->impl.launches();
+  });
+}
+
+int mi_random_half(void *out, size_t count, unsigned long long seed, float scale)
+{
+  return guarded([&] {
+    need(out, "out");
+    mi::launch_random_half(out, count, seed, scale, mi::runtime_stream());
+  });
 }
 
 int mi_kv_downgrade(mi_kv_pages *kv, int layer, int page, int target)

@@ -136,6 +136,15 @@ namespace mi
       // Added to the combine's block index: a launch of mass blocks alone
       // (the deferred fold) starts past the output blocks.
       int block_base;
+      // A launch whose position lives on the device (a graphed decode step):
+      // seq_k is read from *live_seq_k when the kernels run, and the launch
+      // is sized by `pages` and `splits` for the most positions it may see,
+      // which stay the strides of every per-page and per-split array. Null:
+      // seq_k as given. live_pages and live_splits bound the work either way.
+      const int *live_seq_k;
+      int live_pages;
+      int live_splits;
+      int score_every; // a mass block folds only at a seq_k that is a multiple of this
       float *partials;   // [launch layer][kv_heads][splits][group][hd]: each split's output
       float *split_ml;   // [launch layer][kv_heads][group][splits][2]: each split's max and
                          // sum, a head's splits side by side so that they read coalesced
@@ -144,6 +153,21 @@ namespace mi
     };
 
     __device__ inline half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
+
+    // The launch's position, when it lives on the device: seq_k, the first
+    // chunk row (a decode step brings one) and the live bounds.
+    __device__ inline void go_live(DecodeArgs &a)
+    {
+      if (a.live_seq_k != nullptr)
+      {
+        const int seq_k = *a.live_seq_k;
+        a.seq_k = seq_k;
+        a.start = seq_k - 1;
+        a.live_pages = (seq_k + kPageTokens - 1) / kPageTokens;
+        const int per_split = kWaves * a.pages_per_wave;
+        a.live_splits = (a.live_pages + per_split - 1) / per_split;
+      }
+    }
 
     // 2^x as the one hardware instruction (v_exp_f32): softmax weights and
     // rescale factors, where a result below 2^-126 weighs nothing.
@@ -752,6 +776,11 @@ namespace mi
       const int kvh = blockIdx.y;
       const int li = blockIdx.z;
       const int layer = a.first_layer + li;
+      go_live(a);
+      if (split >= a.live_splits)
+      {
+        return; // past the live pages: the combine reads no partial of this split
+      }
       const int G = a.group;
       const std::size_t W = static_cast<std::size_t>(a.kv_heads) * HD;
       const std::size_t run0 = static_cast<std::size_t>(kvh) * HD + g * kRun;
@@ -816,7 +845,7 @@ namespace mi
       for (int i = 0; i < a.pages_per_wave; ++i)
       {
         const int p = p0 + i;
-        if (p >= a.pages)
+        if (p >= a.live_pages)
         {
           break;
         }
@@ -1668,8 +1697,9 @@ namespace mi
     {
       // Fixed splits unless the streaming kernel wrote the partials: the
       // per-layer form carries none of the streaming geometry's code.
+      go_live(a);
       const auto splits_of = [&](int li, int kvh) {
-        return Streamed ? group_splits(a, li, kvh) : a.splits;
+        return Streamed ? group_splits(a, li, kvh) : a.live_splits;
       };
       constexpr int kBlocksAHead = HD / (4 * kQuads);
       __shared__ f32x4 s_o[kSplitRows][kQuads];
@@ -1818,9 +1848,14 @@ namespace mi
       const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
       constexpr int kWavesC = kCombineThreads / 64;
       constexpr int kHeadsAWave = kMaxHeads / kWavesC;
-      const int page = (bx - a.heads * kBlocksAHead) * 64 + lane;
-      const bool has_page = page < a.pages;
-      const int pg = has_page ? page : a.pages - 1; // clamped: loads, never stores
+      const int first_page = (bx - a.heads * kBlocksAHead) * 64;
+      if (first_page >= a.live_pages || (a.score_every > 1 && a.seq_k % a.score_every != 0))
+      {
+        return; // no live page here, or not a step the scores take
+      }
+      const int page = first_page + lane;
+      const bool has_page = page < a.live_pages;
+      const int pg = has_page ? page : a.live_pages - 1; // clamped: loads, never stores
       const float *stats = a.page_stats + static_cast<std::size_t>(li) * a.heads * a.pages * 2;
       float *scores = a.scores != nullptr ? a.scores + li * a.scores_stride : nullptr;
       float *mass = a.mass != nullptr ? a.mass + li * a.mass_stride : nullptr;
@@ -1874,7 +1909,7 @@ namespace mi
           s_share[h][lane] = share;
           if (mass != nullptr && has_page)
           {
-            mass[static_cast<std::size_t>(h) * a.pages + page] = share;
+            mass[static_cast<std::size_t>(h) * a.live_pages + page] = share;
           }
         }
       }
@@ -2034,6 +2069,12 @@ namespace mi
     // every KV head (or, unsplit, one workgroup a KV head). Several layers:
     // the streaming kernel, equal ranges of units a wave.
     const bool streaming = ls.split && ls.layers > 1;
+    if (ls.live_seq_k != nullptr && (!ls.split || ls.layers != 1))
+    {
+      throw InvalidArgument("a decode whose position lives on the device is one split layer");
+    }
+    d.live_seq_k = ls.live_seq_k;
+    d.score_every = 1;
     int stream_blocks = 0;
     if (streaming)
     {
@@ -2069,6 +2110,8 @@ namespace mi
       d.pages_per_wave = (pages + kWaves - 1) / kWaves;
       d.splits = 1;
     }
+    d.live_pages = pages;
+    d.live_splits = d.splits;
     const std::size_t part =
         static_cast<std::size_t>(ls.layers) * a.kv_heads * d.splits * group * a.head_dim;
     const bool kept = ls.keep_ml != nullptr;
@@ -2181,6 +2224,11 @@ namespace mi
     d.scores = f.scores;
     d.scores_stride = f.scores_stride;
     d.alpha = f.alpha;
+    d.live_seq_k = f.live_seq_k;
+    d.live_pages = pages;
+    d.live_splits = d.splits;
+    d.pages_per_wave = 1;
+    d.score_every = std::max(1, f.score_every);
     d.mass_blocks = (pages + 63) / 64;
     const int blocks_a_head = f.head_dim / (4 * kQuads);
     d.block_base = f.heads * blocks_a_head;

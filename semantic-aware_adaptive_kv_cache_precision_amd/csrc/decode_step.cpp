@@ -1,0 +1,304 @@
+// A decode step captured as one HIP graph (the design is described in
+// decode_step.hpp).
+
+#include "decode_step.hpp"
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <string>
+
+namespace mi
+{
+  namespace
+  {
+    std::unique_ptr<DeviceBuffer> device_bytes(std::size_t bytes)
+    {
+      return std::make_unique<DeviceBuffer>(std::max<std::size_t>(bytes, 256));
+    }
+
+    void require(bool ok, const std::string &what)
+    {
+      if (!ok)
+      {
+        throw InvalidArgument(what);
+      }
+    }
+  } // namespace
+
+  DecodeStep::DecodeStep(KVPages &cache, const ModelShape &shape, ModelWeights weights,
+                         ImportanceScores *scores, int score_every)
+      : cache_(cache), shape_(shape), weights_(std::move(weights)), scores_(scores),
+        score_every_(score_every), rope_(shape.head_dim, shape.rope_theta)
+  {
+    const ModelShape &s = shape_;
+    require(s.layers > 0 && s.hidden > 0 && s.intermediate > 0 && s.heads > 0 && s.kv_heads > 0 &&
+                s.head_dim > 0 && s.vocab > 0,
+            "a model's layers, widths, heads and vocabulary are positive");
+    require(s.heads % s.kv_heads == 0, "query heads are a multiple of KV heads");
+    require(s.hidden % 8 == 0 && s.intermediate % 8 == 0 && (s.heads * s.head_dim) % 8 == 0,
+            "a step's projections take inputs of a multiple of 8 values");
+    require(cache.layers() == s.layers && cache.kv_heads() == s.kv_heads &&
+                cache.head_dim() == s.head_dim,
+            "the cache holds " + std::to_string(cache.layers()) + " layers of " +
+                std::to_string(cache.kv_heads()) + " x " + std::to_string(cache.head_dim()) +
+                "; the model has " + std::to_string(s.layers) + " of " +
+                std::to_string(s.kv_heads) + " x " + std::to_string(s.head_dim));
+    require(cache.seals() && cache.halves() == Halves::kBoth,
+            "a graphed decode step runs on a cache that seals its pages (a tier map, a quantised "
+            "tier or always_seal), with both halves at their tiers");
+    require(weights_.embed != nullptr && weights_.final_norm != nullptr && weights_.head != nullptr &&
+                static_cast<int>(weights_.layers.size()) == s.layers,
+            "the model's embedding, final norm, head and every layer's weights are needed");
+    require(score_every >= 1, "score_every is a count of steps, at least 1");
+    require(scores == nullptr || scores->layers() == s.layers,
+            "the scores hold a row a layer of the cache");
+    int biased = 0;
+    for (const LayerWeights &w : weights_.layers)
+    {
+      require(w.input_norm && w.q_w && w.k_w && w.v_w && w.o_w && w.post_norm && w.gate_w &&
+                  w.up_w && w.down_w,
+              "every layer needs its norms and its seven projection weights");
+      biased += w.k_b != nullptr ? 1 : 0;
+    }
+    require(biased == 0 || biased == s.layers, "a key bias on every layer or on none");
+    key_bias_ = biased == s.layers;
+
+    const std::size_t q_width = static_cast<std::size_t>(s.heads) * s.head_dim;
+    const std::size_t kv_width = static_cast<std::size_t>(s.kv_heads) * s.head_dim;
+    state_ = device_bytes(4 * sizeof(int));
+    residual_ = device_bytes(static_cast<std::size_t>(s.hidden) * sizeof(float));
+    normed_ = device_bytes(static_cast<std::size_t>(s.hidden) * 2);
+    qk_raw_ = device_bytes((q_width + kv_width) * 2);
+    qk_ = device_bytes((q_width + kv_width) * 2);
+    v_ = device_bytes(kv_width * 2);
+    attended_ = device_bytes(q_width * 2);
+    activated_ = device_bytes(static_cast<std::size_t>(s.intermediate) * 2);
+    logits_ = device_bytes(static_cast<std::size_t>(s.vocab) * sizeof(float));
+    ProjectArgs head{};
+    head.segments = 1;
+    head.seg[0].rows = s.vocab;
+    head.mode = ProjectMode::kLogits;
+    head_blocks_ = project_blocks(head);
+    best_value_ = device_bytes(static_cast<std::size_t>(head_blocks_) * sizeof(float));
+    best_index_ = device_bytes(static_cast<std::size_t>(head_blocks_) * sizeof(int));
+    hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate step");
+    hip_check(hipEventCreate(&begin_), "hipEventCreate");
+    hip_check(hipEventCreate(&end_), "hipEventCreate");
+  }
+
+  DecodeStep::~DecodeStep()
+  {
+    if (stream_ != nullptr)
+    {
+      (void)hipStreamSynchronize(stream_);
+    }
+    if (exec_ != nullptr)
+    {
+      (void)hipGraphExecDestroy(exec_);
+    }
+    if (begin_ != nullptr)
+    {
+      (void)hipEventDestroy(begin_);
+    }
+    if (end_ != nullptr)
+    {
+      (void)hipEventDestroy(end_);
+    }
+    if (stream_ != nullptr)
+    {
+      (void)hipStreamDestroy(stream_);
+    }
+  }
+
+  void DecodeStep::size_buffers(int steps)
+  {
+    if (steps > token_room_)
+    {
+      tokens_ = device_bytes(static_cast<std::size_t>(steps) * sizeof(std::int32_t));
+      token_room_ = steps;
+    }
+  }
+
+  void DecodeStep::enqueue_step(int max_seq_k, hipStream_t stream)
+  {
+    const ModelShape &s = shape_;
+    const int q_width = s.heads * s.head_dim;
+    const int kv_width = s.kv_heads * s.head_dim;
+    int *state = state_->as<int>();
+    float *residual = residual_->as<float>();
+    auto *normed = normed_->as<std::uint16_t>();
+    auto *qk_raw = qk_raw_->as<std::uint16_t>();
+    auto *qk = qk_->as<std::uint16_t>();
+    auto *v = v_->as<std::uint16_t>();
+    auto *attended = attended_->as<std::uint16_t>();
+    auto *activated = activated_->as<std::uint16_t>();
+    float *kept = scores_ != nullptr ? kept_->as<float>() : nullptr;
+    int launches = 0;
+
+    launch_embed(state + kStepToken, 1, weights_.embed, residual, true, s.hidden, s.vocab, stream);
+    ++launches;
+    for (int l = 0; l < s.layers; ++l)
+    {
+      const LayerWeights &w = weights_.layers[l];
+      launch_rmsnorm(residual, true, w.input_norm, normed, 1, s.hidden, s.rms_eps, stream);
+      ProjectArgs qkv{};
+      qkv.segments = 3;
+      qkv.seg[0] = {w.q_w, w.q_b, qk_raw, q_width};
+      // The key bias, when attention adds it rotated, stays out of k.
+      qkv.seg[1] = {w.k_w, key_bias_ ? nullptr : w.k_b, qk_raw + q_width, kv_width};
+      qkv.seg[2] = {w.v_w, w.v_b, v, kv_width};
+      qkv.in = s.hidden;
+      qkv.x = normed;
+      qkv.mode = ProjectMode::kHalf;
+      launch_project(qkv, stream);
+      // q's heads and k's heads are rows of one buffer: one RoPE launch.
+      launch_rope(qk_raw, state + kStepPosition, qk, 1, s.heads + s.kv_heads, s.head_dim,
+                  s.rope_theta, stream);
+      cache_.store_step(l, qk + q_width, v, state + kStepPosition);
+      cache_.attention_step(l, qk, key_bias_ ? w.k_b : nullptr, &rope_, attended,
+                            state + kStepSeqK, max_seq_k, s.heads, s.kv_heads, s.head_dim,
+                            qk + q_width, v, kept);
+      ProjectArgs o{};
+      o.segments = 1;
+      o.seg[0] = {w.o_w, nullptr, residual, s.hidden};
+      o.in = q_width;
+      o.x = attended;
+      o.mode = ProjectMode::kAccumulate;
+      launch_project(o, stream);
+      launch_rmsnorm(residual, true, w.post_norm, normed, 1, s.hidden, s.rms_eps, stream);
+      ProjectArgs mlp{};
+      mlp.segments = 2;
+      mlp.seg[0] = {w.gate_w, nullptr, activated, s.intermediate};
+      mlp.seg[1] = {w.up_w, nullptr, nullptr, s.intermediate};
+      mlp.in = s.hidden;
+      mlp.x = normed;
+      mlp.mode = ProjectMode::kSwiglu;
+      launch_project(mlp, stream);
+      ProjectArgs down{};
+      down.segments = 1;
+      down.seg[0] = {w.down_w, nullptr, residual, s.hidden};
+      down.in = s.intermediate;
+      down.x = activated;
+      down.mode = ProjectMode::kAccumulate;
+      launch_project(down, stream);
+      launches += 10; // norm, qkv, rope, store, decode + combine, o, norm, gate/up, down
+    }
+    launch_rmsnorm(residual, true, weights_.final_norm, normed, 1, s.hidden, s.rms_eps, stream);
+    ProjectArgs head{};
+    head.segments = 1;
+    head.seg[0] = {weights_.head, nullptr, logits_->as<float>(), s.vocab};
+    head.in = s.hidden;
+    head.x = normed;
+    head.mode = ProjectMode::kLogits;
+    head.best_value = best_value_->as<float>();
+    head.best_index = best_index_->as<int>();
+    launch_project(head, stream);
+    launches += 2;
+    if (scores_ != nullptr)
+    {
+      cache_.fold_step(kept, state + kStepSeqK, max_seq_k, s.heads, s.kv_heads, s.head_dim,
+                       score_every_, scores_->layer_scores(0), scores_->max_pages(),
+                       scores_->alpha());
+      ++launches;
+    }
+    launch_advance(best_value_->as<float>(), best_index_->as<int>(), head_blocks_, s.vocab, state,
+                   tokens_->as<std::int32_t>(), token_room_, stream);
+    ++launches;
+    launches_ = launches;
+  }
+
+  void DecodeStep::capture(int max_seq_k)
+  {
+    const ModelShape &s = shape_;
+    // Everything the launches use is made before the capture: the tables
+    // and scratch at max_seq_k, the RoPE table, the kept statistics.
+    rope_.cover(std::max(max_seq_k, RopeTable::kAngleRows));
+    cache_.prepare_step(max_seq_k, s.heads, s.head_dim);
+    if (scores_ != nullptr)
+    {
+      const int pages = (max_seq_k + cache_.page_tokens() - 1) / cache_.page_tokens();
+      require(pages <= scores_->max_pages(),
+              "the scores hold " + std::to_string(scores_->max_pages()) + " pages a layer; the "
+              "run reaches " + std::to_string(pages));
+      const std::size_t floats = decode_kept_floats(s.heads, s.kv_heads, max_seq_k) * s.layers;
+      if (kept_ == nullptr || kept_->bytes() < floats * sizeof(float))
+      {
+        kept_ = device_bytes(floats * sizeof(float));
+      }
+    }
+    // The step's stream does not wait for other streams: whatever the cache
+    // launched on them (table edits, allocations) is finished first.
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize before capture");
+    if (exec_ != nullptr)
+    {
+      hip_check(hipGraphExecDestroy(exec_), "hipGraphExecDestroy");
+      exec_ = nullptr;
+    }
+    const hipStream_t previous = runtime_stream();
+    set_runtime_stream(stream_);
+    hipGraph_t graph = nullptr;
+    hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal),
+              "hipStreamBeginCapture step");
+    try
+    {
+      enqueue_step(max_seq_k, stream_);
+    }
+    catch (...)
+    {
+      (void)hipStreamEndCapture(stream_, &graph);
+      if (graph != nullptr)
+      {
+        (void)hipGraphDestroy(graph);
+      }
+      set_runtime_stream(previous);
+      throw;
+    }
+    const hipError_t ended = hipStreamEndCapture(stream_, &graph);
+    set_runtime_stream(previous);
+    hip_check(ended, "hipStreamEndCapture step");
+    const hipError_t made = hipGraphInstantiate(&exec_, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    hip_check(made, "hipGraphInstantiate step");
+  }
+
+  double DecodeStep::run(int token, int position, int steps, std::int32_t *tokens)
+  {
+    require(steps > 0 && position >= 0, "a run takes at least one step from a position >= 0");
+    require(tokens != nullptr, "a run writes its tokens to host memory");
+    const int end = position + steps;
+    // The run's pages, then a graph for the most positions it attends.
+    cache_.reserve(end);
+    size_buffers(steps);
+    capture(end);
+    const int state[4] = {token, position, position + 1, 0};
+    hip_check(hipMemcpyAsync(state_->raw(), state, sizeof(state), hipMemcpyHostToDevice, stream_),
+              "hipMemcpyAsync step state");
+    hip_check(hipEventRecord(begin_, stream_), "hipEventRecord");
+    for (int i = 0; i < steps; ++i)
+    {
+      hip_check(hipGraphLaunch(exec_, stream_), "hipGraphLaunch step");
+    }
+    hip_check(hipEventRecord(end_, stream_), "hipEventRecord");
+    hip_check(hipMemcpyAsync(tokens, tokens_->raw(), static_cast<std::size_t>(steps) * 4,
+                             hipMemcpyDeviceToHost, stream_),
+              "hipMemcpyAsync tokens");
+    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize step run");
+    float ms = 0.0f;
+    hip_check(hipEventElapsedTime(&ms, begin_, end_), "hipEventElapsedTime");
+    cache_.stored_on_device(end);
+    return ms;
+  }
+
+  void DecodeStep::logits(float *host, std::size_t count) const
+  {
+    require(count <= static_cast<std::size_t>(shape_.vocab),
+            "the logits are " + std::to_string(shape_.vocab) + " values");
+    hip_check(hipMemcpyAsync(host, logits_->raw(), count * sizeof(float), hipMemcpyDeviceToHost,
+                             stream_),
+              "hipMemcpyAsync logits");
+    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize logits");
+  }
+
+} // namespace mi

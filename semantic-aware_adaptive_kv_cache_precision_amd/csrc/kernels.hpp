@@ -281,6 +281,11 @@ namespace mi
     // its page statistics go here, in a DecodeFold's layout for its layer.
     float *keep_ml;
     float *keep_stats;
+    // A decode whose position lives on the device (one layer, split, not
+    // several layers at once): seq_k is read from *live_seq_k when the
+    // kernels run, and AttentionArgs::seq_k is the most it may be, which
+    // sizes the launch and the strides.
+    const int *live_seq_k;
   };
   // Whether the fast path takes this decode: one query, no key bias, 32-token
   // pages, head_dim 64 or 128, a group of at most 16 heads, 16-byte aligned
@@ -309,8 +314,74 @@ namespace mi
     float *scores;
     long long scores_stride;
     float alpha;
+    // With the position on the device: seq_k read from *live_seq_k, `seq_k`
+    // above the most it may be (the kept layout's size); the fold runs only
+    // where that seq_k is a multiple of score_every.
+    const int *live_seq_k;
+    int score_every;
   };
   std::size_t decode_kept_floats(int heads, int kv_heads, int seq_k);
   void launch_decode_fold(const DecodeFold &f, hipStream_t stream);
+
+  // ---- a decode step's dense half (step.hip) ---------------------------------------------
+  // One token's projections against fp16 weights [rows][in]: q, k and v in
+  // one launch (up to three matrices), gate and up with the SwiGLU, the
+  // fp32 residual accumulated, the head's logits with each block's best.
+  enum class ProjectMode : int
+  {
+    kHalf,       // out fp16 = acc + bias (fp32, one rounding)
+    kAccumulate, // out fp32 += acc
+    kSwiglu,     // seg[0] gate, seg[1] up: seg[0].out fp16 = silu(g) u
+    kLogits,     // out fp32 = acc, and each block's best (value, index)
+  };
+  constexpr int kProjectSegments = 3;
+  struct ProjectSegment
+  {
+    const std::uint16_t *w;
+    const std::uint16_t *bias; // kHalf only; may be null
+    void *out;
+    int rows;
+  };
+  struct ProjectArgs
+  {
+    ProjectSegment seg[kProjectSegments];
+    int segments;
+    int in;
+    const std::uint16_t *x;
+    ProjectMode mode;
+    float *best_value; // kLogits: [project_blocks]
+    int *best_index;
+  };
+  int project_blocks(const ProjectArgs &p);
+  void launch_project(const ProjectArgs &p, hipStream_t stream);
+  // A step's state in device memory, four ints.
+  constexpr int kStepToken = 0;    // the token the step feeds
+  constexpr int kStepPosition = 1; // its position
+  constexpr int kStepSeqK = 2;     // positions attended: position + 1
+  constexpr int kStepIndex = 3;    // steps taken in the run
+  // The greedy token from the head's block bests, written to tokens[step]
+  // (while step < max_tokens) and as the next step's token; the state moved on.
+  void launch_advance(const float *best_value, const int *best_index, int blocks, int vocab,
+                      int *state, std::int32_t *tokens, int max_tokens, hipStream_t stream);
+  // Synthetic fp16 weights: uniform in [-scale, scale), from a seed.
+  void launch_random_half(void *out, std::size_t count, unsigned long long seed, float scale,
+                          hipStream_t stream);
+
+  // A decode step's store with its position on the device (page_jobs.hip):
+  // the rows go to row position % 32 of the layer's open page, and the row
+  // that completes a page seals it, at its tier in the table, from the open
+  // page and the rows (store_sealed's jobs for one row, chosen on the device).
+  struct StepStore
+  {
+    const std::uint16_t *keys;
+    const std::uint16_t *values;
+    const int *position;
+    std::uint16_t *open;
+    const unsigned long long *addresses; // the layer's row of the page table
+    const std::uint8_t *tiers;
+    int kv_heads;
+    PageLayout lay[kTierCount];
+  };
+  void launch_step_store(const StepStore &s, int head_dim, hipStream_t stream);
 
 } // namespace mi

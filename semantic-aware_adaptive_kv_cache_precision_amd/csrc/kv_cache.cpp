@@ -1047,6 +1047,161 @@ namespace mi
     kept_layers_.assign(layers_, 0);
   }
 
+  // ---- a decode step with its position on the device ------------------------------------
+
+  void KVPages::prepare_step(int max_seq_k, int heads, int head_dim)
+  {
+    if (!seals_ || halves_ != Halves::kBoth)
+    {
+      throw InvalidArgument("a decode step with its position on the device runs on a cache that "
+                            "seals its pages, with both halves at their tiers");
+    }
+    if (max_seq_k <= 0 || max_seq_k > capacity_tokens())
+    {
+      throw OutOfRange("a step run to " + std::to_string(max_seq_k) + " positions needs them "
+                       "reserved; " + std::to_string(capacity_tokens()) + " are");
+    }
+    const hipStream_t stream = runtime_stream();
+    sync_tables(stream);
+    // The split decode's partials, split maxima and page statistics at
+    // max_seq_k (the largest launch of the run).
+    const int pages = (max_seq_k + page_tokens_ - 1) / page_tokens_;
+    const int splits = (pages + 7) / 8;
+    workspace_.floats(static_cast<std::size_t>(heads) * splits * (head_dim + 2) +
+                      static_cast<std::size_t>(heads) * pages * 2);
+  }
+
+  void KVPages::store_step(int layer, const void *keys, const void *values, const int *position)
+  {
+    require_layer(layer);
+    if (!seals_ || !open_pages_)
+    {
+      throw LogicError("a store with its position on the device needs a sealing cache with "
+                       "positions reserved");
+    }
+    const hipStream_t stream = runtime_stream();
+    sync_tables(stream);
+    StepStore st{};
+    st.keys = static_cast<const std::uint16_t *>(keys);
+    st.values = static_cast<const std::uint16_t *>(values);
+    st.position = position;
+    st.open = open_page(layer, current_open_[layer]);
+    const std::size_t row = static_cast<std::size_t>(layer) * table_.stride();
+    st.addresses = table_.addresses() + row;
+    st.tiers = table_.tiers() + row;
+    st.kv_heads = kv_heads_;
+    launch_step_store(st, head_dim_, stream);
+    attend_open_[layer] = current_open_[layer];
+  }
+
+  void KVPages::attention_step(int layer, const void *q, const void *k_bias, const RopeTable *rope,
+                               void *out, const int *live_seq_k, int max_seq_k, int heads,
+                               int kv_heads, int head_dim, const void *keys, const void *values,
+                               float *keep)
+  {
+    require_layer(layer);
+    if (static_cast<std::size_t>(kv_heads) * head_dim != kv_width_)
+    {
+      throw InvalidArgument("kv_heads * head_dim is " + std::to_string(kv_heads * head_dim) +
+                            "; this cache holds " + std::to_string(kv_width_) + " per token");
+    }
+    if (!seals_ || !open_pages_ || max_seq_k <= 0 || max_seq_k > capacity_tokens())
+    {
+      throw LogicError("a decode with its position on the device needs a sealing cache with its "
+                       "positions, up to the most the run attends, reserved");
+    }
+    if (k_bias != nullptr &&
+        (rope == nullptr || rope->head_dim() != head_dim || rope->positions() < max_seq_k))
+    {
+      throw InvalidArgument("a key bias needs a RoPE table for head_dim " +
+                            std::to_string(head_dim) + " covering " + std::to_string(max_seq_k) +
+                            " positions");
+    }
+    const hipStream_t stream = runtime_stream();
+    sync_tables(stream);
+    AttentionArgs a{};
+    a.q = static_cast<const std::uint16_t *>(q);
+    a.out = static_cast<std::uint16_t *>(out);
+    a.k_bias = static_cast<const std::uint16_t *>(k_bias);
+    a.rope = k_bias != nullptr ? rope->data() : nullptr;
+    a.rope_positions = k_bias != nullptr ? rope->positions() : 0;
+    a.rope_angles = k_bias != nullptr ? rope->angles() : nullptr;
+    a.seq_q = 1;
+    a.seq_k = max_seq_k;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.workspace = &workspace_;
+    KVSource kv{};
+    kv.page_tokens = page_tokens_;
+    kv.layout = Layout::kCausal;
+    const std::size_t row = static_cast<std::size_t>(layer) * table_.stride();
+    kv.pages = pages_ > 0 ? table_.addresses() + row : nullptr;
+    kv.tiers = pages_ > 0 ? table_.tiers() + row : nullptr;
+    kv.open = open_page(layer, current_open_[layer]);
+    kv.chunk_k = static_cast<const std::uint16_t *>(keys);
+    kv.chunk_v = static_cast<const std::uint16_t *>(values);
+    kv.start = max_seq_k - 1;
+    std::copy(may_be_at_.begin(), may_be_at_.end(), kv.may_be_at);
+    if (!decode_fast_applies(kv, a))
+    {
+      throw InvalidArgument("a decode with its position on the device takes one query per head, "
+                            "32-token pages, head_dim 64 or 128 and at most 16 query heads per KV "
+                            "head, 16-byte aligned");
+    }
+    DecodeLayers ls{};
+    ls.split = true;
+    ls.layers = 1;
+    ls.live_seq_k = live_seq_k;
+    if (keep != nullptr)
+    {
+      const int pages = (max_seq_k + page_tokens_ - 1) / page_tokens_;
+      const std::size_t per_layer = decode_kept_floats(heads, kv_heads, max_seq_k);
+      const std::size_t ml_floats = per_layer - static_cast<std::size_t>(heads) * pages * 2;
+      ls.keep_ml = keep + layer * ml_floats;
+      ls.keep_stats =
+          keep + layers_ * ml_floats + static_cast<std::size_t>(layer) * heads * pages * 2;
+    }
+    launch_decode_layers(kv, a, ls, stream);
+  }
+
+  void KVPages::fold_step(float *keep, const int *live_seq_k, int max_seq_k, int heads,
+                          int kv_heads, int head_dim, int score_every, float *scores,
+                          long long scores_stride, float alpha)
+  {
+    if (keep == nullptr || live_seq_k == nullptr || score_every < 1)
+    {
+      throw InvalidArgument("a step's fold takes the kept statistics, the device's seq_k and a "
+                            "cadence of at least 1");
+    }
+    DecodeFold f{};
+    f.layers = layers_;
+    f.heads = heads;
+    f.kv_heads = kv_heads;
+    f.head_dim = head_dim;
+    f.seq_k = max_seq_k;
+    f.kept = keep;
+    f.scores = scores;
+    f.scores_stride = scores_stride;
+    f.alpha = alpha;
+    f.live_seq_k = live_seq_k;
+    f.score_every = score_every;
+    launch_decode_fold(f, runtime_stream());
+  }
+
+  void KVPages::stored_on_device(int end)
+  {
+    if (end < 0 || end > capacity_tokens())
+    {
+      throw OutOfRange("positions up to " + std::to_string(end) + " are not all reserved");
+    }
+    for (int layer = 0; layer < layers_; ++layer)
+    {
+      sealed_[layer] = std::max(sealed_[layer], end / page_tokens_);
+      attend_open_[layer] = current_open_[layer];
+    }
+  }
+
   void KVPages::attention_layers(int first_layer, int layers, const void *q, long long q_stride,
                                  void *out, long long out_stride, int seq_k, int heads,
                                  int kv_heads, int head_dim, const void *keys, const void *values,

@@ -481,6 +481,47 @@ namespace mi
       run_row_task<HD>(jobs.job[blockIdx.y], jobs.lay, task, kv_heads);
     }
 
+    // A decode step's store, its position read on the device: the one row
+    // fills row position % P of the open page, or, on a page's last row,
+    // the page is sealed from the open page's rows and this one.
+    template <int HD>
+    __global__ void __launch_bounds__(kThreads) step_store_kernel(StepStore s)
+    {
+      const int task = blockIdx.x * kThreads + threadIdx.x;
+      const int W = s.kv_heads * HD;
+      if (task >= W)
+      {
+        return;
+      }
+      const int position = *s.position;
+      const int row = position % kP;
+      const int page = position / kP;
+      RowJob j{};
+      if (row < kP - 1)
+      {
+        j.kind = static_cast<int>(RowJobKind::kFill);
+        j.k_lo = j.k_hi = s.keys;
+        j.v_lo = j.v_hi = s.values;
+        j.rows = 1;
+        j.dst_row = row;
+        j.dst = reinterpret_cast<std::uint8_t *>(s.open);
+        j.tier = kFP16;
+      }
+      else
+      {
+        const int tier = s.tiers[page];
+        j.kind = static_cast<int>(tier == kFP16 ? RowJobKind::kCopy : RowJobKind::kQuantise);
+        j.k_lo = s.open;
+        j.v_lo = s.open + static_cast<std::size_t>(kP) * W;
+        j.k_hi = s.keys;
+        j.v_hi = s.values;
+        j.split = kP - 1;
+        j.dst = reinterpret_cast<std::uint8_t *>(s.addresses[page]);
+        j.tier = tier;
+      }
+      run_row_task<HD>(j, s.lay, task, s.kv_heads);
+    }
+
     // Any other shape: a workgroup a job, the rows staged in LDS.
     __global__ void __launch_bounds__(kThreads)
         row_jobs_lds_kernel(RowJobs jobs, int page_tokens, int kv_heads, int head_dim)
@@ -715,6 +756,30 @@ namespace mi
       }
       hip_check(hipGetLastError(), "row jobs kernel launch");
     }
+  }
+
+  void launch_step_store(const StepStore &s, int head_dim, hipStream_t stream)
+  {
+    if (!register_shape(kP, s.kv_heads, head_dim))
+    {
+      throw InvalidArgument("a store whose position lives on the device takes head_dim 64 or 128 "
+                            "and at least 128 channels a row");
+    }
+    StepStore args = s;
+    for (int t = kINT8; t <= kINT2; ++t)
+    {
+      args.lay[t] = page_layout(t, kP, s.kv_heads, head_dim);
+    }
+    const int blocks = (s.kv_heads * head_dim + kThreads - 1) / kThreads;
+    if (head_dim == 128)
+    {
+      hipLaunchKernelGGL(step_store_kernel<128>, dim3(blocks), dim3(kThreads), 0, stream, args);
+    }
+    else
+    {
+      hipLaunchKernelGGL(step_store_kernel<64>, dim3(blocks), dim3(kThreads), 0, stream, args);
+    }
+    hip_check(hipGetLastError(), "step store kernel launch");
   }
 
   void launch_table_edits(const TableEdit *edits, int count, unsigned long long *addresses,

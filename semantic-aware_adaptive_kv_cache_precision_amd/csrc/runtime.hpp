@@ -450,6 +450,28 @@ namespace mi
                         const void *keys, const void *values);
     void fold_kept(float *mass, long long mass_stride, float *scores, long long scores_stride,
                    float alpha);
+    // Beyond the reference: the pieces of a decode step whose position lives
+    // on the device, so that one captured graph serves every step of a run.
+    // store_step stores one row at *position (sealing the page it
+    // completes); attention_step decodes one layer at seq_k = *live_seq_k,
+    // its launch sized for max_seq_k, keeping its statistics in `keep` (a
+    // DecodeFold's layout for every layer at max_seq_k) when keep is not
+    // null; fold_step folds the kept statistics into the scores where seq_k
+    // is a multiple of score_every. prepare_step readies the tables and
+    // scratch for max_seq_k beforehand, so that the launches allocate and
+    // upload nothing; the pages up to max_seq_k must be reserved, and no
+    // page may move, while they run. stored_on_device(end) then records that
+    // the positions before `end` were stored.
+    void prepare_step(int max_seq_k, int heads, int head_dim);
+    void store_step(int layer, const void *keys, const void *values, const int *position);
+    void attention_step(int layer, const void *q, const void *k_bias, const RopeTable *rope,
+                        void *out, const int *live_seq_k, int max_seq_k, int heads,
+                        int kv_heads, int head_dim, const void *keys, const void *values,
+                        float *keep);
+    void fold_step(float *keep, const int *live_seq_k, int max_seq_k, int heads, int kv_heads,
+                   int head_dim, int score_every, float *scores, long long scores_stride,
+                   float alpha);
+    void stored_on_device(int end);
     void downgrade(int layer, int page, int target);
     void upgrade(int layer, int page, int target);
     void move_pages(const std::vector<PageMove> &moves);

@@ -41,6 +41,20 @@ class _Layout(C.Structure):
                 ("metadata_bytes", _sz), ("page_bytes", _sz), ("effective_bits", C.c_double)]
 
 
+class _ModelShape(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("layers", "hidden", "intermediate", "heads", "kv_heads",
+                                        "head_dim", "vocab")] + \
+               [("rms_eps", C.c_float), ("rope_theta", C.c_double)]
+
+
+_LAYER_TENSORS = ("input_norm", "q_w", "q_b", "k_w", "k_b", "v_w", "v_b", "o_w", "post_norm",
+                  "gate_w", "up_w", "down_w")
+
+
+class _LayerWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in _LAYER_TENSORS]
+
+
 class _KVInfo(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("layers", "page_tokens", "kv_heads", "head_dim",
                                         "pages_per_layer", "capacity_tokens", "tier", "halves",
@@ -61,6 +75,16 @@ SIGNATURES = {
     "mi_device_count": ((_ip,), C.c_int), "mi_device_name": ((C.c_char_p, _sz), C.c_int),
     "mi_runtime_version": ((_ip,), C.c_int),
     "mi_host_alloc": ((C.POINTER(_vp), C.POINTER(_vp), _sz), C.c_int),
+    "mi_kv_store_at": ((_vp, _i, _vp, _vp, _vp), C.c_int),
+    "mi_kv_attention_at": ((_vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp), C.c_int),
+    "mi_kv_stored_on_device": ((_vp, _i), C.c_int),
+    "mi_decode_step_create": ((C.POINTER(_vp), _vp, C.POINTER(_ModelShape), _vp, _vp, _vp,
+                               C.POINTER(_LayerWeights), _vp, _i), C.c_int),
+    "mi_decode_step_destroy": ((_vp,), C.c_int),
+    "mi_decode_step_run": ((_vp, _i, _i, _i, C.POINTER(C.c_int32), C.POINTER(_d)), C.c_int),
+    "mi_decode_step_logits": ((_vp, _fp, _sz), C.c_int),
+    "mi_decode_step_launches": ((_vp, _ip), C.c_int),
+    "mi_random_half": ((_vp, _sz, C.c_ulonglong, _f), C.c_int),
     "mi_host_free": ((_vp,), C.c_int),
     "mi_device_pci_bus_id": ((C.c_char_p, _sz), C.c_int), "mi_memory_info": ((_szp, _szp), C.c_int),
     "mi_granule_bytes": ((_szp,), C.c_int), "mi_malloc": ((C.POINTER(_vp), _sz), C.c_int),
@@ -1050,6 +1074,32 @@ class KVPages:
         _check(lib.mi_kv_attention_kept(self._h, layer, qa, ba, rope._h if rope else None, oa,
                                         seq_k, heads, kv_heads, head_dim, ka, va))
 
+    def store_at(self, layer: int, keys, values, position: DeviceIndex) -> None:
+        """Beyond the reference's surface: one row stored at the position
+        held in device memory (`position`, one int), read when the kernel
+        runs; the row that completes a page seals it."""
+        width = self.kv_width
+        _check(lib.mi_kv_store_at(self._h, layer, _need(_span(keys), width, "keys"),
+                                  _need(_span(values), width, "values"), position.address))
+
+    def attention_at(self, layer: int, q, k_bias, rope, out, seq_k: DeviceIndex, max_seq_k: int,
+                     heads: int, kv_heads: int, head_dim: int, keys, values) -> None:
+        """Beyond the reference's surface: one layer's decode at the seq_k
+        held in device memory, the launch sized for max_seq_k; to the bit
+        attention(..., partials) at that seq_k."""
+        per_q = heads * head_dim
+        width = kv_heads * head_dim
+        ba = _need(_span(k_bias), width, "k_bias") if k_bias is not None else None
+        _check(lib.mi_kv_attention_at(self._h, layer, _need(_span(q), per_q, "q"), ba,
+                                      rope._h if rope else None, _need(_span(out), per_q, "out"),
+                                      seq_k.address, max_seq_k, heads, kv_heads, head_dim,
+                                      _need(_span(keys), width, "keys"),
+                                      _need(_span(values), width, "values")))
+
+    def stored_on_device(self, end: int) -> None:
+        """Records that the positions before `end` were stored by store_at."""
+        _check(lib.mi_kv_stored_on_device(self._h, end))
+
     def fold_kept(self, scores=None, mass=None, seq_k: int | None = None, heads: int = 0) -> None:
         """Every layer's page masses (mass: (layers, heads, pages) floats,
         if given) and their fold into `scores` (an ImportanceScores, if
@@ -1292,6 +1342,60 @@ def _upload_f32(host) -> FloatTensor:
     return t
 
 
+def random_half(tensor, seed: int, scale: float) -> None:
+    """Fill a device fp16 tensor with synthetic values, uniform in
+    [-scale, scale), made on the device from `seed`."""
+    sp = _span(tensor)
+    _check(lib.mi_random_half(sp.address, sp.count, seed, scale))
+
+
+class DecodeStep:
+    """A whole decode step of a Qwen2 / Llama-shaped decoder as one HIP
+    graph (beyond the reference, whose host sequences the step a call at a
+    time: model.py:332-403, engine.py:1180-1206). `shape` has layers,
+    hidden, intermediate, heads, kv_heads, head_dim, vocab, rms_eps and
+    rope_theta; `layers` is a list of dicts of fp16 device tensors named as
+    _LAYER_TENSORS (biases may be None). The cache must seal its pages."""
+
+    def __init__(self, cache: KVPages, shape: dict, embed, final_norm, head, layers,
+                 scores: ImportanceScores | None = None, score_every: int = 1):
+        sh = _ModelShape(**{f: shape[f] for f, _ in _ModelShape._fields_})
+        arr = (_LayerWeights * len(layers))()
+        for i, tensors in enumerate(layers):
+            for name in _LAYER_TENSORS:
+                t = tensors.get(name)
+                setattr(arr[i], name, _span(t).address if t is not None else None)
+        h = _vp()
+        _check(lib.mi_decode_step_create(C.byref(h), cache._h, C.byref(sh), _span(embed).address,
+                                         _span(final_norm).address, _span(head).address, arr,
+                                         scores._h if scores is not None else None, score_every))
+        self._h = h.value
+        # The step reads these while it lives.
+        self._keep = (cache, scores, embed, final_norm, head, layers)
+        self.vocab = shape["vocab"]
+        weakref.finalize(self, lib.mi_decode_step_destroy, self._h)
+
+    def run(self, token: int, position: int, steps: int):
+        """`steps` greedy steps from `position`, feeding `token` first:
+        (tokens chosen, device milliseconds of the replays)."""
+        out = np.empty(steps, np.int32)
+        ms = C.c_double()
+        _check(lib.mi_decode_step_run(self._h, token, position, steps,
+                                      out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(ms)))
+        return out, ms.value
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        _check(lib.mi_decode_step_logits(self._h, out.ctypes.data_as(_fp), out.size))
+        return out
+
+    @property
+    def launches(self) -> int:
+        n = C.c_int()
+        _check(lib.mi_decode_step_launches(self._h, C.byref(n)))
+        return n.value
+
+
 device = SimpleNamespace(
     Span=Span,
     view=lambda tensor, offset, count: Span(tensor, offset, count),
@@ -1321,6 +1425,8 @@ device = SimpleNamespace(
     ImportanceScores=ImportanceScores,
     ShadowStore=ShadowStore,
     KVPages=KVPages,
+    DecodeStep=DecodeStep,
+    random_half=random_half,
     open_pages=(-1, -2),
     staging_page=-3,
     shadow_upload_page=-4,

@@ -1,0 +1,319 @@
+"""The graphed decode step (DecodeStep: a whole token step as one HIP graph,
+its token, position and seq_k in device memory) and the device-positioned
+store and decode it launches.
+
+GPU parity tests:
+  - store_at over positions crossing seals leaves every page, to the bit,
+    what the eager store leaves, and each page sealed on the way is the
+    oracle's quantise_page of its rows;
+  - attention_at at a seq_k held on the device is, to the bit, the eager
+    split attention at that seq_k, with and without the key bias;
+  - one step's logits against a float64 composition of the oracles (the
+    reference's Model.run, model.py:366-403: embed, RMSNorm, q/k/v, RoPE,
+    causal attention over the cache's own pages, output projection, RMSNorm,
+    SwiGLU, down projection, final RMSNorm, head), every fp16 rounding where
+    the device rounds; the greedy token is the oracle's argmax wherever the
+    oracle's margin exceeds the tolerance;
+  - a run of N steps (one graph replayed N times) leaves the tokens, logits,
+    pages and scores that N runs of one step leave, to the bit.
+"""
+
+import numpy as np
+import pytest
+
+from conftest import announce, assert_attention_close, fp16_exact
+from oracle import attention as att
+from oracle import dense, pointwise, quant
+from test_gpu_kv_pages import mi, normal, page_sizes, put
+
+pytestmark = pytest.mark.gpu
+
+P = 32
+
+# Logits: each within this fraction of the largest |logit|. The step rounds
+# to fp16 where the reference does (normed input, q/k/v, attention output,
+# gate, up, activation) and the oracle rounds at the same points, so the two
+# part only by fp32 against float64 accumulation (an fp16 rounding now and
+# then lands on the other side, 2^-11 of that value) and by the attention's
+# 1e-3 gate, carried through the output projection into the residual.
+LOGIT_TOL = 4e-3
+
+
+def f16(x):
+    return np.asarray(x, np.float64).astype(np.float16).astype(np.float64)
+
+
+def small_shape(layers=2, hidden=256, intermediate=512, heads=4, kv_heads=2, head_dim=64,
+                vocab=1000):
+    return dict(layers=layers, hidden=hidden, intermediate=intermediate, heads=heads,
+                kv_heads=kv_heads, head_dim=head_dim, vocab=vocab, rms_eps=1e-6,
+                rope_theta=1000000.0)
+
+
+def make_weights(rng, s, biases):
+    """Host fp16-exact weights of a model of shape s (float32 arrays)."""
+    H, I, V = s["hidden"], s["intermediate"], s["vocab"]
+    qw, kw = s["heads"] * s["head_dim"], s["kv_heads"] * s["head_dim"]
+
+    def uni(scale, *shape):
+        return fp16_exact(rng.uniform(-scale, scale, shape))
+
+    def norm(n):
+        return fp16_exact(1.0 + 0.1 * rng.standard_normal(n))
+
+    host = {"embed": uni(1.0, V, H), "final_norm": norm(H), "head": uni(1 / np.sqrt(H), V, H),
+            "layers": []}
+    for _ in range(s["layers"]):
+        host["layers"].append({
+            "input_norm": norm(H), "post_norm": norm(H),
+            "q_w": uni(1 / np.sqrt(H), qw, H), "k_w": uni(1 / np.sqrt(H), kw, H),
+            "v_w": uni(1 / np.sqrt(H), kw, H), "o_w": uni(1 / np.sqrt(qw), H, qw),
+            "gate_w": uni(1 / np.sqrt(H), I, H), "up_w": uni(1 / np.sqrt(H), I, H),
+            "down_w": uni(1 / np.sqrt(I), H, I),
+            "q_b": uni(0.5, qw) if biases else None, "k_b": uni(4.0, kw) if biases else None,
+            "v_b": uni(0.5, kw) if biases else None,
+        })
+    return host
+
+
+def upload_weights(host):
+    dev = {k: put(host[k]) for k in ("embed", "final_norm", "head")}
+    dev["layers"] = [{k: (put(v) if v is not None else None) for k, v in layer.items()}
+                     for layer in host["layers"]]
+    return dev
+
+
+def make_cache(s, tier_map, capacity_pages=64):
+    m = mi()
+    L, kv, hd = s["layers"], s["kv_heads"], s["head_dim"]
+    cap = [L * capacity_pages + 8] * 4
+    cap[0] += 2 * L
+    alloc = m.PagedKVCache(page_sizes(P, kv, hd), cap)
+    cache = m.device.KVPages(alloc, L, P, kv, hd, 0, m.device.Halves.Both, tier_map, True)
+    return alloc, cache
+
+
+def prefill(cache, s, rows):
+    """Every layer's context rows stored eagerly: rows[l] = (K, V) (n, kv, hd)."""
+    n = rows[0][0].shape[0]
+    cache.reserve(n)
+    for layer, (k, v) in enumerate(rows):
+        cache.store(layer, put(k), put(v), 0, n)
+
+
+def context_rows(rng, s, n):
+    return [(normal(rng, n, s["kv_heads"], s["head_dim"]), normal(rng, n, s["kv_heads"], s["head_dim"]))
+            for _ in range(s["layers"])]
+
+
+def oracle_step(host, s, token, position, rows, alloc):
+    """float64 logits of one step at `position` feeding `token`, and each
+    layer's new (k, v) row: the reference's Model.run with every fp16
+    rounding where the device makes it."""
+    H, eps, theta = s["hidden"], s["rms_eps"], s["rope_theta"]
+    heads, kv, hd = s["heads"], s["kv_heads"], s["head_dim"]
+    key_bias = host["layers"][0]["k_b"] is not None
+    x = dense.embed([token], host["embed"]).astype(np.float64)
+    own = position // P
+    new_rows = []
+    for layer, w in enumerate(host["layers"]):
+        n = f16(pointwise.rmsnorm(x, w["input_norm"], eps))
+        q = f16(dense.linear(n, w["q_w"], w["q_b"])[0])
+        k = f16(dense.linear(n, w["k_w"], None if key_bias else w["k_b"])[0])
+        v = f16(dense.linear(n, w["v_w"], w["v_b"])[0])
+        q = f16(pointwise.rope(q.reshape(1, heads, hd), [position], theta))
+        k = f16(pointwise.rope(k.reshape(1, kv, hd), [position], theta))
+        v = v.reshape(1, kv, hd)
+        new_rows.append((k, v))
+        K = np.concatenate([rows[layer][0], k])
+        V = np.concatenate([rows[layer][1], v])
+        sealed = [alloc.read(layer, i) for i in range(own)]
+        tiers = [int(alloc.locate(layer, i)[0]) for i in range(own)]
+        out = att.causal_chunk(q, sealed, tiers, K, V, kv, hd, P,
+                               w["k_b"].reshape(kv, hd) if key_bias else None, theta)
+        a = f16(out.reshape(1, heads * hd))
+        x = x + dense.linear(a, w["o_w"])[0]
+        n = f16(pointwise.rmsnorm(x, w["post_norm"], eps))
+        g = f16(dense.linear(n, w["gate_w"])[0])
+        u = f16(dense.linear(n, w["up_w"])[0])
+        act = f16(pointwise.swiglu(g, u))
+        x = x + dense.linear(act, w["down_w"])[0]
+    n = f16(pointwise.rmsnorm(x, host["final_norm"], eps))
+    return dense.linear(n, host["head"])[0][0], new_rows
+
+
+def tier_map_for(s, pages, salt=0):
+    return [[(i * 3 + layer + salt) % 4 for i in range(pages)] for layer in range(s["layers"])]
+
+
+def test_store_at_seals_as_the_eager_store():
+    """Rows stored one at a time at a position held on the device leave the
+    pages the eager store leaves, to the bit, across three seals; each page
+    sealed is the oracle's quantise_page of its rows at its tier."""
+    m = mi()
+    s = small_shape(head_dim=128)
+    rng = np.random.default_rng(3)
+    start, n = P * 2 + 20, 60
+    rows = context_rows(rng, s, start + n)
+    tmap = tier_map_for(s, 8)
+    a_alloc, a = make_cache(s, tmap)
+    b_alloc, b = make_cache(s, tmap)
+    ctx = [(k[:start], v[:start]) for k, v in rows]
+    prefill(a, s, ctx)
+    prefill(b, s, ctx)
+    a.reserve(start + n)
+    b.reserve(start + n)
+    announce("store_at", start, n)
+    for p in range(start, start + n):
+        at = m.device.DeviceIndex([p])
+        for layer, (k, v) in enumerate(rows):
+            a.store(layer, put(k[p:p + 1]), put(v[p:p + 1]), p, 1)
+            b.store_at(layer, put(k[p:p + 1]), put(v[p:p + 1]), at)
+    b.stored_on_device(start + n)
+    m.synchronize()
+    np.testing.assert_array_equal(a.page_tiers(), b.page_tiers())
+    sealed = (start + n) // P
+    for layer, (k, v) in enumerate(rows):
+        for page in range(sealed):
+            got = b_alloc.read(layer, page)
+            np.testing.assert_array_equal(got, a_alloc.read(layer, page),
+                                          err_msg=f"layer {layer} page {page}")
+            tier = int(b_alloc.locate(layer, page)[0])
+            kp = k[page * P:(page + 1) * P].astype(np.float16)
+            vp = v[page * P:(page + 1) * P].astype(np.float16)
+            want = quant.fp16_page(kp, vp) if tier == 0 else quant.quantise_page(kp, vp, tier, P)
+            np.testing.assert_array_equal(got, want, err_msg=f"oracle layer {layer} page {page}")
+
+
+@pytest.mark.parametrize("key_bias", [False, True])
+def test_attention_at_a_device_seq_k_is_the_eager_attention(key_bias):
+    """Decode steps whose seq_k is read on the device, the launch sized for
+    the most positions of the run, give the eager split attention's output
+    at each seq_k, to the bit; both meet the oracle's 1e-3 bar."""
+    m = mi()
+    d = m.device
+    s = small_shape(heads=12, kv_heads=2, head_dim=128)
+    heads, kv, hd = s["heads"], s["kv_heads"], s["head_dim"]
+    rng = np.random.default_rng(5 + key_bias)
+    start, n = P * 3 + 25, 12
+    rows = context_rows(rng, s, start + n)
+    tmap = tier_map_for(s, 8, 1)
+    a_alloc, a = make_cache(s, tmap)
+    _, b = make_cache(s, tmap)
+    ctx = [(k[:start], v[:start]) for k, v in rows]
+    prefill(a, s, ctx)
+    prefill(b, s, ctx)
+    end = start + n
+    a.reserve(end)
+    b.reserve(end)
+    rope = d.RopeTable(hd, s["rope_theta"])
+    rope.cover(end)
+    bias = fp16_exact(normal(rng, kv, hd) * 3) if key_bias else None
+    bias_dev = put(bias) if key_bias else None
+    part = d.empty_f32(d.attention_partials(hd))
+    for p in range(start, end):
+        at, seq = d.DeviceIndex([p]), d.DeviceIndex([p + 1])
+        for layer, (k, v) in enumerate(rows):
+            q = normal(rng, 1, heads, hd)
+            kr, vr = put(k[p:p + 1]), put(v[p:p + 1])
+            a.store(layer, kr, vr, p, 1)
+            b.store_at(layer, kr, vr, at)
+            want_out, got_out = d.empty(heads * hd), d.empty(heads * hd)
+            announce("attention_at", key_bias, p, layer)
+            a.attention(layer, put(q), bias_dev, rope if key_bias else None, want_out, 1, p + 1,
+                        heads, kv, hd, kr, vr, None, part)
+            b.attention_at(layer, put(q), bias_dev, rope if key_bias else None, got_out, seq, end,
+                           heads, kv, hd, kr, vr)
+            got = got_out.to_numpy()
+            np.testing.assert_array_equal(got, want_out.to_numpy(), err_msg=f"p {p} layer {layer}")
+            if p in (start, end - 1):
+                own = p // P
+                sealed = [a_alloc.read(layer, i) for i in range(own)]
+                tiers = [int(a_alloc.locate(layer, i)[0]) for i in range(own)]
+                want, bound = att.causal_chunk(q, sealed, tiers, k[:p + 1], v[:p + 1], kv, hd, P,
+                                               bias, s["rope_theta"], with_bound=True)
+                assert_attention_close(got.reshape(1, heads, hd), want, f"oracle p {p}", bound)
+    b.stored_on_device(end)
+
+
+def check_step_against_oracle(s, biases, start, seed):
+    m = mi()
+    rng = np.random.default_rng(seed)
+    host = make_weights(rng, s, biases)
+    dev = upload_weights(host)
+    rows = context_rows(rng, s, start)
+    alloc, cache = make_cache(s, tier_map_for(s, 16, seed))
+    prefill(cache, s, rows)
+    step = m.device.DecodeStep(cache, s, dev["embed"], dev["final_norm"], dev["head"],
+                               dev["layers"])
+    token = int(rng.integers(0, s["vocab"]))
+    announce("decode step", s, biases, start)
+    tokens, ms = step.run(token, start, 1)
+    got = step.logits().astype(np.float64)
+    want, _ = oracle_step(host, s, token, start, rows, alloc)
+    scale = np.abs(want).max()
+    err = np.abs(got - want).max() / scale
+    assert err < LOGIT_TOL, f"logits off the oracle by {err:.3g} of the largest"
+    order = np.argsort(-want)
+    if want[order[0]] - want[order[1]] > 2 * LOGIT_TOL * scale:
+        assert tokens[0] == order[0], (tokens[0], order[:3])
+    assert tokens[0] == dense.argmax_rows(got[None].astype(np.float32))[0]
+    assert ms > 0 and step.launches == 1 + 10 * s["layers"] + 2 + 1
+
+
+def test_one_step_is_the_oracles_composition_qwen_shape():
+    """Biases on q, k and v (the key bias added by attention, rotated), head
+    dims 64 and 128, a step that seals its page and one that does not."""
+    check_step_against_oracle(small_shape(head_dim=64), True, P * 3 + 10, 11)
+    check_step_against_oracle(small_shape(heads=12, kv_heads=2, head_dim=128), True,
+                              P * 4 + 31, 12)
+
+
+def test_one_step_is_the_oracles_composition_llama_shape():
+    """No biases, four query heads a KV head (Llama-3.2's grouping)."""
+    check_step_against_oracle(small_shape(hidden=512, intermediate=1024, heads=16, kv_heads=4,
+                                          head_dim=64, vocab=1500), False, P * 2 + 5, 13)
+
+
+def test_a_run_replays_one_graph_to_the_bits_of_single_steps():
+    """N steps in one run (one graph, replayed N times, crossing two seals)
+    against N runs of one step each (a graph captured each time), on twin
+    caches: the tokens, the last logits, every page and the scores (folded
+    every step, and every third step) agree to the bit."""
+    m = mi()
+    d = m.device
+    s = small_shape(heads=12, kv_heads=2, head_dim=128)
+    rng = np.random.default_rng(21)
+    host = make_weights(rng, s, True)
+    dev = upload_weights(host)
+    start, n = P * 2 + 17, 50
+    rows = context_rows(rng, s, start)
+    tmap = tier_map_for(s, 8, 2)
+    for every in (1, 3):
+        made = []
+        for _ in range(2):
+            alloc, cache = make_cache(s, tmap)
+            prefill(cache, s, rows)
+            scores = d.ImportanceScores(s["layers"], 16)
+            step = d.DecodeStep(cache, s, dev["embed"], dev["final_norm"], dev["head"],
+                                dev["layers"], scores, every)
+            made.append((alloc, cache, scores, step))
+        token = 7
+        announce("one run", n, "score_every", every)
+        run_tokens, _ = made[0][3].run(token, start, n)
+        single = []
+        t = token
+        for i in range(n):
+            out, _ = made[1][3].run(t, start + i, 1)
+            single.append(int(out[0]))
+            t = int(out[0])
+        np.testing.assert_array_equal(run_tokens, single)
+        np.testing.assert_array_equal(made[0][3].logits(), made[1][3].logits())
+        np.testing.assert_array_equal(made[0][2].download(), made[1][2].download())
+        np.testing.assert_array_equal(made[0][1].page_tiers(), made[1][1].page_tiers())
+        for layer in range(s["layers"]):
+            for page in range((start + n) // P):
+                np.testing.assert_array_equal(made[0][0].read(layer, page),
+                                              made[1][0].read(layer, page))
+        scored = made[0][2].download()
+        assert np.isfinite(scored[:, :(start + n) // P]).all()
