@@ -28,6 +28,7 @@ class Shape:
     intermediate: int
     rope_theta: float
     rms_eps: float
+    vocab: int
 
     @property
     def kv_width(self) -> int:
@@ -38,9 +39,9 @@ class Shape:
         return self.heads // self.kv_heads
 
 
-QWEN_05B = Shape("qwen2.5-0.5b", 24, 14, 2, 64, 896, 4864, 1e6, 1e-6)
-QWEN_15B = Shape("qwen2.5-1.5b", 28, 12, 2, 128, 1536, 8960, 1e6, 1e-6)
-LLAMA_1B = Shape("llama-3.2-1b", 16, 32, 8, 64, 2048, 8192, 5e5, 1e-5)
+QWEN_05B = Shape("qwen2.5-0.5b", 24, 14, 2, 64, 896, 4864, 1e6, 1e-6, 151936)
+QWEN_15B = Shape("qwen2.5-1.5b", 28, 12, 2, 128, 1536, 8960, 1e6, 1e-6, 151936)
+LLAMA_1B = Shape("llama-3.2-1b", 16, 32, 8, 64, 2048, 8192, 5e5, 1e-5, 128256)
 SHAPES = {s.name: s for s in (QWEN_05B, QWEN_15B, LLAMA_1B)}
 
 #: Config 3's tier mix, lowest tier first: (tier, fraction of sealed pages).
@@ -85,6 +86,22 @@ def tiers_by_importance(rng: np.random.Generator, pages: int, mix) -> np.ndarray
         tiers[order[at:at + count]] = tier
         at += count
     return tiers
+
+
+def model_dict(shape: Shape) -> dict:
+    """A shape as DecodeStep takes it."""
+    return dict(layers=shape.layers, hidden=shape.hidden, intermediate=shape.intermediate,
+                heads=shape.heads, kv_heads=shape.kv_heads, head_dim=shape.head_dim,
+                vocab=shape.vocab, rms_eps=shape.rms_eps, rope_theta=shape.rope_theta)
+
+
+def weight_bytes_per_step(shape: Shape) -> int:
+    """fp16 weight bytes a decode step reads: every layer's projections and
+    norms, the final norm and the head (the embedding gives one row)."""
+    h, i = shape.hidden, shape.intermediate
+    q, kv = shape.heads * shape.head_dim, shape.kv_heads * shape.head_dim
+    layer = h * (q + 2 * kv) + (q + 2 * kv) + q * h + 3 * h * i + 2 * h
+    return 2 * (shape.layers * layer + h + shape.vocab * h + h)
 
 
 def tier_map(seed: int, layers: int, pages: int, mix) -> list[list[int]]:
