@@ -706,6 +706,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=None, help="fewer layers, for a quick look")
+    ap.add_argument("--legs", default="decode,prefill,config2,step,requant,cpu",
+                    help="the legs to run (comma list; decode is the headline)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-requant", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -729,37 +731,47 @@ def main() -> int:
         m.synchronize()
         log(f"copied {page * count} bytes in one copy_pages launch")
         return 0
+    legs = set(args.legs.split(","))
+    for flag, leg in ((args.no_cpu, "cpu"), (args.no_requant, "requant"),
+                      (args.no_prefill, "prefill"), (args.no_step, "step")):
+        if flag:
+            legs.discard(leg)
     log("device", m.device_name())
     copy_gbs = copy_peak(m)
     log(f"device copy: {copy_gbs:.0f} GB/s (read + write)")
     shape = w.QWEN_15B
     context = 32768
     layers = args.layers or shape.layers
+    stream = m.Stream()
 
-    times, step_bytes, per_layer, held = decode_legs(m, shape, context, layers, args.steps,
-                                                    args.warmup)
-    alloc3, cache3, host3, rows3, rope3, bs3, stream = held
-    ms = times["kept"]
-    gbs = step_bytes / (ms * 1e-3) / 1e9
-    us_token = ms * 1e3 * shape.layers / layers
-    traffic, traffic_note = profiled_traffic()
+    ms = gbs = us_token = traffic = None
+    times, step_bytes, traffic_note = {}, 0, None
+    if "decode" in legs:
+        times, step_bytes, per_layer, held = decode_legs(m, shape, context, layers, args.steps,
+                                                        args.warmup)
+        alloc3, cache3, host3, rows3, rope3, bs3, stream = held
+        ms = times["kept"]
+        gbs = step_bytes / (ms * 1e-3) / 1e9
+        us_token = ms * 1e3 * shape.layers / layers
+        traffic, traffic_note = profiled_traffic()
 
     def leg_gbs(t):
         return round(step_bytes / (t * 1e-3) / 1e9, 1)
 
     prefill = None
-    if not args.no_prefill:
+    if "prefill" in legs and "decode" in legs:
         prefill = {"tile": prefill_tile(m, shape, cache3, host3, rows3, rope3, bs3, layers, context,
                                         stream, args.steps, args.warmup),
                    "chunks": prefill_chunks(m, stream, max(args.steps // 5, 3),
                                             max(args.warmup // 5, 1))}
         log(f"prefill: {prefill}")
-    del alloc3, cache3, host3, rows3
+    if "decode" in legs:
+        del alloc3, cache3, host3, rows3
 
-    c2 = config2(m, args.steps, args.warmup)
+    c2 = config2(m, args.steps, args.warmup) if "config2" in legs else None
 
     steps_out = None
-    if not args.no_step:
+    if "step" in legs:
         steps_out = {
             "qwen2.5-1.5b_32k": full_step(m, w.QWEN_15B, 32768 - 64 - 8, 64, 8, w.MIX_CONFIG3,
                                           True, 3),
@@ -768,7 +780,7 @@ def main() -> int:
                                                        "qwen2.5-1.5b_fp16_16k": 40.1}
 
     requant = None
-    if not args.no_requant:
+    if "requant" in legs:
         t0 = time.perf_counter()
         link = link_rates(m)
         log(f"host link: {link}")
@@ -776,7 +788,7 @@ def main() -> int:
         log(f"requant plan in {time.perf_counter() - t0:.1f}s: {requant}")
 
     cpu = None
-    if not args.no_cpu:
+    if "cpu" in legs:
         threads = blas_threads()
         pass_s = cpu_config1()
         pass_bytes = config1_pass_bytes(m, w.QWEN_05B)
@@ -800,6 +812,11 @@ def main() -> int:
                                  "gb_per_s": round(layer_b / layer_s / 1e9, 4)}}
         log(f"cpu: {cpu}")
 
+    if ms is None:
+        print(json.dumps({"metric": METRIC, "value": None, "legs": sorted(legs), "config2": c2,
+                          "decode_step": steps_out, "requant": requant, "cpu_baseline": cpu}),
+              flush=True)
+        return 0
     result = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
