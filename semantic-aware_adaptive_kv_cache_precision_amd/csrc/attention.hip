@@ -1,550 +1,410 @@
-// Attention over the KV cache: the general kernel, for every layout and any
-// number of queries, with the split-K combine.
+// Attention over the KV cache for every layout and any number of queries:
+// the general path, for the shapes the decode kernel (decode.hip) and the
+// matrix-core chunk kernel (prefill.hip) do not take -- pages of other than
+// 32 tokens, head dims other than 64 and 128, rows that are not 16-byte
+// aligned, a decode's per-page mass over a contiguous cache.
 //
-// Semantics follow the reference (src/core_kernels/attention.cu):
-//   - online softmax over key tiles of 32, scale folded into q in fp32
-//     (:449-540), scores masked by select so a NaN in a masked key cannot
-//     leak (:574-589), the -inf-row guard (:597-615);
-//   - GQA rows: query head h reads KV head h / (heads / kv_heads) (:85-90);
-//   - three layouts (:122-364): contiguous, an FP16 page table, and a cache
-//     that seals, whose pages before a query's own are read at the tier the
-//     table records and dequantised in registers exactly as dequantise_page
-//     does, the own page read at FP16 from the open page and the chunk rows;
-//   - key bias completed as k + RoPE(k_bias, j) from the cos/sin table (:104-116);
-//   - per-page attention mass of a decode step's one query (:375-411, :697-745);
-//   - split-K runs folded by the combine kernel (:754-815).
+// Semantics are the reference's attention (src/core_kernels/attention.cu):
+//   - softmax(q k^T / sqrt(d)) v with the scores and the accumulation in
+//     fp32, query i of seq_q at position seq_k - seq_q + i seeing the keys up
+//     to its own (:449-540); query head h reads KV head h / (heads / kv_heads);
+//   - a key the query may not see contributes nothing, and its bytes are not
+//     read, so a NaN there cannot reach the output (:574-589); a row that
+//     sees no key at all gives zeros (:597-615);
+//   - a cache that seals: every page before a query's own is read at the
+//     tier its table records and dequantised as dequantise_page does, an
+//     unread page (tier 0xFF) not at all, and the query's own page at FP16
+//     from the open page and the chunk's rows (:122-364);
+//   - the key bias completes key j as k + RoPE(bias, j), from the fp32
+//     {cos, sin} table (:104-116);
+//   - a decode query's per-page mass, each page's share of its softmax
+//     (:375-411); a contiguous cache's pages are 32 keys.
 //
-// Where this departs from the reference's shape (not its arithmetic): split
-// runs are whole pages (a multiple of lcm(P, 32) keys), so no page's mass is
-// carried across a run boundary; and each page's running (sum, max) is kept in
-// global memory beside the mass output rather than in LDS, so the LDS a launch
-// takes does not grow with the context.
-//
-// The hot decode path (one query, 32-token pages) has its own kernel in
-// decode.hip; this one is the reference-exact general path and the fallback
-// for every other shape.
+// Work layout (this build's own): a workgroup of 256 lanes owns one
+// (query, head) and one run of keys (a split), and walks the run a tile of
+// whole pages at a time. In a tile every lane scores keys (q, pre-scaled,
+// from LDS against the key's row, widened and dequantised an element at a
+// time), the tile's maximum and the running softmax are formed once for the
+// workgroup, and then each lane owns one output channel and adds the tile's
+// weighted values for it: the lanes read a value row together, coalesced.
+// For the mass, each page keeps the sum of its weights and the maximum they
+// are relative to. A launch of several runs writes each run's (m, l, o); the
+// combine folds them and forms the masses at the folded maximum.
 
 #include "common.hpp"
 #include "kernels.hpp"
 
 #include <algorithm>
 #include <cmath>
-#include <numeric>
 
 namespace mi
 {
   namespace
   {
-
     constexpr int kThreads = 256;
-    constexpr int kTileK = 32;   // keys a tile
-    constexpr int kTileQ = 16;   // queries a prefill tile
-    constexpr int kSplitBlocksPerCU = 8;
+    constexpr int kContiguousPage = 32; // a contiguous cache's pages, for the mass
+    constexpr int kTileKeys = 256;      // keys a tile holds (whole pages; a larger page alone)
+    constexpr int kMaxTile = 4096;
+    constexpr int kBlocksPerCU = 8;
     constexpr int kMinSplitKeys = 256;
+    constexpr int kPartialSlotsPerCU = kBlocksPerCU * 16;
 
-    // What a device-side reader needs: the source, each quantised tier's layout.
-    struct Reader
+    struct GeneralArgs
     {
       KVSource src;
       PageLayout lay[kTierCount];
-      std::size_t row;          // kv_heads * head_dim
+      const std::uint16_t *q;   // (seq_q, heads, hd)
+      std::uint16_t *out;       // (seq_q, heads, hd)
+      const std::uint16_t *k_bias;
+      const float *rope;
+      int seq_q;
+      int seq_k;
+      int heads;
       int kv_heads;
-      int head_dim;
-      int own;                  // the query tile's own page (causal)
-
-      __device__ static float h2f(std::uint16_t h) { return mi::h2f(h); }
-
-      template <int Bits>
-      __device__ static void dequant(const std::uint8_t *page, const PageLayout &L, int t,
-                                     std::size_t at, std::size_t row, int kv_heads, int head_dim,
-                                     float &k, float &v)
-      {
-        constexpr int kPerByte = 8 / Bits;
-        constexpr unsigned kMask = (1u << Bits) - 1;
-        const std::size_t e = static_cast<std::size_t>(t) * row + at;
-        const unsigned kb = page[L.key_codes + e / kPerByte];
-        const unsigned vb = page[L.value_codes + e / kPerByte];
-        const int shift = static_cast<int>(e % kPerByte) * Bits;
-        const auto *ks = reinterpret_cast<const std::uint16_t *>(page + L.key_scales);
-        const auto *kz = reinterpret_cast<const std::uint16_t *>(page + L.key_zeros);
-        const auto *vs = reinterpret_cast<const std::uint16_t *>(page + L.value_scales);
-        const auto *vz = reinterpret_cast<const std::uint16_t *>(page + L.value_zeros);
-        const std::size_t group = static_cast<std::size_t>(t) * kv_heads + at / head_dim;
-        k = h2f(__half_as_ushort(__float2half_rn(
-            fmaf(static_cast<float>((kb >> shift) & kMask), h2f(ks[at]), h2f(kz[at])))));
-        v = h2f(__half_as_ushort(__float2half_rn(
-            fmaf(static_cast<float>((vb >> shift) & kMask), h2f(vs[group]), h2f(vz[group])))));
-      }
-
-      // Whether key j is read at all: only a sealed page before the own page
-      // can be unread.
-      __device__ bool reads(int j) const
-      {
-        if (src.layout != Layout::kCausal)
-        {
-          return true;
-        }
-        const int p = j / src.page_tokens;
-        return p >= own || src.tiers[p] != kUnreadPage;
-      }
-
-      // Element `at` of key j's row and of its value's row, widened to fp32.
-      __device__ void read(int j, std::size_t at, float &k, float &v) const
-      {
-        switch (src.layout)
-        {
-        case Layout::kContiguous:
-          k = h2f(src.k[static_cast<std::size_t>(j) * row + at]);
-          v = h2f(src.v[static_cast<std::size_t>(j) * row + at]);
-          return;
-        case Layout::kPaged:
-        {
-          const int P = src.page_tokens;
-          const auto *page = reinterpret_cast<const std::uint16_t *>(src.pages[j / P]);
-          const std::size_t t = static_cast<std::size_t>(j % P);
-          k = h2f(page[t * row + at]);
-          v = h2f(page[(P + t) * row + at]);
-          return;
-        }
-        case Layout::kCausal:
-        {
-          const int P = src.page_tokens;
-          const int p = j / P;
-          const int t = j % P;
-          if (p < own)
-          {
-            const std::uint8_t tier = src.tiers[p];
-            const auto *page = reinterpret_cast<const std::uint8_t *>(src.pages[p]);
-            switch (tier)
-            {
-            case kINT8: dequant<8>(page, lay[kINT8], t, at, row, kv_heads, head_dim, k, v); return;
-            case kINT4: dequant<4>(page, lay[kINT4], t, at, row, kv_heads, head_dim, k, v); return;
-            case kINT2: dequant<2>(page, lay[kINT2], t, at, row, kv_heads, head_dim, k, v); return;
-            case kFP16:
-            {
-              const auto *h = reinterpret_cast<const std::uint16_t *>(page);
-              k = h2f(h[static_cast<std::size_t>(t) * row + at]);
-              v = h2f(h[static_cast<std::size_t>(P + t) * row + at]);
-              return;
-            }
-            default: // unread: its address is never touched
-              k = 0.0f;
-              v = 0.0f;
-              return;
-            }
-          }
-          if (j >= src.start)
-          {
-            k = h2f(src.chunk_k[static_cast<std::size_t>(j - src.start) * row + at]);
-            v = h2f(src.chunk_v[static_cast<std::size_t>(j - src.start) * row + at]);
-            return;
-          }
-          k = h2f(src.open[static_cast<std::size_t>(t) * row + at]);
-          v = h2f(src.open[static_cast<std::size_t>(P + t) * row + at]);
-          return;
-        }
-        }
-      }
-    };
-
-    __device__ inline float rotated_bias(const std::uint16_t *bias, int position, int d,
-                                         int head_dim, const float *rope)
-    {
-      const int half = head_dim / 2;
-      const int j = d < half ? d : d - half;
-      const float *cs = rope + 2 * (static_cast<std::size_t>(position) * half + j);
-      const float b1 = h2f(bias[j]);
-      const float b2 = h2f(bias[j + half]);
-      return d < half ? b1 * cs[0] - b2 * cs[1] : b2 * cs[0] + b1 * cs[1];
-    }
-
-    struct Shape
-    {
-      int hpb;          // query heads a block (of one KV head)
-      int qpb;          // queries a block
-      int lead;         // rows before the first query, aligning tiles to pages
+      int hd;
+      int mass_page; // keys a mass page holds
+      int tile;      // keys a tile holds: whole mass pages
       int splits;
       int split_keys;
+      float *partials;   // [query][head][split][2 + hd] when splits > 1
+      float *page_stats; // [head][page][2]: a page's (base, sum of exp(s - base)); with mass
+      float *mass;       // [head][page]; with mass
     };
 
-    __host__ __device__ inline std::size_t slot_floats(int head_dim)
+    // Where key j's row is, for reading it an element at a time.
+    struct Row
     {
-      return static_cast<std::size_t>(head_dim) + 2; // m, l, then the output
+      const std::uint16_t *k; // FP16 rows (null for a quantised page)
+      const std::uint16_t *v;
+      const std::uint8_t *page; // a quantised page, its tier and the key's row in it
+      int tier;
+      int t;
+    };
+
+    __device__ inline Row row_of(const GeneralArgs &a, int j, int own)
+    {
+      const KVSource &s = a.src;
+      const std::size_t W = static_cast<std::size_t>(a.kv_heads) * a.hd;
+      Row r{};
+      r.tier = kFP16;
+      if (s.layout == Layout::kContiguous)
+      {
+        r.k = s.k + j * W;
+        r.v = s.v + j * W;
+        return r;
+      }
+      const int P = s.page_tokens;
+      const int p = j / P;
+      const int t = j % P;
+      if (s.layout == Layout::kPaged || p < own)
+      {
+        const int tier = s.layout == Layout::kPaged ? static_cast<int>(kFP16) : s.tiers[p];
+        if (tier == kFP16)
+        {
+          const auto *h = reinterpret_cast<const std::uint16_t *>(s.pages[p]);
+          r.k = h + t * W;
+          r.v = h + (P + t) * W;
+          return r;
+        }
+        r.page = reinterpret_cast<const std::uint8_t *>(s.pages[p]);
+        r.tier = tier;
+        r.t = t;
+        return r;
+      }
+      // The query's own page: rows before `start` in the open page, the rest
+      // the chunk's.
+      if (j >= s.start)
+      {
+        r.k = s.chunk_k + (j - s.start) * W;
+        r.v = s.chunk_v + (j - s.start) * W;
+      }
+      else
+      {
+        r.k = s.open + t * W;
+        r.v = s.open + (P + t) * W;
+      }
+      return r;
     }
 
-    // The kernel. Rows of a block: qpb queries x hpb consecutive heads, row r
-    // being query r / hpb and head r % hpb. A block walks its split's keys in
-    // tiles; in LDS: the rows' scaled q, output accumulators, the tile's scores,
-    // keys (fp32, padded a column against bank conflicts) and values.
-    template <bool kMass>
-    __global__ void __launch_bounds__(kThreads)
-        attention_kernel(Reader rd, AttentionArgs a, Shape s, float *page_max)
+    // Whether key j is read: a page sealed before the own page may be unread.
+    __device__ inline bool readable(const GeneralArgs &a, int j, int own)
     {
-      extern __shared__ float smem[];
-      const int hd = a.head_dim;
-      const int rows = s.hpb * s.qpb;
-      const int ks = hd + 1;
-      const int ss = kTileK + 1;
-      float *q_s = smem;
-      float *o_s = q_s + rows * hd;
-      float *s_s = o_s + rows * hd;
-      float *m_s = s_s + rows * ss;
-      float *l_s = m_s + rows;
-      float *rescale_s = l_s + rows;
-      float *reads_s = rescale_s + rows;
-      float *k_s = reads_s + kTileK;
-      float *v_s = k_s + kTileK * ks;
-
-      const int head_first = blockIdx.y * s.hpb;
-      const int split = blockIdx.z;
-      const int q_first = blockIdx.x * s.qpb - s.lead;
-      const int q_last = min(q_first + s.qpb, a.seq_q) - 1;
-      const int shift = a.seq_k - a.seq_q;
-      const int group = a.heads / a.kv_heads;
-      const std::size_t kv_off = static_cast<std::size_t>(head_first / group) * hd;
-      const std::size_t token_stride = static_cast<std::size_t>(a.heads) * hd;
-      if (rd.src.layout == Layout::kCausal)
+      if (a.src.layout != Layout::kCausal)
       {
-        rd.own = (q_first + shift) / rd.src.page_tokens;
+        return true;
       }
-      const auto query_of = [&](int r) { return q_first + r / s.hpb; };
-      const auto head_of = [&](int r) { return head_first + r % s.hpb; };
-      const auto stored = [&](int r) { return query_of(r) >= 0 && query_of(r) <= q_last; };
-      const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+      const int p = j / a.src.page_tokens;
+      return p >= own || a.src.tiers[p] != kUnreadPage;
+    }
 
-      for (int i = threadIdx.x; i < rows * hd; i += blockDim.x)
-      {
-        const int r = i / hd;
-        const int d = i % hd;
-        q_s[i] = stored(r) ? h2f(a.q[query_of(r) * token_stride +
-                                                    static_cast<std::size_t>(head_of(r)) * hd + d]) *
-                                 scale
-                           : 0.0f;
-        o_s[i] = 0.0f;
-      }
-      for (int r = threadIdx.x; r < rows; r += blockDim.x)
-      {
-        m_s[r] = -INFINITY;
-        l_s[r] = 0.0f;
-      }
+    // code * scale + zero rounded as dequantise_page rounds it (fp32 fma,
+    // then fp16).
+    __device__ inline float dequantised(const std::uint8_t *page, std::size_t codes,
+                                        std::size_t e, int bits, std::size_t scale,
+                                        std::size_t zero, std::size_t group)
+    {
+      const int per_byte = 8 / bits;
+      const unsigned byte = page[codes + e / per_byte];
+      const unsigned code = (byte >> ((e % per_byte) * bits)) & ((1u << bits) - 1);
+      const auto *s = reinterpret_cast<const std::uint16_t *>(page + scale);
+      const auto *z = reinterpret_cast<const std::uint16_t *>(page + zero);
+      return h2f(__half_as_ushort(
+          __float2half_rn(fmaf(static_cast<float>(code), h2f(s[group]), h2f(z[group])))));
+    }
 
-      const int key_first = split * s.split_keys;
-      const int key_end = min(key_first + s.split_keys, q_last + shift + 1);
-      const int P = rd.src.page_tokens;
-      const int pages = kMass ? (a.seq_k + P - 1) / P : 0;
-      // The page a row's thread is summing, its sum of exp(s - max), and max.
-      int open = -1;
-      float page_sum = 0.0f, page_top = -INFINITY;
+    // Element `at` (of the row's kv_heads * hd) of the key, or of the value.
+    __device__ inline float key_at(const GeneralArgs &a, const Row &r, std::size_t at)
+    {
+      if (r.page == nullptr)
+      {
+        return h2f(r.k[at]);
+      }
+      const PageLayout &L = a.lay[r.tier];
+      const std::size_t W = static_cast<std::size_t>(a.kv_heads) * a.hd;
+      return dequantised(r.page, L.key_codes, r.t * W + at, L.bits, L.key_scales, L.key_zeros, at);
+    }
+
+    __device__ inline float value_at(const GeneralArgs &a, const Row &r, std::size_t at)
+    {
+      if (r.page == nullptr)
+      {
+        return h2f(r.v[at]);
+      }
+      const PageLayout &L = a.lay[r.tier];
+      const std::size_t W = static_cast<std::size_t>(a.kv_heads) * a.hd;
+      const std::size_t group = static_cast<std::size_t>(r.t) * a.kv_heads + at / a.hd;
+      return dequantised(r.page, L.value_codes, r.t * W + at, L.bits, L.value_scales,
+                         L.value_zeros, group);
+    }
+
+    // Element c of the key bias turned to position j (rotate-half: channel
+    // c pairs with c +- hd/2), from the {cos, sin} table.
+    __device__ inline float bias_at(const std::uint16_t *bias, const float *rope, int j, int c,
+                                    int hd)
+    {
+      const int half = hd / 2;
+      const int i = c % half;
+      const float *cs = rope + 2 * (static_cast<std::size_t>(j) * half + i);
+      const float x = h2f(bias[i]);
+      const float y = h2f(bias[i + half]);
+      return c < half ? x * cs[0] - y * cs[1] : y * cs[0] + x * cs[1];
+    }
+
+    __global__ void __launch_bounds__(kThreads) general_attention_kernel(GeneralArgs a)
+    {
+      extern __shared__ float lds[];
+      float *q_s = lds;              // hd: q * 1/sqrt(hd)
+      float *w_s = q_s + a.hd;       // tile: the keys' scores, then their weights
+      float *red = w_s + a.tile;     // a float a wave
+      const int tid = threadIdx.x;
+      const int query = blockIdx.x / a.heads;
+      const int head = blockIdx.x % a.heads;
+      const int split = blockIdx.y;
+      const int kvh = head / (a.heads / a.kv_heads);
+      const int position = a.seq_k - a.seq_q + query;
+      const int own = a.src.layout == Layout::kContiguous ? 0 : position / a.src.page_tokens;
+      const std::size_t at0 = static_cast<std::size_t>(kvh) * a.hd;
+      const std::uint16_t *bias = a.k_bias != nullptr ? a.k_bias + at0 : nullptr;
+      const float scale = 1.0f / sqrtf(static_cast<float>(a.hd));
+      for (int c = tid; c < a.hd; c += kThreads)
+      {
+        q_s[c] = h2f(a.q[(static_cast<std::size_t>(query) * a.heads + head) * a.hd + c]) * scale;
+      }
+      const int k0 = split * a.split_keys;
+      const int k1 = min(k0 + a.split_keys, position + 1);
+      const bool with_mass = a.page_stats != nullptr;
+      float m = -INFINITY, l = 0.0f, o = 0.0f; // o: lane tid's channel
       __syncthreads();
-
-      for (int k_first = key_first; k_first < key_end; k_first += kTileK)
+      for (int t0 = k0; t0 < k1; t0 += a.tile)
       {
-        for (int i = threadIdx.x; i < kTileK * hd; i += blockDim.x)
+        const int n = min(a.tile, k1 - t0);
+        for (int u = tid; u < n; u += kThreads)
         {
-          const int c = i / hd;
-          const int d = i % hd;
-          const int j = k_first + c;
-          const bool in_range = j < a.seq_k;
-          float key = 0.0f, value = 0.0f;
-          if (in_range && rd.reads(j))
+          const int j = t0 + u;
+          float score = -INFINITY;
+          if (readable(a, j, own))
           {
-            rd.read(j, kv_off + d, key, value);
-            if (a.k_bias != nullptr)
+            const Row r = row_of(a, j, own);
+            float acc = 0.0f;
+            for (int c = 0; c < a.hd; ++c)
             {
-              key += rotated_bias(a.k_bias + kv_off, j, d, hd, a.rope);
+              float k = key_at(a, r, at0 + c);
+              if (bias != nullptr)
+              {
+                k += bias_at(bias, a.rope, j, c, a.hd);
+              }
+              acc = fmaf(q_s[c], k, acc);
+            }
+            score = acc;
+          }
+          w_s[u] = score;
+        }
+        __syncthreads();
+        float top = -INFINITY;
+        for (int u = tid; u < n; u += kThreads)
+        {
+          top = fmaxf(top, w_s[u]);
+        }
+        top = block_reduce<true>(top, red);
+        const float m_new = fmaxf(m, top);
+        const float base = m_new == -INFINITY ? 0.0f : m_new;
+        const float keep = expf(m - base); // 0 before the first visible key
+        float part = 0.0f;
+        for (int u = tid; u < n; u += kThreads)
+        {
+          const float w = expf(w_s[u] - base); // 0 for a key not seen
+          w_s[u] = w;
+          part += w;
+        }
+        part = block_reduce<false>(part, red); // its barriers publish the weights
+        l = l * keep + part;
+        if (with_mass && query == 0)
+        {
+          const int first = t0 / a.mass_page;
+          const int pages = (n + a.mass_page - 1) / a.mass_page;
+          for (int p = tid; p < pages; p += kThreads)
+          {
+            float sum = 0.0f;
+            const int end = min((p + 1) * a.mass_page, n);
+            for (int u = p * a.mass_page; u < end; ++u)
+            {
+              sum += w_s[u];
+            }
+            const std::size_t at = (static_cast<std::size_t>(head) *
+                                        ((a.seq_k + a.mass_page - 1) / a.mass_page) +
+                                    first + p) * 2;
+            a.page_stats[at] = base;
+            a.page_stats[at + 1] = sum;
+          }
+        }
+        if (tid < a.hd)
+        {
+          float acc = 0.0f;
+          for (int u = 0; u < n; ++u)
+          {
+            const float w = w_s[u];
+            if (w != 0.0f)
+            {
+              acc = fmaf(w, value_at(a, row_of(a, t0 + u, own), at0 + tid), acc);
             }
           }
-          k_s[c * ks + d] = key;
-          v_s[c * hd + d] = value;
-          if (d == 0)
-          {
-            reads_s[c] = !in_range || rd.reads(j) ? 1.0f : 0.0f;
-          }
+          o = o * keep + acc;
         }
-        __syncthreads();
-
-        for (int i = threadIdx.x; i < rows * kTileK; i += blockDim.x)
-        {
-          const int r = i / kTileK;
-          const int c = i % kTileK;
-          float dot = 0.0f;
-          for (int d = 0; d < hd; ++d)
-          {
-            dot += q_s[r * hd + d] * k_s[c * ks + d];
-          }
-          const bool visible = k_first + c <= query_of(r) + shift && reads_s[c] != 0.0f;
-          s_s[r * ss + c] = visible ? dot : -INFINITY;
-        }
-        __syncthreads();
-
-        for (int r = threadIdx.x; r < rows; r += blockDim.x)
-        {
-          float *row = s_s + r * ss;
-          const float m_old = m_s[r];
-          float m_new = m_old;
-          for (int c = 0; c < kTileK; ++c)
-          {
-            m_new = fmaxf(m_new, row[c]);
-          }
-          const float m_from = m_new == -INFINITY ? 0.0f : m_new;
-          float sum = 0.0f;
-          for (int c = 0; c < kTileK; ++c)
-          {
-            const float p = expf(row[c] - m_from);
-            row[c] = p;
-            sum += p;
-          }
-          const float rescale = expf(m_old - m_from);
-          l_s[r] = l_s[r] * rescale + sum;
-          m_s[r] = m_new;
-          rescale_s[r] = rescale;
-          if constexpr (kMass)
-          {
-            // One query: row r is head head_of(r). Keys past seq_k add 0.
-            const std::size_t at = static_cast<std::size_t>(head_of(r)) * pages;
-            for (int c = 0; c < kTileK && k_first + c < a.seq_k; ++c)
-            {
-              const int page = (k_first + c) / P;
-              if (page != open)
-              {
-                if (open >= 0)
-                {
-                  a.mass[at + open] = page_sum;
-                  page_max[at + open] = page_top;
-                }
-                open = page;
-                page_sum = 0.0f;
-                page_top = m_new;
-              }
-              else if (page_top < m_new)
-              {
-                page_sum *= expf(page_top - m_new);
-                page_top = m_new;
-              }
-              page_sum += row[c];
-            }
-          }
-        }
-        __syncthreads();
-
-        for (int i = threadIdx.x; i < rows * hd; i += blockDim.x)
-        {
-          const int r = i / hd;
-          const int d = i % hd;
-          const float *p = s_s + r * ss;
-          float acc = o_s[i] * rescale_s[r];
-          for (int c = 0; c < kTileK; ++c)
-          {
-            acc += p[c] * v_s[c * hd + d];
-          }
-          o_s[i] = acc;
-        }
-        __syncthreads();
+        m = m_new;
+        __syncthreads(); // the next tile's scores overwrite the weights
       }
-
-      const auto slot = [&](int r) {
-        return a.partials + ((static_cast<std::size_t>(split) * a.seq_q + query_of(r)) * a.heads +
-                             head_of(r)) * slot_floats(hd);
-      };
-      for (int i = threadIdx.x; i < rows * hd; i += blockDim.x)
+      const std::size_t row = static_cast<std::size_t>(query) * a.heads + head;
+      if (a.splits > 1)
       {
-        const int r = i / hd;
-        const int d = i % hd;
-        if (!stored(r))
+        float *slot = a.partials + (row * a.splits + split) * (2 + a.hd);
+        if (tid == 0)
         {
-          continue;
+          slot[0] = m;
+          slot[1] = l;
         }
-        if (s.splits == 1)
+        if (tid < a.hd)
         {
-          a.out[query_of(r) * token_stride + static_cast<std::size_t>(head_of(r)) * hd + d] =
-              __half_as_ushort(__float2half(o_s[i] / l_s[r]));
+          slot[2 + tid] = o;
         }
-        else
-        {
-          slot(r)[2 + d] = o_s[i];
-        }
-      }
-      if (s.splits > 1)
-      {
-        for (int r = threadIdx.x; r < rows; r += blockDim.x)
-        {
-          if (stored(r))
-          {
-            slot(r)[0] = m_s[r];
-            slot(r)[1] = l_s[r];
-          }
-        }
-      }
-      if constexpr (kMass)
-      {
-        for (int r = threadIdx.x; r < rows; r += blockDim.x)
-        {
-          if (open >= 0)
-          {
-            const std::size_t at = static_cast<std::size_t>(head_of(r)) * pages;
-            a.mass[at + open] = page_sum;
-            page_max[at + open] = page_top;
-          }
-        }
-        __syncthreads();
-        // This run's pages: whole pages, since runs are.
-        const int first = key_first / P;
-        const int last = (min(key_first + s.split_keys, a.seq_k) - 1) / P;
-        const int local = last - first + 1;
-        for (int i = threadIdx.x; i < rows * local; i += blockDim.x)
-        {
-          const int r = i / local;
-          const int page = first + i % local;
-          const std::size_t at = static_cast<std::size_t>(head_of(r)) * pages + page;
-          const float m = m_s[r];
-          const float sum = a.mass[at];
-          const float top = page_max[at];
-          if (s.splits == 1)
-          {
-            a.mass[at] = sum * expf(top - m) / l_s[r];
-          }
-          else
-          {
-            // Relative to this run's m; the combine brings it to the whole's.
-            a.mass[at] = m == -INFINITY ? 0.0f : sum * expf(top - m);
-          }
-        }
-      }
-    }
-
-    // Folds the runs: M = max m_s, w_s = exp(m_s - M), out = sum(w o) / sum(w l);
-    // a page's mass, relative to its run's m, is weighed by its run's w and
-    // divided by the same sum (reference: attention.cu:754-815; no carry, as
-    // runs are whole pages here). One block a (query, head); a thread a run,
-    // the sums over runs taken through LDS, never by one thread alone.
-    constexpr int kCombineThreads = 256;
-    constexpr int kCombineDims = 32;
-
-    __global__ void __launch_bounds__(kCombineThreads)
-        combine_kernel(const float *__restrict__ partials, std::uint16_t *__restrict__ out,
-                       int seq_q, int heads, int head_dim, int splits, int split_keys,
-                       float *__restrict__ mass, int page_tokens, int seq_k)
-    {
-      extern __shared__ float s_w[]; // a weight per run
-      __shared__ float s_red[kCombineThreads / 64];
-      __shared__ float s_acc[kCombineThreads][kCombineDims + 1];
-      const int query = blockIdx.x / heads;
-      const int head = blockIdx.x % heads;
-      const int t = threadIdx.x;
-      const std::size_t sf = slot_floats(head_dim);
-      const auto slot = [&](int s) {
-        return partials + ((static_cast<std::size_t>(s) * seq_q + query) * heads + head) * sf;
-      };
-      float top = -INFINITY;
-      for (int s = t; s < splits; s += kCombineThreads)
-      {
-        top = fmaxf(top, slot(s)[0]);
-      }
-      top = block_reduce<true>(top, s_red);
-      float l = 0.0f;
-      for (int s = t; s < splits; s += kCombineThreads)
-      {
-        // A run none of whose keys this row reads weighs exactly 0.
-        const float w = expf(slot(s)[0] - top);
-        s_w[s] = w;
-        l += slot(s)[1] * w;
-      }
-      l = block_reduce<false>(l, s_red);
-      for (int d0 = 0; d0 < head_dim; d0 += kCombineDims)
-      {
-        const int n = min(kCombineDims, head_dim - d0);
-        float acc[kCombineDims];
-        for (int d = 0; d < kCombineDims; ++d)
-        {
-          acc[d] = 0.0f;
-        }
-        for (int s = t; s < splits; s += kCombineThreads)
-        {
-          const float *p = slot(s) + 2 + d0;
-          for (int d = 0; d < n; ++d)
-          {
-            acc[d] += p[d] * s_w[s];
-          }
-        }
-        __syncthreads();
-        for (int d = 0; d < kCombineDims; ++d)
-        {
-          s_acc[t][d] = acc[d];
-        }
-        __syncthreads();
-        if (t < n)
-        {
-          float sum = 0.0f;
-          for (int u = 0; u < kCombineThreads; ++u)
-          {
-            sum += s_acc[u][t];
-          }
-          out[(static_cast<std::size_t>(query) * heads + head) * head_dim + d0 + t] =
-              __half_as_ushort(__float2half(sum / l));
-        }
-      }
-      if (mass == nullptr)
-      {
         return;
       }
-      __syncthreads();
-      const int pages = (seq_k + page_tokens - 1) / page_tokens;
-      float *head_mass = mass + static_cast<std::size_t>(head) * pages;
-      for (int page = t; page < pages; page += kCombineThreads)
+      if (tid < a.hd)
       {
-        const int s = page * page_tokens / split_keys;
-        head_mass[page] = head_mass[page] * s_w[s] / l;
+        a.out[row * a.hd + tid] = __half_as_ushort(__float2half(l > 0.0f ? o / l : 0.0f));
+      }
+      if (with_mass)
+      {
+        // The page statistics this workgroup wrote are visible to it after
+        // the loop's last barrier.
+        const int pages = (a.seq_k + a.mass_page - 1) / a.mass_page;
+        for (int p = tid; p < pages; p += kThreads)
+        {
+          const float *st = a.page_stats + (static_cast<std::size_t>(head) * pages + p) * 2;
+          a.mass[static_cast<std::size_t>(head) * pages + p] =
+              l > 0.0f ? st[1] * expf(st[0] - m) / l : 0.0f;
+        }
       }
     }
 
-    std::size_t shared_floats(int head_dim, int rows)
+    // The runs of a (query, head) folded: M = max m_s, L = sum l_s e^(m_s - M),
+    // out = sum o_s e^(m_s - M) / L; a decode's page masses from their page
+    // statistics at M. A workgroup a (query, head), a lane a channel.
+    __global__ void __launch_bounds__(kThreads) general_combine_kernel(GeneralArgs a)
     {
-      return 2 * static_cast<std::size_t>(rows) * head_dim + rows * (kTileK + 1) + 3 * rows +
-             kTileK + static_cast<std::size_t>(kTileK) * (head_dim + 1) +
-             static_cast<std::size_t>(kTileK) * head_dim;
+      __shared__ float red[kThreads / 64];
+      const int tid = threadIdx.x;
+      const std::size_t row = blockIdx.x;
+      const int head = static_cast<int>(row % a.heads);
+      const float *slots = a.partials + row * a.splits * (2 + a.hd);
+      float top = -INFINITY;
+      for (int s = tid; s < a.splits; s += kThreads)
+      {
+        top = fmaxf(top, slots[s * (2 + a.hd)]);
+      }
+      top = block_reduce<true>(top, red);
+      const float base = top == -INFINITY ? 0.0f : top;
+      float l = 0.0f, o = 0.0f;
+      for (int s = 0; s < a.splits; ++s)
+      {
+        const float *slot = slots + s * (2 + a.hd);
+        const float w = expf(slot[0] - base); // 0 for a run that saw no key
+        l += slot[1] * w;
+        if (tid < a.hd)
+        {
+          o += slot[2 + tid] * w;
+        }
+      }
+      if (tid < a.hd)
+      {
+        a.out[row * a.hd + tid] = __half_as_ushort(__float2half(l > 0.0f ? o / l : 0.0f));
+      }
+      if (a.page_stats != nullptr && row < static_cast<std::size_t>(a.heads))
+      {
+        const int pages = (a.seq_k + a.mass_page - 1) / a.mass_page;
+        for (int p = tid; p < pages; p += kThreads)
+        {
+          const float *st = a.page_stats + (static_cast<std::size_t>(head) * pages + p) * 2;
+          a.mass[static_cast<std::size_t>(head) * pages + p] =
+              l > 0.0f ? st[1] * expf(st[0] - top) / l : 0.0f;
+        }
+      }
     }
 
     int ceil_div(int a, int b) { return (a + b - 1) / b; }
-    int round_up(int a, int b) { return ceil_div(a, b) * b; }
 
-    Shape shape_for(int seq_q, int seq_k, int heads, int kv_heads, bool aligned, int page_tokens,
-                    bool may_split)
+    // Keys a tile holds: whole mass pages, about kTileKeys of them.
+    int tile_for(int mass_page)
     {
-      Shape p{1, kTileQ, 0, 1, round_up(std::max(seq_k, 1), kTileK)};
-      if (seq_q == 1)
-      {
-        const int group = heads / kv_heads;
-        p.qpb = 1;
-        for (int h = std::min(group, kTileQ); h >= 1; --h)
-        {
-          if (group % h == 0)
-          {
-            p.hpb = h;
-            break;
-          }
-        }
-      }
-      p.lead = aligned ? (seq_k - seq_q) % p.qpb : 0;
+      return mass_page >= kTileKeys ? mass_page : mass_page * (kTileKeys / mass_page);
+    }
+
+    int partial_slots() { return kPartialSlotsPerCU * device_multiprocessors(); }
+
+    // Runs of whole tiles: enough workgroups to fill the device, none
+    // shorter than kMinSplitKeys, every (query, head, run) a partial slot.
+    Split split_for(int seq_q, int seq_k, int heads, int tile, bool may_split)
+    {
+      const int whole = ceil_div(std::max(seq_k, 1), tile) * tile;
       if (!may_split)
       {
-        return p;
+        return {1, whole};
       }
-      const long blocks = static_cast<long>(ceil_div(p.lead + seq_q, p.qpb)) * (heads / p.hpb);
-      const long target = static_cast<long>(kSplitBlocksPerCU) * device_multiprocessors();
-      const int splits = static_cast<int>(std::min<long>(target / blocks, seq_k / kMinSplitKeys));
+      const long rows = static_cast<long>(seq_q) * heads;
+      const long fill = (static_cast<long>(kBlocksPerCU) * device_multiprocessors() + rows - 1) /
+                        std::max(rows, 1L);
+      const long splits = std::min({fill, static_cast<long>(seq_k / kMinSplitKeys),
+                                    static_cast<long>(partial_slots()) / std::max(rows, 1L)});
       if (splits <= 1)
       {
-        return p;
+        return {1, whole};
       }
-      // Runs are whole tiles and whole pages.
-      const int unit = page_tokens > 0 ? std::lcm(page_tokens, kTileK) : kTileK;
-      p.split_keys = round_up(ceil_div(seq_k, splits), unit);
-      p.splits = ceil_div(seq_k, p.split_keys);
-      if (p.splits == 1)
-      {
-        p.split_keys = round_up(seq_k, kTileK);
-      }
-      return p;
+      const int keys = ceil_div(ceil_div(seq_k, static_cast<int>(splits)), tile) * tile;
+      return {ceil_div(seq_k, keys), keys};
+    }
+
+    int mass_page_of(const KVSource &kv)
+    {
+      return kv.layout == Layout::kContiguous ? kContiguousPage : kv.page_tokens;
     }
 
     void check_grouping(int heads, int kv_heads)
@@ -563,29 +423,6 @@ namespace mi
       }
     }
 
-    // The per-page running maxima a mass launch keeps beside its output: a
-    // library-owned device buffer, grown on demand and kept.
-    float *page_max_buffer(std::size_t floats)
-    {
-      static float *buffer = nullptr;
-      static std::size_t held = 0;
-      if (floats > held)
-      {
-        if (buffer != nullptr)
-        {
-          hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize before growing scratch");
-          hip_check(hipFree(buffer), "hipFree attention scratch");
-          buffer = nullptr;
-          held = 0;
-        }
-        const std::size_t grown = std::max<std::size_t>(floats, 1 << 16);
-        hip_check(hipMalloc(reinterpret_cast<void **>(&buffer), grown * sizeof(float)),
-                  "hipMalloc attention scratch");
-        held = grown;
-      }
-      return buffer;
-    }
-
   } // namespace
 
   int device_multiprocessors()
@@ -602,15 +439,14 @@ namespace mi
 
   std::size_t attention_partials_floats(int head_dim)
   {
-    return static_cast<std::size_t>(kSplitBlocksPerCU) * device_multiprocessors() * kTileQ *
-           slot_floats(head_dim);
+    return static_cast<std::size_t>(partial_slots()) * (static_cast<std::size_t>(head_dim) + 2);
   }
 
   Split attention_split(int seq_q, int seq_k, int heads, int kv_heads, int page_tokens)
   {
     check_grouping(heads, kv_heads);
-    const Shape p = shape_for(seq_q, seq_k, heads, kv_heads, page_tokens > 0, page_tokens, true);
-    return {p.splits, p.split_keys};
+    const int mass_page = page_tokens > 0 ? page_tokens : kContiguousPage;
+    return split_for(seq_q, seq_k, heads, tile_for(mass_page), true);
   }
 
   bool launch_decode_fast(const KVSource &kv, const AttentionArgs &a, hipStream_t stream);
@@ -647,82 +483,63 @@ namespace mi
       launch_prefill(kv, a, stream);
       return;
     }
-    const bool aligned = kv.layout == Layout::kCausal;
-    const int P = kv.layout == Layout::kContiguous ? 0 : kv.page_tokens;
-    Shape s = shape_for(a.seq_q, a.seq_k, a.heads, a.kv_heads, aligned, P, a.partials != nullptr);
-
-    Reader rd{};
-    rd.src = kv;
-    rd.row = static_cast<std::size_t>(a.kv_heads) * a.head_dim;
-    rd.kv_heads = a.kv_heads;
-    rd.head_dim = a.head_dim;
-    rd.own = 0;
+    GeneralArgs g{};
+    g.src = kv;
     for (int t = kINT8; t <= kINT2; ++t)
     {
       if (kv.layout == Layout::kCausal && kv.may_be_at[t])
       {
-        rd.lay[t] = page_layout(t, kv.page_tokens, a.kv_heads, a.head_dim);
+        g.lay[t] = page_layout(t, kv.page_tokens, a.kv_heads, a.head_dim);
       }
     }
-    // A mass over a contiguous layout has no pages: it is over pages of the
-    // kernel's tile size.
-    if (kv.layout == Layout::kContiguous)
+    g.q = a.q;
+    g.out = a.out;
+    g.k_bias = a.k_bias;
+    g.rope = a.k_bias != nullptr ? a.rope : nullptr;
+    g.seq_q = a.seq_q;
+    g.seq_k = a.seq_k;
+    g.heads = a.heads;
+    g.kv_heads = a.kv_heads;
+    g.hd = a.head_dim;
+    g.mass_page = mass_page_of(kv);
+    g.tile = tile_for(g.mass_page);
+    if (g.tile > kMaxTile)
     {
-      rd.src.page_tokens = kTileK;
+      throw InvalidArgument("pages of " + std::to_string(g.mass_page) +
+                            " tokens are more than the general attention path takes (" +
+                            std::to_string(kMaxTile) + ")");
     }
-
-    float *mass = a.mass;
-    AttentionArgs args = a;
-    float *page_max = nullptr;
-    const int mass_pages = (a.seq_k + rd.src.page_tokens - 1) / rd.src.page_tokens;
-    const std::size_t mass_floats = static_cast<std::size_t>(a.heads) * mass_pages;
-    float *own_mass = nullptr;
-    if (a.scores != nullptr && mass == nullptr)
+    const Split split = split_for(a.seq_q, a.seq_k, a.heads, g.tile, a.partials != nullptr);
+    g.splits = split.splits;
+    g.split_keys = split.split_keys;
+    g.partials = a.partials;
+    const bool with_mass = a.mass != nullptr || a.scores != nullptr;
+    const int pages = (a.seq_k + g.mass_page - 1) / g.mass_page;
+    if (with_mass)
     {
-      // Scores need the mass: kept in scratch after the page maxima.
-      float *scratch = page_max_buffer(2 * mass_floats);
-      own_mass = scratch + mass_floats;
-      mass = own_mass;
+      // The page statistics, and the mass itself when the caller wants only
+      // the scores, in scratch.
+      const std::size_t stats = static_cast<std::size_t>(a.heads) * pages * 2;
+      const std::size_t own_mass = a.mass == nullptr ? static_cast<std::size_t>(a.heads) * pages : 0;
+      float *scratch = a.workspace != nullptr ? a.workspace->floats(stats + own_mass)
+                                              : stream_workspace(stream, stats + own_mass);
+      g.page_stats = scratch;
+      g.mass = a.mass != nullptr ? a.mass : scratch + stats;
     }
-    args.mass = mass;
-    if (mass != nullptr)
-    {
-      page_max = page_max_buffer(own_mass ? 2 * mass_floats : mass_floats);
-    }
-
-    const int rows = s.hpb * s.qpb;
-    const std::size_t lds = shared_floats(a.head_dim, rows) * sizeof(float);
-    const dim3 grid(ceil_div(s.lead + a.seq_q, s.qpb), a.heads / s.hpb, s.splits);
-    const auto run = [&](auto kernel) {
-      if (lds > 64 * 1024)
-      {
-        hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      static_cast<int>(lds)),
-                  "hipFuncSetAttribute attention LDS");
-      }
-      hipLaunchKernelGGL(kernel, grid, dim3(kThreads), lds, stream, rd, args, s, page_max);
-    };
-    if (mass != nullptr)
-    {
-      run(attention_kernel<true>);
-    }
-    else
-    {
-      run(attention_kernel<false>);
-    }
+    const std::size_t lds = (static_cast<std::size_t>(a.head_dim) + g.tile + kThreads / 64) *
+                            sizeof(float);
+    hipLaunchKernelGGL(general_attention_kernel, dim3(a.seq_q * a.heads, g.splits), dim3(kThreads),
+                       lds, stream, g);
     hip_check(hipGetLastError(), "attention kernel launch");
-    if (s.splits > 1)
+    if (g.splits > 1)
     {
-      hipLaunchKernelGGL(combine_kernel, dim3(a.seq_q * a.heads), dim3(kCombineThreads),
-                         s.splits * sizeof(float), stream, a.partials, a.out, a.seq_q,
-                         a.heads, a.head_dim, s.splits, s.split_keys, mass, rd.src.page_tokens,
-                         a.seq_k);
+      hipLaunchKernelGGL(general_combine_kernel, dim3(a.seq_q * a.heads), dim3(kThreads), 0,
+                         stream, g);
       hip_check(hipGetLastError(), "attention combine kernel launch");
     }
     if (a.scores != nullptr)
     {
-      launch_fold(a.scores, mass, a.heads, mass_pages, a.alpha, stream);
+      launch_fold(a.scores, g.mass, a.heads, pages, a.alpha, stream);
     }
   }
 

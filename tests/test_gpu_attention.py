@@ -171,3 +171,53 @@ def test_rope_table_is_fp64_cos_sin_rounded():
     for got, want in ((table[..., 0], np.cos(ang)), (table[..., 1], np.sin(ang))):
         ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
         assert np.all(np.abs(got - want) <= ulp)
+
+
+def test_the_general_path_takes_what_the_fast_kernels_do_not():
+    """Head dims 96 and 80 (neither fast kernel's), contiguous, one query
+    and a chunk, with the key bias; a long decode split into runs and not;
+    and a cache of 48-token FP16 pages decoding with per-page mass: all
+    against the float64 oracle."""
+    from conftest import assert_mass_close
+    from test_gpu_kv_pages import page_sizes, put
+    m = mi()
+    d = m.device
+    rng = np.random.default_rng(31)
+    for hd in (96, 80):
+        heads, kv = 8, 2
+        for seq_q, seq_k in ((1, 700), (9, 300)):
+            announce("general", hd, seq_q, seq_k)
+            q, k, v = qkv(seq_q, seq_k, heads, kv, hd, seed=hd + seq_k)
+            bias = fp16_exact(2 * rng.standard_normal((kv, hd)))
+            got = m.attention(q, k, v, k_bias=bias, theta=1e4)
+            want, w = att.attention64(q, k, v, k_bias=bias, theta=1e4)
+            assert_attention_close(got, want, f"general hd {hd} {seq_q}x{seq_k}",
+                                   att.attention_bound(q, k, v, w, k_bias=bias, theta=1e4))
+        seq_k = 5000
+        q, k, v = qkv(1, seq_k, heads, kv, hd, seed=hd)
+        want, w = att.attention64(q, k, v)
+        for partials in (d.empty_f32(d.attention_partials(hd)), None):
+            announce("general split", hd, partials is not None)
+            out = d.empty(q.size)
+            d.attention(m.upload_fp16(q), m.upload_fp16(k), m.upload_fp16(v), None, None, out, 1,
+                        seq_k, heads, kv, hd, partials)
+            assert_attention_close(out.to_numpy().reshape(q.shape), want, f"split hd {hd}",
+                                   att.attention_bound(q, k, v, w))
+    P, heads, kv, hd = 48, 12, 2, 128
+    seq = P * 20 + 7
+    pages = -(-seq // P)
+    alloc = m.PagedKVCache(page_sizes(P, kv, hd), [64] * 4)
+    cache = d.KVPages(alloc, 1, P, kv, hd, 0, d.Halves.Both, [], False)
+    q, k, v = qkv(1, seq, heads, kv, hd, seed=48)
+    cache.reserve(seq)
+    cache.store(0, put(k), put(v), 0, seq)
+    want, w = att.attention64(q, k, v)
+    for partials in (d.empty_f32(d.attention_partials(hd)), None):
+        announce("48-token pages", partials is not None)
+        out, mass = d.empty(heads * hd), d.empty_f32(heads * pages)
+        cache.attention(0, put(q), None, None, out, 1, seq, heads, kv, hd, None, None, mass,
+                        partials)
+        assert_attention_close(out.to_numpy().reshape(1, heads, hd), want, "48-token pages",
+                               att.attention_bound(q, k, v, w))
+        assert_mass_close(mass.to_numpy().reshape(heads, pages), att.page_mass(w[:, -1, :], P),
+                          "48-token page mass")
