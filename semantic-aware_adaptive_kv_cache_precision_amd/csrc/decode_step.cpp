@@ -137,12 +137,20 @@ namespace mi
     float *kept = scores_ != nullptr ? kept_->as<float>() : nullptr;
     int launches = 0;
 
+    // RMSNorm rides in the projection that reads its output (each workgroup
+    // forms the normed row from the fp32 residual, to the RMSNorm kernel's
+    // bits), and RoPE in the store: seven launches a layer.
+    const auto normed_input = [&](ProjectArgs &p, const std::uint16_t *norm) {
+      p.residual = residual;
+      p.norm_weight = norm;
+      p.eps = s.rms_eps;
+      p.x = normed; // unused with a norm
+    };
     launch_embed(state + kStepToken, 1, weights_.embed, residual, true, s.hidden, s.vocab, stream);
     ++launches;
     for (int l = 0; l < s.layers; ++l)
     {
       const LayerWeights &w = weights_.layers[l];
-      launch_rmsnorm(residual, true, w.input_norm, normed, 1, s.hidden, s.rms_eps, stream);
       ProjectArgs qkv{};
       qkv.segments = 3;
       qkv.seg[0] = {w.q_w, w.q_b, qk_raw, q_width};
@@ -150,13 +158,11 @@ namespace mi
       qkv.seg[1] = {w.k_w, key_bias_ ? nullptr : w.k_b, qk_raw + q_width, kv_width};
       qkv.seg[2] = {w.v_w, w.v_b, v, kv_width};
       qkv.in = s.hidden;
-      qkv.x = normed;
       qkv.mode = ProjectMode::kHalf;
+      normed_input(qkv, w.input_norm);
       launch_project(qkv, stream);
-      // q's heads and k's heads are rows of one buffer: one RoPE launch.
-      launch_rope(qk_raw, state + kStepPosition, qk, 1, s.heads + s.kv_heads, s.head_dim,
-                  s.rope_theta, stream);
-      cache_.store_step(l, qk + q_width, v, state + kStepPosition);
+      // q's heads and k's heads are rows of one buffer, rotated with the store.
+      cache_.rope_store_step(l, qk_raw, qk, s.heads, v, state + kStepPosition, rope_);
       cache_.attention_step(l, qk, key_bias_ ? w.k_b : nullptr, &rope_, attended,
                             state + kStepSeqK, max_seq_k, s.heads, s.kv_heads, s.head_dim,
                             qk + q_width, v, kept);
@@ -167,14 +173,13 @@ namespace mi
       o.x = attended;
       o.mode = ProjectMode::kAccumulate;
       launch_project(o, stream);
-      launch_rmsnorm(residual, true, w.post_norm, normed, 1, s.hidden, s.rms_eps, stream);
       ProjectArgs mlp{};
       mlp.segments = 2;
       mlp.seg[0] = {w.gate_w, nullptr, activated, s.intermediate};
       mlp.seg[1] = {w.up_w, nullptr, nullptr, s.intermediate};
       mlp.in = s.hidden;
-      mlp.x = normed;
       mlp.mode = ProjectMode::kSwiglu;
+      normed_input(mlp, w.post_norm);
       launch_project(mlp, stream);
       ProjectArgs down{};
       down.segments = 1;
@@ -183,19 +188,18 @@ namespace mi
       down.x = activated;
       down.mode = ProjectMode::kAccumulate;
       launch_project(down, stream);
-      launches += 10; // norm, qkv, rope, store, decode + combine, o, norm, gate/up, down
+      launches += 7; // norm + qkv, RoPE + store, decode + combine, o, norm + gate/up, down
     }
-    launch_rmsnorm(residual, true, weights_.final_norm, normed, 1, s.hidden, s.rms_eps, stream);
     ProjectArgs head{};
     head.segments = 1;
     head.seg[0] = {weights_.head, nullptr, logits_->as<float>(), s.vocab};
     head.in = s.hidden;
-    head.x = normed;
     head.mode = ProjectMode::kLogits;
+    normed_input(head, weights_.final_norm);
     head.best_value = best_value_->as<float>();
     head.best_index = best_index_->as<int>();
     launch_project(head, stream);
-    launches += 2;
+    ++launches;
     if (scores_ != nullptr)
     {
       cache_.fold_step(kept, state + kStepSeqK, max_seq_k, s.heads, s.kv_heads, s.head_dim,

@@ -351,6 +351,11 @@ namespace mi
     ProjectMode mode;
     float *best_value; // kLogits: [project_blocks]
     int *best_index;
+    // With norm_weight: x is RMSNorm of the fp32 `residual` row (in values),
+    // formed in the launch as the RMSNorm kernel forms it, to the bit.
+    const float *residual;
+    const std::uint16_t *norm_weight;
+    float eps;
   };
   int project_blocks(const ProjectArgs &p);
   void launch_project(const ProjectArgs &p, hipStream_t stream);
@@ -383,5 +388,18 @@ namespace mi
     PageLayout lay[kTierCount];
   };
   void launch_step_store(const StepStore &s, int head_dim, hipStream_t stream);
+  // The same store with the step's RoPE first, in one launch: q's `heads`
+  // and k's heads of qk_raw rotated at *position from the {cos, sin} table
+  // (as the RoPE kernel rotates them, to the bit) into qk, then k's rotated
+  // row and the values stored. One workgroup: kv_heads * head_dim <= 1024.
+  struct StepRopeStore
+  {
+    StepStore store; // store.keys is ignored: the rotated k is qk + heads * head_dim
+    const std::uint16_t *qk_raw;
+    std::uint16_t *qk;
+    const float *rope;
+    int heads;
+  };
+  void launch_step_rope_store(const StepRopeStore &s, int head_dim, hipStream_t stream);
 
 } // namespace mi

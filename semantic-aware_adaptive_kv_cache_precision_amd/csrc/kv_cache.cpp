@@ -1094,6 +1094,38 @@ namespace mi
     attend_open_[layer] = current_open_[layer];
   }
 
+  void KVPages::rope_store_step(int layer, const void *qk_raw, void *qk, int heads,
+                                const void *values, const int *position, const RopeTable &rope)
+  {
+    require_layer(layer);
+    if (!seals_ || !open_pages_)
+    {
+      throw LogicError("a store with its position on the device needs a sealing cache with "
+                       "positions reserved");
+    }
+    if (rope.head_dim() != head_dim_)
+    {
+      throw InvalidArgument("the RoPE table is for head_dim " + std::to_string(rope.head_dim()) +
+                            "; this cache holds " + std::to_string(head_dim_));
+    }
+    const hipStream_t stream = runtime_stream();
+    sync_tables(stream);
+    StepRopeStore st{};
+    st.store.values = static_cast<const std::uint16_t *>(values);
+    st.store.position = position;
+    st.store.open = open_page(layer, current_open_[layer]);
+    const std::size_t row = static_cast<std::size_t>(layer) * table_.stride();
+    st.store.addresses = table_.addresses() + row;
+    st.store.tiers = table_.tiers() + row;
+    st.store.kv_heads = kv_heads_;
+    st.qk_raw = static_cast<const std::uint16_t *>(qk_raw);
+    st.qk = static_cast<std::uint16_t *>(qk);
+    st.rope = rope.data();
+    st.heads = heads;
+    launch_step_rope_store(st, head_dim_, stream);
+    attend_open_[layer] = current_open_[layer];
+  }
+
   void KVPages::attention_step(int layer, const void *q, const void *k_bias, const RopeTable *rope,
                                void *out, const int *live_seq_k, int max_seq_k, int heads,
                                int kv_heads, int head_dim, const void *keys, const void *values,

@@ -522,6 +522,65 @@ namespace mi
       run_row_task<HD>(j, s.lay, task, s.kv_heads);
     }
 
+    // The step's RoPE and its store in one workgroup: every (head, angle)
+    // pair of q and k rotated into qk (the RoPE kernel's arithmetic, the
+    // angle's cos and sin from the table), then, once the workgroup has
+    // them, the store or seal of the rotated k row and the values.
+    template <int HD>
+    __global__ void __launch_bounds__(1024) step_rope_store_kernel(StepRopeStore s)
+    {
+      constexpr int kHalf = HD / 2;
+      const int position = *s.store.position;
+      const int pairs = (s.heads + s.store.kv_heads) * kHalf;
+      const float *cs = s.rope + static_cast<std::size_t>(position) * kHalf * 2;
+      for (int i = threadIdx.x; i < pairs; i += blockDim.x)
+      {
+        const int head = i / kHalf;
+        const int j = i % kHalf;
+        const std::size_t at = static_cast<std::size_t>(head) * HD + j;
+        const float c = cs[2 * j];
+        const float sn = cs[2 * j + 1];
+        const float x1 = f16_bits(s.qk_raw[at]);
+        const float x2 = f16_bits(s.qk_raw[at + kHalf]);
+        s.qk[at] = static_cast<std::uint16_t>(half_of(x1 * c - x2 * sn));
+        s.qk[at + kHalf] = static_cast<std::uint16_t>(half_of(x2 * c + x1 * sn));
+      }
+      __syncthreads();
+      const int task = threadIdx.x;
+      const int W = s.store.kv_heads * HD;
+      if (task >= W)
+      {
+        return;
+      }
+      const std::uint16_t *keys = s.qk + static_cast<std::size_t>(s.heads) * HD;
+      const int row = position % kP;
+      const int page = position / kP;
+      RowJob j{};
+      if (row < kP - 1)
+      {
+        j.kind = static_cast<int>(RowJobKind::kFill);
+        j.k_lo = j.k_hi = keys;
+        j.v_lo = j.v_hi = s.store.values;
+        j.rows = 1;
+        j.dst_row = row;
+        j.dst = reinterpret_cast<std::uint8_t *>(s.store.open);
+        j.tier = kFP16;
+      }
+      else
+      {
+        const int tier = s.store.tiers[page];
+        j.kind = static_cast<int>(tier == kFP16 ? RowJobKind::kCopy : RowJobKind::kQuantise);
+        j.k_lo = s.store.open;
+        j.v_lo = s.store.open + static_cast<std::size_t>(kP) * W;
+        j.k_hi = keys;
+        j.v_hi = s.store.values;
+        j.split = kP - 1;
+        j.dst = reinterpret_cast<std::uint8_t *>(s.store.addresses[page]);
+        j.tier = tier;
+      }
+      run_row_task<HD>(j, s.store.lay, task, s.store.kv_heads);
+    }
+
     // Any other shape: a workgroup a job, the rows staged in LDS.
     __global__ void __launch_bounds__(kThreads)
         row_jobs_lds_kernel(RowJobs jobs, int page_tokens, int kv_heads, int head_dim)
@@ -780,6 +839,32 @@ namespace mi
       hipLaunchKernelGGL(step_store_kernel<64>, dim3(blocks), dim3(kThreads), 0, stream, args);
     }
     hip_check(hipGetLastError(), "step store kernel launch");
+  }
+
+  void launch_step_rope_store(const StepRopeStore &s, int head_dim, hipStream_t stream)
+  {
+    const int W = s.store.kv_heads * head_dim;
+    if (!register_shape(kP, s.store.kv_heads, head_dim) || W > 1024 || s.rope == nullptr ||
+        s.heads <= 0)
+    {
+      throw InvalidArgument("the step's RoPE and store in one launch take head_dim 64 or 128, "
+                            "128 to 1024 channels a row and a RoPE table");
+    }
+    StepRopeStore args = s;
+    for (int t = kINT8; t <= kINT2; ++t)
+    {
+      args.store.lay[t] = page_layout(t, kP, s.store.kv_heads, head_dim);
+    }
+    const int threads = (W + 63) / 64 * 64;
+    if (head_dim == 128)
+    {
+      hipLaunchKernelGGL(step_rope_store_kernel<128>, dim3(1), dim3(threads), 0, stream, args);
+    }
+    else
+    {
+      hipLaunchKernelGGL(step_rope_store_kernel<64>, dim3(1), dim3(threads), 0, stream, args);
+    }
+    hip_check(hipGetLastError(), "step RoPE + store kernel launch");
   }
 
   void launch_table_edits(const TableEdit *edits, int count, unsigned long long *addresses,

@@ -464,6 +464,11 @@ namespace mi
     // the positions before `end` were stored.
     void prepare_step(int max_seq_k, int heads, int head_dim);
     void store_step(int layer, const void *keys, const void *values, const int *position);
+    // store_step with the step's RoPE first, in one launch: q's `heads` and
+    // k's heads of qk_raw ([q | k], fp16) rotated at *position from `rope`
+    // into qk, as the RoPE kernel rotates them, then k's rotated row stored.
+    void rope_store_step(int layer, const void *qk_raw, void *qk, int heads, const void *values,
+                         const int *position, const RopeTable &rope);
     void attention_step(int layer, const void *q, const void *k_bias, const RopeTable *rope,
                         void *out, const int *live_seq_k, int max_seq_k, int heads,
                         int kv_heads, int head_dim, const void *keys, const void *values,

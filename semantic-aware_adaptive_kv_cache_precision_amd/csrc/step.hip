@@ -13,19 +13,24 @@
 //
 // Work layout (MI355X-first): a decode step's projections are one row of
 // activations against a weight matrix, so they are bound by the weight bytes
-// streamed from HBM, not by arithmetic. A wave owns a weight row: the row's
-// 16-byte runs go to the lanes in turn (one coalesced 1 KiB load a
-// wave-instruction, several loads in flight before any is used), the
-// products are v_dot2 of fp16 pairs into fp32 (each product exact), and a
-// wave reduction leaves the row's dot in every lane. Eight rows a workgroup,
-// so that even the 1536-row projections launch 192 workgroups and the
-// vocabulary's ~19K. The projections a step makes from one input run in one
-// launch: q, k and v (three weight matrices, one grid over their rows), gate
-// and up (a wave both rows of one output, the SwiGLU in the epilogue).
+// streamed from HBM, not by arithmetic. A wave owns a weight row at a time:
+// the row's 16-byte runs go to the lanes in turn (one coalesced 1 KiB load a
+// wave-instruction), a batch of runs in flight while the one before it is
+// used, the products v_dot2 of fp16 pairs into fp32 (each product exact),
+// and a wave reduction leaves the row's dot in every lane. The input row is
+// staged once a workgroup in LDS -- or, where an RMSNorm feeds the
+// projection, formed there from the fp32 residual to the RMSNorm kernel's
+// bits -- after each wave's first weight loads are already on their way.
+// Eight rows a workgroup at a time; past 2048 workgroups (the head's
+// vocabulary) each wave takes several rows. The projections a step makes
+// from one input run in one launch: q, k and v (three weight matrices, one
+// grid over their rows), gate and up (a wave both rows of one output, the
+// SwiGLU in the epilogue).
 
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
 #include <cfloat>
 #include <climits>
 
@@ -35,12 +40,14 @@ namespace mi
   {
     constexpr int kWaves = 8;
     constexpr int kThreads = 64 * kWaves;
-    constexpr int kAhead = 4; // 16-byte runs a lane has in flight
     constexpr int kAdvanceThreads = 1024;
+    constexpr long long kMaxBlocks = 2048;
 
     typedef _Float16 half2v __attribute__((ext_vector_type(2)));
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
     typedef const __attribute__((address_space(1))) u32x4 *g_u32x4;
+
+    __device__ inline std::uint16_t to_half(float v) { return __half_as_ushort(__float2half(v)); }
 
     __device__ inline float dot_run(const u32x4 &w, const u32x4 &x, float acc)
     {
@@ -64,36 +71,60 @@ namespace mi
       return v;
     }
 
-    // The dot of a weight row with x (both `in` fp16 values, in a multiple
-    // of 8, 16-byte aligned), in every lane of the wave.
-    __device__ inline float row_dot(const std::uint16_t *w, const std::uint16_t *x, int in, int lane)
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef const __attribute__((address_space(1))) f32x4 *g_f32x4;
+
+    // RMSNorm's scale of the residual row, summed as the RMSNorm kernel sums
+    // it (256 lanes, each over its stride, a wave reduction, the four waves
+    // in order), so that the normed row is that kernel's to the bit.
+    __device__ inline float norm_scale(const float *x, int hidden, float eps, float *partial)
     {
-      const int runs = in / 8;
       float acc = 0.0f;
-      for (int r0 = lane; r0 < runs; r0 += 64 * kAhead)
+      if (threadIdx.x < 256)
       {
-        u32x4 wv[kAhead], xv[kAhead];
-#pragma unroll
-        for (int i = 0; i < kAhead; ++i)
+        for (int i = threadIdx.x; i < hidden; i += 256)
         {
-          const int r = r0 + 64 * i;
-          const int at = r < runs ? r : r0; // a lane past the row re-reads its first run, unused
-          wv[i] = *((g_u32x4)(w + 8 * static_cast<std::size_t>(at)));
-          xv[i] = *((g_u32x4)(x + 8 * static_cast<std::size_t>(at)));
-        }
-#pragma unroll
-        for (int i = 0; i < kAhead; ++i)
-        {
-          if (r0 + 64 * i < runs)
-          {
-            acc = dot_run(wv[i], xv[i], acc);
-          }
+          const float v = x[i];
+          acc += v * v;
         }
       }
-      return wave_total(acc);
+      for (int offset = 32; offset > 0; offset >>= 1)
+      {
+        acc += __shfl_xor(acc, offset);
+      }
+      if (threadIdx.x < 256 && threadIdx.x % 64 == 0)
+      {
+        partial[threadIdx.x / 64] = acc;
+      }
+      __syncthreads();
+      float total = 0.0f;
+      for (int w = 0; w < 4; ++w)
+      {
+        total += partial[w];
+      }
+      return rsqrtf(total / static_cast<float>(hidden) + eps);
     }
 
-    __device__ inline std::uint16_t to_half(float v) { return __half_as_ushort(__float2half(v)); }
+    // Run r (eight values) of RMSNorm of the residual: x * scale * w, one
+    // rounding to fp16, as the RMSNorm kernel stores it.
+    __device__ inline u32x4 normed_run(const float *residual, const std::uint16_t *weight,
+                                       float scale, int r)
+    {
+      const f32x4 a = *((g_f32x4)(residual + 8 * static_cast<std::size_t>(r)));
+      const f32x4 b = *((g_f32x4)(residual + 8 * static_cast<std::size_t>(r) + 4));
+      const u32x4 wv = *((g_u32x4)(weight + 8 * static_cast<std::size_t>(r)));
+      const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      u32x4 out;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+      {
+        const unsigned wi = wv[i];
+        const unsigned lo = to_half(v[2 * i] * scale * h2f(static_cast<std::uint16_t>(wi)));
+        const unsigned hi = to_half(v[2 * i + 1] * scale * h2f(static_cast<std::uint16_t>(wi >> 16)));
+        out[i] = lo | (hi << 16);
+      }
+      return out;
+    }
 
     // The better of two (value, index) candidates, as argmax.cu chooses: the
     // larger value, the lower index on equal values; NaN never wins.
@@ -106,69 +137,179 @@ namespace mi
       }
     }
 
-    // Rows of every segment in turn; a wave a row (two rows, gate and up,
-    // for SwiGLU).
+    // A wave's Ahead runs of one or two weight rows (run lane + 64 i of the
+    // batch at r0), clamped into the row; a lane past the row re-reads a run
+    // it does not use.
+    template <int Ahead, bool Two>
+    __device__ inline void load_batch(u32x4 (&a)[Ahead], u32x4 (&b)[Ahead],
+                                      const std::uint16_t *w0, const std::uint16_t *w1, int r0,
+                                      int runs)
+    {
+#pragma unroll
+      for (int i = 0; i < Ahead; ++i)
+      {
+        const int r = r0 + 64 * i;
+        const std::size_t at = 8 * static_cast<std::size_t>(r < runs ? r : 0);
+        a[i] = *((g_u32x4)(w0 + at));
+        if constexpr (Two)
+        {
+          b[i] = *((g_u32x4)(w1 + at));
+        }
+      }
+    }
+
+    // The dots of one weight row (two, gate and up, with Two) with the input
+    // staged in LDS; the row's first batch was loaded before the input was.
+    // Each batch's successor is in flight while it is used.
+    template <int Ahead, bool Two>
+    __device__ inline void row_dots(float &d0, float &d1, const std::uint16_t *w0,
+                                    const std::uint16_t *w1, const u32x4 *x, int runs, int lane,
+                                    u32x4 (&a)[Ahead], u32x4 (&b)[Ahead])
+    {
+      float acc0 = 0.0f, acc1 = 0.0f;
+      for (int r0 = lane; r0 < runs; r0 += 64 * Ahead)
+      {
+        u32x4 na[Ahead], nb[Ahead];
+        const int next = r0 + 64 * Ahead;
+        if (next < runs)
+        {
+          load_batch<Ahead, Two>(na, nb, w0, w1, next, runs);
+        }
+#pragma unroll
+        for (int i = 0; i < Ahead; ++i)
+        {
+          const int r = r0 + 64 * i;
+          if (r < runs)
+          {
+            const u32x4 xv = x[r];
+            acc0 = dot_run(a[i], xv, acc0);
+            if constexpr (Two)
+            {
+              acc1 = dot_run(b[i], xv, acc1);
+            }
+          }
+        }
+        if (next < runs)
+        {
+#pragma unroll
+          for (int i = 0; i < Ahead; ++i)
+          {
+            a[i] = na[i];
+            if constexpr (Two)
+            {
+              b[i] = nb[i];
+            }
+          }
+        }
+      }
+      d0 = wave_total(acc0);
+      d1 = Two ? wave_total(acc1) : 0.0f;
+    }
+
+    // A wave a row at a time over its rows (row = block's wave + k * the
+    // grid's waves), every segment's rows in turn, or gate's and up's rows
+    // together for SwiGLU. The input -- x, or RMSNorm of the residual -- is
+    // staged once a workgroup in LDS, after each wave's first weight loads
+    // are on their way.
+    template <int Ahead, bool Two>
     __global__ void __launch_bounds__(kThreads) project_kernel(ProjectArgs p)
     {
+      extern __shared__ u32x4 x_lds[];
       __shared__ float s_best[kWaves];
       __shared__ int s_at[kWaves];
+      __shared__ float s_partial[4];
       const int lane = threadIdx.x & 63;
       const int wave = threadIdx.x >> 6;
-      int row = blockIdx.x * kWaves + wave;
-      int seg = 0;
-      // SwiGLU's grid covers gate's rows only (up's ride with them).
-      const int walked = p.mode == ProjectMode::kSwiglu ? 1 : p.segments;
-      while (seg + 1 < walked && row >= p.seg[seg].rows)
+      const int runs = p.in / 8;
+      int total = 0;
+      for (int i = 0; i < (Two ? 1 : p.segments); ++i)
       {
-        row -= p.seg[seg].rows;
-        ++seg;
+        total += p.seg[i].rows;
       }
-      const bool live = row < p.seg[seg].rows;
-      const ProjectSegment &s = p.seg[seg];
+      const int stride = gridDim.x * kWaves;
+      // The wave's first row and its first batch, before the input.
+      const auto locate = [&](int row, int &seg) {
+        seg = 0;
+        while (!Two && seg + 1 < p.segments && row >= p.seg[seg].rows)
+        {
+          row -= p.seg[seg].rows;
+          ++seg;
+        }
+        return row;
+      };
+      int g = blockIdx.x * kWaves + wave;
+      u32x4 a[Ahead], b[Ahead];
+      if (g < total)
+      {
+        int seg;
+        const int row = locate(g, seg);
+        load_batch<Ahead, Two>(a, b, p.seg[seg].w + static_cast<std::size_t>(row) * p.in,
+                               Two ? p.seg[1].w + static_cast<std::size_t>(row) * p.in : nullptr,
+                               lane, runs);
+      }
+      if (p.norm_weight != nullptr)
+      {
+        const float scale = norm_scale(p.residual, p.in, p.eps, s_partial);
+        for (int r = threadIdx.x; r < runs; r += kThreads)
+        {
+          x_lds[r] = normed_run(p.residual, p.norm_weight, scale, r);
+        }
+      }
+      else
+      {
+        for (int r = threadIdx.x; r < runs; r += kThreads)
+        {
+          x_lds[r] = *((g_u32x4)(p.x + 8 * static_cast<std::size_t>(r)));
+        }
+      }
+      __syncthreads();
       float best = -FLT_MAX;
       int at = INT_MAX;
-      if (live)
+      for (bool first = true; g < total; g += stride, first = false)
       {
-        const std::uint16_t *w = s.w + static_cast<std::size_t>(row) * p.in;
-        const float acc = row_dot(w, p.x, p.in, lane);
+        int seg;
+        const int row = locate(g, seg);
+        const ProjectSegment &s = p.seg[seg];
+        const std::uint16_t *w0 = s.w + static_cast<std::size_t>(row) * p.in;
+        const std::uint16_t *w1 = Two ? p.seg[1].w + static_cast<std::size_t>(row) * p.in : nullptr;
+        if (!first)
+        {
+          load_batch<Ahead, Two>(a, b, w0, w1, lane, runs);
+        }
+        float acc, up;
+        row_dots<Ahead, Two>(acc, up, w0, w1, x_lds, runs, lane, a, b);
+        if (lane != 0)
+        {
+          keep_better(best, at, acc, row);
+          continue;
+        }
         switch (p.mode)
         {
         case ProjectMode::kHalf:
-          if (lane == 0)
-          {
-            const float b = s.bias != nullptr ? h2f(s.bias[row]) : 0.0f;
-            static_cast<std::uint16_t *>(s.out)[row] = to_half(acc + b);
-          }
+        {
+          const float bias = s.bias != nullptr ? h2f(s.bias[row]) : 0.0f;
+          static_cast<std::uint16_t *>(s.out)[row] = to_half(acc + bias);
           break;
+        }
         case ProjectMode::kAccumulate:
-          if (lane == 0)
-          {
-            float *out = static_cast<float *>(s.out) + row;
-            *out = *out + acc;
-          }
+        {
+          float *out = static_cast<float *>(s.out) + row;
+          *out = *out + acc;
           break;
+        }
         case ProjectMode::kSwiglu:
         {
-          // seg[1] is up, with gate's rows: the same row of it.
-          const std::uint16_t *wu = p.seg[1].w + static_cast<std::size_t>(row) * p.in;
-          const float up = row_dot(wu, p.x, p.in, lane);
-          if (lane == 0)
-          {
-            const float g = h2f(to_half(acc));
-            const float u = h2f(to_half(up));
-            const float silu = g / (1.0f + expf(-g));
-            static_cast<std::uint16_t *>(s.out)[row] = to_half(silu * u);
-          }
+          const float gv = h2f(to_half(acc));
+          const float uv = h2f(to_half(up));
+          const float silu = gv / (1.0f + expf(-gv));
+          static_cast<std::uint16_t *>(s.out)[row] = to_half(silu * uv);
           break;
         }
         case ProjectMode::kLogits:
-          if (lane == 0)
-          {
-            static_cast<float *>(s.out)[row] = acc;
-          }
-          keep_better(best, at, acc, row);
+          static_cast<float *>(s.out)[row] = acc;
           break;
         }
+        keep_better(best, at, acc, row);
       }
       if (p.mode == ProjectMode::kLogits)
       {
@@ -270,13 +411,19 @@ namespace mi
     {
       rows = p.seg[0].rows; // up's rows ride with gate's
     }
-    return static_cast<int>((rows + kWaves - 1) / kWaves);
+    // A wave a row, up to kMaxBlocks workgroups; past that the waves take
+    // several rows each (the head's vocabulary), so that the staging of the
+    // input is paid once for many rows.
+    return static_cast<int>(std::min<long long>((rows + kWaves - 1) / kWaves, kMaxBlocks));
   }
 
   void launch_project(const ProjectArgs &p, hipStream_t stream)
   {
+    const bool normed = p.norm_weight != nullptr;
     if (p.segments < 1 || p.segments > kProjectSegments || p.in <= 0 || p.in % 8 != 0 ||
-        reinterpret_cast<std::uintptr_t>(p.x) % 16 != 0)
+        reinterpret_cast<std::uintptr_t>(normed ? static_cast<const void *>(p.residual)
+                                                : static_cast<const void *>(p.x)) % 16 != 0 ||
+        (normed && reinterpret_cast<std::uintptr_t>(p.norm_weight) % 16 != 0))
     {
       throw InvalidArgument("a projection takes 1 to 3 weight matrices and an input of a multiple "
                             "of 8 fp16 values, 16-byte aligned; got " +
@@ -300,7 +447,34 @@ namespace mi
     {
       throw InvalidArgument("the head's projection keeps each block's best logit");
     }
-    hipLaunchKernelGGL(project_kernel, dim3(blocks), dim3(kThreads), 0, stream, p);
+    // The input in LDS: in fp16 values. Long rows (the down projection's)
+    // keep more of a row in flight.
+    const std::size_t lds = static_cast<std::size_t>(p.in) * 2;
+    if (lds > 64 * 1024)
+    {
+      throw InvalidArgument("a projection's input is at most 32768 values; got " +
+                            std::to_string(p.in));
+    }
+    const bool two = p.mode == ProjectMode::kSwiglu;
+    if (p.in > 4096)
+    {
+      if (two)
+      {
+        hipLaunchKernelGGL((project_kernel<8, true>), dim3(blocks), dim3(kThreads), lds, stream, p);
+      }
+      else
+      {
+        hipLaunchKernelGGL((project_kernel<8, false>), dim3(blocks), dim3(kThreads), lds, stream, p);
+      }
+    }
+    else if (two)
+    {
+      hipLaunchKernelGGL((project_kernel<4, true>), dim3(blocks), dim3(kThreads), lds, stream, p);
+    }
+    else
+    {
+      hipLaunchKernelGGL((project_kernel<4, false>), dim3(blocks), dim3(kThreads), lds, stream, p);
+    }
     hip_check(hipGetLastError(), "projection kernel launch");
   }
 

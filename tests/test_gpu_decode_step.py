@@ -258,7 +258,7 @@ def check_step_against_oracle(s, biases, start, seed):
     if want[order[0]] - want[order[1]] > 2 * LOGIT_TOL * scale:
         assert tokens[0] == order[0], (tokens[0], order[:3])
     assert tokens[0] == dense.argmax_rows(got[None].astype(np.float32))[0]
-    assert ms > 0 and step.launches == 1 + 10 * s["layers"] + 2 + 1
+    assert ms > 0 and step.launches == 1 + 7 * s["layers"] + 1 + 1
 
 
 def test_one_step_is_the_oracles_composition_qwen_shape():
