@@ -464,6 +464,11 @@ int mi_kv_birth_tier(mi_kv_pages *kv, int layer, int page, int *tier);
 int mi_kv_last_move(mi_kv_pages *kv, int *has, int *ints4, size_t *bytes2, double *seconds2);
 int mi_kv_last_batch(mi_kv_pages *kv, int *has, size_t *moves, size_t *shadows_taken,
                      double *seconds);
+/* Where the last batch's seconds went (no counterpart in the reference):
+ * phases[0] the host's work before the first launch, [1] the new pages'
+ * allocation, [2] the page table's switch, the old pages' release and the
+ * wait for the device. */
+int mi_kv_last_batch_phases(mi_kv_pages *kv, double *phases);
 
 #ifdef __cplusplus
 }

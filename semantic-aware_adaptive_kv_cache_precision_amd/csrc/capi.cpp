@@ -1536,4 +1536,16 @@ int mi_kv_last_batch(mi_kv_pages *kv, int *has, size_t *moves, size_t *shadows_t
   });
 }
 
+int mi_kv_last_batch_phases(mi_kv_pages *kv, double *phases)
+{
+  return guarded([&] {
+    need(kv, "kv");
+    need(phases, "phases");
+    const auto &b = kv->impl.last_batch();
+    phases[0] = b ? b->prepare_seconds : 0.0;
+    phases[1] = b ? b->allocate_seconds : 0.0;
+    phases[2] = b ? b->finish_seconds : 0.0;
+  });
+}
+
 } // extern "C"

@@ -679,7 +679,8 @@ namespace mi
     {
       run_moves(keys, from, targets, nullptr);
     }
-    last_batch_ = BatchRecord{keys.size(), shadows_.count() - shadows_before, since(began)};
+    last_batch_ = BatchRecord{keys.size(), shadows_.count() - shadows_before, since(began),
+                              phases_[0], phases_[1], phases_[2]};
   }
 
   void KVPages::run_moves(const std::vector<PageKey> &keys, const std::vector<int> &from,
@@ -687,49 +688,55 @@ namespace mi
   {
     const hipStream_t stream = runtime_stream();
     const std::size_t n = keys.size();
-    // 1. Every new page under a staging key of its own, a tier's pages in
-    // one allocator call; and pinned room for the shadows first downgrades
-    // take. A failure here gives back what was taken and changes nothing.
-    std::vector<PageKey> staged(n);
-    std::array<std::vector<PageKey>, kTierCount> runs;
-    for (std::size_t i = 0; i < n; ++i)
-    {
-      staged[i] = {keys[i].layer, kBatchStagingPage - static_cast<int>(i)};
-      runs[targets[i]].push_back(staged[i]);
-    }
-    std::vector<PageKey> taken;
+    const Clock::time_point entered = Clock::now();
+    // 1. Pinned room for the shadows first downgrades take (nothing, if it
+    // was pinned ahead). A failure here changes nothing.
     std::size_t first_downgrades = 0;
     for (std::size_t i = 0; i < n; ++i)
     {
       first_downgrades += from[i] == kFP16 && !shadows_.contains(keys[i]);
     }
-    try
+    shadows_.reserve(first_downgrades);
+
+    // 2. Every new page under a staging key of its own, a tier's pages in
+    // one allocator call later. A run is appended at its tier's tail, so
+    // the slots the new pages will take are known now: the device's work is
+    // named by page reference before the host allocates, and the shadows
+    // start over the host link while it does.
+    std::vector<PageKey> staged(n);
+    std::array<std::vector<PageKey>, kTierCount> runs;
+    std::array<std::size_t, kTierCount> next{};
+    for (int t = 0; t < kTierCount; ++t)
     {
-      for (int t = 0; t < kTierCount; ++t)
-      {
-        allocator_.allocate_run(runs[t], t);
-        taken.insert(taken.end(), runs[t].begin(), runs[t].end());
-      }
-      shadows_.reserve(first_downgrades);
+      next[t] = allocator_.held(t);
     }
-    catch (...)
+    std::vector<std::uint32_t> to(n);
+    for (std::size_t i = 0; i < n; ++i)
     {
-      allocator_.free_pages(taken);
-      throw;
+      staged[i] = {keys[i].layer, kBatchStagingPage - static_cast<int>(i)};
+      runs[targets[i]].push_back(staged[i]);
+      to[i] = page_ref(targets[i], static_cast<std::uint32_t>(next[targets[i]]++));
+    }
+    for (int t = 0; t < kTierCount; ++t)
+    {
+      if (next[t] > kRefIndexMask)
+      {
+        throw OutOfRange(std::string("a batch would take ") + tier_name(t) + " past slot " +
+                         std::to_string(kRefIndexMask) + ", beyond what a page reference holds");
+      }
     }
 
-    // 2. The device's work, by page reference: shadows out, restores in, one
+    // The device's work, by page reference: shadows out, restores in, one
     // quantise launch per target tier, each reading pages before any is
-    // freed.
-    // A page quantised from its shadow is first brought to device memory in
-    // one copy (the quantiser reads its rows twice, and host memory is not
-    // cached on the device).
+    // freed. A page quantised from its shadow is first brought to device
+    // memory in one copy (the quantiser reads its rows twice, and host
+    // memory is not cached on the device).
+    const std::size_t shadows_before = shadows_.count();
     std::vector<RefPair> shadows_out, restores, restage;
     std::array<std::vector<RefPair>, kTierCount> requant;
     bool touches_shadow = false;
     for (std::size_t i = 0; i < n; ++i)
     {
-      const std::uint32_t to = allocator_.ref_of(staged[i]);
       std::uint32_t rows;
       if (from[i] == kFP16)
       {
@@ -752,11 +759,11 @@ namespace mi
       }
       if (targets[i] == kFP16)
       {
-        restores.push_back({rows, to});
+        restores.push_back({rows, to[i]});
       }
       else
       {
-        requant[targets[i]].push_back({rows, to});
+        requant[targets[i]].push_back({rows, to[i]});
       }
     }
     touches_shadow = touches_shadow || !shadows_out.empty();
@@ -769,20 +776,50 @@ namespace mi
     {
       all.insert(all.end(), r.begin(), r.end());
     }
-    PageSpaces spaces = allocator_.spaces();
-    spaces.shadows = shadows_.device_table(stream);
     const std::size_t fp16_bytes = bytes_at(kFP16);
     if (!restage.empty() && (staging_ == nullptr || staging_->bytes() < restage.size() * fp16_bytes))
     {
       staging_.reset(); // waits for launches that may read the old one
       staging_ = std::make_unique<DeviceBuffer>(restage.size() * fp16_bytes);
     }
+    PageSpaces spaces = allocator_.spaces();
+    spaces.shadows = shadows_.device_table(stream);
     spaces.staging = staging_ ? reinterpret_cast<unsigned long long>(staging_->raw()) : 0;
     const Clock::time_point device_began = Clock::now();
     const RefPair *on_device = pairs_upload_.send(all, stream);
     std::size_t at = 0;
     launch_copy_refs(on_device + at, static_cast<int>(shadows_out.size()), spaces, stream);
     at += shadows_out.size();
+    phases_[0] = since(entered);
+    const Clock::time_point allocating = Clock::now();
+
+    // The new pages, while the shadows travel. A failure gives back what was
+    // taken and forgets the shadows just numbered (the copies into their
+    // places are harmless: the places are free again, and a later copy into
+    // one is ordered after them on the stream).
+    std::vector<PageKey> taken;
+    try
+    {
+      for (int t = 0; t < kTierCount; ++t)
+      {
+        allocator_.allocate_run(runs[t], t, false);
+        taken.insert(taken.end(), runs[t].begin(), runs[t].end());
+      }
+    }
+    catch (...)
+    {
+      allocator_.free_pages(taken);
+      shadows_.truncate(shadows_before);
+      throw;
+    }
+    for (std::size_t i = 0; i < n; ++i)
+    {
+      if (allocator_.ref_of(staged[i]) != to[i])
+      {
+        throw LogicError("a staged page did not land in the slot its batch named");
+      }
+    }
+    phases_[1] = since(allocating);
     launch_copy_refs(on_device + at, static_cast<int>(restores.size()), spaces, stream);
     at += restores.size();
     launch_copy_refs(on_device + at, static_cast<int>(restage.size()), spaces, stream);
@@ -808,8 +845,10 @@ namespace mi
       pairs[i] = {keys[i], staged[i]};
       may_be_at_[targets[i]] = true;
     }
+    const Clock::time_point finishing = Clock::now();
     allocator_.replace_pages(pairs);
     hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize after a batch");
+    phases_[2] = since(finishing);
   }
 
   // ---- attention ---------------------------------------------------------------------

@@ -371,9 +371,9 @@ namespace mi
     }
   }
 
-  void PagedKVCache::allocate(PageKey key, int tier) { allocate_run({key}, tier); }
+  void PagedKVCache::allocate(PageKey key, int tier) { allocate_run({key}, tier, true); }
 
-  void PagedKVCache::allocate_run(const std::vector<PageKey> &keys, int tier)
+  void PagedKVCache::allocate_run(const std::vector<PageKey> &keys, int tier, bool top_up_spares)
   {
     check_tier(tier);
     Range &r = ranges_[tier];
@@ -411,7 +411,10 @@ namespace mi
     r.owners.insert(r.owners.end(), words.begin(), words.end());
     try
     {
-      fit(r, true);
+      // Spare granules are taken first. A batch's staging run maps only
+      // what its pages need: it is on its caller's critical path, and the
+      // next allocation that tops the spares up maps them then.
+      fit(r, top_up_spares);
     }
     catch (const OutOfMemory &e)
     {
@@ -587,63 +590,85 @@ namespace mi
 
   void PagedKVCache::replace(PageKey key, PageKey staged) { replace_pages({{key, staged}}); }
 
-  void PagedKVCache::map_one(Range &r)
+  void PagedKVCache::map_to(Range &r, std::size_t count)
   {
-    if (g_fail_granules > 0)
+    // Each granule is made and mapped on its own (so that each can be
+    // given back on its own); the access to the whole new span is granted
+    // in one call, the driver's dearest of the three.
+    const std::size_t first = r.granules.size();
+    const auto undo = [&]() {
+      for (std::size_t g = first; g < r.granules.size(); ++g)
+      {
+        (void)hipMemUnmap(r.base + g * granule_, granule_);
+        (void)hipMemRelease(r.granules[g]);
+      }
+      r.granules.resize(first);
+    };
+    try
     {
-      --g_fail_granules;
-      throw OutOfMemory("hipMemCreate: out of memory (injected by the test hook)");
+      while (r.granules.size() < count)
+      {
+        if (g_fail_granules > 0)
+        {
+          --g_fail_granules;
+          throw OutOfMemory("hipMemCreate: out of memory (injected by the test hook)");
+        }
+        char *at = r.base + r.granules.size() * granule_;
+        // The address may be one the releaser still holds.
+        releaser_->wait_for(at);
+        hipMemGenericAllocationHandle_t handle;
+        hipError_t created = hipMemCreate(&handle, granule_, &prop_, 0);
+        if (created == hipErrorOutOfMemory || created == hipErrorMemoryAllocation)
+        {
+          // Memory the releaser has yet to give back may be what is short.
+          (void)hipGetLastError();
+          releaser_->wait_for(nullptr);
+          created = hipMemCreate(&handle, granule_, &prop_, 0);
+        }
+        hip_check(created, "hipMemCreate");
+        const hipError_t mapped = hipMemMap(at, granule_, 0, handle, 0);
+        if (mapped != hipSuccess)
+        {
+          (void)hipMemRelease(handle);
+          hip_check(mapped, "hipMemMap");
+        }
+        r.granules.push_back(handle);
+      }
+      if (r.granules.size() > first)
+      {
+        hipMemAccessDesc access{};
+        access.location = prop_.location;
+        access.flags = hipMemAccessFlagsProtReadWrite;
+        hip_check(hipMemSetAccess(r.base + first * granule_, (r.granules.size() - first) * granule_,
+                                  &access, 1),
+                  "hipMemSetAccess");
+      }
     }
-    char *at = r.base + r.granules.size() * granule_;
-    // The address may be one the releaser still holds.
-    releaser_->wait_for(at);
-    hipMemGenericAllocationHandle_t handle;
-    hipError_t created = hipMemCreate(&handle, granule_, &prop_, 0);
-    if (created == hipErrorOutOfMemory || created == hipErrorMemoryAllocation)
+    catch (...)
     {
-      // Memory the releaser has yet to give back may be what is short.
-      (void)hipGetLastError();
-      releaser_->wait_for(nullptr);
-      created = hipMemCreate(&handle, granule_, &prop_, 0);
+      undo();
+      throw;
     }
-    hip_check(created, "hipMemCreate");
-    const hipError_t mapped = hipMemMap(at, granule_, 0, handle, 0);
-    if (mapped != hipSuccess)
-    {
-      (void)hipMemRelease(handle);
-      hip_check(mapped, "hipMemMap");
-    }
-    hipMemAccessDesc access{};
-    access.location = prop_.location;
-    access.flags = hipMemAccessFlagsProtReadWrite;
-    const hipError_t set = hipMemSetAccess(at, granule_, &access, 1);
-    if (set != hipSuccess)
-    {
-      (void)hipMemUnmap(at, granule_);
-      (void)hipMemRelease(handle);
-      hip_check(set, "hipMemSetAccess");
-    }
-    r.granules.push_back(handle);
   }
 
   void PagedKVCache::fit(Range &r, bool map_spares)
   {
     const std::size_t needed = round_up(r.owners.size() * r.page_bytes, granule_) / granule_;
     const std::size_t keep = std::min(needed + r.spare, r.reserved / granule_);
-    while (r.granules.size() < needed)
+    if (r.granules.size() < needed)
     {
-      map_one(r);
+      map_to(r, needed);
     }
-    try
+    if (map_spares && r.granules.size() < keep)
     {
-      while (map_spares && r.granules.size() < keep)
+      try
       {
-        map_one(r);
+        map_to(r, keep);
       }
-    }
-    catch (const OutOfMemory &)
-    {
-      // A spare is room kept for later, not room a page needs now.
+      catch (const OutOfMemory &)
+      {
+        // A spare is room kept for later, not room a page needs now.
+      }
     }
     if (r.granules.size() > keep)
     {

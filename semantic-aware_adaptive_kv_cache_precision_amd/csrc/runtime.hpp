@@ -156,8 +156,9 @@ namespace mi
 
     void allocate(PageKey key, int tier);
     // Every key at `tier`, in order, mapping the granules they need once;
-    // all or none.
-    void allocate_run(const std::vector<PageKey> &keys, int tier);
+    // all or none. Spare granules are taken first; with top_up_spares the
+    // spares are mapped again afterwards, as a single allocation does.
+    void allocate_run(const std::vector<PageKey> &keys, int tier, bool top_up_spares = true);
     void free(PageKey key);
     void free_pages(const std::vector<PageKey> &keys);
     void replace(PageKey key, PageKey staged);
@@ -168,6 +169,8 @@ namespace mi
     bool contains(PageKey key) const { return where_.count(pack(key)) != 0; }
     std::vector<PageKey> pages(int tier) const;
     std::size_t page_bytes(int tier) const { return ranges_.at(tier).page_bytes; }
+    // Pages a tier holds: the slot the next allocation there takes.
+    std::size_t held(int tier) const { return ranges_.at(tier).owners.size(); }
     std::size_t reserved_bytes(int tier) const { return ranges_.at(tier).reserved; }
     std::size_t mapped_bytes(int tier) const
     {
@@ -216,7 +219,8 @@ namespace mi
     }
     void release_keys(const std::vector<PageKey> &keys);
     void fit(Range &r, bool map_spares);
-    void map_one(Range &r);
+    // Maps granules at the range's end until it has `count`; all or none.
+    void map_to(Range &r, std::size_t count);
     void tell_placed(std::uint64_t key, int tier, std::size_t slot);
     void tell_removed(std::uint64_t key);
 
@@ -252,6 +256,9 @@ namespace mi
     void reserve(std::size_t count);
     // A new shadow's number, its room pinned already or now.
     std::uint32_t add(PageKey key);
+    // Forgets the shadows numbered `count` and above (the last added), as
+    // if they had not been: a batch that fails after taking them.
+    void truncate(std::size_t count);
     bool contains(PageKey key) const { return number_.count(pack(key)) != 0; }
     std::uint32_t number(PageKey key) const;
     const std::uint8_t *shadow(PageKey key) const;
@@ -276,6 +283,8 @@ namespace mi
     std::unordered_map<std::uint64_t, std::uint32_t> number_;
     std::vector<std::uint8_t *> host_;       // by number
     std::vector<unsigned long long> device_; // by number
+    std::vector<std::uint64_t> keys_;        // by number
+    std::vector<std::size_t> block_of_;      // by number
     std::size_t sent_ = 0;                   // entries already in the device table
     std::unique_ptr<DeviceBuffer> table_;
     std::vector<std::unique_ptr<DeviceBuffer>> outgrown_;
@@ -375,6 +384,13 @@ namespace mi
     std::size_t moves;
     std::size_t shadows_taken;
     double seconds;
+    // Where the seconds went: the host's work before the first launch; the
+    // new pages' allocation (while the shadows travel); the page table's
+    // switch to the new pages, the old ones' release and the wait for the
+    // device.
+    double prepare_seconds;
+    double allocate_seconds;
+    double finish_seconds;
   };
 
   // Every layer's page addresses and tiers on the device, [layer][stride]
@@ -536,6 +552,7 @@ namespace mi
     // The tier moves of a batch: validated already, every page held.
     void run_moves(const std::vector<PageKey> &keys, const std::vector<int> &from,
                    const std::vector<int> &targets, double *shadow_seconds);
+    double phases_[3] = {0.0, 0.0, 0.0}; // the last run_moves': prepare, allocate, finish
     void require_layer(int layer) const;
     std::size_t bytes_at(int tier) const;
     void require_page_size(int tier, const char *what) const;

@@ -74,8 +74,28 @@ namespace mi
     const auto number = static_cast<std::uint32_t>(host_.size());
     host_.push_back(block->host + at * page_bytes_);
     device_.push_back(reinterpret_cast<unsigned long long>(block->device + at * page_bytes_));
+    keys_.push_back(pack(key));
+    block_of_.push_back(cursor_);
     number_[pack(key)] = number;
     return number;
+  }
+
+  void ShadowStore::truncate(std::size_t count)
+  {
+    while (host_.size() > count)
+    {
+      // The last shadow is the last used place of its block; blocks before
+      // it are full, so the cursor goes back to it.
+      const std::size_t b = block_of_.back();
+      --blocks_[b].used;
+      cursor_ = b;
+      number_.erase(keys_.back());
+      host_.pop_back();
+      device_.pop_back();
+      keys_.pop_back();
+      block_of_.pop_back();
+    }
+    sent_ = std::min(sent_, host_.size());
   }
 
   void ShadowStore::take(PageKey key, const void *device_page, hipStream_t stream)

@@ -193,6 +193,7 @@ SIGNATURES = {
     "mi_kv_birth_tier": ((_vp, _i, _i, _ip), C.c_int),
     "mi_kv_last_move": ((_vp, _ip, _ip, _szp, C.POINTER(C.c_double)), C.c_int),
     "mi_kv_last_batch": ((_vp, _ip, _szp, _szp, C.POINTER(C.c_double)), C.c_int),
+    "mi_kv_last_batch_phases": ((_vp, C.POINTER(C.c_double)), C.c_int),
 }
 for _name, (_args, _res) in SIGNATURES.items():
     _sig(_name, *_args, restype=_res)
@@ -1160,9 +1161,13 @@ class KVPages:
         _check(lib.mi_kv_upgrade(self._h, layer, page, _tier(target)))
 
     def move_pages(self, moves) -> None:
-        moves = list(moves)
-        flat = [int(x) for layer, page, tier in moves for x in (layer, page, _tier(tier))]
-        _check(lib.mi_kv_move_pages(self._h, _int_array(flat), len(moves)))
+        """`moves`: (layer, page, tier) triples, a list or an (n, 3) array."""
+        flat = np.ascontiguousarray(np.asarray(moves, dtype=np.int64).reshape(-1, 3),
+                                    dtype=np.int32)
+        bad = (flat[:, 2] < 0) | (flat[:, 2] > 3)
+        if bad.any():
+            raise ValueError(f"tier {int(flat[bad][0, 2])} is not one of the four")
+        _check(lib.mi_kv_move_pages(self._h, flat.ctypes.data_as(_ip), len(flat)))
 
     def pin_shadows(self, pages: int) -> None:
         """Pins host memory for `pages` more FP16 shadows now (beyond the
@@ -1198,7 +1203,11 @@ class KVPages:
                                     C.byref(secs)))
         if not has.value:
             return None
-        return {"moves": moves.value, "shadows_taken": shadows.value, "seconds": secs.value}
+        phases = (C.c_double * 3)()
+        _check(lib.mi_kv_last_batch_phases(self._h, phases))
+        return {"moves": moves.value, "shadows_taken": shadows.value, "seconds": secs.value,
+                "prepare_seconds": phases[0], "allocate_seconds": phases[1],
+                "finish_seconds": phases[2]}
 
 
 def page_bytes(page_tokens: int, kv_width: int) -> int:
