@@ -332,12 +332,9 @@ def config2(m, steps, warmup, seed=0):
 
 # ---- whole decode steps (every projection, one graph a token) -------------------------------
 
-def full_step(m, shape, context, steps, warmup, mix, key_bias, seed):
-    """`steps` greedy decode steps of a random-weight model of `shape` from
-    position `context` (the cache born at `mix` over the whole run), after
-    `warmup` steps: tokens/s from the replays' device time, and HBM GB/s of
-    the weights and pages a step reads."""
-    from microinfer import workloads as w
+def random_model(m, shape, key_bias, seed):
+    """Random fp16 weights of `shape` on the device (norm weights ones):
+    (embed, final norm, head, layers)."""
     d = m.device
     L, H, I, V = shape.layers, shape.hidden, shape.intermediate, shape.vocab
     qw, kw = shape.heads * shape.head_dim, shape.kv_width
@@ -362,18 +359,71 @@ def full_step(m, shape, context, steps, warmup, mix, key_bias, seed):
             "v_b": rand(kw, 0.5) if key_bias else None})
     embed = rand(V * H, 1.0)
     head = rand(V * H, H ** -0.5)
+    return embed, ones, head, layers
+
+
+def prefill_flops(shape, start, n):
+    """Flops of a prefill of n prompt rows after `start` positions: every
+    projection (2 flops a weight a row), attention's QK^T and PV over the
+    positions each row attends (causal), and the last row's head."""
+    H, I = shape.hidden, shape.intermediate
+    qw, kw = shape.heads * shape.head_dim, shape.kv_width
+    per_row = 2 * shape.layers * (H * qw + 2 * H * kw + qw * H + 3 * H * I)
+    attended = n * start + n * (n + 1) // 2
+    attention = 4 * shape.layers * shape.heads * shape.head_dim * attended
+    return per_row * n + attention + 2 * H * shape.vocab
+
+
+def full_step(m, shape, context, steps, warmup, mix, key_bias, seed, prompt_chunk=None):
+    """`steps` greedy decode steps of a random-weight model of `shape` from
+    position `context` (the cache born at `mix` over the whole run), after
+    `warmup` steps: tokens/s from the replays' device time, and HBM GB/s of
+    the weights and pages a step reads. With `prompt_chunk`, the context is
+    a random prompt prefilled through the whole model in chunks of that many
+    rows (timed on the device, after one chunk into a throwaway cache);
+    otherwise its rows are stored directly."""
+    from microinfer import workloads as w
+    d = m.device
+    L, H, I, V = shape.layers, shape.hidden, shape.intermediate, shape.vocab
+    embed, ones, head, layers = random_model(m, shape, key_bias, seed)
     end = context + warmup + steps
     pages = -(-end // P)
     tier_map = w.tier_map(seed, L, pages, mix)
     alloc, cache = sealing_cache(m, shape, L, pages, tier_map)
-    t0 = time.perf_counter()
-    fill_rows(m, cache, shape, L, context, np.random.default_rng(seed))
-    log(f"{shape.name}: {context} positions stored in {time.perf_counter() - t0:.1f}s")
     scores = d.ImportanceScores(L, pages)
     step = d.DecodeStep(cache, w.model_dict(shape), embed, ones, head, layers, scores, 1)
-    tokens, _ = step.run(1, context, warmup)
+    rng = np.random.default_rng(seed)
     t0 = time.perf_counter()
-    tokens, ms = step.run(int(tokens[-1]), context + warmup, steps)
+    prefilled = None
+    if prompt_chunk:
+        _, spare = sealing_cache(m, shape, L, -(-prompt_chunk // P), tier_map)
+        spare_step = d.DecodeStep(spare, w.model_dict(shape), embed, ones, head, layers)
+        spare_step.prefill(rng.integers(0, V, prompt_chunk), 0, prompt_chunk)
+        del spare_step, spare
+        ids = rng.integers(0, V, context)
+        t0 = time.perf_counter()
+        first, prefill_ms = step.prefill(ids, 0, prompt_chunk)
+        prefill_wall = time.perf_counter() - t0
+        flops = prefill_flops(shape, 0, context)
+        tflops = flops / (prefill_ms * 1e-3) / 1e12
+        prefilled = {"prompt": context, "chunk": prompt_chunk, "device_ms": round(prefill_ms, 2),
+                     "wall_ms": round(prefill_wall * 1e3, 2),
+                     "tokens_per_s": round(context / (prefill_ms * 1e-3), 1),
+                     "tflops": round(tflops, 1), "flops": flops,
+                     "pct_fp16_mfma_peak": round(100 * tflops / 2500.0, 2),
+                     "first_token": int(first)}
+        log(f"{shape.name}: {context}-token prefill in {prompt_chunk}-row chunks "
+            f"{prefill_ms:.1f} ms on the device ({tflops:.0f} TFLOP/s)")
+        token = int(first)
+    else:
+        fill_rows(m, cache, shape, L, context, rng)
+        log(f"{shape.name}: {context} positions stored in {time.perf_counter() - t0:.1f}s")
+        token = 1
+    if warmup:
+        tokens, _ = step.run(token, context, warmup)
+        token = int(tokens[-1])
+    t0 = time.perf_counter()
+    tokens, ms = step.run(token, context + warmup, steps)
     wall = time.perf_counter() - t0
     logits = step.logits()
     if not np.isfinite(logits).all() or not ((tokens >= 0) & (tokens < V)).all():
@@ -389,7 +439,7 @@ def full_step(m, shape, context, steps, warmup, mix, key_bias, seed):
     gbs = step_bytes / (per_step * 1e-3) / 1e9
     log(f"{shape.name} whole step @{mid}: {per_step * 1e3:.1f} us, {steps / ms * 1e3:.0f} tok/s, "
         f"{gbs:.0f} GB/s")
-    return {"tokens_per_s": round(steps / (ms * 1e-3), 1), "ms_per_token": round(per_step, 4),
+    out = {"tokens_per_s": round(steps / (ms * 1e-3), 1), "ms_per_token": round(per_step, 4),
             "gb_per_s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / PEAK_GBS, 2),
             "weight_bytes": weight_bytes, "kv_bytes": kv_bytes,
             "launches_per_token": step.launches, "positions": [context + warmup, end],
@@ -398,6 +448,12 @@ def full_step(m, shape, context, steps, warmup, mix, key_bias, seed):
                       f"weights, pages at {'/'.join(str(int(f * 100)) for _, f in reversed(mix))} "
                       f"% of FP16..{'INT2' if len(mix) > 3 else 'INT4'}, scores folded every "
                       f"step; {steps} greedy steps replaying one graph"}
+    if prefilled:
+        out["prefill"] = prefilled
+        out["config"] = (f"{context}-token random prompt prefilled in {prompt_chunk}-row chunks "
+                         f"(hipBLASLt projections, matrix-core chunk attention over sealed pages), "
+                         f"then {out['config']}")
+    return out
 
 
 # ---- prefill attention ---------------------------------------------------------------------
@@ -799,7 +855,8 @@ def main() -> int:
         steps_out = {
             "qwen2.5-1.5b_32k": full_step(m, w.QWEN_15B, 32768 - 64 - 8, 64, 8, w.MIX_CONFIG3,
                                           True, 3),
-            "llama-3.2-1b_16k": full_step(m, w.LLAMA_1B, 16384, 256, 8, w.MIX_CONFIG5, False, 5)}
+            "llama-3.2-1b_16k_config5": full_step(m, w.LLAMA_1B, 16384, 256, 0, w.MIX_CONFIG5,
+                                                  False, 5, prompt_chunk=2048)}
         steps_out["reference_rtx4050_tokens_per_s"] = {"qwen2.5-1.5b_fp16_32k": 29.5,
                                                        "qwen2.5-1.5b_fp16_16k": 40.1}
 

@@ -428,6 +428,15 @@ int mi_decode_step_destroy(mi_decode_step *step);
  * run reserves its pages first and records its stores after. */
 int mi_decode_step_run(mi_decode_step *step, int token, int position, int steps,
                        int32_t *tokens, double *device_ms);
+/* The prompt (n tokens from host memory) at positions [position,
+ * position + n) in chunks of `chunk` rows, a layer at a time as the
+ * reference's Model.run (model.py:332-403) takes a chunk: RMSNorm, q/k/v
+ * projections, RoPE, store, the chunk's attention, output projection, MLP;
+ * then the greedy token after the last row, to *first (feed it to
+ * mi_decode_step_run at position + n). *device_ms (may be NULL) the
+ * prefill's device time. */
+int mi_decode_step_prefill(mi_decode_step *step, const int32_t *tokens, int n, int position,
+                           int chunk, int32_t *first, double *device_ms);
 /* The last step's logits, fp32, to host memory (count <= vocab). */
 int mi_decode_step_logits(mi_decode_step *step, float *out, size_t count);
 int mi_decode_step_launches(mi_decode_step *step, int *out);

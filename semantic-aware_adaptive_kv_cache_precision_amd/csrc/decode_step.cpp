@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <string>
+#include <vector>
 
 namespace mi
 {
@@ -292,6 +293,154 @@ namespace mi
     float ms = 0.0f;
     hip_check(hipEventElapsedTime(&ms, begin_, end_), "hipEventElapsedTime");
     cache_.stored_on_device(end);
+    return ms;
+  }
+
+  void DecodeStep::size_chunk(int rows, int prompt)
+  {
+    const ModelShape &s = shape_;
+    const std::size_t q_width = static_cast<std::size_t>(s.heads) * s.head_dim;
+    const std::size_t kv_width = static_cast<std::size_t>(s.kv_heads) * s.head_dim;
+    if (rows > chunk_room_)
+    {
+      const std::size_t r = rows;
+      c_residual_ = device_bytes(r * s.hidden * sizeof(float));
+      c_normed_ = device_bytes(r * s.hidden * 2);
+      c_q_raw_ = device_bytes(r * q_width * 2);
+      c_q_ = device_bytes(r * q_width * 2);
+      c_k_raw_ = device_bytes(r * kv_width * 2);
+      c_k_ = device_bytes(r * kv_width * 2);
+      c_v_ = device_bytes(r * kv_width * 2);
+      c_attended_ = device_bytes(r * q_width * 2);
+      c_gate_ = device_bytes(r * s.intermediate * 2);
+      c_up_ = device_bytes(r * s.intermediate * 2);
+      c_act_ = device_bytes(r * s.intermediate * 2);
+      chunk_room_ = rows;
+    }
+    if (c_partials_ == nullptr)
+    {
+      c_partials_ = device_bytes(attention_partials_floats(s.head_dim) * sizeof(float));
+    }
+    if (prompt > prompt_room_)
+    {
+      c_ids_ = device_bytes(static_cast<std::size_t>(prompt) * sizeof(std::int32_t));
+      c_positions_ = device_bytes(static_cast<std::size_t>(prompt) * sizeof(std::int32_t));
+      prompt_room_ = prompt;
+    }
+  }
+
+  double DecodeStep::prefill(const std::int32_t *tokens, int n, int position, int chunk,
+                             std::int32_t *first)
+  {
+    const ModelShape &s = shape_;
+    require(n > 0 && position >= 0 && chunk > 0, "a prefill takes at least one token, a position "
+                                                 ">= 0 and chunks of at least one row");
+    require(tokens != nullptr && first != nullptr, "a prefill reads its tokens from host memory "
+                                                   "and writes the first decode token there");
+    const int q_width = s.heads * s.head_dim;
+    const int kv_width = s.kv_heads * s.head_dim;
+    const int rows_most = std::min(chunk, n);
+    cache_.reserve(position + n);
+    rope_.cover(std::max(position + n, RopeTable::kAngleRows));
+    size_chunk(rows_most, n);
+    size_buffers(1);
+    std::vector<std::int32_t> at(static_cast<std::size_t>(n));
+    for (int i = 0; i < n; ++i)
+    {
+      at[i] = position + i;
+    }
+    const int state[4] = {0, position + n - 1, position + n, 0};
+    // Whatever the cache launched elsewhere (table edits, the reservation's
+    // pages) is done before this stream starts.
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize before a prefill");
+    const hipStream_t stream = stream_;
+    hip_check(hipMemcpyAsync(c_ids_->raw(), tokens, static_cast<std::size_t>(n) * 4,
+                             hipMemcpyHostToDevice, stream),
+              "hipMemcpyAsync prompt");
+    hip_check(hipMemcpyAsync(c_positions_->raw(), at.data(), static_cast<std::size_t>(n) * 4,
+                             hipMemcpyHostToDevice, stream),
+              "hipMemcpyAsync positions");
+    hip_check(hipMemcpyAsync(state_->raw(), state, sizeof(state), hipMemcpyHostToDevice, stream),
+              "hipMemcpyAsync step state");
+    const hipStream_t previous = runtime_stream();
+    set_runtime_stream(stream);
+    float *residual = c_residual_->as<float>();
+    auto *normed = c_normed_->as<std::uint16_t>();
+    auto *q_raw = c_q_raw_->as<std::uint16_t>();
+    auto *q = c_q_->as<std::uint16_t>();
+    auto *k_raw = c_k_raw_->as<std::uint16_t>();
+    auto *k = c_k_->as<std::uint16_t>();
+    auto *v = c_v_->as<std::uint16_t>();
+    auto *attended = c_attended_->as<std::uint16_t>();
+    auto *gate = c_gate_->as<std::uint16_t>();
+    auto *up = c_up_->as<std::uint16_t>();
+    auto *act = c_act_->as<std::uint16_t>();
+    const auto *ids = c_ids_->as<const std::int32_t>();
+    const auto *positions = c_positions_->as<const std::int32_t>();
+    float ms = 0.0f;
+    try
+    {
+      hip_check(hipEventRecord(begin_, stream), "hipEventRecord");
+      int last_rows = 0;
+      for (int c0 = 0; c0 < n; c0 += chunk)
+      {
+        const int rows = std::min(chunk, n - c0);
+        const int p0 = position + c0;
+        launch_embed(ids + c0, rows, weights_.embed, residual, true, s.hidden, s.vocab, stream);
+        for (int l = 0; l < s.layers; ++l)
+        {
+          const LayerWeights &w = weights_.layers[l];
+          launch_rmsnorm(residual, true, w.input_norm, normed, rows, s.hidden, s.rms_eps, stream);
+          linear_half(normed, w.q_w, w.q_b, q_raw, rows, s.hidden, q_width, stream);
+          // The key bias, when attention adds it rotated, stays out of k.
+          linear_half(normed, w.k_w, key_bias_ ? nullptr : w.k_b, k_raw, rows, s.hidden,
+                      kv_width, stream);
+          linear_half(normed, w.v_w, w.v_b, v, rows, s.hidden, kv_width, stream);
+          launch_rope(q_raw, positions + c0, q, rows, s.heads, s.head_dim, s.rope_theta, stream);
+          launch_rope(k_raw, positions + c0, k, rows, s.kv_heads, s.head_dim, s.rope_theta,
+                      stream);
+          cache_.store(l, k, v, p0, rows);
+          cache_.attention(l, q, key_bias_ ? w.k_b : nullptr, &rope_, attended, rows, p0 + rows,
+                           s.heads, s.kv_heads, s.head_dim, k, v, nullptr, nullptr, 0.0f,
+                           c_partials_->as<float>());
+          linear_float(attended, w.o_w, residual, true, rows, q_width, s.hidden, stream);
+          launch_rmsnorm(residual, true, w.post_norm, normed, rows, s.hidden, s.rms_eps, stream);
+          linear_half(normed, w.gate_w, nullptr, gate, rows, s.hidden, s.intermediate, stream);
+          linear_half(normed, w.up_w, nullptr, up, rows, s.hidden, s.intermediate, stream);
+          launch_swiglu(gate, up, act, static_cast<std::size_t>(rows) * s.intermediate, stream);
+          linear_float(act, w.down_w, residual, true, rows, s.intermediate, s.hidden, stream);
+        }
+        last_rows = rows;
+      }
+      // The last row's logits, its RMSNorm formed in the head's projection,
+      // and the greedy token: the state moves to the first decode step.
+      ProjectArgs head{};
+      head.segments = 1;
+      head.seg[0] = {weights_.head, nullptr, logits_->as<float>(), s.vocab};
+      head.in = s.hidden;
+      head.mode = ProjectMode::kLogits;
+      head.residual = residual + static_cast<std::size_t>(last_rows - 1) * s.hidden;
+      head.norm_weight = weights_.final_norm;
+      head.eps = s.rms_eps;
+      head.x = normed;
+      head.best_value = best_value_->as<float>();
+      head.best_index = best_index_->as<int>();
+      launch_project(head, stream);
+      launch_advance(best_value_->as<float>(), best_index_->as<int>(), head_blocks_, s.vocab,
+                     state_->as<int>(), tokens_->as<std::int32_t>(), token_room_, stream);
+      hip_check(hipEventRecord(end_, stream), "hipEventRecord");
+      hip_check(hipMemcpyAsync(first, state_->as<int>() + kStepToken, sizeof(std::int32_t),
+                               hipMemcpyDeviceToHost, stream),
+                "hipMemcpyAsync first token");
+      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize prefill");
+      hip_check(hipEventElapsedTime(&ms, begin_, end_), "hipEventElapsedTime");
+    }
+    catch (...)
+    {
+      set_runtime_stream(previous);
+      throw;
+    }
+    set_runtime_stream(previous);
     return ms;
   }
 

@@ -80,6 +80,17 @@ namespace mi
     DecodeStep(const DecodeStep &) = delete;
     DecodeStep &operator=(const DecodeStep &) = delete;
 
+    // The prompt `tokens` (n of them) at positions [position, position + n)
+    // in chunks of `chunk` rows, each chunk a layer at a time as the
+    // reference's Model.run takes them (model.py:332-403): RMSNorm, the
+    // q/k/v projections (hipBLASLt), RoPE, the store (sealing pages as they
+    // fill), the chunk's attention (the matrix-core kernel over the pages
+    // before each query's own at their tiers), the output projection into
+    // the fp32 residual, RMSNorm, gate and up, SwiGLU, down. Then the last
+    // row's logits and greedy token: the first decode token, returned in
+    // *first. Returns the device milliseconds of the whole prefill.
+    double prefill(const std::int32_t *tokens, int n, int position, int chunk,
+                   std::int32_t *first);
     // `steps` greedy steps: the first feeds `token` at `position` (the cache
     // holds every position before it), each later one the token before it.
     // The chosen tokens go to `tokens` (host, `steps` of them). Returns the
@@ -126,6 +137,13 @@ namespace mi
     std::unique_ptr<DeviceBuffer> best_index_;
     std::unique_ptr<DeviceBuffer> kept_;
     std::unique_ptr<DeviceBuffer> tokens_;
+    // A prefill's chunk buffers (rows of `chunk_room_`), its token ids and
+    // positions, and the attention's partials.
+    void size_chunk(int rows, int prompt);
+    int chunk_room_ = 0;
+    int prompt_room_ = 0;
+    std::unique_ptr<DeviceBuffer> c_residual_, c_normed_, c_q_raw_, c_q_, c_k_raw_, c_k_, c_v_,
+        c_attended_, c_gate_, c_up_, c_act_, c_partials_, c_ids_, c_positions_;
   };
 
 } // namespace mi

@@ -83,6 +83,8 @@ SIGNATURES = {
     "mi_decode_step_destroy": ((_vp,), C.c_int),
     "mi_decode_step_run": ((_vp, _i, _i, _i, C.POINTER(C.c_int32), C.POINTER(_d)), C.c_int),
     "mi_decode_step_logits": ((_vp, _fp, _sz), C.c_int),
+    "mi_decode_step_prefill": ((_vp, C.POINTER(C.c_int32), _i, _i, _i, C.POINTER(C.c_int32),
+                                C.POINTER(_d)), C.c_int),
     "mi_decode_step_launches": ((_vp, _ip), C.c_int),
     "mi_random_half": ((_vp, _sz, C.c_ulonglong, _f), C.c_int),
     "mi_host_free": ((_vp,), C.c_int),
@@ -1392,6 +1394,18 @@ class DecodeStep:
         _check(lib.mi_decode_step_run(self._h, token, position, steps,
                                       out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(ms)))
         return out, ms.value
+
+    def prefill(self, tokens, position: int = 0, chunk: int = 2048):
+        """The prompt at positions [position, position + len(tokens)) in
+        chunks of `chunk` rows: (the first decode token, device
+        milliseconds). The logits after the last row are logits()."""
+        ids = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        first = C.c_int32()
+        ms = C.c_double()
+        _check(lib.mi_decode_step_prefill(self._h, ids.ctypes.data_as(C.POINTER(C.c_int32)),
+                                          ids.size, position, chunk, C.byref(first),
+                                          C.byref(ms)))
+        return first.value, ms.value
 
     def logits(self) -> np.ndarray:
         out = np.empty(self.vocab, np.float32)

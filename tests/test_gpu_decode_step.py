@@ -15,7 +15,11 @@ GPU parity tests:
     the device rounds; the greedy token is the oracle's argmax wherever the
     oracle's margin exceeds the tolerance;
   - a run of N steps (one graph replayed N times) leaves the tokens, logits,
-    pages and scores that N runs of one step leave, to the bit.
+    pages and scores that N runs of one step leave, to the bit;
+  - a chunked prefill of the whole model (DecodeStep.prefill) gives the last
+    row's logits of the same float64 composition taken a chunk at a time,
+    each chunk's queries reading the pages sealed before their own; the
+    decode step after it continues from the prefill's cache.
 """
 
 import numpy as np
@@ -317,3 +321,92 @@ def test_a_run_replays_one_graph_to_the_bits_of_single_steps():
                                               made[1][0].read(layer, page))
         scored = made[0][2].download()
         assert np.isfinite(scored[:, :(start + n) // P]).all()
+
+
+def oracle_prefill(host, s, ids, position, rows, chunk, alloc):
+    """float64 logits after the last prompt row and each layer's (K, V) rows
+    (positions 0 .. position + len(ids)): the prompt taken `chunk` rows at a
+    time, a layer at a time (the reference's Model.run over a chunk,
+    model.py:332-403), each chunk's queries reading the pages before their
+    own at the bytes the device sealed (`alloc`), every fp16 rounding where
+    the device rounds. `rows` holds each layer's rows before `position`."""
+    eps, theta = s["rms_eps"], s["rope_theta"]
+    heads, kv, hd = s["heads"], s["kv_heads"], s["head_dim"]
+    key_bias = host["layers"][0]["k_b"] is not None
+    K = [np.asarray(k, np.float64) for k, _ in rows]
+    V = [np.asarray(v, np.float64) for _, v in rows]
+    x = None
+    for c0 in range(0, len(ids), chunk):
+        part = ids[c0:c0 + chunk]
+        r = len(part)
+        at = np.arange(position + c0, position + c0 + r)
+        x = dense.embed(part, host["embed"]).astype(np.float64)
+        for layer, w in enumerate(host["layers"]):
+            n = f16(pointwise.rmsnorm(x, w["input_norm"], eps))
+            q = f16(dense.linear(n, w["q_w"], w["q_b"])[0])
+            k = f16(dense.linear(n, w["k_w"], None if key_bias else w["k_b"])[0])
+            v = f16(dense.linear(n, w["v_w"], w["v_b"])[0])
+            q = f16(pointwise.rope(q.reshape(r, heads, hd), at, theta))
+            k = f16(pointwise.rope(k.reshape(r, kv, hd), at, theta))
+            K[layer] = np.concatenate([K[layer], k])
+            V[layer] = np.concatenate([V[layer], v.reshape(r, kv, hd)])
+            own = int(at[-1]) // P
+            sealed = [alloc.read(layer, i) for i in range(own)]
+            tiers = [int(alloc.locate(layer, i)[0]) for i in range(own)]
+            out = att.causal_chunk(q, sealed, tiers, K[layer], V[layer], kv, hd, P,
+                                   w["k_b"].reshape(kv, hd) if key_bias else None, theta)
+            a = f16(out.reshape(r, heads * hd))
+            x = x + dense.linear(a, w["o_w"])[0]
+            n = f16(pointwise.rmsnorm(x, w["post_norm"], eps))
+            g = f16(dense.linear(n, w["gate_w"])[0])
+            u = f16(dense.linear(n, w["up_w"])[0])
+            act = f16(pointwise.swiglu(g, u))
+            x = x + dense.linear(act, w["down_w"])[0]
+    n = f16(pointwise.rmsnorm(x[-1:], host["final_norm"], eps))
+    return dense.linear(n, host["head"])[0][0], list(zip(K, V))
+
+
+def check_logits(got, want, token):
+    scale = np.abs(want).max()
+    err = np.abs(got - want).max() / scale
+    assert err < LOGIT_TOL, f"logits off the oracle by {err:.3g} of the largest"
+    order = np.argsort(-want)
+    if want[order[0]] - want[order[1]] > 2 * LOGIT_TOL * scale:
+        assert token == order[0], (token, order[:3])
+    assert token == dense.argmax_rows(got[None].astype(np.float32))[0]
+
+
+@pytest.mark.parametrize("case", ["qwen_hd128_from_empty", "llama_after_context"])
+def test_chunked_prefill_is_the_oracles_composition(case):
+    """The prompt in chunks (the last one short) through every layer: the
+    last row's logits and greedy token against the float64 composition; the
+    chunks seal pages at the tier map's tiers, which later chunks read. Then
+    one decode step from the prefill's cache against the oracle's step."""
+    m = mi()
+    if case == "qwen_hd128_from_empty":
+        s, biases, start, n, chunk, seed = small_shape(heads=12, kv_heads=2, head_dim=128), \
+            True, 0, 150, 64, 31
+    else:
+        s, biases, start, n, chunk, seed = small_shape(hidden=512, intermediate=1024, heads=16,
+                                                       kv_heads=4, head_dim=64, vocab=1500), \
+            False, 40, 90, 32, 32
+    rng = np.random.default_rng(seed)
+    host = make_weights(rng, s, biases)
+    dev = upload_weights(host)
+    alloc, cache = make_cache(s, tier_map_for(s, 16, seed))
+    rows = context_rows(rng, s, start)
+    if start:
+        prefill(cache, s, rows)
+    step = m.device.DecodeStep(cache, s, dev["embed"], dev["final_norm"], dev["head"],
+                               dev["layers"])
+    ids = rng.integers(0, s["vocab"], n).astype(np.int32)
+    announce("chunked prefill", case, start, n, chunk)
+    first, ms = step.prefill(ids, start, chunk)
+    got = step.logits().astype(np.float64)
+    want, kv_rows = oracle_prefill(host, s, ids, start, rows, chunk, alloc)
+    check_logits(got, want, first)
+    assert ms > 0
+    announce("step after prefill", case)
+    tokens, _ = step.run(first, start + n, 1)
+    want, _ = oracle_step(host, s, first, start + n, kv_rows, alloc)
+    check_logits(step.logits().astype(np.float64), want, tokens[0])
