@@ -4,8 +4,9 @@
 // reading of a cache that seals).
 //
 // The arithmetic is the general kernel's: a query reads each page before its
-// own at the tier the page table records, dequantised exactly as
-// dequantise_page does, and its own page at FP16 from the open page and the
+// own at the tier the page table records, dequantised as dequantise_page
+// does (up to one fp16 ulp where the reference's fp32 value lands on an fp16
+// tie), and its own page at FP16 from the open page and the
 // chunk's rows; an unread page is skipped; the key bias is completed as
 // k + RoPE(k_bias, j); online softmax; split-K runs of whole pages folded by
 // a combine.
@@ -25,9 +26,13 @@
 // With S^T in the accumulator layout, lane l holds row l % 16 and keys
 // 4(l/16)+i and 16+4(l/16)+i: each lane's scores are its own row's, so the
 // softmax needs no transpose, a row's maximum is two lane exchanges, and the
-// lane's eight probabilities are the B operand of PV directly when V^T's key
-// order in LDS is permuted to match (slot 8g+e holds key 4g+e for e < 4 and
-// 16+4g+e-4 after).
+// lane's eight probabilities are the B operand of PV directly. V is staged
+// in key rows and read transposed (ds_read_b64_tr_b16) in that key order.
+//
+// Staging. A step stages NP pages (two at head_dim 64 without a key bias)
+// behind one barrier, double-buffered: the next step's pages are fetched to
+// registers while this step's are multiplied, then dequantised (packed
+// fp16, one rounding of code * scale + zero) into the other buffer.
 //
 // Precision. Q, the dequantised K and V are exact in fp16. With a key bias,
 // k + bias is formed in fp32 as the general kernel forms it and split into a
@@ -44,6 +49,7 @@
 // for the rows on it.
 
 #include "common.hpp"
+#include "dequant.hpp"
 #include "kernels.hpp"
 #include "lane_ops.hpp"
 
@@ -60,7 +66,6 @@ namespace mi
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
     constexpr int kP = 32;              // keys a page, and a key tile
-    constexpr int kVS = kP + 8;         // V^T row stride in halves (80 B: no bank conflicts)
     constexpr float kPScale = 16384.0f; // probabilities are held x2^14 for PV
     constexpr float kPUnscale = 1.0f / 16384.0f;
     constexpr int kMaxWaves = 8;
@@ -101,12 +106,6 @@ namespace mi
 
     __device__ inline half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
-    // The LDS slot of key t in V^T's row (the PV operand's key order).
-    __device__ inline int v_slot(int t)
-    {
-      return 8 * ((t & 15) >> 2) + (t & 3) + ((t >> 4) << 2);
-    }
-
     // The key lane l's accumulator element (tile kt, index i) holds.
     __device__ inline int key_of(int kt, int g, int i) { return 16 * kt + 4 * g + i; }
 
@@ -131,10 +130,25 @@ namespace mi
       static constexpr int kItems = kP * kChunks;  // (key, chunk) pairs a page
     };
 
+    // A page's stage: K rows (high parts, then low parts with a key bias),
+    // kKS halves apart; then V as 16-byte chunks (key t, channels 8c ..
+    // 8c+7) at chunk c * 32 + t, which the transposing LDS read hands out as
+    // keys of one channel.
     template <int HD, bool kBias>
     __host__ __device__ constexpr int stage_halves()
     {
-      return (kBias ? 2 : 1) * kP * Geometry<HD>::kKS + HD * kVS;
+      return (kBias ? 2 : 1) * kP * Geometry<HD>::kKS + HD * kP;
+    }
+
+    typedef short i16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) i16x4 *lds_i16x4;
+
+    // gfx950's transposing LDS read: the 16 lanes of a row group address a
+    // 4-row x 16-channel block (lane s: row s / 4, channels 4 (s % 4) ..
+    // +3) and lane s receives channel s of the four rows.
+    __device__ inline uint2 tr16(const std::uint16_t *p)
+    {
+      return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(p)));
     }
 
     // Fetches one (key t, chunk c) of the item (page p, version) for KV head
@@ -268,61 +282,48 @@ namespace mi
       }
     }
 
-    // Code e of 8 packed codes (first in the low bits).
-    template <int Bits>
-    __device__ inline unsigned code_at(const u32x4 &w, int e)
-    {
-      const int bit = e * Bits;
-      const unsigned word = bit < 32 ? w.x : w.y;
-      return (word >> (bit & 31)) & ((1u << Bits) - 1);
-    }
-
     __device__ inline std::uint16_t half_of(const u32x4 &w, int e)
     {
       const unsigned word = e < 2 ? w.x : e < 4 ? w.y : e < 6 ? w.z : w.w;
       return static_cast<std::uint16_t>(word >> (16 * (e & 1)));
     }
 
-    __device__ inline std::uint16_t dequant(unsigned code, std::uint16_t s, std::uint16_t z)
+    // The 8 fp16 K and V values of a fetch, as words: FP16 rows as read,
+    // zeros for nothing read, codes dequantised in packed fp16 (one rounding
+    // of code * scale + zero). Every lane that reaches the quantised branch
+    // holds the same tier (a sealed page's).
+    __device__ inline void values_of(const Fetched &f, u32x4 &k, u32x4 &v)
     {
-      return __half_as_ushort(
-          __float2half_rn(fmaf(static_cast<float>(code), h2f(s), h2f(z))));
-    }
-
-    // The 8 fp16 K and V values of a fetch.
-    __device__ inline void values_of(const Fetched &f, std::uint16_t k[8], std::uint16_t v[8])
-    {
-      if (f.tier == kFP16 || f.tier < 0)
+      if (f.tier == kFP16)
       {
-        for (int e = 0; e < 8; ++e)
-        {
-          k[e] = half_of(f.k, e);
-          v[e] = half_of(f.v, e);
-        }
+        k = f.k;
+        v = f.v;
         return;
       }
-      const std::uint16_t vs = static_cast<std::uint16_t>(f.vsz);
-      const std::uint16_t vz = static_cast<std::uint16_t>(f.vsz >> 16);
-      for (int e = 0; e < 8; ++e)
+      if (f.tier < 0)
       {
-        unsigned kc, vc;
-        if (f.tier == kINT8)
-        {
-          kc = code_at<8>(f.k, e);
-          vc = code_at<8>(f.v, e);
-        }
-        else if (f.tier == kINT4)
-        {
-          kc = code_at<4>(f.k, e);
-          vc = code_at<4>(f.v, e);
-        }
-        else
-        {
-          kc = code_at<2>(f.k, e);
-          vc = code_at<2>(f.v, e);
-        }
-        k[e] = dequant(kc, half_of(f.ks, e), half_of(f.kz, e));
-        v[e] = dequant(vc, vs, vz);
+        k = u32x4{0, 0, 0, 0};
+        v = u32x4{0, 0, 0, 0};
+        return;
+      }
+      const unsigned sp = (f.vsz & 0xFFFFu) * 0x10001u;
+      const unsigned zp = (f.vsz >> 16) * 0x10001u;
+      const u32x4 vs2 = {sp, sp, sp, sp};
+      const u32x4 vz2 = {zp, zp, zp, zp};
+      switch (__builtin_amdgcn_readfirstlane(f.tier))
+      {
+      case kINT8:
+        k = __builtin_bit_cast(u32x4, dq::dequant_step<8>(f.k.x, f.k.y, f.ks, f.kz));
+        v = __builtin_bit_cast(u32x4, dq::dequant_step<8>(f.v.x, f.v.y, vs2, vz2));
+        break;
+      case kINT4:
+        k = __builtin_bit_cast(u32x4, dq::dequant_step<4>(f.k.x, 0u, f.ks, f.kz));
+        v = __builtin_bit_cast(u32x4, dq::dequant_step<4>(f.v.x, 0u, vs2, vz2));
+        break;
+      default:
+        k = __builtin_bit_cast(u32x4, dq::dequant_step<2>(f.k.x, 0u, f.ks, f.kz));
+        v = __builtin_bit_cast(u32x4, dq::dequant_step<2>(f.v.x, 0u, vs2, vz2));
+        break;
       }
     }
 
@@ -357,16 +358,17 @@ namespace mi
       }
     }
 
-    // Writes a fetch into a stage: K (hi, and lo with a bias) row t, and V^T.
+    // Writes a fetch into a stage: K (hi, and lo with a bias) row t, and V
+    // chunk (t, c).
     template <int HD, bool kBias>
     __device__ inline void commit(const Fetched &f, const f32x4 cs[4], const u32x4 &b_first,
                                   const u32x4 &b_second, int t, int c, std::uint16_t *stage)
     {
       constexpr int KS = Geometry<HD>::kKS;
-      std::uint16_t k[8], v[8];
-      values_of(f, k, v);
+      u32x4 kw, vw;
+      values_of(f, kw, vw);
       std::uint16_t *k_hi = stage;
-      std::uint16_t *vt = stage + (kBias ? 2 : 1) * kP * KS;
+      std::uint16_t *v_chunks = stage + (kBias ? 2 : 1) * kP * KS;
       if constexpr (kBias)
       {
         std::uint16_t *k_lo = stage + kP * KS;
@@ -377,7 +379,7 @@ namespace mi
           rotated_bias8(b_first, b_second, cs, 8 * c < HD / 2, rb);
           for (int e = 0; e < 8; ++e)
           {
-            const float x = h2f(k[e]) + rb[e];
+            const float x = h2f(half_of(kw, e)) + rb[e];
             const __half h = __float2half_rn(x);
             hi[e] = __half_as_ushort(h);
             lo[e] = __half_as_ushort(__float2half_rn(x - __half2float(h)));
@@ -405,18 +407,9 @@ namespace mi
       }
       else
       {
-        u32x4 w;
-        w.x = k[0] | (unsigned(k[1]) << 16);
-        w.y = k[2] | (unsigned(k[3]) << 16);
-        w.z = k[4] | (unsigned(k[5]) << 16);
-        w.w = k[6] | (unsigned(k[7]) << 16);
-        *reinterpret_cast<u32x4 *>(k_hi + t * KS + 8 * c) = w;
+        *reinterpret_cast<u32x4 *>(k_hi + t * KS + 8 * c) = kw;
       }
-      const int slot = v_slot(t);
-      for (int e = 0; e < 8; ++e)
-      {
-        vt[(8 * c + e) * kVS + slot] = v[e];
-      }
+      *reinterpret_cast<u32x4 *>(v_chunks + 8 * (c * kP + t)) = vw;
     }
 
     // The (page, version) items a workgroup visits, in order: a page before
@@ -441,15 +434,34 @@ namespace mi
       }
     }
 
-    template <int HD, int TPW, bool kBias>
+    // The (page, version) items of a step, item j in element j: its table
+    // entry, and whether it has keys to read (inside the workgroup's pages,
+    // not an unread page). Vectors, not arrays of structures, so that a
+    // thread's item index, which varies across the workgroup, selects in
+    // registers.
+    typedef int i32x2 __attribute__((ext_vector_type(2)));
+    typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+    constexpr int kMaxStepPages = 2;
+
+    struct Step
+    {
+      i32x2 p;
+      i32x2 version;
+      i32x2 tier;
+      i32x2 live;
+      u64x2 page;
+    };
+
+    template <int HD, int TPW, int NP, bool kBias>
     __global__ void __launch_bounds__(kMaxWaves * 64)
         prefill_kernel(PrefillArgs a)
     {
       constexpr int KS = Geometry<HD>::kKS;
-      constexpr int kChunks = Geometry<HD>::kChunks;
       constexpr int kItems = Geometry<HD>::kItems;
       constexpr int kStage = stage_halves<HD, kBias>();
-      constexpr int kFetch = (kItems + kMinThreads - 1) / kMinThreads; // fetches a thread holds
+      constexpr int kStepItems = NP * kItems;
+      constexpr int kFetch = (kStepItems + kMinThreads - 1) / kMinThreads; // fetches a thread holds
+      static_assert(NP >= 1 && NP <= kMaxStepPages, "pages a step");
       extern __shared__ std::uint16_t smem[];
 
       const int lane = threadIdx.x & 63;
@@ -476,7 +488,8 @@ namespace mi
       half8 qf[TPW][HD / 32];
       f32x4 o[TPW][HD / 16];
       float m[TPW];
-      float l[TPW];
+      float l[TPW]; // in units of 2^-14 (the probabilities' scale)
+      #pragma unroll
       for (int tt = 0; tt < TPW; ++tt)
       {
         const int r = (wave + tt * waves) * 16 + col;
@@ -511,13 +524,15 @@ namespace mi
       const int p_begin = split * a.pages_per_split;
       const int p_end = min(p_begin + a.pages_per_split, o_hi + 1);
 
-      // Staging items run key-fastest: item = key + 32 * chunk. A wave then
-      // stores V^T rows of two chunks for all 32 keys at once, 32 distinct
-      // LDS dwords a store, where key-major order put several chunks on one
-      // bank. A thread's items keep their channel chunks from page to page,
-      // so its bias channels are loaded once.
+      // Staging items run key-fastest within a page: item = key + 32 *
+      // chunk, page j of the step at j * kItems. A wave then stores V^T rows
+      // of two chunks for all 32 keys at once, 32 distinct LDS dwords a
+      // store, where key-major order put several chunks on one bank. A
+      // thread's items keep their channel chunks from step to step, so its
+      // bias channels are loaded once.
       u32x4 b_first[kFetch];
       u32x4 b_second[kFetch];
+      #pragma unroll
       for (int u = 0; u < kFetch; ++u)
       {
         b_first[u] = u32x4{0, 0, 0, 0};
@@ -525,9 +540,9 @@ namespace mi
         const int item = threadIdx.x + u * threads;
         if constexpr (kBias)
         {
-          if (item < kItems)
+          if (item < kStepItems)
           {
-            const int d0 = 8 * (item / kP);
+            const int d0 = 8 * ((item % kItems) / kP);
             const int j0 = d0 < HD / 2 ? d0 : d0 - HD / 2;
             const std::uint16_t *b = a.k_bias + static_cast<std::size_t>(kvh) * HD;
             b_first[u] = *reinterpret_cast<const u32x4 *>(b + j0);
@@ -536,161 +551,234 @@ namespace mi
         }
       }
 
-      Fetched f[kFetch];
-      f32x4 cs[kFetch][4];
-      const auto fetch_item = [&](int p, int version, const Entry &entry) {
-        for (int u = 0; u < kFetch; ++u)
+      // The items of the steps, NP a step, in visiting order from a cursor.
+      int cursor_p = p_begin;
+      int cursor_v = first_version(cursor_p, causal, o_hi);
+      const auto take = [&](Step &st) {
+        st.p = i32x2{p_end, p_end};
+        st.version = i32x2{kOwn, kOwn};
+        st.tier = i32x2{kFP16, kFP16};
+        st.live = i32x2{0, 0};
+        st.page = u64x2{0ull, 0ull};
+#pragma unroll
+        for (int j = 0; j < NP; ++j)
         {
-          const int item = threadIdx.x + u * threads;
-          if (item < kItems)
-          {
-            const int t = item % kP;
-            const int c = item / kP;
-            fetch<HD>(a, p, version, entry, kvh, t, c, f[u]);
-            if constexpr (kBias)
-            {
-              if (p * kP + t < a.seq_k)
-              {
-                fetch_rope<HD>(a.rope, p * kP + t, 8 * c, cs[u]);
-              }
-            }
-          }
-        }
-      };
-      const auto commit_item = [&](std::uint16_t *stage) {
-        for (int u = 0; u < kFetch; ++u)
-        {
-          const int item = threadIdx.x + u * threads;
-          if (item < kItems)
-          {
-            commit<HD, kBias>(f[u], cs[u], b_first[u], b_second[u], item % kP, item / kP, stage);
-          }
+          const Entry e = entry_of(a.kv, cursor_p, cursor_v, p_end);
+          st.p[j] = cursor_p;
+          st.version[j] = cursor_v;
+          st.tier[j] = e.tier;
+          st.page[j] = e.page;
+          advance(cursor_p, cursor_v, causal, o_lo, o_hi);
         }
       };
       // Whether an item has anything to read: an unread sealed page has not.
-      const auto readable = [&](int version, const Entry &entry) {
-        return !(causal && version == kSealed && entry.tier == kUnreadPage);
+      const auto settle = [&](Step &st) {
+#pragma unroll
+        for (int j = 0; j < NP; ++j)
+        {
+          st.live[j] = st.p[j] < p_end &&
+                       !(causal && st.version[j] == kSealed && st.tier[j] == kUnreadPage);
+        }
       };
 
-      // The item being computed, the next (being fetched) and the one after
-      // (its table entry in flight).
-      int p = p_begin;
-      int version = first_version(p, causal, o_hi);
-      Entry entry = entry_of(a.kv, p, version, p_end);
-      int p1 = p, v1 = version;
-      advance(p1, v1, causal, o_lo, o_hi);
-      Entry e1 = entry_of(a.kv, p1, v1, p_end);
-      int p2 = p1, v2 = v1;
-      advance(p2, v2, causal, o_lo, o_hi);
-      Entry e2 = entry_of(a.kv, p2, v2, p_end);
-      int buf = 0;
-      if (p < p_end && readable(version, entry))
-      {
-        fetch_item(p, version, entry);
-        commit_item(smem);
-      }
-      __syncthreads();
-
-      while (p < p_end)
-      {
-        int p3 = p2, v3 = v2;
-        advance(p3, v3, causal, o_lo, o_hi);
-        const Entry e3 = entry_of(a.kv, p3, v3, p_end);
-        const bool has_next = p1 < p_end && readable(v1, e1);
-        if (has_next)
+      Fetched f[kFetch];
+      f32x4 cs[kFetch][4];
+      const auto fetch_step = [&](const Step &st) {
+        #pragma unroll
+        for (int u = 0; u < kFetch; ++u)
         {
-          fetch_item(p1, v1, e1);
-        }
-        if (computes && readable(version, entry))
-        {
-          const std::uint16_t *stage = smem + buf * kStage;
-          const std::uint16_t *k_hi = stage;
-          const std::uint16_t *k_lo = stage + kP * KS;
-          const std::uint16_t *vt = stage + (kBias ? 2 : 1) * kP * KS;
-          // Whether every row of the workgroup sees all 32 keys: a sealed page
-          // before every row's own page, or (no sealing) a page wholly before
-          // the first query. Rows past the chunk's end see them too; their
-          // outputs are never stored.
-          const bool full = causal ? version == kSealed && p < o_lo
-                                   : p * kP + kP - 1 <= shift + q_first;
-          // Each row's last visible key position on this item (-1: none).
-          int limit[TPW];
-          for (int tt = 0; tt < TPW; ++tt)
+          const int item = threadIdx.x + u * threads;
+          if (item < kStepItems)
           {
-            if (!causal)
+            const int j = item / kItems;
+            const int t = (item % kItems) % kP;
+            const int c = (item % kItems) / kP;
+            const int p = st.p[j];
+            f[u].tier = -1;
+            if (st.live[j])
             {
-              limit[tt] = pos[tt];
-            }
-            else if (version == kSealed)
-            {
-              limit[tt] = p < own[tt] ? 0x7fffffff : -1;
-            }
-            else
-            {
-              limit[tt] = p == own[tt] ? pos[tt] : -1;
-            }
-          }
-          // S^T = K . Q^T, two 16-key tiles.
-          f32x4 s[TPW][2];
-          for (int tt = 0; tt < TPW; ++tt)
-          {
-            s[tt][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            s[tt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-          }
-          for (int kt = 0; kt < 2; ++kt)
-          {
-            for (int cc = 0; cc < HD / 32; ++cc)
-            {
-              const int off = (16 * kt + col) * KS + 32 * cc + 8 * g;
-              const half8 ka = as_half8(*reinterpret_cast<const u32x4 *>(k_hi + off));
-              for (int tt = 0; tt < TPW; ++tt)
-              {
-                s[tt][kt] = mfma(ka, qf[tt][cc], s[tt][kt]);
-              }
+              const Entry e{st.page[j], st.tier[j]};
+              fetch<HD>(a, p, st.version[j], e, kvh, t, c, f[u]);
               if constexpr (kBias)
               {
-                const half8 kb = as_half8(*reinterpret_cast<const u32x4 *>(k_lo + off));
-                for (int tt = 0; tt < TPW; ++tt)
+                if (p * kP + t < a.seq_k)
                 {
-                  s[tt][kt] = mfma(kb, qf[tt][cc], s[tt][kt]);
+                  fetch_rope<HD>(a.rope, p * kP + t, 8 * c, cs[u]);
                 }
               }
             }
           }
-          // Online softmax per row, then P^T as the B operand of PV.
-          half8 p_hi[TPW], p_lo[TPW];
+        }
+      };
+      const auto commit_step = [&](const Step &st, std::uint16_t *stages) {
+        #pragma unroll
+        for (int u = 0; u < kFetch; ++u)
+        {
+          const int item = threadIdx.x + u * threads;
+          if (item < kStepItems)
+          {
+            const int j = item / kItems;
+            if (st.live[j])
+            {
+              commit<HD, kBias>(f[u], cs[u], b_first[u], b_second[u], (item % kItems) % kP,
+                                (item % kItems) / kP, stages + j * kStage);
+            }
+          }
+        }
+      };
+
+      // The step being computed, the next (being fetched) and the one after
+      // (its table entries in flight).
+      Step cur, nxt, nn;
+      take(cur);
+      take(nxt);
+      settle(cur);
+      int buf = 0;
+      fetch_step(cur);
+      commit_step(cur, smem);
+      __syncthreads();
+
+      while (cur.p[0] < p_end)
+      {
+        take(nn);
+        settle(nxt);
+        bool has_next = false;
+#pragma unroll
+        for (int j = 0; j < NP; ++j)
+        {
+          has_next = has_next || nxt.live[j];
+        }
+        if (has_next)
+        {
+          fetch_step(nxt);
+        }
+        if (computes)
+        {
+          const std::uint16_t *stages = smem + buf * NP * kStage;
+          // S^T = K . Q^T, two 16-key tiles a page.
+          f32x4 s[TPW][2 * NP];
+          #pragma unroll
           for (int tt = 0; tt < TPW; ++tt)
           {
-            float sc[8];
-            float top = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2 * NP; ++kt)
+            {
+              s[tt][kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < NP; ++j)
+          {
+            if (!cur.live[j])
+            {
+              continue;
+            }
+            const std::uint16_t *k_hi = stages + j * kStage;
+            const std::uint16_t *k_lo = k_hi + kP * KS;
             for (int kt = 0; kt < 2; ++kt)
             {
-              for (int i = 0; i < 4; ++i)
+              for (int cc = 0; cc < HD / 32; ++cc)
               {
-                const int j = p * kP + key_of(kt, g, i);
-                const float x = s[tt][kt][i] * a.scale2;
-                const float v = full || j <= limit[tt] ? x : -INFINITY;
-                sc[4 * kt + i] = v;
-                top = fmaxf(top, v);
+                const int off = (16 * kt + col) * KS + 32 * cc + 8 * g;
+                const half8 ka = as_half8(*reinterpret_cast<const u32x4 *>(k_hi + off));
+                #pragma unroll
+                for (int tt = 0; tt < TPW; ++tt)
+                {
+                  s[tt][2 * j + kt] = mfma(ka, qf[tt][cc], s[tt][2 * j + kt]);
+                }
+                if constexpr (kBias)
+                {
+                  const half8 kb = as_half8(*reinterpret_cast<const u32x4 *>(k_lo + off));
+                  #pragma unroll
+                  for (int tt = 0; tt < TPW; ++tt)
+                  {
+                    s[tt][2 * j + kt] = mfma(kb, qf[tt][cc], s[tt][2 * j + kt]);
+                  }
+                }
               }
             }
-            top = lane_max32(lane_max16(top));
+          }
+          // Online softmax per row over the step's keys, then P^T as the B
+          // operand of PV. An item every row sees whole (a sealed page before
+          // every row's own page, or without sealing a page wholly before the
+          // first query) is not masked; a dead item is masked whole.
+          half8 p_hi[TPW][NP], p_lo[TPW][NP];
+          #pragma unroll
+          for (int tt = 0; tt < TPW; ++tt)
+          {
+            float sc[8 * NP];
+            float top = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < NP; ++j)
+            {
+              const int p = cur.p[j];
+              const bool live = cur.live[j];
+              const bool sealed = cur.version[j] == kSealed;
+              const bool full = causal ? sealed && p < o_lo
+                                       : p * kP + kP - 1 <= shift + q_first;
+              // The row's last visible key position on this item (-1: none).
+              int limit;
+              if (!causal)
+              {
+                limit = pos[tt];
+              }
+              else if (sealed)
+              {
+                limit = p < own[tt] ? 0x7fffffff : -1;
+              }
+              else
+              {
+                limit = p == own[tt] ? pos[tt] : -1;
+              }
+              if (!live)
+              {
+                limit = -1;
+              }
+              if (live && full)
+              {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                {
+                  sc[8 * j + e] = s[tt][2 * j + e / 4][e % 4];
+                  top = fmaxf(top, sc[8 * j + e]);
+                }
+              }
+              else
+              {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                {
+                  const int key = p * kP + key_of(e / 4, g, e % 4);
+                  sc[8 * j + e] = key <= limit ? s[tt][2 * j + e / 4][e % 4] : -INFINITY;
+                  top = fmaxf(top, sc[8 * j + e]);
+                }
+              }
+            }
+            // Scores to base 2: the scale is positive, so the scaled maximum
+            // is the maximum scaled.
+            top = lane_max32(lane_max16(top)) * a.scale2;
             const float m_new = fmaxf(m[tt], top);
             const float from = m_new == -INFINITY ? 0.0f : m_new;
             const float keep = exp2_fast(m[tt] - from);
             m[tt] = m_new;
+            // The probabilities come out x2^14 (the shift in the exponent).
+            const float bias2 = 14.0f - from;
             float sum = 0.0f;
-            for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int j = 0; j < NP; ++j)
             {
-              const float pe = exp2_fast(sc[e] - from);
-              sum += pe;
-              const float ps = pe * kPScale;
-              const _Float16 h = static_cast<_Float16>(ps);
-              p_hi[tt][e] = h;
-              p_lo[tt][e] = static_cast<_Float16>(ps - static_cast<float>(h));
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+              {
+                const float ps = exp2_fast(fmaf(sc[8 * j + e], a.scale2, bias2));
+                sum += ps;
+                const _Float16 h = static_cast<_Float16>(ps);
+                p_hi[tt][j][e] = h;
+                p_lo[tt][j][e] = static_cast<_Float16>(ps - static_cast<float>(h));
+              }
             }
             l[tt] = l[tt] * keep + sum;
-            // Most pages leave every row's maximum where it was: rescale only
+            // Most steps leave every row's maximum where it was: rescale only
             // when some lane's moved.
             if (__any(keep != 1.0f))
             {
@@ -700,36 +788,50 @@ namespace mi
               }
             }
           }
-          // O^T += V^T . P^T.
-          for (int dt = 0; dt < HD / 16; ++dt)
+          // O^T += V^T . P^T, the high parts of every row tile before the
+          // low parts, so that no product waits on the one before it.
+#pragma unroll
+          for (int j = 0; j < NP; ++j)
           {
-            const half8 va = as_half8(
-                *reinterpret_cast<const u32x4 *>(vt + (16 * dt + col) * kVS + 8 * g));
-            for (int tt = 0; tt < TPW; ++tt)
+            if (!cur.live[j])
             {
-              o[tt][dt] = mfma(va, p_hi[tt], o[tt][dt]);
-              o[tt][dt] = mfma(va, p_lo[tt], o[tt][dt]);
+              continue;
+            }
+            // Lane (g, col) reads keys 4g .. 4g+3 and 16+4g .. 16+4g+3 of
+            // channel 16 dt + col: P's key order.
+            const std::uint16_t *vt = stages + j * kStage + (kBias ? 2 : 1) * kP * KS +
+                                      8 * (((col & 3) >> 1) * kP + 4 * g + (col >> 2)) +
+                                      4 * (col & 1);
+            for (int dt = 0; dt < HD / 16; ++dt)
+            {
+              const uint2 x0 = tr16(vt + 8 * (2 * dt * kP));
+              const uint2 x1 = tr16(vt + 8 * (2 * dt * kP + 16));
+              const half8 va = as_half8(u32x4{x0.x, x0.y, x1.x, x1.y});
+              #pragma unroll
+              for (int tt = 0; tt < TPW; ++tt)
+              {
+                o[tt][dt] = mfma(va, p_hi[tt][j], o[tt][dt]);
+              }
+              #pragma unroll
+              for (int tt = 0; tt < TPW; ++tt)
+              {
+                o[tt][dt] = mfma(va, p_lo[tt][j], o[tt][dt]);
+              }
             }
           }
         }
         if (has_next)
         {
-          commit_item(smem + (buf ^ 1) * kStage);
+          commit_step(nxt, smem + (buf ^ 1) * NP * kStage);
         }
         __syncthreads();
         buf ^= 1;
-        p = p1;
-        version = v1;
-        entry = e1;
-        p1 = p2;
-        v1 = v2;
-        e1 = e2;
-        p2 = p3;
-        v2 = v3;
-        e2 = e3;
+        cur = nxt;
+        nxt = nn;
       }
 
       // Each row's sum over its four lanes; then the output or the run's slot.
+      #pragma unroll
       for (int tt = 0; tt < TPW; ++tt)
       {
         float total = l[tt];
@@ -740,7 +842,7 @@ namespace mi
         }
         if (a.partials == nullptr)
         {
-          const float inv = kPUnscale / total;
+          const float inv = 1.0f / total;
           std::uint16_t *dst = a.out + qrow[tt] * token_stride +
                                static_cast<std::size_t>(head[tt]) * HD + 4 * g;
           for (int dt = 0; dt < HD / 16; ++dt)
@@ -759,7 +861,7 @@ namespace mi
           if (g == 0)
           {
             slot[0] = m[tt]; // base 2, -inf for a run that saw no key
-            slot[1] = total;
+            slot[1] = total * kPUnscale;
           }
           for (int dt = 0; dt < HD / 16; ++dt)
           {
@@ -846,11 +948,11 @@ namespace mi
     // set): the keys split into runs of whole pages when the attention
     // workspace is given and the query blocks alone would not fill every
     // workgroup slot the kernel's occupancy allows, then a combine.
-    template <int HD, int TPW, bool kBias>
+    template <int HD, int TPW, int NP, bool kBias>
     void run(PrefillArgs args, float *partials, int qblocks, int waves, hipStream_t stream)
     {
-      const std::size_t lds = 2 * stage_halves<HD, kBias>() * sizeof(std::uint16_t);
-      auto kernel = prefill_kernel<HD, TPW, kBias>;
+      const std::size_t lds = 2 * NP * stage_halves<HD, kBias>() * sizeof(std::uint16_t);
+      auto kernel = prefill_kernel<HD, TPW, NP, kBias>;
       if (lds > 64 * 1024)
       {
         hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
@@ -894,11 +996,12 @@ namespace mi
     {
       if (bias)
       {
-        run<HD, TPW, true>(args, partials, qblocks, waves, stream);
+        run<HD, TPW, 1, true>(args, partials, qblocks, waves, stream);
       }
       else
       {
-        run<HD, TPW, false>(args, partials, qblocks, waves, stream);
+        // Two pages a barrier where the registers allow (no key bias).
+        run<HD, TPW, HD == 64 ? 2 : 1, false>(args, partials, qblocks, waves, stream);
       }
     }
 
