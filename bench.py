@@ -546,6 +546,49 @@ def prefill_chunks(m, stream, steps, warmup, seed=5):
             "config": "llama-3.2-1b 32q/8kv/hd64, 16K in 2K chunks, tiers FP16/INT8/INT4 30/40/30 %"}
 
 
+# ---- the batch quantiser ---------------------------------------------------------------------
+
+def quantise_batches(m, stream, steps, warmup, seed=4):
+    """The batch quantiser (mi_quantise_pages; reference quant.cu:419-436)
+    at the 1.5B page shape (2 KV heads x head_dim 128, 32 tokens): N FP16
+    pages quantised to a tier in one launch, timed as a HIP graph. Bytes a
+    launch must move: every FP16 page read (32 KiB) and every quantised page
+    written (its layout's page_bytes)."""
+    from microinfer import workloads as w
+    shape = w.QWEN_15B
+    kv, hd = shape.kv_heads, shape.head_dim
+    fp16 = m.device.page_bytes(P, shape.kv_width)
+    most = 4096
+    rng = np.random.default_rng(seed)
+    k, v = w.kv_rows(rng, most * P, shape, w.outlier_channels(rng, shape.kv_width))
+    pages = np.concatenate([k.reshape(most, P * shape.kv_width),
+                            v.reshape(most, P * shape.kv_width)], axis=1)
+    src = m._Storage(most * fp16)
+    m._h2d(src.ptr, pages.view(np.uint8).reshape(-1))
+    out = {}
+    for tier, n in ((2, 409), (1, 409), (3, 102), (2, 4096), (1, 4096), (3, 4096)):
+        pb = m.quantised_page_layout(tier, kv, hd, P)["page_bytes"]
+        dst = m._Storage(n * pb)
+        table = np.array([src.ptr + i * fp16 for i in range(n)] +
+                         [dst.ptr + i * pb for i in range(n)], np.uint64)
+        tab = m._Storage(table.nbytes)
+        m._h2d(tab.ptr, table)
+
+        def body():
+            m._check(m.lib.mi_quantise_pages(tab.ptr, tab.ptr + 8 * n, n, tier, P, kv, hd, None))
+
+        # Launches of tens of microseconds: enough replays that the clocks
+        # have risen and the timed region is not a handful of launches.
+        ms = timed_graph(m, stream, body, max(steps, 400), max(warmup, 400))
+        moved = n * (fp16 + pb)
+        gbs = moved / (ms * 1e-3) / 1e9
+        name = {1: "INT8", 2: "INT4", 3: "INT2"}[tier]
+        out[f"{name}_{n}"] = {"us": round(ms * 1e3, 2), "gb_per_s": round(gbs, 1),
+                              "frac_hbm": round(gbs / PEAK_GBS, 4), "bytes": moved}
+        log(f"quantise {n} pages to {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+    return out
+
+
 # ---- config 4: the requantisation plan against its host-link bound ---------------------------
 
 def link_rates(m, nbytes=256 << 20, reps=3):
@@ -786,7 +829,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=None, help="fewer layers, for a quick look")
-    ap.add_argument("--legs", default="decode,prefill,config2,step,requant,cpu",
+    ap.add_argument("--legs", default="decode,prefill,config2,step,quantise,requant,cpu",
                     help="the legs to run (comma list; decode is the headline)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-requant", action="store_true")
@@ -860,6 +903,8 @@ def main() -> int:
         steps_out["reference_rtx4050_tokens_per_s"] = {"qwen2.5-1.5b_fp16_32k": 29.5,
                                                        "qwen2.5-1.5b_fp16_16k": 40.1}
 
+    quantise = quantise_batches(m, stream, args.steps, args.warmup) if "quantise" in legs else None
+
     requant = None
     if "requant" in legs:
         t0 = time.perf_counter()
@@ -895,7 +940,8 @@ def main() -> int:
 
     if ms is None:
         print(json.dumps({"metric": METRIC, "value": None, "legs": sorted(legs), "config2": c2,
-                          "decode_step": steps_out, "requant": requant, "cpu_baseline": cpu}),
+                          "decode_step": steps_out, "quantise": quantise, "requant": requant,
+                          "cpu_baseline": cpu}),
               flush=True)
         return 0
     result = {
@@ -935,6 +981,7 @@ def main() -> int:
         "config2": c2,
         "decode_step": steps_out,
         "cpu_baseline": cpu,
+        "quantise": quantise,
         "requant": requant,
         "prefill": prefill,
     }

@@ -62,6 +62,12 @@ namespace mi
   // 64 elements, nothing staged); any other shape the LDS one.
   void launch_requant_refs(const RefPair *pairs, int count, int tier, const PageSpaces &spaces,
                            int page_tokens, int kv_heads, int head_dim, hipStream_t stream);
+  // The register quantiser over pages named by address (launch_quantise_pages'
+  // arguments): false, launching nothing, for a shape it does not take
+  // (not 32-token pages at head_dim 64/128, or rows not 16-byte aligned).
+  bool launch_quantise_registers(const void *const *rows, void *const *pages, const void *row0,
+                                 void *page0, std::ptrdiff_t values_offset, int count, int tier,
+                                 int page_tokens, int kv_heads, int head_dim, hipStream_t stream);
 
   // A job on one page's rows, as a cache's store makes them. A page's keys
   // are rows of kv_heads * head_dim fp16; rows [0, split) come from k_lo /

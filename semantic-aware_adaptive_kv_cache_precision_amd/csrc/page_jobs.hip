@@ -105,20 +105,55 @@ namespace mi
     };
 
     // Eight codes of one 16-byte run (eight fp16 values), packed the first
-    // lowest: 8 (INT8), 4 (INT4) or 2 (INT2) bytes.
+    // lowest: 8 (INT8), 4 (INT4) or 2 (INT2) bytes. The codes are exact
+    // integers in floats: two INT4 (or four INT2) codes are combined into
+    // one byte's value exactly (q0 + 16 q1, ...) and each byte is placed by
+    // v_cvt_pk_u8_f32 (of an integer: no rounding).
     template <int Bits>
     __device__ __forceinline__ unsigned long long codes8(const uint4 &v, const float (&lo)[8],
-                                                         const float (&scale)[8])
+                                                         const float (&scale)[8],
+                                                         const float (&inv)[8])
     {
-      unsigned long long packed = 0;
+      float x[8], q[8];
 #pragma unroll
       for (int c = 0; c < 8; ++c)
       {
-        packed |= static_cast<unsigned long long>(
-                      quant_core::code_of<Bits>(half_at(v, c), lo[c], scale[c]))
-                  << (Bits * c);
+        x[c] = half_at(v, c);
       }
-      return packed;
+      quant_core::quotients_of<Bits>(x, lo, scale, inv, q);
+      if constexpr (Bits == 8)
+      {
+        unsigned w0 = 0, w1 = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+        {
+          w0 = __builtin_amdgcn_cvt_pk_u8_f32(q[c], c, w0);
+          w1 = __builtin_amdgcn_cvt_pk_u8_f32(q[4 + c], c, w1);
+        }
+        return static_cast<unsigned long long>(w0) | (static_cast<unsigned long long>(w1) << 32);
+      }
+      else if constexpr (Bits == 4)
+      {
+        unsigned w = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+        {
+          w = __builtin_amdgcn_cvt_pk_u8_f32(fmaf(q[2 * c + 1], 16.0f, q[2 * c]), c, w);
+        }
+        return w;
+      }
+      else
+      {
+        unsigned w = 0;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+        {
+          const float b = fmaf(q[4 * c + 3], 64.0f,
+                               fmaf(q[4 * c + 2], 16.0f, fmaf(q[4 * c + 1], 4.0f, q[4 * c])));
+          w = __builtin_amdgcn_cvt_pk_u8_f32(b, c, w);
+        }
+        return w;
+      }
     }
 
     template <int Bits>
@@ -142,15 +177,20 @@ namespace mi
     // fmaf(code, scale, zero) to fp16 for eight codes, as dequantise_page.
     template <int Bits>
     __device__ __forceinline__ uint4 round8(const uint4 &v, const float (&lo)[8],
-                                            const float (&scale)[8])
+                                            const float (&scale)[8], const float (&inv)[8])
     {
+      float x[8], q[8];
       unsigned h[8];
 #pragma unroll
       for (int c = 0; c < 8; ++c)
       {
-        const float code =
-            static_cast<float>(quant_core::code_of<Bits>(half_at(v, c), lo[c], scale[c]));
-        h[c] = half_of(fmaf(code, scale[c], lo[c]));
+        x[c] = half_at(v, c);
+      }
+      quant_core::quotients_of<Bits>(x, lo, scale, inv, q);
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+      {
+        h[c] = half_of(fmaf(q[c], scale[c], lo[c]));
       }
       return uint4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
                    h[6] | (h[7] << 16)};
@@ -189,23 +229,22 @@ namespace mi
         lo[c] = INFINITY;
         hi[c] = -INFINITY;
       }
+      // The eight rows stay in registers from the range to the codes.
+      uint4 raw[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
       {
-        uint4 raw[8];
+        raw[i] = load16(keys.row(8 * g + i) + 8 * j);
+      }
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 8; ++i)
+      {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
         {
-          raw[i] = load16(keys.row(8 * g + i) + 8 * j);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-        {
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-          {
-            const float x = half_at(raw[i], c);
-            lo[c] = fminf(lo[c], x);
-            hi[c] = fmaxf(hi[c], x);
-          }
+          const float x = half_at(raw[i], c);
+          lo[c] = fminf(lo[c], x);
+          hi[c] = fmaxf(hi[c], x);
         }
       }
       // The chunk's four row groups: lanes that differ in the low two bits.
@@ -217,13 +256,14 @@ namespace mi
         lo[c] = fminf(lo[c], __shfl_xor(lo[c], 2));
         hi[c] = fmaxf(hi[c], __shfl_xor(hi[c], 2));
       }
-      float scale[8];
+      float scale[8], inv[8];
       unsigned sword[4] = {0, 0, 0, 0}, zword[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int c = 0; c < 8; ++c)
       {
-        const std::uint16_t s = scale_bits_of(lo[c], hi[c], Bits);
+        const std::uint16_t s = quant_core::scale_bits_fast(lo[c], hi[c], Bits);
         scale[c] = f16_bits(s);
+        inv[c] = quant_core::inverse_of(scale[c]);
         sword[c / 2] |= static_cast<unsigned>(s) << (16 * (c % 2));
         zword[c / 2] |= half_of(lo[c]) << (16 * (c % 2));
       }
@@ -236,24 +276,24 @@ namespace mi
           store16(reinterpret_cast<std::uint16_t *>(dst + L.key_zeros) + 8 * j,
                   uint4{zword[0], zword[1], zword[2], zword[3]});
         }
-#pragma unroll 1
+#pragma unroll
         for (int i = 0; i < 8; ++i)
         {
           const int t = 8 * g + i;
-          const uint4 v = load16(keys.row(t) + 8 * j);
           const std::size_t e = static_cast<std::size_t>(t) * W + 8 * j; // first element
-          store_codes8<Bits>(dst + L.key_codes + e * Bits / 8, codes8<Bits>(v, lo, scale));
+          store_codes8<Bits>(dst + L.key_codes + e * Bits / 8,
+                             codes8<Bits>(raw[i], lo, scale, inv));
         }
         return;
       }
       // Round trip: each code back to fp16, as dequantise_page gives it.
       auto *out = reinterpret_cast<std::uint16_t *>(dst);
-#pragma unroll 1
+#pragma unroll
       for (int i = 0; i < 8; ++i)
       {
         const int t = 8 * g + i;
-        const uint4 v = load16(keys.row(t) + 8 * j);
-        store16(out + static_cast<std::size_t>(t) * W + 8 * j, round8<Bits>(v, lo, scale));
+        store16(out + static_cast<std::size_t>(t) * W + 8 * j,
+                round8<Bits>(raw[i], lo, scale, inv));
       }
     }
 
@@ -285,23 +325,21 @@ namespace mi
         return;
       }
       float lo = INFINITY, hi = -INFINITY;
+      uint4 raw[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
       {
-        uint4 raw[8];
+        raw[i] = load16(src + 8 * i);
+      }
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 8; ++i)
+      {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
         {
-          raw[i] = load16(src + 8 * i);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-        {
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-          {
-            const float x = half_at(raw[i], c);
-            lo = fminf(lo, x);
-            hi = fmaxf(hi, x);
-          }
+          const float x = half_at(raw[i], c);
+          lo = fminf(lo, x);
+          hi = fmaxf(hi, x);
         }
       }
       if constexpr (HD == 128)
@@ -309,14 +347,16 @@ namespace mi
         lo = fminf(lo, __shfl_xor(lo, 1));
         hi = fmaxf(hi, __shfl_xor(hi, 1));
       }
-      const std::uint16_t sbits = scale_bits_of(lo, hi, Bits);
+      const std::uint16_t sbits = quant_core::scale_bits_fast(lo, hi, Bits);
       const float scale = f16_bits(sbits);
-      float los[8], scales[8];
+      const float inverse = quant_core::inverse_of(scale);
+      float los[8], scales[8], invs[8];
 #pragma unroll
       for (int c = 0; c < 8; ++c)
       {
         los[c] = lo;
         scales[c] = scale;
+        invs[c] = inverse;
       }
       if (emit == Emit::kCodes)
       {
@@ -327,20 +367,46 @@ namespace mi
           reinterpret_cast<std::uint16_t *>(dst + L.value_zeros)[group] =
               static_cast<std::uint16_t>(half_of(lo));
         }
+        // The run's 64 codes (8 Bits bytes), 16-byte aligned: whole
+        // 16-byte stores.
         std::uint8_t *at =
             dst + L.value_codes + (static_cast<std::size_t>(r) * W + ch0) * Bits / 8;
-#pragma unroll 1
+        unsigned words[2 * Bits];
+#pragma unroll
         for (int i = 0; i < 8; ++i)
         {
-          store_codes8<Bits>(at + i * Bits, codes8<Bits>(load16(src + 8 * i), los, scales));
+          const unsigned long long packed = codes8<Bits>(raw[i], los, scales, invs);
+          if constexpr (Bits == 8)
+          {
+            words[2 * i] = static_cast<unsigned>(packed);
+            words[2 * i + 1] = static_cast<unsigned>(packed >> 32);
+          }
+          else if constexpr (Bits == 4)
+          {
+            words[i] = static_cast<unsigned>(packed);
+          }
+          else if (i % 2 == 0)
+          {
+            words[i / 2] = static_cast<unsigned>(packed);
+          }
+          else
+          {
+            words[i / 2] |= static_cast<unsigned>(packed) << 16;
+          }
+        }
+#pragma unroll
+        for (int w = 0; w < 2 * Bits; w += 4)
+        {
+          *reinterpret_cast<uint4 *>(at + 4 * w) =
+              uint4{words[w], words[w + 1], words[w + 2], words[w + 3]};
         }
         return;
       }
-#pragma unroll 1
+#pragma unroll
       for (int i = 0; i < 8; ++i)
       {
         store16(out + static_cast<std::size_t>(r) * W + ch0 + 8 * i,
-                round8<Bits>(load16(src + 8 * i), los, scales));
+                round8<Bits>(raw[i], los, scales, invs));
       }
     }
 
@@ -392,7 +458,7 @@ namespace mi
     // The register quantiser over a batch: lane (blockIdx.x * 256 + tid)
     // is task (lane % W) of pair (lane / W).
     template <int Bits, int HD>
-    __global__ void __launch_bounds__(kThreads)
+    __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
         requant_refs_kernel(const RefPair *__restrict__ pairs, int count, PageSpaces s,
                             PageLayout L, int kv_heads)
     {
@@ -409,6 +475,33 @@ namespace mi
       const Rows keys{src, src, kP, W};
       const Rows values{src + static_cast<std::size_t>(kP) * W, src + static_cast<std::size_t>(kP) * W,
                         kP, W};
+      page_task<Bits, HD>(static_cast<int>(lane % W), keys, values, kv_heads, dst, L, Emit::kCodes,
+                          Emit::kCodes);
+    }
+
+    // The register quantiser over pages named by address (the batch API):
+    // page i's keys at rows[i] (or row0), its values `values_offset` bytes
+    // on, quantised into pages[i] (or page0); lane (blockIdx.x * 256 + tid)
+    // is task (lane % W) of page (lane / W).
+    template <int Bits, int HD>
+    __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+        quantise_ptrs_kernel(const void *const *__restrict__ rows, void *const *__restrict__ pages,
+                             const void *row0, void *page0, std::ptrdiff_t values_offset,
+                             int count, PageLayout L, int kv_heads)
+    {
+      const int W = kv_heads * HD;
+      const long long lane = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+      const long long page = lane / W;
+      if (page >= count)
+      {
+        return; // whole waves: W is a multiple of 64
+      }
+      const auto *src = static_cast<const std::uint8_t *>(rows ? rows[page] : row0);
+      auto *dst = static_cast<std::uint8_t *>(pages ? pages[page] : page0);
+      const auto *k = reinterpret_cast<const std::uint16_t *>(src);
+      const auto *v = reinterpret_cast<const std::uint16_t *>(src + values_offset);
+      const Rows keys{k, k, kP, W};
+      const Rows values{v, v, kP, W};
       page_task<Bits, HD>(static_cast<int>(lane % W), keys, values, kv_heads, dst, L, Emit::kCodes,
                           Emit::kCodes);
     }
@@ -761,6 +854,41 @@ namespace mi
                          pairs, spaces, L, page_tokens, kv_heads, head_dim);
       hip_check(hipGetLastError(), "requant refs (LDS) kernel launch");
     });
+  }
+
+  bool launch_quantise_registers(const void *const *rows, void *const *pages, const void *row0,
+                                 void *page0, std::ptrdiff_t values_offset, int count, int tier,
+                                 int page_tokens, int kv_heads, int head_dim, hipStream_t stream)
+  {
+    // The register tasks load 16 bytes at a time from every row.
+    const bool aligned = row0 == nullptr ||
+                         ((reinterpret_cast<std::uintptr_t>(row0) | values_offset) & 15) == 0;
+    if (!register_shape(page_tokens, kv_heads, head_dim) || values_offset % 16 != 0 || !aligned)
+    {
+      return false;
+    }
+    if (count <= 0)
+    {
+      return true;
+    }
+    const PageLayout L = page_layout(tier, page_tokens, kv_heads, head_dim);
+    const long long lanes = static_cast<long long>(count) * kv_heads * head_dim;
+    const int blocks = static_cast<int>((lanes + kThreads - 1) / kThreads);
+    with_bits(tier, [&](auto bits) {
+      constexpr int B = decltype(bits)::value;
+      if (head_dim == 128)
+      {
+        hipLaunchKernelGGL((quantise_ptrs_kernel<B, 128>), dim3(blocks), dim3(kThreads), 0, stream,
+                           rows, pages, row0, page0, values_offset, count, L, kv_heads);
+      }
+      else
+      {
+        hipLaunchKernelGGL((quantise_ptrs_kernel<B, 64>), dim3(blocks), dim3(kThreads), 0, stream,
+                           rows, pages, row0, page0, values_offset, count, L, kv_heads);
+      }
+      hip_check(hipGetLastError(), "quantise (registers) kernel launch");
+    });
+    return true;
   }
 
   void launch_row_jobs(const RowJob *jobs, int count, int page_tokens, int kv_heads, int head_dim,

@@ -118,6 +118,13 @@ namespace mi
     {
       return;
     }
+    // 32-token pages at head_dim 64 or 128 (16-byte aligned rows): the
+    // register quantiser, a lane a task, every page of the batch at once.
+    if (launch_quantise_registers(rows, pages, row0, page0, values_offset, count, tier,
+                                  page_tokens, kv_heads, head_dim, stream))
+    {
+      return;
+    }
     const std::size_t lds = quant_lds_bytes(L, page_tokens, kv_heads, head_dim);
     if (lds > kMaxLds)
     {

@@ -58,6 +58,104 @@ namespace mi
       return static_cast<unsigned>(fminf(fmaxf(q, 0.0f), kLevels));
     }
 
+    // The IEEE quotients of the elements whose product quotient lies near a
+    // half-integer (quotients_of's rare path).
+    __device__ inline void ieee_quotients(const float (&d)[8], const float (&scale)[8],
+                                                const float (&inv)[8], float (&q)[8])
+    {
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+      {
+        const float p = d[c] * inv[c];
+        if (fabsf(p - rintf(p)) > 0.5f - 0x1p-13f && scale[c] != 0.0f)
+        {
+          q[c] = rintf(d[c] / scale[c]);
+        }
+      }
+    }
+
+    // scale_bits_of for the ranges scale_bits_fast leaves to it (negative,
+    // huge or NaN), out of line.
+    __device__ __noinline__ std::uint16_t scale_bits_general(float lo, float hi, int bits)
+    {
+      return scale_bits_of(lo, hi, bits);
+    }
+
+    // Eight codes as code_of gives them, as integer-valued floats: the
+    // quotients formed as (x - zero) * inv, inv = 1 / scale (IEEE, 0 for a
+    // zero scale), where that settles the rounding. With x in
+    // [zero, zero + levels * scale] a quotient q is at most ~256 and the
+    // product is within 1.5 * 2^-23 * q <= 4.6e-5 of the IEEE quotient, so
+    // the two round to the same integer unless q lies within that of a
+    // half-integer. Where some lane of the wave has a q within 2^-13 of one,
+    // the IEEE quotients are formed for those elements (a branch the wave
+    // takes in ~1 row of 8; the empty volatile asm keeps the compiler from
+    // computing the divisions on every path). For such x the rounded
+    // quotient already lies in [0, levels] (scale >= (hi - lo) / levels, and
+    // the product's excess over levels is under 1e-4), so the reference's
+    // clamp leaves it unchanged and is not applied. Same codes as code_of,
+    // bit for bit, for finite inputs.
+    template <int Bits>
+    __device__ inline void quotients_of(const float (&x)[8], const float (&zero)[8],
+                                        const float (&scale)[8], const float (&inv)[8],
+                                        float (&q)[8])
+    {
+      float d[8];
+      bool near = false;
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+      {
+        d[c] = x[c] - zero[c];
+        const float p = d[c] * inv[c];
+        q[c] = rintf(p);
+        near |= fabsf(p - q[c]) > 0.5f - 0x1p-13f;
+      }
+      if (__builtin_amdgcn_ballot_w64(near) != 0)
+      {
+        // The empty volatile asm keeps the compiler from forming the
+        // divisions on the common path.
+        asm volatile("" ::: "memory");
+        ieee_quotients(d, scale, inv, q);
+      }
+    }
+
+    // scale_bits_of without a double division: the smallest fp16 s with
+    // s * levels >= hi - lo (what scale_bits_of's nearest-then-up gives:
+    // hi - lo is a multiple of 2^-24 and levels <= 255, so the double
+    // rounding of (hi - lo) / levels cannot move it across an fp16 value).
+    // The fp32 estimate rounded to fp16 is within half an fp16 ulp (plus
+    // 2^-22 relative) of the quotient, so the answer is it or the next up;
+    // products and differences in double are exact.
+    __device__ inline std::uint16_t scale_bits_fast(float lo, float hi, int bits)
+    {
+      const double range = static_cast<double>(hi) - static_cast<double>(lo);
+      const double levels = static_cast<double>((1 << bits) - 1);
+      if (range == 0.0)
+      {
+        return 0; // a constant group
+      }
+      if (!(range > 0.0) || !(range < 65504.0))
+      {
+        return scale_bits_general(lo, hi, bits); // negative, huge or NaN ranges
+      }
+      const float estimate = static_cast<float>(range) * (1.0f / static_cast<float>(levels));
+      const std::uint16_t c = __half_as_ushort(__float2half_rn(estimate));
+      if (static_cast<double>(half_bits_to_float(c)) * levels < range)
+      {
+        return static_cast<std::uint16_t>(c + 1);
+      }
+      if (c > 0 && static_cast<double>(half_bits_to_float(static_cast<std::uint16_t>(c - 1))) *
+                           levels >= range)
+      {
+        return static_cast<std::uint16_t>(c - 1);
+      }
+      return c;
+    }
+
+    // 1 / scale for codes_of: IEEE, and 0 for a zero scale (every element
+    // of such a group equals its zero, so q = 0).
+    __device__ inline float inverse_of(float scale) { return scale != 0.0f ? 1.0f / scale : 0.0f; }
+
     __device__ inline float lds_half(const std::uint16_t *p, std::size_t i)
     {
       return __half2float(__ushort_as_half(p[i]));

@@ -134,3 +134,45 @@ def test_what_is_not_a_full_page_is_refused():
             m.dequantise_page(page[:-1], tier, 2, 64)
     with pytest.raises(ValueError, match="FP16"):
         m.quantise_page(keys, values, m.Tier.FP16)
+
+
+def tie_page(kv, hd, bits, seed):
+    """Keys and values whose every group holds its minimum, its maximum and
+    elements exactly on (and one fp16 ulp beside) the half-levels of a scale
+    with an odd mantissa: quotients that are exact ties, where a code formed
+    through 1 / scale could round the other way."""
+    rng = np.random.default_rng(seed)
+    levels = (1 << bits) - 1
+
+    def group(n):
+        s = np.float16(int(rng.choice(np.arange(3, 32, 2))) * 2.0 ** int(rng.integers(-14, 0)))
+        lo = np.float16(int(rng.integers(-8, 8)) * np.float64(s))
+        hi = np.float16(lo.astype(np.float64) + levels * np.float64(s))
+        k = rng.integers(0, levels, n - 2).astype(np.float64)
+        mid = (lo.astype(np.float64) + (k + 0.5) * np.float64(s)).astype(np.float16)
+        step = rng.integers(-1, 2, n - 2).astype(np.int32)
+        near = (mid.view(np.uint16).astype(np.int32) + np.where(mid >= 0, step, -step))
+        near = near.astype(np.uint16).view(np.float16)
+        out = np.concatenate([[lo, hi], near]).astype(np.float64)
+        return np.clip(out, float(lo), float(hi))
+
+    keys = np.stack([group(32) for _ in range(kv * hd)], axis=1).reshape(32, kv, hd)
+    values = np.stack([group(hd) for _ in range(32 * kv)]).reshape(32, kv, hd)
+    return fp16_exact(keys), fp16_exact(values)
+
+
+def test_ties_quantise_as_the_oracle_to_the_bit():
+    """Pages built from exact and near ties at every tier, through the
+    quantiser the batch and single-page entry points take at the cache's
+    shapes (32-token pages, head_dim 64 and 128)."""
+    m = mi()
+
+    def check(kv, hd, tier, seed):
+        announce("quantise ties", kv, hd, tier, seed)
+        keys, values = tie_page(kv, hd, 8 >> (tier - 1), seed)
+        got = m.quantise_page(keys, values, tier, 32)
+        want = quant.quantise_page(keys.astype(np.float16), values.astype(np.float16), tier, 32)
+        np.testing.assert_array_equal(got, want)
+
+    each([(kv, hd, t, s) for kv, hd in ((2, 128), (2, 64), (8, 64)) for t in QUANTISED
+          for s in range(4)], check)

@@ -239,3 +239,103 @@ def test_open_and_malformed_pages_are_refused():
         page = quant.quantise_page(keys, values, tier)
         with pytest.raises(ValueError, match="bytes"):
             quant.dequantise_page(page[:-1], tier, 2, 64)
+
+
+def fast_code_model(x, zero, scale, bits):
+    """The device's code with the quotient taken as (x - zero) * (1 / scale)
+    and the IEEE quotient only inside a 2^-13 band around a half-integer
+    (quant_core.hpp code_of_fast), restated in NumPy float32."""
+    levels = np.float32((1 << bits) - 1)
+    x = np.asarray(x, np.float32)
+    zero = np.asarray(zero, np.float32)
+    scale = np.asarray(scale, np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        inv = np.where(scale != 0, np.float32(1) / scale, np.float32(0)).astype(np.float32)
+        d = (x - zero).astype(np.float32)
+        q = (d * inv).astype(np.float32)
+        band = (np.abs((q - np.floor(q)) - np.float32(0.5)) < np.float32(2.0 ** -13)) & (scale != 0)
+        q = np.where(band, d / scale, q).astype(np.float32)
+    q = np.minimum(np.maximum(np.rint(q), np.float32(0)), levels)
+    return q.astype(np.uint8)
+
+
+def test_the_fast_code_path_is_the_division_to_the_bit():
+    """Codes through (x - zero) * (1 / scale), with the IEEE quotient only
+    near a half-integer, equal code_of's rintf((x - zero) / scale) for every
+    element of every group the quantiser forms: random groups at every tier,
+    groups whose elements sit exactly on and one fp16 ulp either side of
+    every half-level (ties), and groups with subnormal and zero scales."""
+    rng = np.random.default_rng(7)
+    for bits in (8, 4, 2):
+        levels = (1 << bits) - 1
+        cases = []
+        for _ in range(400):
+            g = fp16_exact(rng.normal(rng.normal(0, 4), np.exp(rng.uniform(-12, 6)), 64))
+            cases.append(g.astype(np.float16))
+        # Scales with odd mantissas (1 / s inexact) and a zero point on the
+        # scale's grid, so that every half-level zero + (k + 1/2) s is an
+        # fp16 value: exact ties of the IEEE quotient.
+        for mant, exp in [(m, e) for m in range(3, 32, 2) for e in range(-20, 4, 3)]:
+            s = np.float16(mant * 2.0 ** exp)
+            lo = np.float16(int(rng.integers(-8, 8)) * np.float64(s))
+            k = np.arange(levels, dtype=np.float64)
+            mid = (lo.astype(np.float64) + (k + 0.5) * np.float64(s)).astype(np.float16)
+            up = (mid.view(np.uint16) + 1).view(np.float16)
+            down = (mid.view(np.uint16) - 1).view(np.float16)
+            hi = np.float16(lo.astype(np.float64) + levels * np.float64(s))
+            g = np.concatenate([[lo, hi], mid, up, down]).astype(np.float16)
+            g = g[np.isfinite(g)]
+            cases.append(np.clip(g, min(lo, hi), max(lo, hi)).astype(np.float16))
+        cases.append(np.full(64, np.float16(1.5)))
+        cases.append(np.array([0, 2.0 ** -24, 2.0 ** -23, 3 * 2.0 ** -24], np.float16))
+        for g in cases:
+            lo, hi = g.min(), g.max()
+            s = quant.scale_of(lo, hi, bits)
+            want = quant.code_of(g, lo, s, bits)
+            got = fast_code_model(g, lo, s, bits)
+            np.testing.assert_array_equal(got, want, err_msg=f"bits {bits} scale {s}")
+
+
+def fast_scale_model(lo, hi, bits):
+    """The device's scale without a double division (quant_core.hpp
+    scale_bits_fast), restated: the fp32 estimate rounded to fp16, then that
+    or the next fp16 up, whichever is the least s with s * levels >= hi - lo
+    (products and the range exact in float64)."""
+    levels = float((1 << bits) - 1)
+    rng_ = float(np.float64(hi) - np.float64(lo))
+    if rng_ == 0.0:
+        return np.float16(0)
+    est = np.float32(np.float32(rng_) * (np.float32(1.0) / np.float32(levels)))
+    c = np.float16(est).view(np.uint16)
+    if float(c.view(np.float16)) * levels < rng_:
+        return (c + np.uint16(1)).view(np.float16)
+    below = (c - np.uint16(1)).view(np.float16)
+    if c > 0 and float(below) * levels >= rng_:
+        return below
+    return c.view(np.float16)
+
+
+def test_the_fast_scale_is_scale_of_to_the_bit():
+    """scale_bits_fast equals scale_of (the reference's fp64 nearest-then-up)
+    over random groups at every tier, ranges that are exact multiples of an
+    fp16 value times the levels (the nearest is exact), ranges one 2^-24
+    either side of those, subnormal ranges and binade edges."""
+    rng = np.random.default_rng(11)
+    for bits in (8, 4, 2):
+        levels = (1 << bits) - 1
+        pairs = []
+        for _ in range(3000):
+            lo = np.float16(rng.normal(0, 8))
+            hi = np.float16(lo + abs(rng.normal(0, 1)) * np.exp(rng.uniform(-14, 3)))
+            pairs.append((lo, hi))
+        for raw in list(range(1, 64)) + list(range(0x3000, 0x3040)) + list(range(0x7000, 0x7010)):
+            s = np.uint16(raw).view(np.float16)
+            for lo in (np.float16(0), np.float16(-1.5), np.float16(2.0 ** -14)):
+                for nudge in (-2.0 ** -24, 0.0, 2.0 ** -24):
+                    hi = np.float16(float(lo) + levels * float(s) + nudge)
+                    if np.isfinite(hi) and hi >= lo:
+                        pairs.append((lo, hi))
+        for lo, hi in pairs:
+            want = quant.scale_of(lo, hi, bits)
+            got = fast_scale_model(lo, hi, bits)
+            assert got.view(np.uint16) == want.view(np.uint16), (bits, lo, hi, got, want)
