@@ -428,6 +428,11 @@ int mi_decode_step_destroy(mi_decode_step *step);
  * run reserves its pages first and records its stores after. */
 int mi_decode_step_run(mi_decode_step *step, int token, int position, int steps,
                        int32_t *tokens, double *device_ms);
+/* The same run with each step's launches made from the host in turn (no
+ * graph), as the reference sequences a step: bit-identical to
+ * mi_decode_step_run, for tools that follow individual launches. */
+int mi_decode_step_run_eager(mi_decode_step *step, int token, int position, int steps,
+                             int32_t *tokens, double *device_ms);
 /* The prompt (n tokens from host memory) at positions [position,
  * position + n) in chunks of `chunk` rows, a layer at a time as the
  * reference's Model.run (model.py:332-403) takes a chunk: RMSNorm, q/k/v

@@ -1336,6 +1336,19 @@ int mi_decode_step_run(mi_decode_step *step, int token, int position, int steps,
   });
 }
 
+int mi_decode_step_run_eager(mi_decode_step *step, int token, int position, int steps,
+                             int32_t *tokens, double *device_ms)
+{
+  return guarded([&] {
+    need(step, "step");
+    const double ms = step->impl.run(token, position, steps, tokens, false);
+    if (device_ms != nullptr)
+    {
+      *device_ms = ms;
+    }
+  });
+}
+
 int mi_decode_step_prefill(mi_decode_step *step, const int32_t *tokens, int n, int position,
                            int chunk, int32_t *first, double *device_ms)
 {

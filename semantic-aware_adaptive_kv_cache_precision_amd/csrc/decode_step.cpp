@@ -80,6 +80,7 @@ namespace mi
     ProjectArgs head{};
     head.segments = 1;
     head.seg[0].rows = s.vocab;
+    head.in = s.hidden;
     head.mode = ProjectMode::kLogits;
     head_blocks_ = project_blocks(head);
     best_value_ = device_bytes(static_cast<std::size_t>(head_blocks_) * sizeof(float));
@@ -199,6 +200,7 @@ namespace mi
     normed_input(head, weights_.final_norm);
     head.best_value = best_value_->as<float>();
     head.best_index = best_index_->as<int>();
+    head.best_count = head_blocks_;
     launch_project(head, stream);
     ++launches;
     if (scores_ != nullptr)
@@ -214,7 +216,7 @@ namespace mi
     launches_ = launches;
   }
 
-  void DecodeStep::capture(int max_seq_k)
+  void DecodeStep::prepare_launches(int max_seq_k)
   {
     const ModelShape &s = shape_;
     // Everything the launches use is made before the capture: the tables
@@ -236,6 +238,11 @@ namespace mi
     // The step's stream does not wait for other streams: whatever the cache
     // launched on them (table edits, allocations) is finished first.
     hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize before capture");
+  }
+
+  void DecodeStep::capture(int max_seq_k)
+  {
+    prepare_launches(max_seq_k);
     if (exec_ != nullptr)
     {
       hip_check(hipGraphExecDestroy(exec_), "hipGraphExecDestroy");
@@ -268,22 +275,51 @@ namespace mi
     hip_check(made, "hipGraphInstantiate step");
   }
 
-  double DecodeStep::run(int token, int position, int steps, std::int32_t *tokens)
+  double DecodeStep::run(int token, int position, int steps, std::int32_t *tokens, bool graphed)
   {
     require(steps > 0 && position >= 0, "a run takes at least one step from a position >= 0");
     require(tokens != nullptr, "a run writes its tokens to host memory");
     const int end = position + steps;
-    // The run's pages, then a graph for the most positions it attends.
+    // The run's pages, then a graph for the most positions it attends (or,
+    // eager, the same launches made from the host a step at a time).
     cache_.reserve(end);
     size_buffers(steps);
-    capture(end);
+    if (graphed)
+    {
+      capture(end);
+    }
+    else
+    {
+      prepare_launches(end);
+    }
     const int state[4] = {token, position, position + 1, 0};
     hip_check(hipMemcpyAsync(state_->raw(), state, sizeof(state), hipMemcpyHostToDevice, stream_),
               "hipMemcpyAsync step state");
     hip_check(hipEventRecord(begin_, stream_), "hipEventRecord");
-    for (int i = 0; i < steps; ++i)
+    if (graphed)
     {
-      hip_check(hipGraphLaunch(exec_, stream_), "hipGraphLaunch step");
+      for (int i = 0; i < steps; ++i)
+      {
+        hip_check(hipGraphLaunch(exec_, stream_), "hipGraphLaunch step");
+      }
+    }
+    else
+    {
+      const hipStream_t previous = runtime_stream();
+      set_runtime_stream(stream_);
+      try
+      {
+        for (int i = 0; i < steps; ++i)
+        {
+          enqueue_step(end, stream_);
+        }
+      }
+      catch (...)
+      {
+        set_runtime_stream(previous);
+        throw;
+      }
+      set_runtime_stream(previous);
     }
     hip_check(hipEventRecord(end_, stream_), "hipEventRecord");
     hip_check(hipMemcpyAsync(tokens, tokens_->raw(), static_cast<std::size_t>(steps) * 4,
@@ -425,6 +461,7 @@ namespace mi
       head.x = normed;
       head.best_value = best_value_->as<float>();
       head.best_index = best_index_->as<int>();
+      head.best_count = head_blocks_;
       launch_project(head, stream);
       launch_advance(best_value_->as<float>(), best_index_->as<int>(), head_blocks_, s.vocab,
                      state_->as<int>(), tokens_->as<std::int32_t>(), token_room_, stream);

@@ -94,8 +94,10 @@ namespace mi
     // `steps` greedy steps: the first feeds `token` at `position` (the cache
     // holds every position before it), each later one the token before it.
     // The chosen tokens go to `tokens` (host, `steps` of them). Returns the
-    // device milliseconds of the graph's replays (the run's steps).
-    double run(int token, int position, int steps, std::int32_t *tokens);
+    // device milliseconds of the graph's replays (the run's steps). With
+    // `graphed` false the same launches are made from the host, a step at a
+    // time (bit-identical; for tools that follow individual launches).
+    double run(int token, int position, int steps, std::int32_t *tokens, bool graphed = true);
     // The last step's logits (fp32, vocab of them) to host memory.
     void logits(float *host, std::size_t count) const;
     // Launches a step makes (the graph's kernel nodes).
@@ -103,6 +105,7 @@ namespace mi
 
   private:
     void size_buffers(int steps);
+    void prepare_launches(int max_seq_k);
     void capture(int max_seq_k);
     void enqueue_step(int max_seq_k, hipStream_t stream);
 

@@ -357,12 +357,15 @@ namespace mi
     ProjectMode mode;
     float *best_value; // kLogits: [project_blocks]
     int *best_index;
+    int best_count; // kLogits: the entries best_value and best_index hold
     // With norm_weight: x is RMSNorm of the fp32 `residual` row (in values),
     // formed in the launch as the RMSNorm kernel forms it, to the bit.
     const float *residual;
     const std::uint16_t *norm_weight;
     float eps;
   };
+  // The workgroups launch_project makes for `p` (its mode, segments' rows
+  // and input length): the entries a kLogits call's best arrays need.
   int project_blocks(const ProjectArgs &p);
   void launch_project(const ProjectArgs &p, hipStream_t stream);
   // A step's state in device memory, four ints.

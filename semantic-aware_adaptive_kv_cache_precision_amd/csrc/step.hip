@@ -21,8 +21,10 @@
 // staged once a workgroup in LDS -- or, where an RMSNorm feeds the
 // projection, formed there from the fp32 residual to the RMSNorm kernel's
 // bits -- after each wave's first weight loads are already on their way.
-// Eight rows a workgroup at a time; past 2048 workgroups (the head's
-// vocabulary) each wave takes several rows. The projections a step makes
+// A row a wave (a long row split over four or eight waves) when the
+// device holds the whole grid at once; otherwise as many workgroups as it
+// holds, each wave taking several rows with the next row's runs in flight
+// while one is used (the head's vocabulary, gate and up). The projections a step makes
 // from one input run in one launch: q, k and v (three weight matrices, one
 // grid over their rows), gate and up (a wave both rows of one output, the
 // SwiGLU in the epilogue).
@@ -33,15 +35,15 @@
 #include <algorithm>
 #include <cfloat>
 #include <climits>
+#include <map>
+#include <mutex>
 
 namespace mi
 {
   namespace
   {
     constexpr int kWaves = 8;
-    constexpr int kThreads = 64 * kWaves;
     constexpr int kAdvanceThreads = 1024;
-    constexpr long long kMaxBlocks = 2048;
 
     typedef _Float16 half2v __attribute__((ext_vector_type(2)));
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -137,19 +139,23 @@ namespace mi
       }
     }
 
-    // A wave's Ahead runs of one or two weight rows (run lane + 64 i of the
-    // batch at r0), clamped into the row; a lane past the row re-reads a run
-    // it does not use.
+    // The runs of a wave's part of one or two weight rows: run
+    // begin + lane + 64 i for i < Ahead, clamped into the part (a lane past
+    // its part re-reads the part's first run, which it does not use).
     template <int Ahead, bool Two>
-    __device__ inline void load_batch(u32x4 (&a)[Ahead], u32x4 (&b)[Ahead],
-                                      const std::uint16_t *w0, const std::uint16_t *w1, int r0,
-                                      int runs)
+    __device__ inline void load_part(u32x4 (&a)[Ahead], u32x4 (&b)[Ahead],
+                                     const std::uint16_t *w0, const std::uint16_t *w1, int begin,
+                                     int end, int lane)
     {
+      if (begin >= end)
+      {
+        return; // an empty part reads nothing (not even its row's next run)
+      }
 #pragma unroll
       for (int i = 0; i < Ahead; ++i)
       {
-        const int r = r0 + 64 * i;
-        const std::size_t at = 8 * static_cast<std::size_t>(r < runs ? r : 0);
+        const int r = begin + lane + 64 * i;
+        const std::size_t at = 8 * static_cast<std::size_t>(r < end ? r : begin);
         a[i] = *((g_u32x4)(w0 + at));
         if constexpr (Two)
         {
@@ -158,38 +164,165 @@ namespace mi
       }
     }
 
-    // The dots of one weight row (two, gate and up, with Two) with the input
-    // staged in LDS; the row's first batch was loaded before the input was.
-    // Each batch's successor is in flight while it is used.
-    template <int Ahead, bool Two>
-    __device__ inline void row_dots(float &d0, float &d1, const std::uint16_t *w0,
-                                    const std::uint16_t *w1, const u32x4 *x, int runs, int lane,
-                                    u32x4 (&a)[Ahead], u32x4 (&b)[Ahead])
+    // Which segment a row (counted over the segments in turn) falls in.
+    __device__ inline int locate(const ProjectArgs &p, bool two, int row, int &seg)
     {
-      float acc0 = 0.0f, acc1 = 0.0f;
-      for (int r0 = lane; r0 < runs; r0 += 64 * Ahead)
+      seg = 0;
+      while (!two && seg + 1 < p.segments && row >= p.seg[seg].rows)
       {
-        u32x4 na[Ahead], nb[Ahead];
-        const int next = r0 + 64 * Ahead;
-        if (next < runs)
-        {
-          load_batch<Ahead, Two>(na, nb, w0, w1, next, runs);
-        }
+        row -= p.seg[seg].rows;
+        ++seg;
+      }
+      return row;
+    }
+
+    // A weight row (gate's and up's rows together with Two) is read by
+    // Split consecutive waves of a workgroup (of Waves waves), each a
+    // contiguous part of its 16-byte runs, every run of the part in flight
+    // at once (Ahead a lane);
+    // the parts' dots meet in LDS and are summed in part order. A
+    // workgroup holds Waves / Split rows at a time; with Pipe a wave's next
+    // row is loaded while the current one is used (the head: many rows a
+    // wave). The input -- x, or RMSNorm of the residual -- is staged once a
+    // workgroup in LDS, after each wave's first loads are on their way.
+    template <int Waves, int Ahead, bool Two, int Split, bool Pipe>
+    __global__ void __launch_bounds__(64 * Waves) project_kernel(ProjectArgs p)
+    {
+      constexpr int kSlots = Waves / Split;
+      constexpr int kBlockThreads = 64 * Waves;
+      extern __shared__ u32x4 x_lds[];
+      __shared__ float s_best[Waves];
+      __shared__ int s_at[Waves];
+      __shared__ float s_partial[4];
+      __shared__ float s_dot[Waves];
+      const int lane = threadIdx.x & 63;
+      const int wave = threadIdx.x >> 6;
+      const int slot = wave / Split;
+      const int part = wave % Split;
+      const int runs = p.in / 8;
+      const int part_runs = (runs + Split - 1) / Split;
+      const int begin = min(runs, part * part_runs);
+      const int end = min(runs, begin + part_runs);
+      int total = 0;
+      for (int i = 0; i < (Two ? 1 : p.segments); ++i)
+      {
+        total += p.seg[i].rows;
+      }
+      const int stride = gridDim.x * kSlots;
+      const auto row_weights = [&](int g, int &seg, int &row) {
+        row = locate(p, Two, g, seg);
+        return p.seg[seg].w + static_cast<std::size_t>(row) * p.in;
+      };
+      const auto up_weights = [&](int row) {
+        return Two ? p.seg[1].w + static_cast<std::size_t>(row) * p.in : nullptr;
+      };
+      // The wave's first row's runs, before the input.
+      int g = blockIdx.x * kSlots + slot;
+      u32x4 a[Ahead], b[Ahead];
+      if (g < total)
+      {
+        int seg, row;
+        const std::uint16_t *w0 = row_weights(g, seg, row);
+        load_part<Ahead, Two>(a, b, w0, up_weights(row), begin, end, lane);
+      }
+      // A row split over waves reads x (no RMSNorm) straight from global
+      // memory, a lane its own runs, with the weights: staging a long input
+      // once a workgroup would read it more times than the weights' bytes.
+      constexpr bool kDirect = Split > 1;
+      u32x4 xd[kDirect ? Ahead : 1];
+      if constexpr (kDirect)
+      {
 #pragma unroll
         for (int i = 0; i < Ahead; ++i)
         {
-          const int r = r0 + 64 * i;
-          if (r < runs)
+          const int r = begin + lane + 64 * i;
+          xd[i] = r < end ? *((g_u32x4)(p.x + 8 * static_cast<std::size_t>(r)))
+                          : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+      else if (p.norm_weight != nullptr)
+      {
+        const float scale = norm_scale(p.residual, p.in, p.eps, s_partial);
+        for (int r = threadIdx.x; r < runs; r += kBlockThreads)
+        {
+          x_lds[r] = normed_run(p.residual, p.norm_weight, scale, r);
+        }
+        __syncthreads();
+      }
+      else
+      {
+        for (int r = threadIdx.x; r < runs; r += kBlockThreads)
+        {
+          x_lds[r] = *((g_u32x4)(p.x + 8 * static_cast<std::size_t>(r)));
+        }
+        __syncthreads();
+      }
+      float best = -FLT_MAX;
+      int at = INT_MAX;
+      // Every wave of the workgroup takes the same number of turns (the
+      // parts of a row meet at a barrier); a slot past the rows idles.
+      for (int base = blockIdx.x * kSlots; base < total; base += stride, g += stride)
+      {
+        const bool live = g < total;
+        int seg = 0, row = 0;
+        if (live)
+        {
+          row = locate(p, Two, g, seg);
+        }
+        u32x4 na[Pipe ? Ahead : 1], nb[Pipe ? Ahead : 1];
+        if constexpr (Pipe)
+        {
+          if (g + stride < total)
           {
-            const u32x4 xv = x[r];
-            acc0 = dot_run(a[i], xv, acc0);
-            if constexpr (Two)
+            int nseg, nrow;
+            const std::uint16_t *w0 = row_weights(g + stride, nseg, nrow);
+            load_part<Ahead, Two>(na, nb, w0, up_weights(nrow), begin, end, lane);
+          }
+        }
+        float acc0 = 0.0f, acc1 = 0.0f;
+        if (live)
+        {
+#pragma unroll
+          for (int i = 0; i < Ahead; ++i)
+          {
+            const int r = begin + lane + 64 * i;
+            if (r < end)
             {
-              acc1 = dot_run(b[i], xv, acc1);
+              u32x4 xv;
+              if constexpr (kDirect)
+              {
+                xv = xd[i];
+              }
+              else
+              {
+                xv = x_lds[r];
+              }
+              acc0 = dot_run(a[i], xv, acc0);
+              if constexpr (Two)
+              {
+                acc1 = dot_run(b[i], xv, acc1);
+              }
             }
           }
         }
-        if (next < runs)
+        float dot = wave_total(acc0);
+        const float up = Two ? wave_total(acc1) : 0.0f;
+        if constexpr (Split > 1)
+        {
+          if (lane == 0)
+          {
+            s_dot[wave] = dot;
+          }
+          __syncthreads();
+          dot = 0.0f;
+#pragma unroll
+          for (int q = 0; q < Split; ++q)
+          {
+            dot += s_dot[slot * Split + q];
+          }
+          __syncthreads();
+        }
+        if constexpr (Pipe)
         {
 #pragma unroll
           for (int i = 0; i < Ahead; ++i)
@@ -201,119 +334,54 @@ namespace mi
             }
           }
         }
-      }
-      d0 = wave_total(acc0);
-      d1 = Two ? wave_total(acc1) : 0.0f;
-    }
-
-    // A wave a row at a time over its rows (row = block's wave + k * the
-    // grid's waves), every segment's rows in turn, or gate's and up's rows
-    // together for SwiGLU. The input -- x, or RMSNorm of the residual -- is
-    // staged once a workgroup in LDS, after each wave's first weight loads
-    // are on their way.
-    template <int Ahead, bool Two>
-    __global__ void __launch_bounds__(kThreads) project_kernel(ProjectArgs p)
-    {
-      extern __shared__ u32x4 x_lds[];
-      __shared__ float s_best[kWaves];
-      __shared__ int s_at[kWaves];
-      __shared__ float s_partial[4];
-      const int lane = threadIdx.x & 63;
-      const int wave = threadIdx.x >> 6;
-      const int runs = p.in / 8;
-      int total = 0;
-      for (int i = 0; i < (Two ? 1 : p.segments); ++i)
-      {
-        total += p.seg[i].rows;
-      }
-      const int stride = gridDim.x * kWaves;
-      // The wave's first row and its first batch, before the input.
-      const auto locate = [&](int row, int &seg) {
-        seg = 0;
-        while (!Two && seg + 1 < p.segments && row >= p.seg[seg].rows)
+        else if (g + stride < total)
         {
-          row -= p.seg[seg].rows;
-          ++seg;
+          int nseg, nrow;
+          const std::uint16_t *w0 = row_weights(g + stride, nseg, nrow);
+          load_part<Ahead, Two>(a, b, w0, up_weights(nrow), begin, end, lane);
         }
-        return row;
-      };
-      int g = blockIdx.x * kWaves + wave;
-      u32x4 a[Ahead], b[Ahead];
-      if (g < total)
-      {
-        int seg;
-        const int row = locate(g, seg);
-        load_batch<Ahead, Two>(a, b, p.seg[seg].w + static_cast<std::size_t>(row) * p.in,
-                               Two ? p.seg[1].w + static_cast<std::size_t>(row) * p.in : nullptr,
-                               lane, runs);
-      }
-      if (p.norm_weight != nullptr)
-      {
-        const float scale = norm_scale(p.residual, p.in, p.eps, s_partial);
-        for (int r = threadIdx.x; r < runs; r += kThreads)
+        if (!live || part != 0)
         {
-          x_lds[r] = normed_run(p.residual, p.norm_weight, scale, r);
-        }
-      }
-      else
-      {
-        for (int r = threadIdx.x; r < runs; r += kThreads)
-        {
-          x_lds[r] = *((g_u32x4)(p.x + 8 * static_cast<std::size_t>(r)));
-        }
-      }
-      __syncthreads();
-      float best = -FLT_MAX;
-      int at = INT_MAX;
-      for (bool first = true; g < total; g += stride, first = false)
-      {
-        int seg;
-        const int row = locate(g, seg);
-        const ProjectSegment &s = p.seg[seg];
-        const std::uint16_t *w0 = s.w + static_cast<std::size_t>(row) * p.in;
-        const std::uint16_t *w1 = Two ? p.seg[1].w + static_cast<std::size_t>(row) * p.in : nullptr;
-        if (!first)
-        {
-          load_batch<Ahead, Two>(a, b, w0, w1, lane, runs);
-        }
-        float acc, up;
-        row_dots<Ahead, Two>(acc, up, w0, w1, x_lds, runs, lane, a, b);
-        if (lane != 0)
-        {
-          keep_better(best, at, acc, row);
           continue;
         }
+        if (lane != 0)
+        {
+          keep_better(best, at, dot, row);
+          continue;
+        }
+        const ProjectSegment &sg = p.seg[seg];
         switch (p.mode)
         {
         case ProjectMode::kHalf:
         {
-          const float bias = s.bias != nullptr ? h2f(s.bias[row]) : 0.0f;
-          static_cast<std::uint16_t *>(s.out)[row] = to_half(acc + bias);
+          const float bias = sg.bias != nullptr ? h2f(sg.bias[row]) : 0.0f;
+          static_cast<std::uint16_t *>(sg.out)[row] = to_half(dot + bias);
           break;
         }
         case ProjectMode::kAccumulate:
         {
-          float *out = static_cast<float *>(s.out) + row;
-          *out = *out + acc;
+          float *out = static_cast<float *>(sg.out) + row;
+          *out = *out + dot;
           break;
         }
         case ProjectMode::kSwiglu:
         {
-          const float gv = h2f(to_half(acc));
+          const float gv = h2f(to_half(dot));
           const float uv = h2f(to_half(up));
           const float silu = gv / (1.0f + expf(-gv));
-          static_cast<std::uint16_t *>(s.out)[row] = to_half(silu * uv);
+          static_cast<std::uint16_t *>(sg.out)[row] = to_half(silu * uv);
           break;
         }
         case ProjectMode::kLogits:
-          static_cast<float *>(s.out)[row] = acc;
+          static_cast<float *>(sg.out)[row] = dot;
           break;
         }
-        keep_better(best, at, acc, row);
+        keep_better(best, at, dot, row);
       }
       if (p.mode == ProjectMode::kLogits)
       {
-        // The workgroup's best logit, for the advance to choose from.
+        // The workgroup's best logit, for the advance to choose from (parts
+        // other than the first hold no candidate).
         if (lane == 0)
         {
           s_best[wave] = best;
@@ -322,7 +390,7 @@ namespace mi
         __syncthreads();
         if (threadIdx.x == 0)
         {
-          for (int w2 = 0; w2 < kWaves; ++w2)
+          for (int w2 = 0; w2 < Waves; ++w2)
           {
             keep_better(best, at, s_best[w2], s_at[w2]);
           }
@@ -400,21 +468,141 @@ namespace mi
 
   } // namespace
 
+  namespace
+  {
+    // The waves a row is split over: one, unless a part of more than 512
+    // runs (8 a lane) would be left, as a long input (the down projection)
+    // gives; then 4 or 8, which also puts more waves on the bytes.
+    int project_split(int in)
+    {
+      const int runs = in / 8;
+      return runs <= 512 ? 1 : runs <= 4 * 512 ? 4 : 8;
+    }
+
+    using ProjectFn = void (*)(ProjectArgs);
+
+    template <int Waves, int Ahead>
+    ProjectFn project_variant(bool two, int split, bool pipe)
+    {
+      if (two)
+      {
+        return pipe ? project_kernel<Waves, Ahead, true, 1, true>
+                    : project_kernel<Waves, Ahead, true, 1, false>;
+      }
+      if (split == 1)
+      {
+        return pipe ? project_kernel<Waves, Ahead, false, 1, true>
+                    : project_kernel<Waves, Ahead, false, 1, false>;
+      }
+      return split == 4 ? project_kernel<Waves, Ahead, false, 4, false>
+                        : project_kernel<Waves, Ahead, false, 8, false>;
+    }
+
+    template <int Ahead>
+    ProjectFn project_variant(int waves, bool two, int split, bool pipe)
+    {
+      return waves == 8 ? project_variant<8, Ahead>(two, split, pipe)
+                        : project_variant<4, Ahead>(two, split, pipe);
+    }
+
+    ProjectFn project_variant(int ahead, int waves, bool two, int split, bool pipe)
+    {
+      switch (ahead)
+      {
+      case 1: return project_variant<1>(waves, two, split, pipe);
+      case 2: return project_variant<2>(waves, two, split, pipe);
+      case 3: return project_variant<3>(waves, two, split, pipe);
+      case 4: return project_variant<4>(waves, two, split, pipe);
+      case 5: return project_variant<5>(waves, two, split, pipe);
+      case 6: return project_variant<6>(waves, two, split, pipe);
+      case 7: return project_variant<7>(waves, two, split, pipe);
+      default: return project_variant<8>(waves, two, split, pipe);
+      }
+    }
+
+    // Workgroups of a kernel the device holds at once, queried once a
+    // (kernel, LDS) pair.
+    int resident_blocks(ProjectFn fn, int threads, std::size_t lds)
+    {
+      static std::mutex lock;
+      static std::map<std::pair<const void *, std::size_t>, int> known;
+      const std::pair<const void *, std::size_t> key{reinterpret_cast<const void *>(fn), lds};
+      {
+        std::lock_guard<std::mutex> hold(lock);
+        const auto it = known.find(key);
+        if (it != known.end())
+        {
+          return it->second;
+        }
+      }
+      int per_cu = 0;
+      hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, key.first, threads, lds),
+                "hipOccupancyMaxActiveBlocksPerMultiprocessor projection");
+      const int blocks = std::max(per_cu, 1) * device_multiprocessors();
+      std::lock_guard<std::mutex> hold(lock);
+      known[key] = blocks;
+      return blocks;
+    }
+
+    struct ProjectPlan
+    {
+      ProjectFn fn;
+      int waves;
+      int blocks;
+      std::size_t lds;
+    };
+
+    // A wave a row (Split waves with a long input) in one grid when the
+    // device holds that many workgroups at once; otherwise as many
+    // workgroups as it holds, each wave over several rows with the next
+    // row's runs in flight while one is used.
+    ProjectPlan plan_projection(const ProjectArgs &p)
+    {
+      const bool two = p.mode == ProjectMode::kSwiglu;
+      long long rows = 0;
+      for (int i = 0; i < (two ? 1 : p.segments); ++i)
+      {
+        rows += p.seg[i].rows;
+      }
+      const int split = two ? 1 : project_split(p.in);
+      const int waves = split == 8 ? 8 : 4;
+      const int slots = waves / split;
+      const int runs = p.in / 8;
+      const int ahead = ((runs + split - 1) / split + 63) / 64;
+      if (ahead > (two ? 4 : 8))
+      {
+        throw InvalidArgument("a SwiGLU projection's input is at most 2048 values; got " +
+                              std::to_string(p.in));
+      }
+      if (split > 1 && p.norm_weight != nullptr)
+      {
+        throw InvalidArgument("an input of more than 4096 values is projected as it comes, "
+                              "without an RMSNorm formed in the launch");
+      }
+      // A split row reads x as it comes; otherwise x (or its RMSNorm) is
+      // staged in LDS, in fp16 values.
+      const std::size_t lds = split > 1 ? 0 : static_cast<std::size_t>(p.in) * 2;
+      const long long needed = (rows + slots - 1) / slots;
+      ProjectFn plain = project_variant(ahead, waves, two, split, false);
+      if (split > 1 || needed <= resident_blocks(plain, 64 * waves, lds))
+      {
+        return {plain, waves, static_cast<int>(needed), lds};
+      }
+      ProjectFn pipe = project_variant(ahead, waves, two, split, true);
+      const int held = resident_blocks(pipe, 64 * waves, lds);
+      return {pipe, waves, static_cast<int>(std::min<long long>(needed, held)), lds};
+    }
+  } // namespace
+
   int project_blocks(const ProjectArgs &p)
   {
-    long long rows = 0;
-    for (int i = 0; i < p.segments; ++i)
+    if (p.in <= 0 || p.in % 8 != 0 || p.segments < 1 || p.segments > kProjectSegments)
     {
-      rows += p.seg[i].rows;
+      throw InvalidArgument("a projection's plan needs its input length (a positive multiple "
+                            "of 8) and 1 to 3 segments; got " + std::to_string(p.in) + " and " +
+                            std::to_string(p.segments));
     }
-    if (p.mode == ProjectMode::kSwiglu)
-    {
-      rows = p.seg[0].rows; // up's rows ride with gate's
-    }
-    // A wave a row, up to kMaxBlocks workgroups; past that the waves take
-    // several rows each (the head's vocabulary), so that the staging of the
-    // input is paid once for many rows.
-    return static_cast<int>(std::min<long long>((rows + kWaves - 1) / kWaves, kMaxBlocks));
+    return plan_projection(p).blocks;
   }
 
   void launch_project(const ProjectArgs &p, hipStream_t stream)
@@ -442,40 +630,29 @@ namespace mi
                               " needs 16-byte aligned weights, rows and an output");
       }
     }
-    const int blocks = project_blocks(p);
     if (p.mode == ProjectMode::kLogits && (p.best_value == nullptr || p.best_index == nullptr))
     {
       throw InvalidArgument("the head's projection keeps each block's best logit");
     }
-    // The input in LDS: in fp16 values. Long rows (the down projection's)
-    // keep more of a row in flight.
-    const std::size_t lds = static_cast<std::size_t>(p.in) * 2;
-    if (lds > 64 * 1024)
+    // The input in LDS: in fp16 values.
+    if (static_cast<std::size_t>(p.in) * 2 > 64 * 1024)
     {
       throw InvalidArgument("a projection's input is at most 32768 values; got " +
                             std::to_string(p.in));
     }
-    const bool two = p.mode == ProjectMode::kSwiglu;
-    if (p.in > 4096)
+    const ProjectPlan plan = plan_projection(p);
+    // Each workgroup of the head writes its best logit: the arrays must hold
+    // one an entry a workgroup.
+    if (p.mode == ProjectMode::kLogits && plan.blocks > p.best_count)
     {
-      if (two)
-      {
-        hipLaunchKernelGGL((project_kernel<8, true>), dim3(blocks), dim3(kThreads), lds, stream, p);
-      }
-      else
-      {
-        hipLaunchKernelGGL((project_kernel<8, false>), dim3(blocks), dim3(kThreads), lds, stream, p);
-      }
+      throw InvalidArgument("the head's projection runs " + std::to_string(plan.blocks) +
+                            " workgroups; its best arrays hold " + std::to_string(p.best_count));
     }
-    else if (two)
-    {
-      hipLaunchKernelGGL((project_kernel<4, true>), dim3(blocks), dim3(kThreads), lds, stream, p);
-    }
-    else
-    {
-      hipLaunchKernelGGL((project_kernel<4, false>), dim3(blocks), dim3(kThreads), lds, stream, p);
-    }
-    hip_check(hipGetLastError(), "projection kernel launch");
+    ProjectArgs args = p;
+    void *params[] = {&args};
+    hip_check(hipLaunchKernel(reinterpret_cast<const void *>(plan.fn), dim3(plan.blocks),
+                              dim3(64 * plan.waves), params, plan.lds, stream),
+              "projection kernel launch");
   }
 
   void launch_advance(const float *best_value, const int *best_index, int blocks, int vocab,

@@ -82,6 +82,8 @@ SIGNATURES = {
                                C.POINTER(_LayerWeights), _vp, _i), C.c_int),
     "mi_decode_step_destroy": ((_vp,), C.c_int),
     "mi_decode_step_run": ((_vp, _i, _i, _i, C.POINTER(C.c_int32), C.POINTER(_d)), C.c_int),
+    "mi_decode_step_run_eager": ((_vp, _i, _i, _i, C.POINTER(C.c_int32), C.POINTER(_d)),
+                                 C.c_int),
     "mi_decode_step_logits": ((_vp, _fp, _sz), C.c_int),
     "mi_decode_step_prefill": ((_vp, C.POINTER(C.c_int32), _i, _i, _i, C.POINTER(C.c_int32),
                                 C.POINTER(_d)), C.c_int),
@@ -1386,13 +1388,15 @@ class DecodeStep:
         self.vocab = shape["vocab"]
         weakref.finalize(self, lib.mi_decode_step_destroy, self._h)
 
-    def run(self, token: int, position: int, steps: int):
+    def run(self, token: int, position: int, steps: int, graphed: bool = True):
         """`steps` greedy steps from `position`, feeding `token` first:
-        (tokens chosen, device milliseconds of the replays)."""
+        (tokens chosen, device milliseconds of the replays). graphed=False
+        makes the same launches from the host a step at a time."""
         out = np.empty(steps, np.int32)
         ms = C.c_double()
-        _check(lib.mi_decode_step_run(self._h, token, position, steps,
-                                      out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(ms)))
+        fn = lib.mi_decode_step_run if graphed else lib.mi_decode_step_run_eager
+        _check(fn(self._h, token, position, steps, out.ctypes.data_as(C.POINTER(C.c_int32)),
+                  C.byref(ms)))
         return out, ms.value
 
     def prefill(self, tokens, position: int = 0, chunk: int = 2048):

@@ -376,6 +376,37 @@ def check_logits(got, want, token):
     assert token == dense.argmax_rows(got[None].astype(np.float32))[0]
 
 
+def test_an_eager_run_is_the_graphed_run_to_the_bit():
+    """The same steps with the launches made from the host (no graph): the
+    tokens, logits, pages and scores of the graphed run, to the bit."""
+    m = mi()
+    d = m.device
+    s = small_shape(heads=12, kv_heads=2, head_dim=128)
+    rng = np.random.default_rng(23)
+    host = make_weights(rng, s, True)
+    dev = upload_weights(host)
+    start, n = P * 2 + 20, 20
+    rows = context_rows(rng, s, start)
+    tmap = tier_map_for(s, 8, 3)
+    made = []
+    for graphed in (True, False):
+        alloc, cache = make_cache(s, tmap)
+        prefill(cache, s, rows)
+        scores = d.ImportanceScores(s["layers"], 16)
+        step = d.DecodeStep(cache, s, dev["embed"], dev["final_norm"], dev["head"], dev["layers"],
+                            scores, 1)
+        announce("run", "graphed" if graphed else "eager", n)
+        tokens, ms = step.run(5, start, n, graphed=graphed)
+        assert ms > 0
+        made.append((alloc, cache, scores, step, tokens))
+    np.testing.assert_array_equal(made[0][4], made[1][4])
+    np.testing.assert_array_equal(made[0][3].logits(), made[1][3].logits())
+    np.testing.assert_array_equal(made[0][2].download(), made[1][2].download())
+    for layer in range(s["layers"]):
+        for page in range((start + n) // P):
+            np.testing.assert_array_equal(made[0][0].read(layer, page), made[1][0].read(layer, page))
+
+
 @pytest.mark.parametrize("case", ["qwen_hd128_from_empty", "llama_after_context"])
 def test_chunked_prefill_is_the_oracles_composition(case):
     """The prompt in chunks (the last one short) through every layer: the
