@@ -162,7 +162,7 @@ def copy_peak(m, page=32768, count=32768, reps=10) -> float:
 
 def decode_source_hash() -> str:
     h = hashlib.sha256()
-    for name in ("decode.hip", "kernels.hpp", "common.hpp", "lane_ops.hpp"):
+    for name in ("decode.hip", "dequant.hpp", "common.hpp", "lane_ops.hpp"):
         h.update((PKG / "csrc" / name).read_bytes())
     return h.hexdigest()[:16]
 
@@ -374,7 +374,8 @@ def prefill_flops(shape, start, n):
     return per_row * n + attention + 2 * H * shape.vocab
 
 
-def full_step(m, shape, context, steps, warmup, mix, key_bias, seed, prompt_chunk=None):
+def full_step(m, shape, context, steps, warmup, mix, key_bias, seed, prompt_chunk=None,
+              graphed=True):
     """`steps` greedy decode steps of a random-weight model of `shape` from
     position `context` (the cache born at `mix` over the whole run), after
     `warmup` steps: tokens/s from the replays' device time, and HBM GB/s of
@@ -420,10 +421,10 @@ def full_step(m, shape, context, steps, warmup, mix, key_bias, seed, prompt_chun
         log(f"{shape.name}: {context} positions stored in {time.perf_counter() - t0:.1f}s")
         token = 1
     if warmup:
-        tokens, _ = step.run(token, context, warmup)
+        tokens, _ = step.run(token, context, warmup, graphed=graphed)
         token = int(tokens[-1])
     t0 = time.perf_counter()
-    tokens, ms = step.run(token, context + warmup, steps)
+    tokens, ms = step.run(token, context + warmup, steps, graphed=graphed)
     wall = time.perf_counter() - t0
     logits = step.logits()
     if not np.isfinite(logits).all() or not ((tokens >= 0) & (tokens < V)).all():
@@ -835,6 +836,9 @@ def main() -> int:
     ap.add_argument("--no-requant", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-step", action="store_true", help="skip the whole-step legs")
+    ap.add_argument("--eager-step", action="store_true",
+                    help="whole steps with their launches made from the host (no graph), so "
+                         "that a kernel tracer sees each launch")
     ap.add_argument("--traffic-reference", action="store_true",
                     help="only copy 128 MiB with the page-copy kernel (4096 pages of 32 KiB): "
                          "the known-size launch HBM byte counters are scaled by")
@@ -882,11 +886,13 @@ def main() -> int:
         return round(step_bytes / (t * 1e-3) / 1e9, 1)
 
     prefill = None
-    if "prefill" in legs and "decode" in legs:
-        prefill = {"tile": prefill_tile(m, shape, cache3, host3, rows3, rope3, bs3, layers, context,
-                                        stream, args.steps, args.warmup),
-                   "chunks": prefill_chunks(m, stream, max(args.steps // 5, 3),
+    if "prefill" in legs:
+        # The tile runs on the headline's cache; the chunks build their own.
+        prefill = {"chunks": prefill_chunks(m, stream, max(args.steps // 5, 3),
                                             max(args.warmup // 5, 1))}
+        if "decode" in legs:
+            prefill["tile"] = prefill_tile(m, shape, cache3, host3, rows3, rope3, bs3, layers,
+                                           context, stream, args.steps, args.warmup)
         log(f"prefill: {prefill}")
     if "decode" in legs:
         del alloc3, cache3, host3, rows3
@@ -897,9 +903,10 @@ def main() -> int:
     if "step" in legs:
         steps_out = {
             "qwen2.5-1.5b_32k": full_step(m, w.QWEN_15B, 32768 - 64 - 8, 64, 8, w.MIX_CONFIG3,
-                                          True, 3),
+                                          True, 3, graphed=not args.eager_step),
             "llama-3.2-1b_16k_config5": full_step(m, w.LLAMA_1B, 16384, 256, 0, w.MIX_CONFIG5,
-                                                  False, 5, prompt_chunk=2048)}
+                                                  False, 5, prompt_chunk=2048,
+                                                  graphed=not args.eager_step)}
         steps_out["reference_rtx4050_tokens_per_s"] = {"qwen2.5-1.5b_fp16_32k": 29.5,
                                                        "qwen2.5-1.5b_fp16_16k": 40.1}
 
@@ -940,8 +947,8 @@ def main() -> int:
 
     if ms is None:
         print(json.dumps({"metric": METRIC, "value": None, "legs": sorted(legs), "config2": c2,
-                          "decode_step": steps_out, "quantise": quantise, "requant": requant,
-                          "cpu_baseline": cpu}),
+                          "decode_step": steps_out, "prefill": prefill, "quantise": quantise,
+                          "requant": requant, "cpu_baseline": cpu}),
               flush=True)
         return 0
     result = {
