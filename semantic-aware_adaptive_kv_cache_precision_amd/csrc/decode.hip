@@ -150,6 +150,16 @@ namespace mi
                          // sum, a head's splits side by side so that they read coalesced
       float *page_stats; // [launch layer][kv_heads][pages][group][2]: each page's max and
                          // sum, a page's heads side by side so that one store writes them
+      // Two KV heads of head_dim 64 read as one 128-channel unit (pack = 2;
+      // 0 otherwise): kv_heads and group then count packs and a pack's
+      // heads, q enters block-diagonal (a head's query in its own KV head's
+      // channels, zeros in the other's), a value row's scale and zero come
+      // from the lane's own KV head (value_kv_heads of them a row), and each
+      // head's partial keeps its own 64 channels. Page statistics stay in
+      // the layout of stat_group heads a KV head in every case.
+      int pack;
+      int value_kv_heads;
+      int stat_group;
     };
 
     __device__ inline half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
@@ -584,8 +594,9 @@ namespace mi
     template <int HD, int Bits, bool kBias = false>
     __device__ inline void quantised_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
                                           const std::uint8_t *page, const PageLayout &L,
-                                          std::size_t W, int kvh, int kv_heads, int lane,
-                                          unsigned *meta, const KeyBias<HD> *bias = nullptr)
+                                          std::size_t W, int kvh, int value_kv_heads,
+                                          int value_kvh, int lane, unsigned *meta,
+                                          const KeyBias<HD> *bias = nullptr)
     {
       using Raw = QuantRaw<HD, Bits>;
       constexpr int kRun = HD / 4;
@@ -614,7 +625,7 @@ namespace mi
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
       {
-        const std::size_t grp = static_cast<std::size_t>(kb * 16 + r) * kv_heads + kvh;
+        const std::size_t grp = static_cast<std::size_t>(kb * 16 + r) * value_kv_heads + value_kvh;
         raw.vs[kb] = *((g_u16)(page + L.value_scales + 2 * grp));
         raw.vz[kb] = *((g_u16)(page + L.value_zeros + 2 * grp));
       }
@@ -746,10 +757,19 @@ namespace mi
       const std::uint8_t *tiers = a.tiers != nullptr ? a.tiers + layer * a.table_stride : nullptr;
       const int own = a.causal ? (a.seq_k - 1) / kPageTokens : -1;
       const int p0 = (split * kWaves + wave) * a.pages_per_wave;
-      const std::uint16_t *q_row = a.q + li * a.q_stride +
-                                   static_cast<std::size_t>(kvh * G + (r < G ? r : 0)) * HD +
-                                   g * kRun;
+      // A pack's rows: its first KV head's heads, then its second's; lane
+      // groups 0-1 hold the first head's 64 channels, 2-3 the second's.
+      const int head_row = kvh * G + (r < G ? r : 0);
+      const bool pack = a.pack != 0;
+      const bool q_off = pack && (r < G ? r : 0) / (G / 2) != g / 2;
+      const std::uint16_t *q_row =
+          a.q + li * a.q_stride +
+          (pack ? static_cast<std::size_t>(head_row) * (HD / 2) + (g % 2) * kRun
+                : static_cast<std::size_t>(head_row) * HD + g * kRun);
+      // A value row's metadata: the lane's own KV head's.
+      const int value_kvh = pack ? 2 * kvh + g / 2 : kvh;
       float *stats = a.page_stats + static_cast<std::size_t>(li) * a.heads * a.pages * 2;
+      const int SG = a.stat_group;
 
       Running<HD> run;
       run.m = -INFINITY;
@@ -765,6 +785,14 @@ namespace mi
       // their own columns and are never stored.
       half8 qb[S];
       load_fp16_run<HD>(qb, q_row);
+      if (q_off)
+      {
+#pragma unroll
+        for (int si = 0; si < S; ++si)
+        {
+          qb[si] = as_half8(u32x4{0u, 0u, 0u, 0u});
+        }
+      }
 
       // The key bias: lane i holds b_i and b_i' of this KV head; the
       // workgroup's angle rows follow the epilogue's LDS.
@@ -814,7 +842,10 @@ namespace mi
         c.partial = c.last < kPageTokens - 1;
         c.first = first;
         c.scale = a.scale;
-        c.stat = stats + ((static_cast<std::size_t>(kvh) * a.pages + p) * G + r) * 2;
+        {
+          const int h = kvh * G + r; // rows past the group are never stored
+          c.stat = stats + ((static_cast<std::size_t>(h / SG) * a.pages + p) * SG + h % SG) * 2;
+        }
         KeyBias<HD> bias;
         if constexpr (kBias)
         {
@@ -839,16 +870,16 @@ namespace mi
         switch (tier)
         {
         case kINT8:
-          quantised_page<HD, 8, kBias>(run, c, qb, page, a.lay[kINT8], W, kvh, a.kv_heads,
-                                         lane, meta, page_bias);
+          quantised_page<HD, 8, kBias>(run, c, qb, page, a.lay[kINT8], W, kvh,
+                                         a.value_kv_heads, value_kvh, lane, meta, page_bias);
           break;
         case kINT4:
-          quantised_page<HD, 4, kBias>(run, c, qb, page, a.lay[kINT4], W, kvh, a.kv_heads,
-                                         lane, meta, page_bias);
+          quantised_page<HD, 4, kBias>(run, c, qb, page, a.lay[kINT4], W, kvh,
+                                         a.value_kv_heads, value_kvh, lane, meta, page_bias);
           break;
         case kINT2:
-          quantised_page<HD, 2, kBias>(run, c, qb, page, a.lay[kINT2], W, kvh, a.kv_heads,
-                                         lane, meta, page_bias);
+          quantised_page<HD, 2, kBias>(run, c, qb, page, a.lay[kINT2], W, kvh,
+                                         a.value_kv_heads, value_kvh, lane, meta, page_bias);
           break;
         case kOwnPage:
         {
@@ -932,13 +963,18 @@ namespace mi
         }
       }
       __syncthreads();
+      // A head's partial: its HD channels, or with a pack its own KV head's
+      // HD / 2 of the unit's.
+      constexpr int kPackHD = HD / 2;
+      const int out_hd = pack ? kPackHD : HD;
       float *part = a.partials +
-                    ((static_cast<std::size_t>(li) * a.kv_heads + kvh) * a.splits + split) * G * HD;
+                    ((static_cast<std::size_t>(li) * a.kv_heads + kvh) * a.splits + split) * G * out_hd;
       float *ml = a.split_ml + (static_cast<std::size_t>(li) * a.kv_heads + kvh) * G * a.splits * 2;
-      for (int idx = threadIdx.x; idx < G * (HD + 2); idx += kThreads)
+      for (int idx = threadIdx.x; idx < G * (out_hd + 2); idx += kThreads)
       {
-        const int h = idx / (HD + 2);
-        const int col = idx % (HD + 2);
+        const int h = idx / (out_hd + 2);
+        const int col = idx % (out_hd + 2);
+        const int from = col - 2 + (pack && h >= G / 2 ? kPackHD : 0); // unit channel
         float acc = s_w[kWaves * G + h];
         if (col != 0)
         {
@@ -946,7 +982,7 @@ namespace mi
 #pragma unroll
           for (int w = 0; w < kWaves; ++w)
           {
-            const float v = col == 1 ? s_l[w * G + h] : s_o[(w * G + h) * kRow + col - 2];
+            const float v = col == 1 ? s_l[w * G + h] : s_o[(w * G + h) * kRow + from];
             acc += v * s_w[w * G + h];
           }
         }
@@ -956,7 +992,7 @@ namespace mi
         }
         else
         {
-          part[h * HD + col - 2] = acc;
+          part[h * out_hd + col - 2] = acc;
         }
       }
     }
@@ -1819,8 +1855,9 @@ namespace mi
         {
           const int h = min(wave + kWavesC * (j0 + j), a.heads - 1);
           splits[j] = splits_of(li, h / G);
+          const int SG = a.stat_group;
           st[j] = *reinterpret_cast<const float2 *>(
-              stats + ((static_cast<std::size_t>(h / G) * a.pages + pg) * G + h % G) * 2);
+              stats + ((static_cast<std::size_t>(h / SG) * a.pages + pg) * SG + h % SG) * 2);
           const float2 *mls = head_ml(h);
 #pragma unroll
           for (int k = 0; k < 2; ++k)
@@ -2012,6 +2049,8 @@ namespace mi
     d.heads = a.heads;
     d.kv_heads = a.kv_heads;
     d.group = group;
+    d.value_kv_heads = a.kv_heads;
+    d.stat_group = group;
     d.pages = pages;
     // Scores in base-2 units: the softmax weights are exp2 of them.
     d.scale = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(a.head_dim)));
@@ -2062,6 +2101,18 @@ namespace mi
     }
     d.live_pages = pages;
     d.live_splits = d.splits;
+    // head_dim 64 with an even number of KV heads and no key bias (the
+    // Llama shapes): two KV heads a wave, as one 128-channel unit, so that a
+    // launch has half the waves, each with a unit of the size the kernel's
+    // fixed costs are paid for.
+    const bool packed = !streaming && a.head_dim == 64 && d.k_bias == nullptr &&
+                        a.kv_heads % 2 == 0 && 2 * group <= kMaxGroup;
+    if (packed)
+    {
+      d.pack = 2;
+      d.kv_heads = a.kv_heads / 2;
+      d.group = 2 * group;
+    }
     const std::size_t part =
         static_cast<std::size_t>(ls.layers) * a.kv_heads * d.splits * group * a.head_dim;
     const bool kept = ls.keep_ml != nullptr;
@@ -2086,7 +2137,8 @@ namespace mi
     d.warm_tiers = warm ? kv.warm_tiers : nullptr;
     d.warm_count = warm ? kv.warm_count : 0;
     const auto run = [&](auto pages_kernel, auto stream_kernel, auto combine_kernel,
-                         auto combine_streamed, int hd, std::size_t stream_lds) {
+                         auto combine_streamed, int hd, std::size_t stream_lds,
+                         int pages_hd) {
       if (stream_blocks > 0)
       {
         hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(stream_kernel),
@@ -2099,7 +2151,7 @@ namespace mi
       }
       else
       {
-        const std::size_t lds = pages_kernel_lds(group, hd, d.k_bias != nullptr);
+        const std::size_t lds = pages_kernel_lds(d.group, pages_hd, d.k_bias != nullptr);
         if (lds > 64 * 1024)
         {
           hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(pages_kernel),
@@ -2107,7 +2159,7 @@ namespace mi
                                         static_cast<int>(lds)),
                     "hipFuncSetAttribute decode LDS");
         }
-        hipLaunchKernelGGL(pages_kernel, dim3(d.splits, a.kv_heads, ls.layers), dim3(kThreads),
+        hipLaunchKernelGGL(pages_kernel, dim3(d.splits, d.kv_heads, ls.layers), dim3(kThreads),
                            lds, stream, d);
         hip_check(hipGetLastError(), "decode pages kernel launch");
       }
@@ -2123,25 +2175,32 @@ namespace mi
       {
         run(decode_pages_kernel<128, true>, decode_stream_kernel<128>,
             decode_combine_kernel<128, false>, decode_combine_kernel<128, true>, 128,
-            stream_kernel_lds<128>());
+            stream_kernel_lds<128>(), 128);
       }
       else
       {
         run(decode_pages_kernel<128, false>, decode_stream_kernel<128>,
             decode_combine_kernel<128, false>, decode_combine_kernel<128, true>, 128,
-            stream_kernel_lds<128>());
+            stream_kernel_lds<128>(), 128);
       }
+    }
+    else if (packed)
+    {
+      // The pack's unit is 128 channels; each head's output is its own 64.
+      run(decode_pages_kernel<128, false>, decode_stream_kernel<64>,
+          decode_combine_kernel<64, false>, decode_combine_kernel<64, true>, 64,
+          stream_kernel_lds<64>(), 128);
     }
     else if (d.k_bias != nullptr)
     {
       run(decode_pages_kernel<64, true>, decode_stream_kernel<64>, decode_combine_kernel<64, false>,
-          decode_combine_kernel<64, true>, 64, stream_kernel_lds<64>());
+          decode_combine_kernel<64, true>, 64, stream_kernel_lds<64>(), 64);
     }
     else
     {
       run(decode_pages_kernel<64, false>, decode_stream_kernel<64>,
           decode_combine_kernel<64, false>, decode_combine_kernel<64, true>, 64,
-          stream_kernel_lds<64>());
+          stream_kernel_lds<64>(), 64);
     }
   }
 
@@ -2164,6 +2223,8 @@ namespace mi
     d.heads = f.heads;
     d.kv_heads = f.kv_heads;
     d.group = f.heads / f.kv_heads;
+    d.value_kv_heads = f.kv_heads;
+    d.stat_group = d.group;
     d.pages = pages;
     d.seq_k = f.seq_k;
     d.splits = (pages + kWaves - 1) / kWaves;
