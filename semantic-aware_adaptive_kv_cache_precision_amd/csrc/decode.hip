@@ -44,6 +44,7 @@
 #include "common.hpp"
 #include "dequant.hpp"
 #include "kernels.hpp"
+#include "page_tasks.hpp"
 #include "lane_ops.hpp"
 
 #include <algorithm>
@@ -160,6 +161,10 @@ namespace mi
       int pack;
       int value_kv_heads;
       int stat_group;
+      // A step's page seal (DecodeLayers::seal) by the combine's block
+      // seal_block - 1; 0: none.
+      StepStore seal;
+      int seal_block;
     };
 
     __device__ inline half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
@@ -1678,9 +1683,51 @@ namespace mi
     // conditional. Blocks past that: 256 pages' masses and the layer's scores
     // (importance_scores.cu:31-50: heads summed in order, every operation
     // rounded once). blockIdx.y is the launch's layer.
-    template <int HD, bool Streamed>
-    __global__ void __launch_bounds__(kCombineThreads) decode_combine_kernel(DecodeArgs a)
+    // A step's page seal (one workgroup): when the step's position is its
+    // page's last row, the page -- rows 0..30 from the open page, the last
+    // from the step's k and v -- quantised at its tier (copied at FP16) into
+    // its slot, a task a lane (page_tasks.hpp), as the store's seal does.
+    template <int HD>
+    __device__ inline void seal_step_page(const StepStore &s)
     {
+      const int position = *s.position;
+      if (position % kPageTokens != kPageTokens - 1)
+      {
+        return;
+      }
+      const int page = position / kPageTokens;
+      const int W = s.kv_heads * HD;
+      const int tier = s.tiers[page];
+      RowJob j{};
+      j.kind = static_cast<int>(tier == kFP16 ? RowJobKind::kCopy : RowJobKind::kQuantise);
+      j.k_lo = s.open;
+      j.v_lo = s.open + static_cast<std::size_t>(kPageTokens) * W;
+      j.k_hi = s.keys;
+      j.v_hi = s.values;
+      j.split = kPageTokens - 1;
+      j.dst = reinterpret_cast<std::uint8_t *>(s.addresses[page]);
+      j.tier = tier;
+      for (int task = threadIdx.x; task < W; task += kCombineThreads)
+      {
+        page_tasks::run_row_task<HD>(j, s.lay, task, s.kv_heads);
+      }
+    }
+
+    template <int HD, bool Streamed>
+    __global__ void __launch_bounds__(kCombineThreads) decode_combine_kernel(const DecodeArgs args)
+    {
+      if constexpr (!Streamed)
+      {
+        // The seal reads the launch's own (constant) arguments: its index
+        // into the layouts, taken from memory, would otherwise pin the
+        // combine's mutable copy below to private memory.
+        if (args.seal_block != 0 && static_cast<int>(blockIdx.x) == args.seal_block - 1)
+        {
+          seal_step_page<HD>(args.seal);
+          return;
+        }
+      }
+      DecodeArgs a = args;
       // Fixed splits unless the streaming kernel wrote the partials: the
       // per-layer form carries none of the streaming geometry's code.
       go_live(a);
@@ -2064,6 +2111,19 @@ namespace mi
     }
     d.live_seq_k = ls.live_seq_k;
     d.score_every = 1;
+    if (ls.seal != nullptr)
+    {
+      if (ls.live_seq_k == nullptr || !ls.split || ls.layers != 1)
+      {
+        throw InvalidArgument("a step's seal rides with one split layer whose position lives on "
+                              "the device");
+      }
+      d.seal = *ls.seal;
+      for (int t = kINT8; t <= kINT2; ++t)
+      {
+        d.seal.lay[t] = page_layout(t, kPageTokens, d.seal.kv_heads, a.head_dim);
+      }
+    }
     int stream_blocks = 0;
     if (streaming)
     {
@@ -2163,9 +2223,11 @@ namespace mi
                            lds, stream, d);
         hip_check(hipGetLastError(), "decode pages kernel launch");
       }
+      const int combine_blocks = a.heads * (hd / (4 * kQuads)) + mass_blocks +
+                                 (warm ? kWarmBlocks : 0);
+      d.seal_block = ls.seal != nullptr ? combine_blocks + 1 : 0;
       hipLaunchKernelGGL(stream_blocks > 0 ? combine_streamed : combine_kernel,
-                         dim3(a.heads * (hd / (4 * kQuads)) + mass_blocks + (warm ? kWarmBlocks : 0),
-                              ls.layers),
+                         dim3(combine_blocks + (ls.seal != nullptr ? 1 : 0), ls.layers),
                          dim3(kCombineThreads), 0, stream, d);
       hip_check(hipGetLastError(), "decode combine kernel launch");
     };

@@ -71,7 +71,6 @@ namespace mi
     state_ = device_bytes(4 * sizeof(int));
     residual_ = device_bytes(static_cast<std::size_t>(s.hidden) * sizeof(float));
     normed_ = device_bytes(static_cast<std::size_t>(s.hidden) * 2);
-    qk_raw_ = device_bytes((q_width + kv_width) * 2);
     qk_ = device_bytes((q_width + kv_width) * 2);
     v_ = device_bytes(kv_width * 2);
     attended_ = device_bytes(q_width * 2);
@@ -127,11 +126,9 @@ namespace mi
   {
     const ModelShape &s = shape_;
     const int q_width = s.heads * s.head_dim;
-    const int kv_width = s.kv_heads * s.head_dim;
     int *state = state_->as<int>();
     float *residual = residual_->as<float>();
     auto *normed = normed_->as<std::uint16_t>();
-    auto *qk_raw = qk_raw_->as<std::uint16_t>();
     auto *qk = qk_->as<std::uint16_t>();
     auto *v = v_->as<std::uint16_t>();
     auto *attended = attended_->as<std::uint16_t>();
@@ -153,21 +150,34 @@ namespace mi
     for (int l = 0; l < s.layers; ++l)
     {
       const LayerWeights &w = weights_.layers[l];
-      ProjectArgs qkv{};
-      qkv.segments = 3;
-      qkv.seg[0] = {w.q_w, w.q_b, qk_raw, q_width};
+      // q, k and v with the input's RMSNorm, RoPE and the open page's row in
+      // one launch; the page's seal, when the row is its last, rides in the
+      // decode's combine.
+      const StepStore target = cache_.step_store(l, qk + q_width, v, state + kStepPosition);
+      QkvStep qkv{};
+      qkv.w[0] = w.q_w;
+      qkv.w[1] = w.k_w;
+      qkv.w[2] = w.v_w;
+      qkv.b[0] = w.q_b;
       // The key bias, when attention adds it rotated, stays out of k.
-      qkv.seg[1] = {w.k_w, key_bias_ ? nullptr : w.k_b, qk_raw + q_width, kv_width};
-      qkv.seg[2] = {w.v_w, w.v_b, v, kv_width};
+      qkv.b[1] = key_bias_ ? nullptr : w.k_b;
+      qkv.b[2] = w.v_b;
       qkv.in = s.hidden;
-      qkv.mode = ProjectMode::kHalf;
-      normed_input(qkv, w.input_norm);
-      launch_project(qkv, stream);
-      // q's heads and k's heads are rows of one buffer, rotated with the store.
-      cache_.rope_store_step(l, qk_raw, qk, s.heads, v, state + kStepPosition, rope_);
+      qkv.residual = residual;
+      qkv.norm_weight = w.input_norm;
+      qkv.eps = s.rms_eps;
+      qkv.heads = s.heads;
+      qkv.kv_heads = s.kv_heads;
+      qkv.head_dim = s.head_dim;
+      qkv.rope = rope_.data();
+      qkv.position = state + kStepPosition;
+      qkv.qk = qk;
+      qkv.v = v;
+      qkv.open = target.open;
+      launch_qkv_step(qkv, stream);
       cache_.attention_step(l, qk, key_bias_ ? w.k_b : nullptr, &rope_, attended,
                             state + kStepSeqK, max_seq_k, s.heads, s.kv_heads, s.head_dim,
-                            qk + q_width, v, kept);
+                            qk + q_width, v, kept, &target);
       ProjectArgs o{};
       o.segments = 1;
       o.seg[0] = {w.o_w, nullptr, residual, s.hidden};
@@ -190,7 +200,8 @@ namespace mi
       down.x = activated;
       down.mode = ProjectMode::kAccumulate;
       launch_project(down, stream);
-      launches += 7; // norm + qkv, RoPE + store, decode + combine, o, norm + gate/up, down
+      launches += 6; // norm + qkv + RoPE + store, decode + combine (+ seal), o, norm + gate/up,
+                     // down
     }
     ProjectArgs head{};
     head.segments = 1;

@@ -124,13 +124,12 @@ namespace mi
     int head_blocks_ = 0;
     int token_room_ = 0;
     // Device buffers: the step's state (four ints), the residual (fp32),
-    // the normed input, [q | k] before and after RoPE, v, the attention's
+    // the normed input, [q | k] after RoPE, v, the attention's
     // output, the MLP's activation, the logits, the head's block bests, the
     // kept page statistics, and the run's tokens.
     std::unique_ptr<DeviceBuffer> state_;
     std::unique_ptr<DeviceBuffer> residual_;
     std::unique_ptr<DeviceBuffer> normed_;
-    std::unique_ptr<DeviceBuffer> qk_raw_;
     std::unique_ptr<DeviceBuffer> qk_;
     std::unique_ptr<DeviceBuffer> v_;
     std::unique_ptr<DeviceBuffer> attended_;

@@ -270,6 +270,8 @@ namespace mi
   // and its q, chunk rows, output, mass and scores at i times the strides
   // (in elements) from the AttentionArgs / KVSource bases. AttentionArgs'
   // partials are not read: the fast path keeps its own workspace.
+  struct StepStore;
+
   struct DecodeLayers
   {
     bool split; // a wave a page and a combine; else a workgroup a KV head
@@ -292,6 +294,11 @@ namespace mi
     // kernels run, and AttentionArgs::seq_k is the most it may be, which
     // sizes the launch and the strides.
     const int *live_seq_k;
+    // With a live position: the step's page seal, done by one more
+    // workgroup of the combine when *seal->position is its page's last row
+    // (the page quantised, or copied at FP16, from the open page's rows and
+    // the step's k and v rows into its slot). Null: no seal.
+    const StepStore *seal;
   };
   // Whether the fast path takes this decode: one query, no key bias, 32-token
   // pages, head_dim 64 or 128, a group of at most 16 heads, 16-byte aligned
@@ -397,18 +404,34 @@ namespace mi
     PageLayout lay[kTierCount];
   };
   void launch_step_store(const StepStore &s, int head_dim, hipStream_t stream);
-  // The same store with the step's RoPE first, in one launch: q's `heads`
-  // and k's heads of qk_raw rotated at *position from the {cos, sin} table
-  // (as the RoPE kernel rotates them, to the bit) into qk, then k's rotated
-  // row and the values stored. One workgroup: kv_heads * head_dim <= 1024.
-  struct StepRopeStore
+
+  // One decode step's q, k and v of a layer in one launch: the projections
+  // of RMSNorm(residual) (formed in the launch, to the RMSNorm kernel's
+  // bits), a wave the two rows of one rotation pair (channels j and
+  // j + head_dim/2 of a head), each row's bias added before its one rounding
+  // to fp16 (the projection's arithmetic); q and k then rotated at
+  // *position (the RoPE kernel's arithmetic) into qk = [q | k], v into v;
+  // k's and v's rows also written into the open page at row *position % 32
+  // unless that is the page's last row, whose seal reads them from qk and v
+  // (DecodeLayers::seal). Bit-identical to the projection, RoPE and store
+  // launched apart.
+  struct QkvStep
   {
-    StepStore store; // store.keys is ignored: the rotated k is qk + heads * head_dim
-    const std::uint16_t *qk_raw;
-    std::uint16_t *qk;
-    const float *rope;
+    const std::uint16_t *w[3]; // q, k, v weights, [rows][in]
+    const std::uint16_t *b[3]; // their biases, or null
+    int in;
+    const float *residual;
+    const std::uint16_t *norm_weight;
+    float eps;
     int heads;
+    int kv_heads;
+    int head_dim;
+    const float *rope; // {cos, sin} per (position, j < head_dim / 2)
+    const int *position;
+    std::uint16_t *qk; // heads * head_dim of q, then kv_heads * head_dim of k
+    std::uint16_t *v;
+    std::uint16_t *open; // the layer's open page: P rows of keys, then P of values
   };
-  void launch_step_rope_store(const StepRopeStore &s, int head_dim, hipStream_t stream);
+  void launch_qkv_step(const QkvStep &s, hipStream_t stream);
 
 } // namespace mi

@@ -1133,8 +1133,8 @@ namespace mi
     attend_open_[layer] = current_open_[layer];
   }
 
-  void KVPages::rope_store_step(int layer, const void *qk_raw, void *qk, int heads,
-                                const void *values, const int *position, const RopeTable &rope)
+  StepStore KVPages::step_store(int layer, const void *keys, const void *values,
+                                const int *position)
   {
     require_layer(layer);
     if (!seals_ || !open_pages_)
@@ -1142,33 +1142,24 @@ namespace mi
       throw LogicError("a store with its position on the device needs a sealing cache with "
                        "positions reserved");
     }
-    if (rope.head_dim() != head_dim_)
-    {
-      throw InvalidArgument("the RoPE table is for head_dim " + std::to_string(rope.head_dim()) +
-                            "; this cache holds " + std::to_string(head_dim_));
-    }
-    const hipStream_t stream = runtime_stream();
-    sync_tables(stream);
-    StepRopeStore st{};
-    st.store.values = static_cast<const std::uint16_t *>(values);
-    st.store.position = position;
-    st.store.open = open_page(layer, current_open_[layer]);
+    sync_tables(runtime_stream());
+    StepStore st{};
+    st.keys = static_cast<const std::uint16_t *>(keys);
+    st.values = static_cast<const std::uint16_t *>(values);
+    st.position = position;
+    st.open = open_page(layer, current_open_[layer]);
     const std::size_t row = static_cast<std::size_t>(layer) * table_.stride();
-    st.store.addresses = table_.addresses() + row;
-    st.store.tiers = table_.tiers() + row;
-    st.store.kv_heads = kv_heads_;
-    st.qk_raw = static_cast<const std::uint16_t *>(qk_raw);
-    st.qk = static_cast<std::uint16_t *>(qk);
-    st.rope = rope.data();
-    st.heads = heads;
-    launch_step_rope_store(st, head_dim_, stream);
+    st.addresses = table_.addresses() + row;
+    st.tiers = table_.tiers() + row;
+    st.kv_heads = kv_heads_;
     attend_open_[layer] = current_open_[layer];
+    return st;
   }
 
   void KVPages::attention_step(int layer, const void *q, const void *k_bias, const RopeTable *rope,
                                void *out, const int *live_seq_k, int max_seq_k, int heads,
                                int kv_heads, int head_dim, const void *keys, const void *values,
-                               float *keep)
+                               float *keep, const StepStore *seal)
   {
     require_layer(layer);
     if (static_cast<std::size_t>(kv_heads) * head_dim != kv_width_)
@@ -1224,6 +1215,7 @@ namespace mi
     ls.split = true;
     ls.layers = 1;
     ls.live_seq_k = live_seq_k;
+    ls.seal = seal;
     if (keep != nullptr)
     {
       const int pages = (max_seq_k + page_tokens_ - 1) / page_tokens_;

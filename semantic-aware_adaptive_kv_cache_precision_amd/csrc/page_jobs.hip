@@ -9,27 +9,15 @@
 //     value (a decode step's store uploads nothing);
 //   - table_edits: a page table's changed entries applied on the device.
 //
-// The register quantiser. A 32-token page of W = kv_heads * head_dim
-// channels (head_dim 64 or 128) is split into W tasks of 64 elements, a lane
-// each, none staged through LDS:
-//   - key task (j, g), W/2 of them: channels [8j, 8j + 8) of rows
-//     [8g, 8g + 8), eight 16-byte loads. A key channel's range is over all
-//     32 rows, so the four tasks of a chunk (adjacent lanes) fold their
-//     minima and maxima with two lane exchanges; each then codes its own
-//     8 rows, one 2/4/8-byte store a row;
-//   - value task (r, h, part), W/2 of them: channels [64 part, 64 part + 64)
-//     of head h in row r, eight 16-byte loads; at head_dim 128 the two
-//     parts of a (row, head) group fold their range with one exchange; the
-//     codes leave in 16-byte stores.
-// Every input byte is read once and every output byte written once; a page
-// is W lanes (a workgroup of 256 covers one 1.5B page, two 0.5B pages), so a
-// batch of pages fills the device with no serial walk over rows.
-//
-// Codes, scales and zeros follow quant_core.hpp (the reference's rules,
-// quant.cu:44-199) to the bit.
+// The register quantiser's tasks (page_tasks.hpp): a 32-token page is W =
+// kv_heads * head_dim tasks of 64 elements, a lane each, none staged through
+// LDS. Every input byte is read once and every output byte written once; a
+// page is W lanes (a workgroup of 256 covers one 1.5B page, two 0.5B pages),
+// so a batch of pages fills the device with no serial walk over rows.
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "page_tasks.hpp"
 #include "quant_core.hpp"
 
 #include <algorithm>
@@ -39,7 +27,7 @@ namespace mi
   namespace
   {
     constexpr int kThreads = 256;
-    constexpr int kP = 32; // the register quantiser's page
+    using namespace page_tasks;
 
     __device__ inline std::uint8_t *resolve(const PageSpaces &s, std::uint32_t ref)
     {
@@ -60,375 +48,6 @@ namespace mi
     {
       const std::uint32_t space = ref >> kRefIndexBits;
       return space >= kShadowSpace ? s.shadow_bytes : s.bytes[space];
-    }
-
-    // Rows [0, split) at lo, rows [split, P) at hi; `width` halves a row.
-    struct Rows
-    {
-      const std::uint16_t *lo;
-      const std::uint16_t *hi;
-      int split;
-      int width;
-      __device__ const std::uint16_t *row(int t) const
-      {
-        return t < split ? lo + static_cast<std::size_t>(t) * width
-                         : hi + static_cast<std::size_t>(t - split) * width;
-      }
-    };
-
-    __device__ inline uint4 load16(const std::uint16_t *p)
-    {
-      return *reinterpret_cast<const uint4 *>(p);
-    }
-    __device__ inline void store16(std::uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
-
-    // fp16 bits to fp32 by the hardware conversion (exact, denormals kept).
-    __device__ inline float f16_bits(unsigned bits)
-    {
-      return __half2float(__ushort_as_half(static_cast<unsigned short>(bits)));
-    }
-
-    __device__ inline float half_at(const uint4 &v, int c)
-    {
-      const unsigned w = c < 2 ? v.x : c < 4 ? v.y : c < 6 ? v.z : v.w;
-      return f16_bits((c & 1) ? (w >> 16) : (w & 0xFFFFu));
-    }
-
-    __device__ inline unsigned half_of(float x) { return __half_as_ushort(__float2half_rn(x)); }
-
-    // What a task does with the page it reads.
-    enum class Emit : int
-    {
-      kCodes,  // the quantised page at dst
-      kRound,  // this half through the tier and back, as FP16 rows at dst
-      kRaw,    // this half's rows as they are, at dst
-    };
-
-    // Eight codes of one 16-byte run (eight fp16 values), packed the first
-    // lowest: 8 (INT8), 4 (INT4) or 2 (INT2) bytes. The codes are exact
-    // integers in floats: two INT4 (or four INT2) codes are combined into
-    // one byte's value exactly (q0 + 16 q1, ...) and each byte is placed by
-    // v_cvt_pk_u8_f32 (of an integer: no rounding).
-    template <int Bits>
-    __device__ __forceinline__ unsigned long long codes8(const uint4 &v, const float (&lo)[8],
-                                                         const float (&scale)[8],
-                                                         const float (&inv)[8])
-    {
-      float x[8], q[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-      {
-        x[c] = half_at(v, c);
-      }
-      quant_core::quotients_of<Bits>(x, lo, scale, inv, q);
-      if constexpr (Bits == 8)
-      {
-        unsigned w0 = 0, w1 = 0;
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-        {
-          w0 = __builtin_amdgcn_cvt_pk_u8_f32(q[c], c, w0);
-          w1 = __builtin_amdgcn_cvt_pk_u8_f32(q[4 + c], c, w1);
-        }
-        return static_cast<unsigned long long>(w0) | (static_cast<unsigned long long>(w1) << 32);
-      }
-      else if constexpr (Bits == 4)
-      {
-        unsigned w = 0;
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-        {
-          w = __builtin_amdgcn_cvt_pk_u8_f32(fmaf(q[2 * c + 1], 16.0f, q[2 * c]), c, w);
-        }
-        return w;
-      }
-      else
-      {
-        unsigned w = 0;
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-        {
-          const float b = fmaf(q[4 * c + 3], 64.0f,
-                               fmaf(q[4 * c + 2], 16.0f, fmaf(q[4 * c + 1], 4.0f, q[4 * c])));
-          w = __builtin_amdgcn_cvt_pk_u8_f32(b, c, w);
-        }
-        return w;
-      }
-    }
-
-    template <int Bits>
-    __device__ __forceinline__ void store_codes8(std::uint8_t *at, unsigned long long packed)
-    {
-      if constexpr (Bits == 8)
-      {
-        *reinterpret_cast<uint2 *>(at) =
-            uint2{static_cast<unsigned>(packed), static_cast<unsigned>(packed >> 32)};
-      }
-      else if constexpr (Bits == 4)
-      {
-        *reinterpret_cast<unsigned *>(at) = static_cast<unsigned>(packed);
-      }
-      else
-      {
-        *reinterpret_cast<std::uint16_t *>(at) = static_cast<std::uint16_t>(packed);
-      }
-    }
-
-    // fmaf(code, scale, zero) to fp16 for eight codes, as dequantise_page.
-    template <int Bits>
-    __device__ __forceinline__ uint4 round8(const uint4 &v, const float (&lo)[8],
-                                            const float (&scale)[8], const float (&inv)[8])
-    {
-      float x[8], q[8];
-      unsigned h[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-      {
-        x[c] = half_at(v, c);
-      }
-      quant_core::quotients_of<Bits>(x, lo, scale, inv, q);
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-      {
-        h[c] = half_of(fmaf(q[c], scale[c], lo[c]));
-      }
-      return uint4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                   h[6] | (h[7] << 16)};
-    }
-
-    // A key task: channels [8j, 8j + 8) of rows [8g, 8g + 8). The four tasks
-    // of chunk j sit in lanes 4j .. 4j + 3 of one wave. Two passes: the
-    // ranges, with all eight rows' loads in flight at once; then the codes a
-    // row at a time, each row read again (from cache: the first pass just
-    // brought it), so that the 64 divisions never hold all eight rows.
-    template <int Bits>
-    __device__ __forceinline__ void key_task(const Rows &keys, int j, int g, int W,
-                                             std::uint8_t *dst, const PageLayout &L, Emit emit,
-                                             int rows_limit, int dst_row)
-    {
-      if (emit == Emit::kRaw)
-      {
-        auto *out = reinterpret_cast<std::uint16_t *>(dst);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-        {
-          // A fill brings fewer rows than a page: rows past them are not read.
-          const int t = 8 * g + i;
-          if (t < rows_limit)
-          {
-            store16(out + static_cast<std::size_t>(dst_row + t) * W + 8 * j,
-                    load16(keys.row(t) + 8 * j));
-          }
-        }
-        return;
-      }
-      float lo[8], hi[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-      {
-        lo[c] = INFINITY;
-        hi[c] = -INFINITY;
-      }
-      // The eight rows stay in registers from the range to the codes.
-      uint4 raw[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-      {
-        raw[i] = load16(keys.row(8 * g + i) + 8 * j);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-      {
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-        {
-          const float x = half_at(raw[i], c);
-          lo[c] = fminf(lo[c], x);
-          hi[c] = fmaxf(hi[c], x);
-        }
-      }
-      // The chunk's four row groups: lanes that differ in the low two bits.
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-      {
-        lo[c] = fminf(lo[c], __shfl_xor(lo[c], 1));
-        hi[c] = fmaxf(hi[c], __shfl_xor(hi[c], 1));
-        lo[c] = fminf(lo[c], __shfl_xor(lo[c], 2));
-        hi[c] = fmaxf(hi[c], __shfl_xor(hi[c], 2));
-      }
-      float scale[8], inv[8];
-      unsigned sword[4] = {0, 0, 0, 0}, zword[4] = {0, 0, 0, 0};
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-      {
-        const std::uint16_t s = quant_core::scale_bits_fast(lo[c], hi[c], Bits);
-        scale[c] = f16_bits(s);
-        inv[c] = quant_core::inverse_of(scale[c]);
-        sword[c / 2] |= static_cast<unsigned>(s) << (16 * (c % 2));
-        zword[c / 2] |= half_of(lo[c]) << (16 * (c % 2));
-      }
-      if (emit == Emit::kCodes)
-      {
-        if (g == 0)
-        {
-          store16(reinterpret_cast<std::uint16_t *>(dst + L.key_scales) + 8 * j,
-                  uint4{sword[0], sword[1], sword[2], sword[3]});
-          store16(reinterpret_cast<std::uint16_t *>(dst + L.key_zeros) + 8 * j,
-                  uint4{zword[0], zword[1], zword[2], zword[3]});
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-        {
-          const int t = 8 * g + i;
-          const std::size_t e = static_cast<std::size_t>(t) * W + 8 * j; // first element
-          store_codes8<Bits>(dst + L.key_codes + e * Bits / 8,
-                             codes8<Bits>(raw[i], lo, scale, inv));
-        }
-        return;
-      }
-      // Round trip: each code back to fp16, as dequantise_page gives it.
-      auto *out = reinterpret_cast<std::uint16_t *>(dst);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-      {
-        const int t = 8 * g + i;
-        store16(out + static_cast<std::size_t>(t) * W + 8 * j,
-                round8<Bits>(raw[i], lo, scale, inv));
-      }
-    }
-
-    // A value task: channels [64 part, 64 part + 64) of head h in row r.
-    // At head_dim 128 the group's two parts sit in adjacent lanes. The same
-    // two passes as a key task, over the row's eight 16-byte runs.
-    template <int Bits, int HD>
-    __device__ __forceinline__ void value_task(const Rows &values, int r, int h, int part,
-                                               int kv_heads, int W, std::uint8_t *dst,
-                                               const PageLayout &L, Emit emit, int rows_limit,
-                                               int dst_row)
-    {
-      const int ch0 = h * HD + 64 * part;
-      if (r >= rows_limit)
-      {
-        return; // a fill's row past those it brings: nothing to read or write
-      }
-      const std::uint16_t *src = values.row(r) + ch0;
-      // FP16 output rows (raw and round trip) sit in the page's second half.
-      auto *out = reinterpret_cast<std::uint16_t *>(dst) + static_cast<std::size_t>(kP) * W;
-      if (emit == Emit::kRaw)
-      {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-        {
-          store16(out + static_cast<std::size_t>(dst_row + r) * W + ch0 + 8 * i,
-                  load16(src + 8 * i));
-        }
-        return;
-      }
-      float lo = INFINITY, hi = -INFINITY;
-      uint4 raw[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-      {
-        raw[i] = load16(src + 8 * i);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-      {
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-        {
-          const float x = half_at(raw[i], c);
-          lo = fminf(lo, x);
-          hi = fmaxf(hi, x);
-        }
-      }
-      if constexpr (HD == 128)
-      {
-        lo = fminf(lo, __shfl_xor(lo, 1));
-        hi = fmaxf(hi, __shfl_xor(hi, 1));
-      }
-      const std::uint16_t sbits = quant_core::scale_bits_fast(lo, hi, Bits);
-      const float scale = f16_bits(sbits);
-      const float inverse = quant_core::inverse_of(scale);
-      float los[8], scales[8], invs[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-      {
-        los[c] = lo;
-        scales[c] = scale;
-        invs[c] = inverse;
-      }
-      if (emit == Emit::kCodes)
-      {
-        if (part == 0)
-        {
-          const int group = r * kv_heads + h;
-          reinterpret_cast<std::uint16_t *>(dst + L.value_scales)[group] = sbits;
-          reinterpret_cast<std::uint16_t *>(dst + L.value_zeros)[group] =
-              static_cast<std::uint16_t>(half_of(lo));
-        }
-        // The run's 64 codes (8 Bits bytes), 16-byte aligned: whole
-        // 16-byte stores.
-        std::uint8_t *at =
-            dst + L.value_codes + (static_cast<std::size_t>(r) * W + ch0) * Bits / 8;
-        unsigned words[2 * Bits];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-        {
-          const unsigned long long packed = codes8<Bits>(raw[i], los, scales, invs);
-          if constexpr (Bits == 8)
-          {
-            words[2 * i] = static_cast<unsigned>(packed);
-            words[2 * i + 1] = static_cast<unsigned>(packed >> 32);
-          }
-          else if constexpr (Bits == 4)
-          {
-            words[i] = static_cast<unsigned>(packed);
-          }
-          else if (i % 2 == 0)
-          {
-            words[i / 2] = static_cast<unsigned>(packed);
-          }
-          else
-          {
-            words[i / 2] |= static_cast<unsigned>(packed) << 16;
-          }
-        }
-#pragma unroll
-        for (int w = 0; w < 2 * Bits; w += 4)
-        {
-          *reinterpret_cast<uint4 *>(at + 4 * w) =
-              uint4{words[w], words[w + 1], words[w + 2], words[w + 3]};
-        }
-        return;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-      {
-        store16(out + static_cast<std::size_t>(r) * W + ch0 + 8 * i,
-                round8<Bits>(raw[i], los, scales, invs));
-      }
-    }
-
-    // Task `task` (of W) of one 32-token page: keys first, then values.
-    template <int Bits, int HD>
-    __device__ __forceinline__ void page_task(int task, const Rows &keys, const Rows &values, int kv_heads,
-                              std::uint8_t *dst, const PageLayout &L, Emit key_emit,
-                              Emit value_emit, int rows_limit = kP, int dst_row = 0)
-    {
-      const int W = kv_heads * HD;
-      if (task < W / 2)
-      {
-        key_task<Bits>(keys, task >> 2, task & 3, W, dst, L, key_emit, rows_limit, dst_row);
-      }
-      else
-      {
-        constexpr int kParts = HD / 64;
-        const int v = task - W / 2;
-        const int group = v / kParts;
-        value_task<Bits, HD>(values, group / kv_heads, group % kv_heads, v % kParts, kv_heads, W,
-                             dst, L, value_emit, rows_limit, dst_row);
-      }
     }
 
     // ---- batches by reference ------------------------------------------------
@@ -534,34 +153,6 @@ namespace mi
       PageLayout lay[kTierCount];
     };
 
-    template <int HD>
-    __device__ __forceinline__ void run_row_task(const RowJob &j, const PageLayout *lay, int task, int kv_heads)
-    {
-      const int W = kv_heads * HD;
-      const RowJobKind kind = static_cast<RowJobKind>(j.kind);
-      const Rows keys{j.k_lo, j.k_hi, j.split, W};
-      const Rows values{j.v_lo, j.v_hi, j.split, W};
-      const Emit ke = kind == RowJobKind::kQuantise   ? Emit::kCodes
-                      : kind == RowJobKind::kRoundKeys ? Emit::kRound
-                                                       : Emit::kRaw;
-      const Emit ve = kind == RowJobKind::kQuantise     ? Emit::kCodes
-                      : kind == RowJobKind::kRoundValues ? Emit::kRound
-                                                         : Emit::kRaw;
-      const int rows = kind == RowJobKind::kFill ? j.rows : kP;
-      const int dst_row = kind == RowJobKind::kFill ? j.dst_row : 0;
-      const bool coded = ke != Emit::kRaw || ve != Emit::kRaw;
-      const PageLayout &L = lay[coded ? j.tier : kINT8];
-      const int bits = coded ? L.bits : 0;
-      switch (bits)
-      {
-      case 8: page_task<8, HD>(task, keys, values, kv_heads, j.dst, L, ke, ve, rows, dst_row); break;
-      case 4: page_task<4, HD>(task, keys, values, kv_heads, j.dst, L, ke, ve, rows, dst_row); break;
-      case 2: page_task<2, HD>(task, keys, values, kv_heads, j.dst, L, ke, ve, rows, dst_row); break;
-      default: page_task<8, HD>(task, keys, values, kv_heads, j.dst, L, Emit::kRaw, Emit::kRaw, rows,
-                                dst_row);
-      }
-    }
-
     // Job blockIdx.y, tasks blockIdx.x * 256 + tid (of W).
     template <int HD>
     __global__ void __launch_bounds__(kThreads) row_jobs_kernel(RowJobs jobs, int kv_heads)
@@ -613,65 +204,6 @@ namespace mi
         j.tier = tier;
       }
       run_row_task<HD>(j, s.lay, task, s.kv_heads);
-    }
-
-    // The step's RoPE and its store in one workgroup: every (head, angle)
-    // pair of q and k rotated into qk (the RoPE kernel's arithmetic, the
-    // angle's cos and sin from the table), then, once the workgroup has
-    // them, the store or seal of the rotated k row and the values.
-    template <int HD>
-    __global__ void __launch_bounds__(1024) step_rope_store_kernel(StepRopeStore s)
-    {
-      constexpr int kHalf = HD / 2;
-      const int position = *s.store.position;
-      const int pairs = (s.heads + s.store.kv_heads) * kHalf;
-      const float *cs = s.rope + static_cast<std::size_t>(position) * kHalf * 2;
-      for (int i = threadIdx.x; i < pairs; i += blockDim.x)
-      {
-        const int head = i / kHalf;
-        const int j = i % kHalf;
-        const std::size_t at = static_cast<std::size_t>(head) * HD + j;
-        const float c = cs[2 * j];
-        const float sn = cs[2 * j + 1];
-        const float x1 = f16_bits(s.qk_raw[at]);
-        const float x2 = f16_bits(s.qk_raw[at + kHalf]);
-        s.qk[at] = static_cast<std::uint16_t>(half_of(x1 * c - x2 * sn));
-        s.qk[at + kHalf] = static_cast<std::uint16_t>(half_of(x2 * c + x1 * sn));
-      }
-      __syncthreads();
-      const int task = threadIdx.x;
-      const int W = s.store.kv_heads * HD;
-      if (task >= W)
-      {
-        return;
-      }
-      const std::uint16_t *keys = s.qk + static_cast<std::size_t>(s.heads) * HD;
-      const int row = position % kP;
-      const int page = position / kP;
-      RowJob j{};
-      if (row < kP - 1)
-      {
-        j.kind = static_cast<int>(RowJobKind::kFill);
-        j.k_lo = j.k_hi = keys;
-        j.v_lo = j.v_hi = s.store.values;
-        j.rows = 1;
-        j.dst_row = row;
-        j.dst = reinterpret_cast<std::uint8_t *>(s.store.open);
-        j.tier = kFP16;
-      }
-      else
-      {
-        const int tier = s.store.tiers[page];
-        j.kind = static_cast<int>(tier == kFP16 ? RowJobKind::kCopy : RowJobKind::kQuantise);
-        j.k_lo = s.store.open;
-        j.v_lo = s.store.open + static_cast<std::size_t>(kP) * W;
-        j.k_hi = keys;
-        j.v_hi = s.store.values;
-        j.split = kP - 1;
-        j.dst = reinterpret_cast<std::uint8_t *>(s.store.addresses[page]);
-        j.tier = tier;
-      }
-      run_row_task<HD>(j, s.store.lay, task, s.store.kv_heads);
     }
 
     // Any other shape: a workgroup a job, the rows staged in LDS.
@@ -967,32 +499,6 @@ namespace mi
       hipLaunchKernelGGL(step_store_kernel<64>, dim3(blocks), dim3(kThreads), 0, stream, args);
     }
     hip_check(hipGetLastError(), "step store kernel launch");
-  }
-
-  void launch_step_rope_store(const StepRopeStore &s, int head_dim, hipStream_t stream)
-  {
-    const int W = s.store.kv_heads * head_dim;
-    if (!register_shape(kP, s.store.kv_heads, head_dim) || W > 1024 || s.rope == nullptr ||
-        s.heads <= 0)
-    {
-      throw InvalidArgument("the step's RoPE and store in one launch take head_dim 64 or 128, "
-                            "128 to 1024 channels a row and a RoPE table");
-    }
-    StepRopeStore args = s;
-    for (int t = kINT8; t <= kINT2; ++t)
-    {
-      args.store.lay[t] = page_layout(t, kP, s.store.kv_heads, head_dim);
-    }
-    const int threads = (W + 63) / 64 * 64;
-    if (head_dim == 128)
-    {
-      hipLaunchKernelGGL(step_rope_store_kernel<128>, dim3(1), dim3(threads), 0, stream, args);
-    }
-    else
-    {
-      hipLaunchKernelGGL(step_rope_store_kernel<64>, dim3(1), dim3(threads), 0, stream, args);
-    }
-    hip_check(hipGetLastError(), "step RoPE + store kernel launch");
   }
 
   void launch_table_edits(const TableEdit *edits, int count, unsigned long long *addresses,

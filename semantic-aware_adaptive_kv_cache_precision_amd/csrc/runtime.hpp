@@ -480,15 +480,19 @@ namespace mi
     // the positions before `end` were stored.
     void prepare_step(int max_seq_k, int heads, int head_dim);
     void store_step(int layer, const void *keys, const void *values, const int *position);
-    // store_step with the step's RoPE first, in one launch: q's `heads` and
-    // k's heads of qk_raw ([q | k], fp16) rotated at *position from `rope`
-    // into qk, as the RoPE kernel rotates them, then k's rotated row stored.
-    void rope_store_step(int layer, const void *qk_raw, void *qk, int heads, const void *values,
-                         const int *position, const RopeTable &rope);
+    // The layer's store target for a step whose projection writes its row
+    // (launch_qkv_step): the open page (the step's row goes there unless it
+    // is the page's last) and the page table row for the seal; `keys` and
+    // `values` are where the step's k and v rows are, which the seal reads
+    // for the last row. The store is recorded by stored_on_device as any
+    // store_step's.
+    StepStore step_store(int layer, const void *keys, const void *values, const int *position);
+    // With `seal` (step_store's target), the combine's extra workgroup seals
+    // the step's page when its position is the page's last row.
     void attention_step(int layer, const void *q, const void *k_bias, const RopeTable *rope,
                         void *out, const int *live_seq_k, int max_seq_k, int heads,
                         int kv_heads, int head_dim, const void *keys, const void *values,
-                        float *keep);
+                        float *keep, const StepStore *seal = nullptr);
     void fold_step(float *keep, const int *live_seq_k, int max_seq_k, int heads, int kv_heads,
                    int head_dim, int score_every, float *scores, long long scores_stride,
                    float alpha);

@@ -400,6 +400,116 @@ namespace mi
       }
     }
 
+    // A decode step's q, k and v of a layer (QkvStep): an item a wave, the
+    // rotation pair j of unit u (q's heads, then k's, then v's), its two
+    // weight rows' dots with the normed input staged in LDS (the
+    // projection's runs and order, so the same bits), then the bias, the
+    // rounding, RoPE for q and k, and the open page's row for k and v.
+    template <int Waves, int Ahead>
+    __global__ void __launch_bounds__(64 * Waves) qkv_step_kernel(QkvStep p)
+    {
+      constexpr int kBlockThreads = 64 * Waves;
+      constexpr int kPage = 32;
+      extern __shared__ u32x4 x_lds[];
+      __shared__ float s_partial[4];
+      const int lane = threadIdx.x & 63;
+      const int wave = threadIdx.x >> 6;
+      const int half = p.head_dim / 2;
+      const int total = (p.heads + 2 * p.kv_heads) * half;
+      const int runs = p.in / 8;
+      const int stride = gridDim.x * Waves;
+      const auto item_rows = [&](int item, int &seg, int &head, int &j) {
+        const int u = item / half;
+        j = item % half;
+        seg = u < p.heads ? 0 : u < p.heads + p.kv_heads ? 1 : 2;
+        head = seg == 0 ? u : seg == 1 ? u - p.heads : u - p.heads - p.kv_heads;
+      };
+      u32x4 a[Ahead], b[Ahead];
+      const auto load = [&](int item) {
+        int seg, head, j;
+        item_rows(item, seg, head, j);
+        const std::size_t r0 = static_cast<std::size_t>(head) * p.head_dim + j;
+        load_part<Ahead, true>(a, b, p.w[seg] + r0 * p.in, p.w[seg] + (r0 + half) * p.in, 0,
+                               runs, lane);
+      };
+      int item = blockIdx.x * Waves + wave;
+      if (item < total)
+      {
+        load(item);
+      }
+      const float scale = norm_scale(p.residual, p.in, p.eps, s_partial);
+      for (int r = threadIdx.x; r < runs; r += kBlockThreads)
+      {
+        x_lds[r] = normed_run(p.residual, p.norm_weight, scale, r);
+      }
+      __syncthreads();
+      const int position = *p.position;
+      const int row = position % kPage;
+      const std::size_t W = static_cast<std::size_t>(p.kv_heads) * p.head_dim;
+      for (; item < total; item += stride)
+      {
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < Ahead; ++i)
+        {
+          const int r = lane + 64 * i;
+          if (r < runs)
+          {
+            const u32x4 xv = x_lds[r];
+            acc0 = dot_run(a[i], xv, acc0);
+            acc1 = dot_run(b[i], xv, acc1);
+          }
+        }
+        const float d0 = wave_total(acc0);
+        const float d1 = wave_total(acc1);
+        if (item + stride < total)
+        {
+          load(item + stride);
+        }
+        if (lane != 0)
+        {
+          continue;
+        }
+        int seg, head, j;
+        item_rows(item, seg, head, j);
+        const std::size_t r0 = static_cast<std::size_t>(head) * p.head_dim + j;
+        const std::size_t r1 = r0 + half;
+        const std::uint16_t *bias = p.b[seg];
+        const unsigned h0 = to_half(d0 + (bias != nullptr ? h2f(bias[r0]) : 0.0f));
+        const unsigned h1 = to_half(d1 + (bias != nullptr ? h2f(bias[r1]) : 0.0f));
+        if (seg == 2)
+        {
+          p.v[r0] = static_cast<std::uint16_t>(h0);
+          p.v[r1] = static_cast<std::uint16_t>(h1);
+          if (row < kPage - 1)
+          {
+            std::uint16_t *at = p.open + (kPage + row) * W;
+            at[r0] = static_cast<std::uint16_t>(h0);
+            at[r1] = static_cast<std::uint16_t>(h1);
+          }
+          continue;
+        }
+        // RoPE of the rounded pair, as the RoPE kernel rotates it.
+        const float x1 = h2f(static_cast<std::uint16_t>(h0));
+        const float x2 = h2f(static_cast<std::uint16_t>(h1));
+        const float *cs = p.rope + (static_cast<std::size_t>(position) * half + j) * 2;
+        const float c = cs[0];
+        const float sn = cs[1];
+        const std::uint16_t o1 = to_half(x1 * c - x2 * sn);
+        const std::uint16_t o2 = to_half(x2 * c + x1 * sn);
+        const std::size_t at = static_cast<std::size_t>(seg == 0 ? head : p.heads + head) *
+                                   p.head_dim + j;
+        p.qk[at] = o1;
+        p.qk[at + half] = o2;
+        if (seg == 1 && row < kPage - 1)
+        {
+          std::uint16_t *keys = p.open + row * W;
+          keys[r0] = o1;
+          keys[r1] = o2;
+        }
+      }
+    }
+
     // The step's greedy token from the head's per-block bests, then the
     // step's state moved on: the token is the next step's input and the
     // run's output, the position and seq_k advance by one.
@@ -653,6 +763,45 @@ namespace mi
     hip_check(hipLaunchKernel(reinterpret_cast<const void *>(plan.fn), dim3(plan.blocks),
                               dim3(64 * plan.waves), params, plan.lds, stream),
               "projection kernel launch");
+  }
+
+  void launch_qkv_step(const QkvStep &s, hipStream_t stream)
+  {
+    const int runs = s.in / 8;
+    const int ahead = (runs + 63) / 64;
+    const bool aligned = reinterpret_cast<std::uintptr_t>(s.residual) % 16 == 0 &&
+                         reinterpret_cast<std::uintptr_t>(s.norm_weight) % 16 == 0;
+    if ((s.head_dim != 64 && s.head_dim != 128) || s.in <= 0 || s.in % 8 != 0 || ahead > 4 ||
+        !aligned || s.heads <= 0 || s.kv_heads <= 0 || s.rope == nullptr ||
+        s.position == nullptr || s.open == nullptr)
+    {
+      throw InvalidArgument("a step's q/k/v projection takes head_dim 64 or 128, an input of a "
+                            "multiple of 8 up to 2048 values, 16-byte aligned, a RoPE table, the "
+                            "device position and the open page; got head_dim " +
+                            std::to_string(s.head_dim) + ", input " + std::to_string(s.in));
+    }
+    for (int i = 0; i < 3; ++i)
+    {
+      if (s.w[i] == nullptr || reinterpret_cast<std::uintptr_t>(s.w[i]) % 16 != 0)
+      {
+        throw InvalidArgument("a step's q/k/v projection needs 16-byte aligned weights");
+      }
+    }
+    constexpr int kStepWaves = 4;
+    const int items = (s.heads + 2 * s.kv_heads) * (s.head_dim / 2);
+    const int blocks = (items + kStepWaves - 1) / kStepWaves;
+    const std::size_t lds = static_cast<std::size_t>(s.in) * 2;
+    const auto go = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * kStepWaves), lds, stream, s);
+    };
+    switch (ahead)
+    {
+    case 1: go(qkv_step_kernel<kStepWaves, 1>); break;
+    case 2: go(qkv_step_kernel<kStepWaves, 2>); break;
+    case 3: go(qkv_step_kernel<kStepWaves, 3>); break;
+    default: go(qkv_step_kernel<kStepWaves, 4>); break;
+    }
+    hip_check(hipGetLastError(), "step q/k/v kernel launch");
   }
 
   void launch_advance(const float *best_value, const int *best_index, int blocks, int vocab,

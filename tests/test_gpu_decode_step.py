@@ -262,7 +262,7 @@ def check_step_against_oracle(s, biases, start, seed):
     if want[order[0]] - want[order[1]] > 2 * LOGIT_TOL * scale:
         assert tokens[0] == order[0], (tokens[0], order[:3])
     assert tokens[0] == dense.argmax_rows(got[None].astype(np.float32))[0]
-    assert ms > 0 and step.launches == 1 + 7 * s["layers"] + 1 + 1
+    assert ms > 0 and step.launches == 1 + 6 * s["layers"] + 1 + 1
 
 
 def test_one_step_is_the_oracles_composition_qwen_shape():
@@ -374,6 +374,59 @@ def check_logits(got, want, token):
     if want[order[0]] - want[order[1]] > 2 * LOGIT_TOL * scale:
         assert token == order[0], (token, order[:3])
     assert token == dense.argmax_rows(got[None].astype(np.float32))[0]
+
+
+def test_a_step_seals_its_page_as_quantise_page_of_its_rows():
+    """A step at a page's last row seals the page (in its decode's combine).
+    A cache whose pages are all FP16, fed a token: its page holds the
+    context's 31 rows and the step's own row (the oracle's, within an fp16
+    step). Caches whose layer under test is at a quantised tier, every layer
+    before it FP16 (so the layer's input, and its row, is the FP16 cache's),
+    fed the same token: the layer's page is the oracle's quantise_page of the
+    FP16 page's rows at that tier, to the bit."""
+    m = mi()
+    for shape, biases, seed in ((small_shape(heads=12, kv_heads=2, head_dim=128), True, 41),
+                                (small_shape(hidden=512, intermediate=1024, heads=16,
+                                             kv_heads=4, head_dim=64, vocab=1500), False, 42)):
+        rng = np.random.default_rng(seed)
+        host = make_weights(rng, shape, biases)
+        dev = upload_weights(host)
+        start = P * 3 + 31
+        rows = context_rows(rng, shape, start)
+        token = int(rng.integers(0, shape["vocab"]))
+        L, kv, hd = shape["layers"], shape["kv_heads"], shape["head_dim"]
+
+        def sealed(tmap):
+            alloc, cache = make_cache(shape, tmap)
+            prefill(cache, shape, rows)
+            step = m.device.DecodeStep(cache, shape, dev["embed"], dev["final_norm"],
+                                       dev["head"], dev["layers"])
+            step.run(token, start, 1)
+            # The cache and step ride along: the cache's pages leave the
+            # allocator with it.
+            return (alloc, cache, step), [alloc.read(layer, start // P) for layer in range(L)]
+
+        announce("seal step", hd, "fp16")
+        kept, fp16 = sealed([[0] * 8 for _ in range(L)])
+        _, new_rows = oracle_step(host, shape, token, start, rows, kept[0])
+        for layer in range(L):
+            k, v = quant.read_fp16_page(fp16[layer], P, kv, hd)
+            ctx_k, ctx_v = rows[layer]
+            np.testing.assert_array_equal(k[:31], ctx_k[P * 3:].astype(np.float16))
+            np.testing.assert_array_equal(v[:31], ctx_v[P * 3:].astype(np.float16))
+            if layer == 0:
+                # The first layer's row depends on the token alone: the
+                # oracle's float64 row within an fp16 step or two of the
+                # row's largest entry (RoPE mixes two rounded inputs).
+                for got, want in ((k[31], new_rows[0][0][0]), (v[31], new_rows[0][1][0])):
+                    np.testing.assert_allclose(got.astype(np.float64), want, rtol=2 ** -10,
+                                               atol=2 ** -9 * np.abs(want).max())
+            for tier in (1, 2, 3):
+                announce("seal step", hd, "layer", layer, "tier", tier)
+                tmap = [[tier if l >= layer else 0] * 8 for l in range(L)]
+                _, got = sealed(tmap)
+                np.testing.assert_array_equal(got[layer], quant.quantise_page(k, v, tier, P),
+                                              err_msg=f"tier {tier} head_dim {hd} layer {layer}")
 
 
 def test_an_eager_run_is_the_graphed_run_to_the_bit():
