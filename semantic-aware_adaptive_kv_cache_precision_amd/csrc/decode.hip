@@ -1980,6 +1980,35 @@ namespace mi
 
     bool aligned16(const void *p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 
+    // Waves of the head_dim-64 pages kernel (a wave a page of one KV head)
+    // that the current device holds at once, for a workgroup's LDS of `lds`
+    // bytes: whole workgroups a CU times the CUs.
+    long long resident_pages_waves_64(std::size_t lds)
+    {
+      static std::mutex lock;
+      static std::map<std::pair<int, std::size_t>, long long> known;
+      int device = 0;
+      hip_check(hipGetDevice(&device), "hipGetDevice");
+      std::lock_guard<std::mutex> guard(lock);
+      const auto key = std::make_pair(device, lds);
+      const auto found = known.find(key);
+      if (found != known.end())
+      {
+        return found->second;
+      }
+      int blocks = 0;
+      hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &blocks, reinterpret_cast<const void *>(decode_pages_kernel<64, false>),
+                    kThreads, lds),
+                "hipOccupancyMaxActiveBlocksPerMultiprocessor decode");
+      int cus = 0;
+      hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                "hipDeviceGetAttribute CUs");
+      const long long waves = static_cast<long long>(std::max(blocks, 1)) * kWaves * cus;
+      known.emplace(key, waves);
+      return waves;
+    }
+
   } // namespace
 
   float *stream_workspace(hipStream_t stream, std::size_t count)
@@ -2164,9 +2193,14 @@ namespace mi
     // head_dim 64 with an even number of KV heads and no key bias (the
     // Llama shapes): two KV heads a wave, as one 128-channel unit, so that a
     // launch has half the waves, each with a unit of the size the kernel's
-    // fixed costs are paid for.
-    const bool packed = !streaming && a.head_dim == 64 && d.k_bias == nullptr &&
-                        a.kv_heads % 2 == 0 && 2 * group <= kMaxGroup;
+    // fixed costs are paid for. Only where a wave a KV head would not all be
+    // resident at once: below that, halving the waves halves the launch's
+    // parallelism (Qwen2.5-0.5B at 8K: 6.8 us a layer unpacked, 9.9 packed).
+    const bool packed =
+        !streaming && a.head_dim == 64 && d.k_bias == nullptr && a.kv_heads % 2 == 0 &&
+        2 * group <= kMaxGroup &&
+        static_cast<long long>(pages) * a.kv_heads * ls.layers >
+            resident_pages_waves_64(pages_kernel_lds(group, 64, false));
     if (packed)
     {
       d.pack = 2;

@@ -528,6 +528,30 @@ def test_chained_store_and_decode_steps_across_a_seal_at_llama_shape():
     np.testing.assert_array_equal(scores.download(), ewma.host_ewma(folded, LAYERS, max_pages))
 
 
+def test_llama_shape_at_16k_two_kv_heads_a_wave_is_the_oracle():
+    """At the Llama-3.2-1B shape and 16K positions (more waves of one KV head
+    each than the device holds at once) the decode takes two KV heads a wave
+    as one 128-channel unit: output and masses against the float64 causal
+    view of a 30/40/30 FP16/INT8/INT4 cache, and the scores the oracle's
+    fold of the kernel's masses, to the bit."""
+    from microinfer import workloads as w
+    P, shape = 32, w.LLAMA_1B
+    heads, kv, hd = shape.heads, shape.kv_heads, shape.head_dim
+    seq = 16384 + 10
+    pages = seq // P + 1
+    tmap = w.tier_map(1, LAYERS, pages, w.MIX_CONFIG5)
+    announce("llama 16K decode", seq)
+    m, alloc, cache, k, v, q, _ = decode_case(P, kv, hd, heads, tmap, seq, seed=23)
+    scores = m.device.ImportanceScores(LAYERS, pages)
+    got, mass = run_decode(m, cache, k, v, q, heads, kv, hd, scores=scores)
+    want, want_mass, bound = oracle_decode(alloc, P, kv, hd, k, v, q)
+    assert_attention_close(got, want, "llama 16K", bound)
+    assert_mass_close(mass, want_mass, "llama 16K mass")
+    np.testing.assert_allclose(mass.sum(1), 1.0, atol=1e-5)
+    np.testing.assert_array_equal(scores.download(),
+                                  ewma.host_ewma([(0, mass.astype(np.float32))], LAYERS, pages))
+
+
 def test_decode_after_pages_move_reads_them_where_they_now_are():
     """tests/test_kv_pages.py:112-150 and tests/test_quantised_pages.py:
     202-224: the cache's page tables are resolved by a first decode; then
