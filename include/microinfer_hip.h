@@ -309,6 +309,14 @@ int mi_rope_table_create(int head_dim, double theta, mi_rope_table **out);
 void mi_rope_table_destroy(mi_rope_table *t);
 int mi_rope_table_cover(mi_rope_table *t, int positions);
 int mi_rope_table_info(mi_rope_table *t, int *positions, const float **data);
+/* Beyond the reference (whose rope kernel forms every angle, rope.cu:57-68):
+ * mi_rope's rotation of x (seq, heads, head_dim) fp16 at positions[token],
+ * the angles read from a table that mi_rope_table_cover filled for
+ * `table_positions` positions (every position must be below it); the rows are
+ * mi_rope's to the bit. x == out is refused. */
+int mi_rope_from_table(const void *x, const int32_t *positions, const float *table,
+                       int table_positions, void *out, int seq, int heads, int head_dim,
+                       void *stream);
 
 /* ---- KVPages: the cache manager ---------------------------------------------------
  * reference: kv_pages.h:105-412, bindings_device.cpp:688-978. tier_map: a

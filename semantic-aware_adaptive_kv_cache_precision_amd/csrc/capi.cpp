@@ -734,6 +734,28 @@ int mi_rope(const void *x, const int32_t *positions, void *out, int seq, int hea
   });
 }
 
+int mi_rope_from_table(const void *x, const int32_t *positions, const float *table,
+                       int table_positions, void *out, int seq, int heads, int head_dim,
+                       void *stream)
+{
+  return guarded([&] {
+    if (x == out && seq > 0)
+    {
+      throw mi::InvalidArgument("RoPE from a table writes a separate output; x == out");
+    }
+    mi::RopeRows r{};
+    r.x[0] = x;
+    r.out[0] = out;
+    r.heads[0] = heads;
+    r.positions = positions;
+    r.table = table;
+    r.table_positions = table_positions;
+    r.seq = seq;
+    r.head_dim = head_dim;
+    mi::launch_rope_rows(r, as_stream(stream));
+  });
+}
+
 int mi_rope_table_fill(float *table, int positions, int head_dim, double theta, void *stream)
 {
   return guarded(

@@ -443,9 +443,21 @@ namespace mi
           linear_half(normed, w.k_w, key_bias_ ? nullptr : w.k_b, k_raw, rows, s.hidden,
                       kv_width, stream);
           linear_half(normed, w.v_w, w.v_b, v, rows, s.hidden, kv_width, stream);
-          launch_rope(q_raw, positions + c0, q, rows, s.heads, s.head_dim, s.rope_theta, stream);
-          launch_rope(k_raw, positions + c0, k, rows, s.kv_heads, s.head_dim, s.rope_theta,
-                      stream);
+          // RoPE of q and k in one launch, the angles from the step's table
+          // (the RoPE kernel's rows to the bit).
+          RopeRows rope{};
+          rope.x[0] = q_raw;
+          rope.out[0] = q;
+          rope.heads[0] = s.heads;
+          rope.x[1] = k_raw;
+          rope.out[1] = k;
+          rope.heads[1] = s.kv_heads;
+          rope.positions = positions + c0;
+          rope.table = rope_.data();
+          rope.table_positions = rope_.positions();
+          rope.seq = rows;
+          rope.head_dim = s.head_dim;
+          launch_rope_rows(rope, stream);
           cache_.store(l, k, v, p0, rows);
           cache_.attention(l, q, key_bias_ ? w.k_b : nullptr, &rope_, attended, rows, p0 + rows,
                            s.heads, s.kv_heads, s.head_dim, k, v, nullptr, nullptr, 0.0f,

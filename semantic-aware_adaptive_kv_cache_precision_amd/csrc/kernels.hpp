@@ -138,6 +138,22 @@ namespace mi
                           hipStream_t stream);
   void launch_rope_table(float *table, int positions, int head_dim, double theta,
                          hipStream_t stream);
+  // RoPE of up to two sets of rows ((seq, heads[i], head_dim) fp16 each;
+  // heads[1] 0 for one set) at positions[token], the angles from a table
+  // launch_rope_table filled for table_positions positions: launch_rope's
+  // rows to the bit, without forming an angle a pair.
+  struct RopeRows
+  {
+    const void *x[2];
+    void *out[2];
+    int heads[2];
+    const std::int32_t *positions;
+    const float *table;
+    int table_positions;
+    int seq;
+    int head_dim;
+  };
+  void launch_rope_rows(const RopeRows &r, hipStream_t stream);
   void launch_rmsnorm(const void *x, bool x_is_f32, const void *weight, void *out, int rows,
                       int hidden, float eps, hipStream_t stream);
   void launch_swiglu(const void *gate, const void *up, void *out, std::size_t count,

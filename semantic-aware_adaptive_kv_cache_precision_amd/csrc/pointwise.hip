@@ -2,8 +2,10 @@
 //
 // Arithmetic follows the reference:
 //   - RoPE rotate-half with the angle pos * theta^(-2j/hd) formed and reduced
-//     in fp64 (rope.cu:32-54, rope_angle.cuh:15-21); gfx950 runs fp64 at full
-//     rate, so this costs nothing here;
+//     in fp64 (rope.cu:32-54, rope_angle.cuh:15-21), per pair, or read from a
+//     table of those angles' fp32 cos and sin (the same bits, without the
+//     fp64 pow and sincos a pair: a 2048-token Llama chunk's q and k in
+//     12.5 us against 50);
 //   - RMSNorm in fp32 from fp16 or fp32 input, one fp16 rounding at the store
 //     (rmsnorm.cu:33-84);
 //   - SwiGLU as g / (1 + expf(-g)) * up in fp32 (swiglu.cu:26-38).
@@ -46,6 +48,39 @@ namespace mi
         const float x2 = h2f(x[base + j + half]);
         out[base + j] = __half_as_ushort(__float2half(x1 * cf - x2 * sf));
         out[base + j + half] = __half_as_ushort(__float2half(x2 * cf + x1 * sf));
+      }
+    }
+
+    // RoPE of up to two row sets (a chunk's q and k) with the angles read
+    // from a RopeTable ({cos, sin} in fp32 per (position, j), filled by
+    // rope_table_kernel from the same double-precision angle rope_kernel
+    // forms): a thread a rotation pair, the rotation the RoPE kernel's fp32
+    // arithmetic, so the rows are rope_kernel's to the bit. A position past
+    // the table reads its last row (the launcher's caller covers every
+    // position first).
+    __global__ void rope_rows_kernel(RopeRows r)
+    {
+      const int half = r.head_dim / 2;
+      const std::size_t first = static_cast<std::size_t>(r.seq) * r.heads[0] * half;
+      const std::size_t total = first + static_cast<std::size_t>(r.seq) * r.heads[1] * half;
+      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+           i < total; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+      {
+        const int set = i < first ? 0 : 1;
+        const std::size_t k = set == 0 ? i : i - first;
+        const std::size_t row = k / half; // (token, head)
+        const int j = static_cast<int>(k % half);
+        const int token = static_cast<int>(row / r.heads[set]);
+        const int position = min(max(r.positions[token], 0), r.table_positions - 1);
+        const float2 cs = *reinterpret_cast<const float2 *>(
+            r.table + 2 * (static_cast<std::size_t>(position) * half + j));
+        const std::size_t base = row * r.head_dim;
+        const auto *x = static_cast<const std::uint16_t *>(r.x[set]);
+        auto *out = static_cast<std::uint16_t *>(r.out[set]);
+        const float x1 = h2f(x[base + j]);
+        const float x2 = h2f(x[base + j + half]);
+        out[base + j] = __half_as_ushort(__float2half(x1 * cs.x - x2 * cs.y));
+        out[base + j + half] = __half_as_ushort(__float2half(x2 * cs.x + x1 * cs.y));
       }
     }
 
@@ -146,6 +181,36 @@ namespace mi
       }
     }
 
+    // The same, eight values a thread through 16-byte loads and stores.
+    __global__ void swiglu8_kernel(const uint4 *__restrict__ gate, const uint4 *__restrict__ up,
+                                   uint4 *__restrict__ out, std::size_t groups)
+    {
+      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+           i < groups; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+      {
+        const uint4 gw = gate[i];
+        const uint4 uw = up[i];
+        const unsigned gs[4] = {gw.x, gw.y, gw.z, gw.w};
+        const unsigned us[4] = {uw.x, uw.y, uw.z, uw.w};
+        unsigned os[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+          unsigned word = 0;
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+          {
+            const float g = h2f(static_cast<std::uint16_t>(gs[k] >> (16 * h)));
+            const float silu = g / (1.0f + expf(-g));
+            const float u = h2f(static_cast<std::uint16_t>(us[k] >> (16 * h)));
+            word |= static_cast<unsigned>(__half_as_ushort(__float2half(silu * u))) << (16 * h);
+          }
+          os[k] = word;
+        }
+        out[i] = uint4{os[0], os[1], os[2], os[3]};
+      }
+    }
+
     __global__ void add_kernel(const std::uint16_t *a, const std::uint16_t *b, std::uint16_t *out,
                                std::size_t count)
     {
@@ -175,6 +240,23 @@ namespace mi
                        static_cast<const std::uint16_t *>(x), positions,
                        static_cast<std::uint16_t *>(out), heads, head_dim, theta);
     hip_check(hipGetLastError(), "rope kernel launch");
+  }
+
+  void launch_rope_rows(const RopeRows &r, hipStream_t stream)
+  {
+    if (r.head_dim <= 0 || r.head_dim % 2 != 0 || r.table == nullptr || r.table_positions <= 0 ||
+        r.seq < 0 || r.heads[0] < 0 || r.heads[1] < 0)
+    {
+      throw InvalidArgument("RoPE from a table takes an even head_dim and a filled table");
+    }
+    const std::size_t pairs =
+        static_cast<std::size_t>(r.seq) * (r.heads[0] + r.heads[1]) * (r.head_dim / 2);
+    if (pairs == 0)
+    {
+      return;
+    }
+    hipLaunchKernelGGL(rope_rows_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0, stream, r);
+    hip_check(hipGetLastError(), "rope rows kernel launch");
   }
 
   void launch_rope_table(float *table, int positions, int head_dim, double theta,
@@ -232,10 +314,23 @@ namespace mi
     {
       return;
     }
-    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(count, 256)), dim3(256), 0, stream,
-                       static_cast<const std::uint16_t *>(gate),
-                       static_cast<const std::uint16_t *>(up), static_cast<std::uint16_t *>(out),
-                       count);
+    const auto aligned = [](const void *p) {
+      return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0;
+    };
+    if (count % 8 == 0 && aligned(gate) && aligned(up) && aligned(out))
+    {
+      const std::size_t groups = count / 8;
+      hipLaunchKernelGGL(swiglu8_kernel, dim3(grid_for(groups, 256)), dim3(256), 0, stream,
+                         static_cast<const uint4 *>(gate), static_cast<const uint4 *>(up),
+                         static_cast<uint4 *>(out), groups);
+    }
+    else
+    {
+      hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(count, 256)), dim3(256), 0, stream,
+                         static_cast<const std::uint16_t *>(gate),
+                         static_cast<const std::uint16_t *>(up), static_cast<std::uint16_t *>(out),
+                         count);
+    }
     hip_check(hipGetLastError(), "swiglu kernel launch");
   }
 

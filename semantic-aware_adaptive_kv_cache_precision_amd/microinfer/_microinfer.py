@@ -122,6 +122,7 @@ SIGNATURES = {
     "mi_fold_scores": ((_vp, _vp, _i, _i, _f, _vp), C.c_int),
     "mi_rope": ((_vp, _vp, _vp, _i, _i, _i, _d, _vp), C.c_int),
     "mi_rope_table_fill": ((_vp, _i, _i, _d, _vp), C.c_int),
+    "mi_rope_from_table": ((_vp, _vp, _vp, _i, _vp, _i, _i, _i, _vp), C.c_int),
     "mi_rmsnorm": ((_vp, _i, _vp, _vp, _i, _i, _f, _vp), C.c_int),
     "mi_swiglu": ((_vp, _vp, _vp, _sz, _vp), C.c_int),
     "mi_add": ((_vp, _vp, _vp, _sz, _vp), C.c_int),
@@ -1263,6 +1264,23 @@ def _device_rope(x, positions: DeviceIndex, out, seq, heads, head_dim, theta):
     _check(lib.mi_rope(xa, positions.address, oa, seq, heads, head_dim, theta, None))
 
 
+def _device_rope_from_table(x, positions: DeviceIndex, table: "RopeTable", out, seq, heads,
+                            head_dim):
+    """_device_rope's rows with the angles read from `table` (beyond the
+    reference): every position must be below table.positions."""
+    xa = _need(_span(x), seq * heads * head_dim, "x")
+    if positions.count < seq:
+        raise ValueError(f"positions holds {positions.count}, and the operation needs {seq}")
+    oa = _need(_span(out), seq * heads * head_dim, "out")
+    if xa == oa:
+        raise ValueError("rope cannot write over its input")
+    if table.head_dim != head_dim:
+        raise ValueError(f"the table is for head_dim {table.head_dim}, not {head_dim}")
+    covered, data = table._info()
+    _check(lib.mi_rope_from_table(xa, positions.address, data, covered, oa, seq, heads, head_dim,
+                                  None))
+
+
 def _device_swiglu(gate, up, out, count):
     ga = _need(_span(gate), count, "gate")
     ua = _need(_span(up), count, "up")
@@ -1439,6 +1457,7 @@ device = SimpleNamespace(
     rmsnorm=_device_rmsnorm,
     rmsnorm_f32=_device_rmsnorm_f32,
     rope=_device_rope,
+    rope_from_table=_device_rope_from_table,
     attention=_device_attention,
     attention_partials=_attention_partials,
     attention_split=lambda seq_q, seq_k, heads, kv_heads, page_tokens=0: _split(

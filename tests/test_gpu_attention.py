@@ -150,13 +150,15 @@ def test_rope_rmsnorm_swiglu_are_the_float64_references():
         want = pointwise.rmsnorm(x, w, 1e-6)
         ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
         assert np.all(np.abs(got - want) <= ulp)
-    announce("swiglu")
-    g = fp16_exact(4 * rng.standard_normal((2, 8192)))
-    u = fp16_exact(rng.standard_normal((2, 8192)))
-    got = m.swiglu(g, u)
-    want = pointwise.swiglu(g, u)
-    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
-    assert np.all(np.abs(got - want) <= ulp)
+    # SwiGLU eight values a thread (a multiple of 8) and one a thread.
+    for shape in ((2, 8192), (3, 1001)):
+        announce("swiglu", shape)
+        g = fp16_exact(4 * rng.standard_normal(shape))
+        u = fp16_exact(rng.standard_normal(shape))
+        got = m.swiglu(g, u)
+        want = pointwise.swiglu(g, u)
+        ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+        assert np.all(np.abs(got - want) <= ulp)
 
 
 def test_rope_table_is_fp64_cos_sin_rounded():
@@ -171,6 +173,31 @@ def test_rope_table_is_fp64_cos_sin_rounded():
     for got, want in ((table[..., 0], np.cos(ang)), (table[..., 1], np.sin(ang))):
         ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
         assert np.all(np.abs(got - want) <= ulp)
+
+
+def test_rope_from_a_table_is_the_rope_kernel_to_the_bit():
+    """RoPE with its angles read from a RopeTable (what the prefill runs)
+    gives the RoPE kernel's rows bit for bit, head dims 64 and 128, positions
+    across the table; both are within the float64 reference's bound."""
+    m = mi()
+    d = m.device
+    rng = np.random.default_rng(4)
+    for heads, hd in ((32, 64), (12, 128)):
+        announce("rope from table", heads, hd)
+        pos = np.array([0, 1, 31, 32, 2047, 4096, 16383, 32767, 5, 32766], np.int32)
+        x = fp16_exact(rng.standard_normal((len(pos), heads, hd)))
+        table = d.RopeTable(hd, 1e6)
+        table.cover(32768)
+        at = d.DeviceIndex(pos)
+        xs = m.upload_fp16(x.reshape(-1))
+        a, b = d.empty(x.size), d.empty(x.size)
+        d.rope(xs, at, a, len(pos), heads, hd, 1e6)
+        d.rope_from_table(xs, at, table, b, len(pos), heads, hd)
+        np.testing.assert_array_equal(b.to_numpy(), a.to_numpy())
+        want = pointwise.rope(x, pos, 1e6)
+        ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+        got = b.to_numpy().reshape(x.shape)
+        assert np.all(np.abs(got - want) <= 2 * ulp + 1e-6 * np.abs(x).max())
 
 
 def test_the_general_path_takes_what_the_fast_kernels_do_not():
