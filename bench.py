@@ -575,18 +575,30 @@ def quantise_batches(m, stream, steps, warmup, seed=4):
         tab = m._Storage(table.nbytes)
         m._h2d(tab.ptr, table)
 
-        def body():
-            m._check(m.lib.mi_quantise_pages(tab.ptr, tab.ptr + 8 * n, n, tier, P, kv, hd, None))
+        def launches(count):
+            def body():
+                for _ in range(count):
+                    m._check(m.lib.mi_quantise_pages(tab.ptr, tab.ptr + 8 * n, n, tier, P, kv,
+                                                     hd, None))
+            return body
 
         # Launches of tens of microseconds: enough replays that the clocks
-        # have risen and the timed region is not a handful of launches.
-        ms = timed_graph(m, stream, body, max(steps, 400), max(warmup, 400))
+        # have risen and the timed region is not a handful of launches. A
+        # launch is timed as one of ten back to back in a graph (a batch
+        # among others, as a plan's tiers go), and alone in its graph (the
+        # graph launch's own overhead included).
+        back_to_back = 10
+        ms = timed_graph(m, stream, launches(back_to_back), max(steps, 100),
+                         max(warmup, 100)) / back_to_back
+        alone = timed_graph(m, stream, launches(1), max(steps, 400), max(warmup, 400))
         moved = n * (fp16 + pb)
         gbs = moved / (ms * 1e-3) / 1e9
         name = {1: "INT8", 2: "INT4", 3: "INT2"}[tier]
         out[f"{name}_{n}"] = {"us": round(ms * 1e3, 2), "gb_per_s": round(gbs, 1),
-                              "frac_hbm": round(gbs / PEAK_GBS, 4), "bytes": moved}
-        log(f"quantise {n} pages to {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+                              "frac_hbm": round(gbs / PEAK_GBS, 4), "bytes": moved,
+                              "us_alone_in_a_graph": round(alone * 1e3, 2)}
+        log(f"quantise {n} pages to {name}: {ms * 1e3:.2f} us ({alone * 1e3:.2f} alone), "
+            f"{gbs:.0f} GB/s")
     return out
 
 
