@@ -549,7 +549,7 @@ def prefill_chunks(m, stream, steps, warmup, seed=5):
 
 # ---- the batch quantiser ---------------------------------------------------------------------
 
-def quantise_batches(m, stream, steps, warmup, seed=4):
+def quantise_batches(m, stream, steps, warmup, seed=4, single_launch_graphs=False):
     """The batch quantiser (mi_quantise_pages; reference quant.cu:419-436)
     at the 1.5B page shape (2 KV heads x head_dim 128, 32 tokens): N FP16
     pages quantised to a tier in one launch, timed as a HIP graph. Bytes a
@@ -587,10 +587,13 @@ def quantise_batches(m, stream, steps, warmup, seed=4):
         # launch is timed as one of ten back to back in a graph (a batch
         # among others, as a plan's tiers go), and alone in its graph (the
         # graph launch's own overhead included).
-        back_to_back = 10
-        ms = timed_graph(m, stream, launches(back_to_back), max(steps, 100),
-                         max(warmup, 100)) / back_to_back
         alone = timed_graph(m, stream, launches(1), max(steps, 400), max(warmup, 400))
+        if single_launch_graphs:
+            ms = alone
+        else:
+            back_to_back = 10
+            ms = timed_graph(m, stream, launches(back_to_back), max(steps, 100),
+                             max(warmup, 100)) / back_to_back
         moved = n * (fp16 + pb)
         gbs = moved / (ms * 1e-3) / 1e9
         name = {1: "INT8", 2: "INT4", 3: "INT2"}[tier]
@@ -851,6 +854,9 @@ def main() -> int:
     ap.add_argument("--eager-step", action="store_true",
                     help="whole steps with their launches made from the host (no graph), so "
                          "that a kernel tracer sees each launch")
+    ap.add_argument("--single-launch-graphs", action="store_true",
+                    help="quantise batches timed one launch a graph only (for a kernel "
+                         "tracer, which fails on the ten-launch graphs)")
     ap.add_argument("--traffic-reference", action="store_true",
                     help="only copy 128 MiB with the page-copy kernel (4096 pages of 32 KiB): "
                          "the known-size launch HBM byte counters are scaled by")
@@ -922,7 +928,9 @@ def main() -> int:
         steps_out["reference_rtx4050_tokens_per_s"] = {"qwen2.5-1.5b_fp16_32k": 29.5,
                                                        "qwen2.5-1.5b_fp16_16k": 40.1}
 
-    quantise = quantise_batches(m, stream, args.steps, args.warmup) if "quantise" in legs else None
+    quantise = (quantise_batches(m, stream, args.steps, args.warmup,
+                                 single_launch_graphs=args.single_launch_graphs)
+                if "quantise" in legs else None)
 
     requant = None
     if "requant" in legs:
