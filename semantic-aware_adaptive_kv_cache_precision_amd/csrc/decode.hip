@@ -1111,25 +1111,29 @@ namespace mi
       }
     }
 
-    // Range of wave w: units [w U / W, (w+1) U / W).
+    // Range of wave w: units [w U / W, (w+1) U / W) (in 32 bits where the
+    // product fits).
     __host__ __device__ inline long long range_start(long long w, long long units, int waves)
     {
-      return w * units / waves;
+      const unsigned long long top = static_cast<unsigned long long>(w) * units;
+      return top <= 0xFFFFFFFFull
+                 ? static_cast<long long>(static_cast<unsigned>(top) / static_cast<unsigned>(waves))
+                 : static_cast<long long>(top / static_cast<unsigned long long>(waves));
     }
 
-    // The wave whose range holds unit x.
+    // The wave whose range holds unit x: the largest w < waves with
+    // floor(w units / waves) <= x, i.e. w units < (x + 1) waves, so
+    // w = ((x + 1) waves - 1) / units (waves <= units). One division, in 32
+    // bits where the product fits (the scalar unit divides 64-bit values in
+    // software).
     __host__ __device__ inline int wave_of(long long x, long long units, int waves)
     {
-      long long w = x * waves / units;
-      while (w + 1 < waves && range_start(w + 1, units, waves) <= x)
-      {
-        ++w;
-      }
-      while (w > 0 && range_start(w, units, waves) > x)
-      {
-        --w;
-      }
-      return static_cast<int>(w);
+      const unsigned long long top = static_cast<unsigned long long>(x + 1) * waves - 1;
+      const unsigned long long w =
+          top <= 0xFFFFFFFFull && units <= 0xFFFFFFFFll
+              ? static_cast<unsigned>(top) / static_cast<unsigned>(units)
+              : top / static_cast<unsigned long long>(units);
+      return static_cast<int>(w < static_cast<unsigned long long>(waves) ? w : waves - 1);
     }
 
     // The first unit of (layer li, KV head kvh)'s group in the streaming
