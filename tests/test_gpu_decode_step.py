@@ -247,7 +247,8 @@ def check_step_against_oracle(s, biases, start, seed):
     dev = upload_weights(host)
     rows = context_rows(rng, s, start)
     alloc, cache = make_cache(s, tier_map_for(s, 16, seed))
-    prefill(cache, s, rows)
+    if start > 0:
+        prefill(cache, s, rows)
     step = m.device.DecodeStep(cache, s, dev["embed"], dev["final_norm"], dev["head"],
                                dev["layers"])
     token = int(rng.integers(0, s["vocab"]))
@@ -271,6 +272,18 @@ def test_one_step_is_the_oracles_composition_qwen_shape():
     check_step_against_oracle(small_shape(head_dim=64), True, P * 3 + 10, 11)
     check_step_against_oracle(small_shape(heads=12, kv_heads=2, head_dim=128), True,
                               P * 4 + 31, 12)
+
+
+def test_a_step_on_an_empty_cache_and_the_step_that_seals_its_first_page():
+    """Position 0 (the step's row is the whole context: no page sealed, no
+    page table yet) and position 31 (the first page's last row, which the
+    step seals), with and without biases, head dims 128 and 64."""
+    check_step_against_oracle(small_shape(heads=12, kv_heads=2, head_dim=128), True, 0, 14)
+    check_step_against_oracle(small_shape(heads=12, kv_heads=2, head_dim=128), True, 31, 15)
+    llama = small_shape(hidden=512, intermediate=1024, heads=16, kv_heads=4, head_dim=64,
+                        vocab=1500)
+    check_step_against_oracle(llama, False, 0, 16)
+    check_step_against_oracle(llama, False, 31, 17)
 
 
 def test_one_step_is_the_oracles_composition_llama_shape():
