@@ -138,7 +138,8 @@ namespace mi
 
     // RMSNorm rides in the projection that reads its output (each workgroup
     // forms the normed row from the fp32 residual, to the RMSNorm kernel's
-    // bits), and RoPE in the store: seven launches a layer.
+    // bits), RoPE and the open page's row in the q/k/v launch, the page's
+    // seal in the decode's combine: six launches a layer.
     const auto normed_input = [&](ProjectArgs &p, const std::uint16_t *norm) {
       p.residual = residual;
       p.norm_weight = norm;
