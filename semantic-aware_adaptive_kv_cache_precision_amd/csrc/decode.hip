@@ -951,7 +951,7 @@ namespace mi
         }
       }
       __syncthreads();
-      if (threadIdx.x < kWaves * G)
+      if (static_cast<int>(threadIdx.x) < kWaves * G)
       {
         const int h = threadIdx.x % G;
         float top = -INFINITY;
@@ -962,7 +962,7 @@ namespace mi
         }
         const float from = top == -INFINITY ? 0.0f : top;
         s_w[threadIdx.x] = exp2_fast(s_m[threadIdx.x] - from);
-        if (threadIdx.x < G)
+        if (static_cast<int>(threadIdx.x) < G)
         {
           s_w[kWaves * G + h] = top;
         }
@@ -1019,15 +1019,11 @@ namespace mi
     constexpr int kBufferWord3 = 0x00020000;
     typedef const __attribute__((address_space(1))) void *global_void;
 
-    // Direct global-to-LDS copies (global_load_lds): lane l's 16 (or 4)
-    // bytes land at block + 16 l (4 l); `block` must be wave-uniform.
+    // A direct global-to-LDS copy (global_load_lds): lane l's 16 bytes land
+    // at block + 16 l; `block` must be wave-uniform.
     __device__ inline void dma16(const void *src, void *block)
     {
       __builtin_amdgcn_global_load_lds((global_void)src, (lds_void)block, 16, 0, 0);
-    }
-    __device__ inline void dma4(const void *src, void *block)
-    {
-      __builtin_amdgcn_global_load_lds((global_void)src, (lds_void)block, 4, 0, 0);
     }
     // s_waitcnt vmcnt(0): every copy into LDS has landed.
     __device__ inline void wait_copies()

@@ -66,7 +66,7 @@ namespace mi
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
     constexpr int kP = 32;              // keys a page, and a key tile
-    constexpr float kPScale = 16384.0f; // probabilities are held x2^14 for PV
+    // Probabilities are held x2^14 for PV (14 added in the exponent).
     constexpr float kPUnscale = 1.0f / 16384.0f;
     constexpr int kMaxWaves = 8;
     constexpr int kMinThreads = 256; // a workgroup stages with at least this many threads

@@ -42,7 +42,6 @@ namespace mi
 {
   namespace
   {
-    constexpr int kWaves = 8;
     constexpr int kAdvanceThreads = 1024;
 
     typedef _Float16 half2v __attribute__((ext_vector_type(2)));
