@@ -327,7 +327,8 @@ def config2(m, steps, warmup, seed=0):
             "pct_hbm_peak": round(100 * gbs / PEAK_GBS, 2), "bytes_per_token": step_bytes,
             "config": "qwen2.5-0.5b 14q/2kv/hd64, 24 layers, 8K FP16 pages (cache that does not "
                       "seal); a layer: RMSNorm (hidden 896), RoPE of q and k, the decode row "
-                      "stored, split decode; HIP graph of the 96 launches"}
+                      "stored, split decode (pages kernel + combine); HIP graph of the 120 "
+                      "launches"}
 
 
 # ---- whole decode steps (every projection, one graph a token) -------------------------------
