@@ -41,7 +41,8 @@ def test_half_rounding_from_double_is_numpy_s():
     mids = (h + np.nextafter(h.astype(np.float16), np.float16(np.inf)).astype(np.float64)) / 2
     x = np.concatenate([x, mids, -mids])
     got = np.array([_microinfer.lib.mi_half_bits_from_double(float(v)) for v in x], np.uint16)
-    want = x.astype(np.float16).view(np.uint16)
+    with np.errstate(over="ignore"):  # values past fp16's range round to inf
+        want = x.astype(np.float16).view(np.uint16)
     np.testing.assert_array_equal(got, want)
 
 
