@@ -162,7 +162,9 @@ def copy_peak(m, page=32768, count=32768, reps=10) -> float:
 
 def decode_source_hash() -> str:
     h = hashlib.sha256()
-    for name in ("decode.hip", "dequant.hpp", "common.hpp", "lane_ops.hpp"):
+    # decode.hip and every header it includes.
+    for name in ("decode.hip", "dequant.hpp", "common.hpp", "lane_ops.hpp", "kernels.hpp",
+                 "page_tasks.hpp", "quant_core.hpp"):
         h.update((PKG / "csrc" / name).read_bytes())
     return h.hexdigest()[:16]
 

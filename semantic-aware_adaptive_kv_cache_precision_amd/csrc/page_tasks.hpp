@@ -42,11 +42,29 @@ namespace mi
       }
     };
 
+    // Rows and pages are device (or host-mapped) memory, never LDS: reached
+    // through global-address-space pointers, so that the compiler issues
+    // global rather than flat instructions (a flat access also counts
+    // against the LDS and scalar-load wait counter).
+    // (Native vectors: HIP's uint4 and uint2 are classes, whose copy
+    // constructor would take the value back through a generic reference.)
+    typedef unsigned words4 __attribute__((ext_vector_type(4)));
+    typedef unsigned words2 __attribute__((ext_vector_type(2)));
+    typedef const __attribute__((address_space(1))) words4 *global_cw4;
+    typedef __attribute__((address_space(1))) words4 *global_w4;
+    typedef __attribute__((address_space(1))) words2 *global_w2;
+    typedef __attribute__((address_space(1))) unsigned *global_u32;
+    typedef __attribute__((address_space(1))) std::uint16_t *global_u16;
+
     __device__ inline uint4 load16(const std::uint16_t *p)
     {
-      return *reinterpret_cast<const uint4 *>(p);
+      const words4 w = *((global_cw4)(p));
+      return uint4{w.x, w.y, w.z, w.w};
     }
-    __device__ inline void store16(std::uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
+    __device__ inline void store16(void *p, uint4 v)
+    {
+      *((global_w4)(p)) = words4{v.x, v.y, v.z, v.w};
+    }
 
     // fp16 bits to fp32 by the hardware conversion (exact, denormals kept).
     __device__ inline float f16_bits(unsigned bits)
@@ -127,16 +145,16 @@ namespace mi
     {
       if constexpr (Bits == 8)
       {
-        *reinterpret_cast<uint2 *>(at) =
-            uint2{static_cast<unsigned>(packed), static_cast<unsigned>(packed >> 32)};
+        *((global_w2)(at)) =
+            words2{static_cast<unsigned>(packed), static_cast<unsigned>(packed >> 32)};
       }
       else if constexpr (Bits == 4)
       {
-        *reinterpret_cast<unsigned *>(at) = static_cast<unsigned>(packed);
+        *((global_u32)(at)) = static_cast<unsigned>(packed);
       }
       else
       {
-        *reinterpret_cast<std::uint16_t *>(at) = static_cast<std::uint16_t>(packed);
+        *((global_u16)(at)) = static_cast<std::uint16_t>(packed);
       }
     }
 
@@ -328,9 +346,8 @@ namespace mi
         if (part == 0)
         {
           const int group = r * kv_heads + h;
-          reinterpret_cast<std::uint16_t *>(dst + L.value_scales)[group] = sbits;
-          reinterpret_cast<std::uint16_t *>(dst + L.value_zeros)[group] =
-              static_cast<std::uint16_t>(half_of(lo));
+          ((global_u16)(dst + L.value_scales))[group] = sbits;
+          ((global_u16)(dst + L.value_zeros))[group] = static_cast<std::uint16_t>(half_of(lo));
         }
         // The run's 64 codes (8 Bits bytes), 16-byte aligned: whole
         // 16-byte stores.
@@ -362,8 +379,7 @@ namespace mi
 #pragma unroll
         for (int w = 0; w < 2 * Bits; w += 4)
         {
-          *reinterpret_cast<uint4 *>(at + 4 * w) =
-              uint4{words[w], words[w + 1], words[w + 2], words[w + 3]};
+          store16(at + 4 * w, uint4{words[w], words[w + 1], words[w + 2], words[w + 3]});
         }
         return;
       }

@@ -106,6 +106,17 @@ namespace mi
 
     __device__ inline half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
+    // A load from device memory through a global-address-space pointer.
+    // Pages are reached through addresses held as integers, which the
+    // compiler would otherwise read with flat instructions; a flat load
+    // counts against the LDS wait counter as well, so every LDS read of the
+    // products would wait for the next step's page fetch.
+    template <typename T>
+    __device__ inline T load_global(const void *p)
+    {
+      return *((const __attribute__((address_space(1))) T *)(p));
+    }
+
     // The key lane l's accumulator element (tile kt, index i) holds.
     __device__ inline int key_of(int kt, int g, int i) { return 16 * kt + 4 * g + i; }
 
@@ -170,12 +181,12 @@ namespace mi
       }
       if (kv.layout == Layout::kCausal && version == kSealed)
       {
-        e.page = kv.pages[p];
-        e.tier = kv.tiers[p];
+        e.page = load_global<unsigned long long>(kv.pages + p);
+        e.tier = load_global<std::uint8_t>(kv.tiers + p);
       }
       else if (kv.layout == Layout::kPaged)
       {
-        e.page = kv.pages[p];
+        e.page = load_global<unsigned long long>(kv.pages + p);
       }
       return e;
     }
@@ -213,29 +224,28 @@ namespace mi
           f.v = u32x4{0, 0, 0, 0};
           if (bits == 8)
           {
-            const auto *k2 = reinterpret_cast<const unsigned *>(kc);
-            const auto *v2 = reinterpret_cast<const unsigned *>(vc);
-            f.k.x = k2[0];
-            f.k.y = k2[1];
-            f.v.x = v2[0];
-            f.v.y = v2[1];
+            f.k.x = load_global<unsigned>(kc);
+            f.k.y = load_global<unsigned>(kc + 4);
+            f.v.x = load_global<unsigned>(vc);
+            f.v.y = load_global<unsigned>(vc + 4);
           }
           else if (bits == 4)
           {
-            f.k.x = *reinterpret_cast<const unsigned *>(kc);
-            f.v.x = *reinterpret_cast<const unsigned *>(vc);
+            f.k.x = load_global<unsigned>(kc);
+            f.v.x = load_global<unsigned>(vc);
           }
           else
           {
-            f.k.x = *reinterpret_cast<const unsigned short *>(kc);
-            f.v.x = *reinterpret_cast<const unsigned short *>(vc);
+            f.k.x = load_global<unsigned short>(kc);
+            f.v.x = load_global<unsigned short>(vc);
           }
-          f.ks = *reinterpret_cast<const u32x4 *>(page + L.key_scales + 2 * at);
-          f.kz = *reinterpret_cast<const u32x4 *>(page + L.key_zeros + 2 * at);
+          f.ks = load_global<u32x4>(page + L.key_scales + 2 * at);
+          f.kz = load_global<u32x4>(page + L.key_zeros + 2 * at);
           const std::size_t group = static_cast<std::size_t>(t) * a.kv_heads + kvh;
           const auto *vs = reinterpret_cast<const std::uint16_t *>(page + L.value_scales);
           const auto *vz = reinterpret_cast<const std::uint16_t *>(page + L.value_zeros);
-          f.vsz = static_cast<unsigned>(vs[group]) | (static_cast<unsigned>(vz[group]) << 16);
+          f.vsz = static_cast<unsigned>(load_global<std::uint16_t>(vs + group)) |
+                  (static_cast<unsigned>(load_global<std::uint16_t>(vz + group)) << 16);
           f.tier = tier;
           return;
         }
@@ -271,8 +281,8 @@ namespace mi
       }
       if (k_row != nullptr)
       {
-        f.k = *reinterpret_cast<const u32x4 *>(k_row + at);
-        f.v = *reinterpret_cast<const u32x4 *>(v_row + at);
+        f.k = load_global<u32x4>(k_row + at);
+        f.v = load_global<u32x4>(v_row + at);
         f.tier = kFP16;
       }
       else
@@ -334,11 +344,10 @@ namespace mi
     {
       constexpr int half = HD / 2;
       const int j0 = d0 < half ? d0 : d0 - half;
-      const auto *src =
-          reinterpret_cast<const f32x4 *>(rope + 2 * (static_cast<std::size_t>(j) * half + j0));
+      const float *src = rope + 2 * (static_cast<std::size_t>(j) * half + j0);
       for (int i = 0; i < 4; ++i)
       {
-        cs[i] = src[i];
+        cs[i] = load_global<f32x4>(src + 4 * i);
       }
     }
 
