@@ -395,10 +395,10 @@ namespace mi
 #pragma unroll
       for (int e = 0; e < 8; ++e)
       {
-        const float pe = pv[e] * p_scale;
-        const _Float16 hi = static_cast<_Float16>(pe);
+        _Float16 hi, lo;
+        split_half(pv[e] * p_scale, hi, lo);
         p_hi[e] = hi;
-        p_lo[e] = static_cast<_Float16>(pe - static_cast<float>(hi));
+        p_lo[e] = lo;
       }
     }
 
@@ -500,9 +500,10 @@ namespace mi
         for (int e = 0; e < 8; ++e)
         {
           const float ab = static_cast<float>(q1[e]) * y1[e] + static_cast<float>(q2[e]) * y2[e];
-          const _Float16 hi = static_cast<_Float16>(ab);
+          _Float16 hi, lo;
+          split_half(ab, hi, lo);
           ab_hi[e] = hi;
-          ab_lo[e] = static_cast<_Float16>(ab - static_cast<float>(hi));
+          ab_lo[e] = lo;
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)

@@ -11,6 +11,21 @@
 
 namespace mi
 {
+  // x as the sum of two fp16 values: hi = fp16(x), lo = fp16(x - hi). The
+  // difference is exact in fp32 (hi is x rounded to fp16), formed here by
+  // one fma whose -1 comes through an empty asm the compiler cannot see
+  // into, so that it stays an fma of an fp16 operand and is issued as
+  // v_fma_mix_f32 (the conversion inside the instruction) instead of a
+  // conversion back to fp32 and a subtraction. The bits are those of
+  // fp16(x - float(hi)).
+  __device__ inline void split_half(float x, _Float16 &hi, _Float16 &lo)
+  {
+    float neg_one = -1.0f;
+    asm("" : "+s"(neg_one));
+    hi = static_cast<_Float16>(x);
+    lo = static_cast<_Float16>(__builtin_fmaf(static_cast<float>(hi), neg_one, x));
+  }
+
   // The pair's (lower, upper) values of v over lanes l and l ^ 16.
   __device__ inline void lane_pair16(float v, float &lo, float &hi)
   {

@@ -781,9 +781,10 @@ namespace mi
               {
                 const float ps = exp2_fast(fmaf(sc[8 * j + e], a.scale2, bias2));
                 sum += ps;
-                const _Float16 h = static_cast<_Float16>(ps);
+                _Float16 h, h_lo;
+                split_half(ps, h, h_lo);
                 p_hi[tt][j][e] = h;
-                p_lo[tt][j][e] = static_cast<_Float16>(ps - static_cast<float>(h));
+                p_lo[tt][j][e] = h_lo;
               }
             }
             l[tt] = l[tt] * keep + sum;
