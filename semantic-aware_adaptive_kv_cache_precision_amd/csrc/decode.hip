@@ -800,20 +800,6 @@ namespace mi
         }
       }
 
-      // The key bias: lane i holds b_i and b_i' of this KV head; the
-      // workgroup's angle rows follow the epilogue's LDS.
-      float bias_b = 0.0f, bias_b2 = 0.0f;
-      auto *angle_rows = reinterpret_cast<std::uint16_t *>(s_o + kWaves * G * kRow);
-      if constexpr (kBias)
-      {
-        copy_angle_rows<HD>(angle_rows, a.rope_angles);
-        __syncthreads();
-        const int i = lane % (HD / 2);
-        const std::uint16_t *bh = a.k_bias + static_cast<std::size_t>(kvh) * HD;
-        bias_b = static_cast<float>(__builtin_bit_cast(_Float16, bh[i]));
-        bias_b2 = static_cast<float>(__builtin_bit_cast(_Float16, bh[HD / 2 + i]));
-      }
-
       // Where the tiers and addresses are read from: q (always readable)
       // stands in for a table that has no entries (a causal cache with no
       // page sealed yet has no tables at all: both pointers are null).
@@ -821,6 +807,37 @@ namespace mi
           a.causal && own > 0 ? tiers : reinterpret_cast<const std::uint8_t *>(a.q);
       const auto *page_base =
           !a.causal || own > 0 ? table : reinterpret_cast<const unsigned long long *>(a.q);
+      // A page's tier and address, requested together with no branch
+      // between them, so that both are one trip to memory. The tier (a
+      // byte: a vector load) is made uniform where it is used, so that
+      // nothing waits for it before then.
+      const auto entry = [&](int p, int &tier_lane, unsigned long long &page_raw) {
+        const bool sealed = !a.causal || p < own;
+        tier_lane = tier_base[a.causal && p < own ? p : 0];
+        page_raw = page_base[sealed ? p : 0];
+      };
+      // The wave's first page's entry is asked for before the key bias's
+      // prologue, whose angle-row copy then shares its trip to memory.
+      int first_tier_lane = 0;
+      unsigned long long first_page_raw = 0;
+      if (p0 < a.live_pages)
+      {
+        entry(p0, first_tier_lane, first_page_raw);
+      }
+
+      // The key bias: lane i holds b_i and b_i' of this KV head; the
+      // workgroup's angle rows follow the epilogue's LDS.
+      float bias_b = 0.0f, bias_b2 = 0.0f;
+      auto *angle_rows = reinterpret_cast<std::uint16_t *>(s_o + kWaves * G * kRow);
+      if constexpr (kBias)
+      {
+        const int i = lane % (HD / 2);
+        const std::uint16_t *bh = a.k_bias + static_cast<std::size_t>(kvh) * HD;
+        bias_b = static_cast<float>(__builtin_bit_cast(_Float16, bh[i]));
+        bias_b2 = static_cast<float>(__builtin_bit_cast(_Float16, bh[HD / 2 + i]));
+        copy_angle_rows<HD>(angle_rows, a.rope_angles);
+        __syncthreads();
+      }
       // The open page's rows, asked for with q, not after the tier.
       const auto *open = a.open_table != nullptr
                              ? reinterpret_cast<const std::uint16_t *>(a.open_table[layer])
@@ -833,11 +850,14 @@ namespace mi
         {
           break;
         }
-        // The page's tier and address are requested together, with no
-        // branch between them, so that both are one trip to memory.
         const bool sealed = !a.causal || p < own;
-        const int tier_raw = __builtin_amdgcn_readfirstlane(tier_base[a.causal && p < own ? p : 0]);
-        const unsigned long long page_raw = page_base[sealed ? p : 0];
+        int tier_lane = first_tier_lane;
+        unsigned long long page_raw = first_page_raw;
+        if (i > 0)
+        {
+          entry(p, tier_lane, page_raw);
+        }
+        const int tier_raw = __builtin_amdgcn_readfirstlane(tier_lane);
         const int tier = !a.causal ? static_cast<int>(kFP16) : (p < own ? tier_raw : kOwnPage);
         const auto *page = reinterpret_cast<const std::uint8_t *>(sealed ? page_raw : 0ull);
         PageCtx c;
