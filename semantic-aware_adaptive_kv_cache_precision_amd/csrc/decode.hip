@@ -789,15 +789,18 @@ namespace mi
       // q of head r, the lane's run of channels. Columns past the group
       // repeat the group's first head: their scores and outputs stay in
       // their own columns and are never stored.
+      // The zeros are written first and the lanes that keep them do not
+      // load: zeroing after the load would wait for it here, before the
+      // page table is asked for.
       half8 qb[S];
-      load_fp16_run<HD>(qb, q_row);
-      if (q_off)
-      {
 #pragma unroll
-        for (int si = 0; si < S; ++si)
-        {
-          qb[si] = as_half8(u32x4{0u, 0u, 0u, 0u});
-        }
+      for (int si = 0; si < S; ++si)
+      {
+        qb[si] = as_half8(u32x4{0u, 0u, 0u, 0u});
+      }
+      if (!q_off)
+      {
+        load_fp16_run<HD>(qb, q_row);
       }
 
       // Where the tiers and addresses are read from: q (always readable)
@@ -1505,14 +1508,16 @@ namespace mi
           const std::uint16_t *q_row =
               a.q + u.li * a.q_stride + static_cast<std::size_t>(u.kvh * G + (r < G ? r : 0)) * HD +
               g * kRun;
-          load_fp16_run<HD>(qb, q_row);
-          if (r >= G)
-          {
+          // Zeros first, and only the group's lanes load (zeroing after
+          // the load would wait for it before the unit's page is asked for).
 #pragma unroll
-            for (int s = 0; s < S; ++s)
-            {
-              qb[s] = as_half8(u32x4{0u, 0u, 0u, 0u});
-            }
+          for (int s = 0; s < S; ++s)
+          {
+            qb[s] = as_half8(u32x4{0u, 0u, 0u, 0u});
+          }
+          if (r < G)
+          {
+            load_fp16_run<HD>(qb, q_row);
           }
         }
         const int tier = tier_of(i);
