@@ -453,6 +453,14 @@ int mi_decode_step_prefill(mi_decode_step *step, const int32_t *tokens, int n, i
 /* The last step's logits, fp32, to host memory (count <= vocab). */
 int mi_decode_step_logits(mi_decode_step *step, float *out, size_t count);
 int mi_decode_step_launches(mi_decode_step *step, int *out);
+/* No counterpart in the reference (its projections are cuBLAS calls,
+ * linear.cu:85-142): the plans the last step's GEMVs ran as, seven ints
+ * each -- which one (0 layer 0's output projection, 1 its gate/up, 2 its
+ * down projection, 3 the head), rows, input length, the waves a row is
+ * split over, 1 if the grid was the device's resident one with several rows
+ * a wave, waves a workgroup, workgroups. *count the ints there are; up to
+ * `capacity` of them to `out` (may be NULL). */
+int mi_decode_step_plans(mi_decode_step *step, int *out, size_t capacity, size_t *count);
 /* Synthetic fp16 weights made on the device: uniform in [-scale, scale)
  * from `seed`. */
 int mi_random_half(void *out, size_t count, unsigned long long seed, float scale);

@@ -7,6 +7,7 @@
 #include "kernels.hpp"
 #include "runtime.hpp"
 
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -1399,6 +1400,20 @@ int mi_decode_step_launches(mi_decode_step *step, int *out)
     need(step, "step");
     need(out, "out");
     *out = step->impl.launches();
+  });
+}
+
+int mi_decode_step_plans(mi_decode_step *step, int *out, size_t capacity, size_t *count)
+{
+  return guarded([&] {
+    need(step, "step");
+    need(count, "count");
+    const std::vector<int> &plans = step->impl.plans();
+    *count = plans.size();
+    if (out != nullptr)
+    {
+      std::copy(plans.begin(), plans.begin() + std::min(capacity, plans.size()), out);
+    }
   });
 }
 

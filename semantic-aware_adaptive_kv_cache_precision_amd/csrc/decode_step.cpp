@@ -135,6 +135,13 @@ namespace mi
     auto *activated = activated_->as<std::uint16_t>();
     float *kept = scores_ != nullptr ? kept_->as<float>() : nullptr;
     int launches = 0;
+    plans_.clear();
+    // The plan each of the step's GEMVs ran as (layer 0's and the head's),
+    // for tools and tests that check which variant a shape takes.
+    const auto record = [&](int what, const ProjectArgs &p, ProjectPlanInfo info) {
+      plans_.insert(plans_.end(), {what, p.seg[0].rows, p.in, info.split, info.pipelined,
+                                   info.waves, info.blocks});
+    };
 
     // RMSNorm rides in the projection that reads its output (each workgroup
     // forms the normed row from the fp32 residual, to the RMSNorm kernel's
@@ -185,7 +192,7 @@ namespace mi
       o.in = q_width;
       o.x = attended;
       o.mode = ProjectMode::kAccumulate;
-      launch_project(o, stream);
+      const ProjectPlanInfo o_plan = launch_project(o, stream);
       ProjectArgs mlp{};
       mlp.segments = 2;
       mlp.seg[0] = {w.gate_w, nullptr, activated, s.intermediate};
@@ -193,14 +200,20 @@ namespace mi
       mlp.in = s.hidden;
       mlp.mode = ProjectMode::kSwiglu;
       normed_input(mlp, w.post_norm);
-      launch_project(mlp, stream);
+      const ProjectPlanInfo mlp_plan = launch_project(mlp, stream);
       ProjectArgs down{};
       down.segments = 1;
       down.seg[0] = {w.down_w, nullptr, residual, s.hidden};
       down.in = s.intermediate;
       down.x = activated;
       down.mode = ProjectMode::kAccumulate;
-      launch_project(down, stream);
+      const ProjectPlanInfo down_plan = launch_project(down, stream);
+      if (l == 0)
+      {
+        record(kPlanOutput, o, o_plan);
+        record(kPlanGateUp, mlp, mlp_plan);
+        record(kPlanDown, down, down_plan);
+      }
       launches += 6; // norm + qkv + RoPE + store, decode + combine (+ seal), o, norm + gate/up,
                      // down
     }
@@ -213,7 +226,7 @@ namespace mi
     head.best_value = best_value_->as<float>();
     head.best_index = best_index_->as<int>();
     head.best_count = head_blocks_;
-    launch_project(head, stream);
+    record(kPlanHead, head, launch_project(head, stream));
     ++launches;
     if (scores_ != nullptr)
     {

@@ -102,6 +102,14 @@ namespace mi
     void logits(float *host, std::size_t count) const;
     // Launches a step makes (the graph's kernel nodes).
     int launches() const { return launches_; }
+    // The plans the last step's GEMVs ran as, seven ints each: which
+    // projection (kPlanOutput, kPlanGateUp, kPlanDown: layer 0's; kPlanHead),
+    // its rows, its input length, the waves a row is split over, whether the
+    // grid was the resident one (several rows a wave), the waves a
+    // workgroup, the workgroups.
+    static constexpr int kPlanOutput = 0, kPlanGateUp = 1, kPlanDown = 2, kPlanHead = 3;
+    static constexpr int kPlanInts = 7;
+    const std::vector<int> &plans() const { return plans_; }
 
   private:
     void size_buffers(int steps);
@@ -121,6 +129,7 @@ namespace mi
     hipEvent_t begin_ = nullptr;
     hipEvent_t end_ = nullptr;
     int launches_ = 0;
+    std::vector<int> plans_;
     int head_blocks_ = 0;
     int token_room_ = 0;
     // Device buffers: the step's state (four ints), the residual (fp32),

@@ -390,7 +390,17 @@ namespace mi
   // The workgroups launch_project makes for `p` (its mode, segments' rows
   // and input length): the entries a kLogits call's best arrays need.
   int project_blocks(const ProjectArgs &p);
-  void launch_project(const ProjectArgs &p, hipStream_t stream);
+  // The variant a projection ran as: the waves a row is split over, whether
+  // the grid is the device's resident one with several rows a wave, the
+  // waves a workgroup and the workgroups launched.
+  struct ProjectPlanInfo
+  {
+    int split;
+    int pipelined;
+    int waves;
+    int blocks;
+  };
+  ProjectPlanInfo launch_project(const ProjectArgs &p, hipStream_t stream);
   // A step's state in device memory, four ints.
   constexpr int kStepToken = 0;    // the token the step feeds
   constexpr int kStepPosition = 1; // its position

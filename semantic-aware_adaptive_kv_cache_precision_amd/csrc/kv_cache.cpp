@@ -797,6 +797,8 @@ namespace mi
     // taken and forgets the shadows just numbered (the copies into their
     // places are harmless: the places are free again, and a later copy into
     // one is ordered after them on the stream).
+    // A staged page that landed anywhere but the slot its batch named is
+    // refused the same way, before any device work names that slot.
     std::vector<PageKey> taken;
     try
     {
@@ -805,19 +807,19 @@ namespace mi
         allocator_.allocate_run(runs[t], t, false);
         taken.insert(taken.end(), runs[t].begin(), runs[t].end());
       }
+      for (std::size_t i = 0; i < n; ++i)
+      {
+        if (allocator_.ref_of(staged[i]) != to[i])
+        {
+          throw LogicError("a staged page did not land in the slot its batch named");
+        }
+      }
     }
     catch (...)
     {
       allocator_.free_pages(taken);
       shadows_.truncate(shadows_before);
       throw;
-    }
-    for (std::size_t i = 0; i < n; ++i)
-    {
-      if (allocator_.ref_of(staged[i]) != to[i])
-      {
-        throw LogicError("a staged page did not land in the slot its batch named");
-      }
     }
     phases_[1] = since(allocating);
     launch_copy_refs(on_device + at, static_cast<int>(restores.size()), spaces, stream);

@@ -428,12 +428,13 @@ namespace mi
       catch (...)
       {
       }
-      throw OutOfMemory("allocating " + describe(keys.front()) +
-                        (keys.size() > 1 ? " and " + std::to_string(keys.size() - 1) + " more"
+      throw OutOfMemory(std::string("out of device memory: the ") + tier_name(tier) +
+                        " range could not map " +
+                        std::to_string(granule_) + " more bytes for " + describe(keys.front()) +
+                        (keys.size() > 1 ? " (+" + std::to_string(keys.size() - 1) + " pages)"
                                          : std::string()) +
-                        " at " + tier_name(tier) + " needed a " + std::to_string(granule_) +
-                        "-byte granule: " + e.what() +
-                        (known ? "; " + std::to_string(free_bytes) + " bytes were free"
+                        " (" + e.what() + ")" +
+                        (known ? ", with " + std::to_string(free_bytes) + " B free on the device"
                                : std::string()));
     }
     catch (...)

@@ -659,6 +659,8 @@ namespace mi
       int waves;
       int blocks;
       std::size_t lds;
+      int split;
+      bool pipelined;
     };
 
     // A wave a row (Split waves with a long input) in one grid when the
@@ -695,11 +697,11 @@ namespace mi
       ProjectFn plain = project_variant(ahead, waves, two, split, false);
       if (split > 1 || needed <= resident_blocks(plain, 64 * waves, lds))
       {
-        return {plain, waves, static_cast<int>(needed), lds};
+        return {plain, waves, static_cast<int>(needed), lds, split, false};
       }
       ProjectFn pipe = project_variant(ahead, waves, two, split, true);
       const int held = resident_blocks(pipe, 64 * waves, lds);
-      return {pipe, waves, static_cast<int>(std::min<long long>(needed, held)), lds};
+      return {pipe, waves, static_cast<int>(std::min<long long>(needed, held)), lds, split, true};
     }
   } // namespace
 
@@ -714,7 +716,7 @@ namespace mi
     return plan_projection(p).blocks;
   }
 
-  void launch_project(const ProjectArgs &p, hipStream_t stream)
+  ProjectPlanInfo launch_project(const ProjectArgs &p, hipStream_t stream)
   {
     const bool normed = p.norm_weight != nullptr;
     if (p.segments < 1 || p.segments > kProjectSegments || p.in <= 0 || p.in % 8 != 0 ||
@@ -762,6 +764,7 @@ namespace mi
     hip_check(hipLaunchKernel(reinterpret_cast<const void *>(plan.fn), dim3(plan.blocks),
                               dim3(64 * plan.waves), params, plan.lds, stream),
               "projection kernel launch");
+    return {plan.split, plan.pipelined ? 1 : 0, plan.waves, plan.blocks};
   }
 
   void launch_qkv_step(const QkvStep &s, hipStream_t stream)

@@ -88,6 +88,7 @@ SIGNATURES = {
     "mi_decode_step_prefill": ((_vp, C.POINTER(C.c_int32), _i, _i, _i, C.POINTER(C.c_int32),
                                 C.POINTER(_d)), C.c_int),
     "mi_decode_step_launches": ((_vp, _ip), C.c_int),
+    "mi_decode_step_plans": ((_vp, _ip, _sz, _szp), C.c_int),
     "mi_random_half": ((_vp, _sz, C.c_ulonglong, _f), C.c_int),
     "mi_host_free": ((_vp,), C.c_int),
     "mi_device_pci_bus_id": ((C.c_char_p, _sz), C.c_int), "mi_memory_info": ((_szp, _szp), C.c_int),
@@ -1439,6 +1440,28 @@ class DecodeStep:
         n = C.c_int()
         _check(lib.mi_decode_step_launches(self._h, C.byref(n)))
         return n.value
+
+    #: The GEMVs projection_plans() names, in its order.
+    PLAN_NAMES = ("output", "gate_up", "down", "head")
+
+    def projection_plans(self) -> dict:
+        """The plans the last step's GEMVs ran as (beyond the reference):
+        {name: {rows, in, split, pipelined, waves, blocks}} for layer 0's
+        output, gate/up and down projections and the head. `split` is the
+        waves a row is split over; `pipelined` that the grid was the
+        device's resident one, each wave taking several rows."""
+        count = C.c_size_t()
+        _check(lib.mi_decode_step_plans(self._h, None, 0, C.byref(count)))
+        ints = np.zeros(count.value, np.int32)
+        _check(lib.mi_decode_step_plans(self._h, ints.ctypes.data_as(_ip), ints.size,
+                                        C.byref(count)))
+        plans = {}
+        for row in ints.reshape(-1, 7):
+            what, rows, n_in, split, pipelined, waves, blocks = (int(x) for x in row)
+            plans[self.PLAN_NAMES[what]] = dict(rows=rows, n_in=n_in, split=split,
+                                                pipelined=bool(pipelined), waves=waves,
+                                                blocks=blocks)
+        return plans
 
 
 device = SimpleNamespace(

@@ -264,6 +264,7 @@ def check_step_against_oracle(s, biases, start, seed):
         assert tokens[0] == order[0], (tokens[0], order[:3])
     assert tokens[0] == dense.argmax_rows(got[None].astype(np.float32))[0]
     assert ms > 0 and step.launches == 1 + 6 * s["layers"] + 1 + 1
+    return step
 
 
 def test_one_step_is_the_oracles_composition_qwen_shape():
@@ -290,6 +291,37 @@ def test_one_step_is_the_oracles_composition_llama_shape():
     """No biases, four query heads a KV head (Llama-3.2's grouping)."""
     check_step_against_oracle(small_shape(hidden=512, intermediate=1024, heads=16, kv_heads=4,
                                           head_dim=64, vocab=1500), False, P * 2 + 5, 13)
+
+
+@pytest.mark.parametrize("name", ["qwen2.5-1.5b", "llama-3.2-1b"])
+def test_one_step_at_full_model_widths_takes_the_real_gemv_variants(name):
+    """Two layers at the model's full hidden, FFN and vocabulary widths
+    (Qwen2.5-1.5B 1536 / 8960 / 151,936 with q/k/v biases; Llama-3.2-1B
+    2048 / 8192 / 128,256 without): the step's logits against the float64
+    composition, its greedy token the argmax of its logits (the head's
+    per-block bests reduced right over every block of the resident grid).
+    The shapes reach the GEMV variants the real steps run, and the test
+    asserts that they did: the down projection's long input split over four
+    waves a row, read as it comes; gate/up and the head on the device's
+    resident grid, each wave taking several rows with the next in flight."""
+    from microinfer import workloads as w
+    shape = w.SHAPES[name]
+    s = dict(w.model_dict(shape), layers=2)
+    step = check_step_against_oracle(s, name.startswith("qwen"), P * 3 + 10,
+                                     31 if name.startswith("qwen") else 32)
+    plans = step.projection_plans()
+    announce("plans", name, plans)
+    q_width = shape.heads * shape.head_dim
+    assert plans["output"]["rows"] == shape.hidden and plans["output"]["n_in"] == q_width
+    assert plans["output"]["split"] == 1
+    assert plans["down"]["n_in"] == shape.intermediate and plans["down"]["split"] == 4
+    assert not plans["down"]["pipelined"]
+    assert plans["gate_up"]["rows"] == shape.intermediate and plans["gate_up"]["pipelined"]
+    head = plans["head"]
+    assert head["rows"] == shape.vocab and head["pipelined"]
+    # The resident grid: fewer workgroups than a row a wave would need.
+    assert head["blocks"] * head["waves"] < shape.vocab
+    assert plans["gate_up"]["blocks"] * plans["gate_up"]["waves"] < shape.intermediate
 
 
 def test_a_run_replays_one_graph_to_the_bits_of_single_steps():

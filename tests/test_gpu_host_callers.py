@@ -4,8 +4,9 @@ fixed move lists in place of the precision controller's plans, and of
 PagedCache.attend (src/microinfer/model.py:273-286).
 
 The reference's own host code is the drop-in caller: nothing here is a
-planner. Each replay makes exactly the calls the reference makes, in its
-order, with its arguments, and checks what the device then holds.
+planner. Each replay restates the device calls those functions make (the
+batch loop, its free-memory margin and its retry at half size; not the
+engine's time budget) and checks what the device then holds.
 
 GPU parity tests: after each plan every page holds, to the bit, the oracle's
 quantise_page of its FP16 rows at the tier the plan leaves it (an upgrade,
@@ -41,18 +42,22 @@ def check_pages(alloc, cache, k, v, tiers, what):
 
 
 def apply_like_the_engine(pages, plan, page_bytes, bytes_cap=None):
-    """Engine._apply's device calls over a plan of (layer, page, from, to)
-    steps: each batch takes the plan's moves from the cursor whose page is
-    where the step expects (page_tiers()), each page once, while its new
-    pages fit the device's free memory (device_memory_info()["free"]) and
-    the cap; move_pages(batch); on OutOfMemory the same batch again at half
-    its bytes, and a single move that cannot allocate ends the plan. Returns
-    (moves applied, batches, skipped, stopped, retries)."""
+    """A restatement (not the reference's own code) of the device calls
+    Engine._apply makes (engine.py:1750-1802) over a plan of (layer, page,
+    from, to) steps, without its time budget: each batch takes the plan's
+    moves from the cursor whose page is where the step expects
+    (page_tiers()), each page once, while its new pages fit the device's free
+    memory less the engine's batch margin (two granules a tier,
+    engine.py:1804-1809) and the cap; move_pages(batch); on OutOfMemory the
+    same batch again at half its bytes, and a single move that cannot
+    allocate ends the plan. Returns (moves applied, batches, skipped,
+    stopped, retries)."""
     m = mi()
     i, applied, batches, skipped, stopped, retries = 0, 0, 0, 0, None, 0
     cap = bytes_cap
+    margin = 2 * 4 * m.granule_bytes()
     while i < len(plan):
-        free = m.device_memory_info()["free"]
+        free = m.device_memory_info()["free"] - margin
         limit = free if cap is None else min(free, cap)
         held = pages.page_tiers()
         shadowed = pages.shadowed()

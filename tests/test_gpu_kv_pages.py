@@ -468,6 +468,13 @@ def test_full_size_config3_layer_against_the_oracle():
     store_in_runs(cache, 0, k.astype(np.float32), v.astype(np.float32), [seq - 1, 1])
     counts = np.bincount(cache.page_tiers()[0][:seq // P - 1], minlength=4)
     assert list(counts) == [205, 307, 409, 102]
+    # The pages the decode reads are, byte for byte, the oracle's quantise_page
+    # of their rows at their birth tiers (sealed by the batched store launches).
+    for page in range(seq // P - 1):
+        tier = tmap[0][page]
+        kp, vp = k[page * P:(page + 1) * P], v[page * P:(page + 1) * P]
+        want_page = quant.fp16_page(kp, vp) if tier == 0 else quant.quantise_page(kp, vp, tier, P)
+        np.testing.assert_array_equal(alloc.read(0, page), want_page, err_msg=f"page {page}")
     q = fp16_exact(rng.standard_normal((1, shape.heads, shape.head_dim)))
     scores = d.ImportanceScores(LAYERS, seq // P)
     announce("config3 full layer: decode")
@@ -478,6 +485,43 @@ def test_full_size_config3_layer_against_the_oracle():
     assert_mass_close(mass, want_mass, "config3 mass")
     np.testing.assert_array_equal(scores.download()[0],
                                   ewma.host_ewma([(0, mass.astype(np.float32))], 1, seq // P)[0])
+
+
+def test_the_shadow_store_binding_takes_a_page_once():
+    """The standalone shadow store (bindings_device.cpp:652-680; the store a
+    KVPages holds): take copies the first page_bytes of a device tensor into
+    a new pinned shadow; a second take for the same page is refused ("has a
+    shadow already", RuntimeError) and the first shadow kept; contains and
+    count follow; shadows pack into pinned allocations of whole pages
+    (shadow_store.h:28), a new allocation only when the last is full; a page
+    with no shadow is a PageNotFound, a tensor short of a page a ValueError."""
+    m = mi()
+    d = m.device
+    page_bytes = quant.page_bytes(0, 2, 128)
+    store = d.ShadowStore(page_bytes)
+    rng = np.random.default_rng(96)
+    first = normal(rng, page_bytes // 2)
+    announce("shadow store")
+    store.take(0, 1, put(first))
+    with pytest.raises(RuntimeError, match="has a shadow already"):
+        store.take(0, 1, put(normal(rng, page_bytes // 2)))
+    np.testing.assert_array_equal(store.shadow(0, 1), first.astype(np.float16).view(np.uint8))
+    assert store.count == 1 and store.contains(0, 1) and not store.contains(1, 0)
+    per_allocation = max(1, d.ShadowStore.allocation_bytes // page_bytes)
+    taken = {}
+    for page in range(2, per_allocation + 2):
+        taken[page] = normal(rng, page_bytes // 2)
+        store.take(3, page, put(taken[page]))
+    assert store.count == per_allocation + 1
+    assert store.bytes == 2 * per_allocation * page_bytes
+    for page, rows in taken.items():
+        assert store.contains(3, page)
+        np.testing.assert_array_equal(store.shadow(3, page), rows.astype(np.float16).view(np.uint8))
+    with pytest.raises(m.PageNotFound):
+        store.shadow(5, 5)
+    with pytest.raises(ValueError):
+        store.take(0, 99, put(first[:16]))
+    assert store.count == per_allocation + 1 and not store.contains(0, 99)
 
 
 def test_chained_store_and_decode_steps_across_a_seal_at_llama_shape():
