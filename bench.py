@@ -679,10 +679,20 @@ def requant_plan(m, shape, context, layers, link, seed=0):
     release_s = time.perf_counter() - t0
     n8 = int(round(0.1 * n4))  # 10% of the INT4 pages: 1,434 of 14,336
     up = np.asarray([(*keys[i], 1) for i in order[:n8]], np.int32)
+    # The restores' INT8 granules mapped ahead as well, as a spare run.
+    up_ahead = -(-n8 * sizes[1] // g)
+    t0 = time.perf_counter()
+    alloc.keep_spare_granules(1, up_ahead)
+    up_map_s = time.perf_counter() - t0
+    m.synchronize()
     t0 = time.perf_counter()
     cache.move_pages(up)
     up_s = time.perf_counter() - t0
     up_batch = cache.last_batch
+    alloc.keep_spare_granules(1, 0)
+    t0 = time.perf_counter()
+    alloc.drain_releases()
+    up_release_s = time.perf_counter() - t0
     tiers = cache.page_tiers()
     if any(int(tiers[l, p]) != t for l, p, t in down[n8:] + [tuple(x) for x in up]):
         raise AssertionError("a moved page is not at the tier its move named")
@@ -715,6 +725,10 @@ def requant_plan(m, shape, context, layers, link, seed=0):
                                                    "allocate_seconds", "finish_seconds")},
             "restores_int4_to_int8": len(up), "restore_seconds": round(up_s, 5),
             "restore_pages_per_s": round(len(up) / up_s),
+            "restore_granule_map_ahead_seconds": round(up_map_s, 5),
+            "restore_granule_release_seconds": round(up_release_s, 5),
+            "restore_pages_per_s_with_map_ahead_and_release":
+                round(len(up) / (up_s + up_map_s + up_release_s)),
             "link_gb_per_s": link,
             "roofline": {
                 "downgrade": {"bound": "host link" if down_link / d2h > down_hbm / PEAK_GBS
@@ -726,6 +740,171 @@ def requant_plan(m, shape, context, layers, link, seed=0):
                             "bound_seconds": round(up_bound, 5), "host_link_bytes": up_link,
                             "hbm_bytes": up_hbm, "frac": round(up_bound / up_s, 4)}},
             "reference_rtx4050": {"downgrade_moves_per_s": 183000, "restore_pages_per_s": 201700}}
+
+
+def restore_all(m, shape, context, layers, seed=0):
+    """The reference's batched restore (benchmark.jsonl:3320): every page
+    of a 28-layer 1.5B cache at 32K (28,672 pages) downgraded to INT4 in
+    one batch, then every page back to FP16 from its shadow in one batch,
+    timed with the given-back granules' release counted."""
+    pages = context // P
+    alloc, cache = sealing_cache(m, shape, layers, pages, [])
+    fill_rows(m, cache, shape, layers, context, np.random.default_rng(seed))
+    keys = np.asarray([(l, p) for l in range(layers) for p in range(pages)], np.int32)
+    sizes = tier_sizes(m, shape)
+    g = alloc.granule_bytes
+    cache.pin_shadows(len(keys))
+    alloc.keep_spare_granules(2, -(-len(keys) * sizes[2] // g))
+    cache.move_pages(np.column_stack([keys, np.full(len(keys), 2, np.int32)]))
+    alloc.keep_spare_granules(2, 0)
+    alloc.drain_releases()
+    m.synchronize()
+    alloc.keep_spare_granules(0, -(-len(keys) * sizes[0] // g))
+    m.synchronize()
+    t0 = time.perf_counter()
+    cache.move_pages(np.column_stack([keys, np.zeros(len(keys), np.int32)]))
+    up_s = time.perf_counter() - t0
+    alloc.keep_spare_granules(0, 0)
+    t0 = time.perf_counter()
+    alloc.drain_releases()
+    release_s = time.perf_counter() - t0
+    tiers = cache.page_tiers()[:, :pages]
+    if not (tiers == 0).all():
+        raise AssertionError("a restored page is not at FP16")
+    return {"pages": len(keys), "seconds": round(up_s, 5),
+            "pages_per_s": round(len(keys) / up_s),
+            "granule_release_seconds": round(release_s, 5),
+            "pages_per_s_with_release": round(len(keys) / (up_s + release_s)),
+            "reference_rtx4050_pages_per_s": 201700}
+
+
+#: The reference's single-move latency groups (tools/requantisation_latency.py:
+#: 53-55): the INT8 group's round of the quantised tiers after FP16 -> INT8.
+MOVE_ROUND = (("downgrade", 2), ("downgrade", 3), ("upgrade", 1), ("downgrade", 3),
+              ("upgrade", 2), ("upgrade", 1))
+
+
+def move_latency(m, shape, positions=4096, samples=256, seed=97):
+    """Single-page moves by tier pair, each timed by last_move (the whole
+    move's wall time, once the device has finished earlier work; the
+    shadow's copy apart), as tools/requantisation_latency.py times them:
+    three groups of `samples` pages, one a quantised tier T, go FP16 -> T (a
+    first downgrade), T -> FP16, FP16 -> T (the shadow held); the INT8 group
+    then goes round the quantised tiers. Three pages make every move first,
+    untimed. Median, P90 and max microseconds a pair."""
+    layers = shape.layers
+    pages = positions // P
+    alloc, cache = sealing_cache(m, shape, layers, pages, [])
+    fill_rows(m, cache, shape, layers, positions, np.random.default_rng(seed))
+    keys = [(l, i) for i in range(pages) for l in range(layers)]
+    warm, groups = keys[:3], [keys[3 + k * samples:3 + (k + 1) * samples] for k in range(3)]
+    names = {0: "FP16", 1: "INT8", 2: "INT4", 3: "INT2"}
+    records = {}
+
+    def move(layer, page, frm, to, first=False):
+        (cache.downgrade if to > frm else cache.upgrade)(layer, page, to)
+        last = cache.last_move
+        name = f"{names[frm]}->{names[to]}" + (" first" if first else "")
+        records.setdefault(name, []).append((last["seconds"], last["shadow_seconds"]))
+
+    for layer, page in warm:
+        for frm, to in ((0, 1), (1, 2), (2, 3), (3, 1), (1, 0)):
+            (cache.downgrade if to > frm else cache.upgrade)(layer, page, to)
+    for tier, group in zip((1, 2, 3), groups):
+        for layer, page in group:
+            move(layer, page, 0, tier, first=True)
+        for layer, page in group:
+            move(layer, page, tier, 0)
+        for layer, page in group:
+            move(layer, page, 0, tier)
+    at = 1
+    for _, to in MOVE_ROUND:
+        for layer, page in groups[0]:
+            move(layer, page, at, to)
+        at = to
+    out = {}
+    for name, rec in records.items():
+        sec = np.asarray([r[0] for r in rec]) * 1e6
+        sh = np.asarray([r[1] for r in rec]) * 1e6
+        out[name] = {"moves": len(rec), "median_us": round(float(np.median(sec)), 2),
+                     "p90_us": round(float(np.percentile(sec, 90)), 2),
+                     "max_us": round(float(sec.max()), 2),
+                     "shadow_median_us": round(float(np.median(sh)), 2)}
+    out["reference_rtx4050_median_us"] = {
+        "FP16->INT8": 13.4, "FP16->INT4": 19.3, "FP16->INT2": 29.7, "FP16->INT8 first": 23.0,
+        "FP16->INT4 first": 28.8, "FP16->INT2 first": 39.3, "INT8->FP16": 7.7,
+        "INT4->FP16": 7.7, "INT2->FP16": 7.7, "INT8->INT4": 31.7, "INT8->INT2": 37.0,
+        "INT4->INT2": 37.2, "INT4->INT8": 20.7, "INT2->INT8": 20.7, "INT2->INT4": 26.3}
+    return out
+
+
+def decode_tier_rows(m, shape, stream, steps, warmup, seed=204):
+    """The reference's per-tier decode rows (tools/attention_speed.py,
+    benchmark.jsonl:3292-3296): a one-layer cache of `length` positions at
+    one tier (FP16, INT8, INT4, INT2) or born from a map cycling the four
+    tiers page by page, keys completed by a key bias (x30) with RoPE, one
+    query over every position with the per-page mass and without; one
+    launch's device time (a graph of 20 launches), microseconds, and the
+    whole model's ms a token (x28)."""
+    d = m.device
+    heads, kv, hd = shape.heads, shape.kv_heads, shape.head_dim
+    sizes = tier_sizes(m, shape)
+    out = {}
+    for length in (32768, 16384):
+        pages = -(-length // P)
+        for name, tier in (("FP16", 0), ("INT8", 1), ("INT4", 2), ("INT2", 3), ("mixed", None)):
+            rng = np.random.default_rng(seed)
+            if tier is None:
+                tmap = [[(0, 1, 2, 3)[i % 4] for i in range(pages)]]
+                born, cap = 0, [pages + 4] * 4
+            else:
+                tmap, born = [], tier
+                cap = [0, 0, 0, 0]
+                cap[tier] = pages + 2
+            cap[0] += 2
+            alloc = m.PagedKVCache(sizes, cap)
+            cache = d.KVPages(alloc, 1, P, kv, hd, born, d.Halves.Both, tmap, False)
+            width = kv * hd
+            start = 0
+            for n in [4096] * ((length - 1) // 4096) + [(length - 1) % 4096, 1]:
+                if n == 0:
+                    continue
+                cache.reserve(start + n)
+                k = m.upload_fp16(rng.standard_normal(n * width).astype(np.float32))
+                v = m.upload_fp16(rng.standard_normal(n * width).astype(np.float32))
+                cache.store(0, k, v, start, n)
+                start += n
+            rope = d.RopeTable(hd, shape.rope_theta)
+            rope.cover(length)
+            bias = m.upload_fp16((rng.standard_normal(width) * 30).astype(np.float32))
+            q = m.upload_fp16(rng.standard_normal(heads * hd).astype(np.float32))
+            o = d.empty(heads * hd)
+            mass = d.empty_f32(heads * pages)
+            part = d.empty_f32(d.attention_partials(hd))
+            row = {}
+            for with_mass in (True, False):
+                def body():
+                    for _ in range(20):
+                        cache.attention(0, q, bias, rope, o, 1, length, heads, kv, hd, k, v,
+                                        mass if with_mass else None, part)
+                us = timed_graph(m, stream, body, max(steps // 5, 3), max(warmup // 5, 1)) \
+                    * 1e3 / 20
+                row["with_mass" if with_mass else "plain"] = {
+                    "us_per_launch": round(us, 2), "ms_per_token_x28": round(us * 28 / 1e3, 3)}
+            kv_bytes = sum(sizes[int(alloc.locate(0, i)[0])] for i in range(pages - 1)) + sizes[0]
+            row["kv_bytes"] = kv_bytes
+            row["gb_per_s_plain"] = round(kv_bytes / (row["plain"]["us_per_launch"] * 1e-6) / 1e9,
+                                          1)
+            out[f"{name}_{length // 1024}K"] = row
+            del cache, alloc
+    out["reference_rtx4050_us_per_launch"] = {
+        "32K": {"FP16": 572.0, "INT8": 683.8, "INT4": 751.8, "INT2": 728.5, "mixed": 792.2},
+        "32K_with_mass": {"FP16": 672.6, "INT8": 879.6, "INT4": 886.4, "INT2": 777.2,
+                          "mixed": 886.6},
+        "16K": {"FP16": 391.5, "INT8": 361.8, "INT4": 378.8, "INT2": 389.6, "mixed": 363.3}}
+    out["note"] = ("one layer, key bias on, a launch = decode pages kernel + combine; the "
+                   "reference times the host launch loop over batches of 20")
+    return out
 
 
 # ---- the CPU reference path (the oracle) -----------------------------------------------------
@@ -848,7 +1027,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=None, help="fewer layers, for a quick look")
-    ap.add_argument("--legs", default="decode,prefill,config2,step,quantise,requant,cpu",
+    ap.add_argument("--legs",
+                    default="decode,tiers,prefill,config2,step,quantise,requant,moves,cpu",
                     help="the legs to run (comma list; decode is the headline)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-requant", action="store_true")
@@ -918,6 +1098,11 @@ def main() -> int:
     if "decode" in legs:
         del alloc3, cache3, host3, rows3
 
+    tier_rows = (decode_tier_rows(m, shape, stream, args.steps, args.warmup)
+                 if "tiers" in legs else None)
+    if tier_rows is not None:
+        log(f"decode rows by tier: {tier_rows}")
+
     c2 = config2(m, args.steps, args.warmup) if "config2" in legs else None
 
     steps_out = None
@@ -941,7 +1126,13 @@ def main() -> int:
         link = link_rates(m)
         log(f"host link: {link}")
         requant = requant_plan(m, shape, context, layers, link)
+        requant["restore_all_int4_to_fp16"] = restore_all(m, shape, context, layers)
         log(f"requant plan in {time.perf_counter() - t0:.1f}s: {requant}")
+
+    moves = None
+    if "moves" in legs:
+        moves = move_latency(m, shape)
+        log(f"single-page moves: {moves}")
 
     cpu = None
     if "cpu" in legs:
@@ -971,7 +1162,8 @@ def main() -> int:
     if ms is None:
         print(json.dumps({"metric": METRIC, "value": None, "legs": sorted(legs), "config2": c2,
                           "decode_step": steps_out, "prefill": prefill, "quantise": quantise,
-                          "requant": requant, "cpu_baseline": cpu}),
+                          "requant": requant, "single_page_moves": moves,
+                          "decode_by_tier": tier_rows, "cpu_baseline": cpu}),
               flush=True)
         return 0
     result = {
@@ -1008,11 +1200,13 @@ def main() -> int:
             "one_launch_vs_per_layer_gap": round(times["one_launch_gap"], 6),
             "note": "same bytes; the one launch takes every layer's query at once, not the "
                     "per-layer decode order"},
+        "decode_by_tier": tier_rows,
         "config2": c2,
         "decode_step": steps_out,
         "cpu_baseline": cpu,
         "quantise": quantise,
         "requant": requant,
+        "single_page_moves": moves,
         "prefill": prefill,
     }
     print(json.dumps(result), flush=True)

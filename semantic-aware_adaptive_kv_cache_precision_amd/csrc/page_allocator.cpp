@@ -16,10 +16,18 @@
 //   - every compaction copy of a call, over all four tiers, is one launch of
 //     copy_refs (slot references, addresses formed on the device), queued on
 //     the runtime stream without waiting for it;
-//   - a granule the tail gives up is unmapped by the releaser thread once an
-//     event recorded after the call's copies has completed, so no caller
-//     waits for the device or for the driver's unmap; an address about to be
-//     mapped again waits for its own release only;
+//   - granules are mapped in runs (one physical allocation and one map call
+//     for up to kMaxRunGranules of them): the driver's unmap costs the same
+//     ~0.26 ms for a run of any length, so a range gives back a 704 MB tail
+//     in a dozen calls, not 352;
+//   - whole runs the tail gives up are unmapped by the releaser thread once
+//     an event recorded after the call's copies has completed, so no caller
+//     waits for the driver's unmap; a run the new tail cuts is replaced, on
+//     the caller's thread, by a shorter one holding the same bytes;
+//   - access is granted over a range from its base only (an unmapped guard
+//     granule before it) once nothing past the new end is mapped: the
+//     driver refuses a span that starts where another mapping ends or that
+//     a mapping follows, and then leaves the span without access;
 //   - every page whose slot changes is reported to the watching KVPages,
 //     which edit their device page tables instead of rebuilding them.
 
@@ -134,7 +142,7 @@ namespace mi
   class GranuleReleaser
   {
   public:
-    GranuleReleaser(int device, std::size_t granule) : device_(device), granule_(granule) {}
+    explicit GranuleReleaser(int device) : device_(device) {}
 
     ~GranuleReleaser()
     {
@@ -149,8 +157,14 @@ namespace mi
       }
     }
 
-    void retire(std::vector<std::pair<char *, hipMemGenericAllocationHandle_t>> granules,
-                hipStream_t stream)
+    struct Retired
+    {
+      char *at;
+      std::size_t bytes;
+      hipMemGenericAllocationHandle_t handle;
+    };
+
+    void retire(std::vector<Retired> granules, hipStream_t stream)
     {
       if (granules.empty())
       {
@@ -171,9 +185,9 @@ namespace mi
       }
       {
         std::lock_guard<std::mutex> lock(mutex_);
-        for (const auto &[at, handle] : granules)
+        for (const Retired &g : granules)
         {
-          queue_.push_back({at, handle, gate});
+          queue_.push_back({g.at, g.bytes, g.handle, gate});
         }
         if (!thread_.joinable())
         {
@@ -183,22 +197,26 @@ namespace mi
       wake_.notify_one();
     }
 
-    // Waits until the granule at `at` (nullptr: every granule) is released;
-    // raises the first failure of the thread.
-    void wait_for(const char *at)
+    // Waits until no run queued or being released holds an address of
+    // [at, at + bytes) (at nullptr: every run is released); raises the first
+    // failure of the thread.
+    void wait_for(const char *at, std::size_t bytes = 0)
     {
       std::unique_lock<std::mutex> lock(mutex_);
+      const auto meets = [&](const char *from, std::size_t n) {
+        return from < at + bytes && at < from + n;
+      };
       const auto pending = [&] {
         if (at == nullptr)
         {
           return !queue_.empty() || busy_ != nullptr;
         }
-        if (busy_ == at)
+        if (busy_ != nullptr && meets(busy_, busy_bytes_))
         {
           return true;
         }
         return std::any_of(queue_.begin(), queue_.end(),
-                           [at](const Item &i) { return i.at == at; });
+                           [&](const Item &i) { return meets(i.at, i.bytes); });
       };
       done_.wait(lock, [&] { return !pending(); });
       if (!error_.empty())
@@ -224,6 +242,7 @@ namespace mi
     struct Item
     {
       char *at;
+      std::size_t bytes;
       hipMemGenericAllocationHandle_t handle;
       std::shared_ptr<Gate> gate;
     };
@@ -242,6 +261,7 @@ namespace mi
         Item item = std::move(queue_.front());
         queue_.pop_front();
         busy_ = item.at;
+        busy_bytes_ = item.bytes;
         lock.unlock();
         hipError_t e = set;
         if (e == hipSuccess && item.gate->event != nullptr)
@@ -250,7 +270,7 @@ namespace mi
         }
         if (e == hipSuccess)
         {
-          e = hipMemUnmap(item.at, granule_);
+          e = hipMemUnmap(item.at, item.bytes);
         }
         const hipError_t released = hipMemRelease(item.handle);
         if (e == hipSuccess)
@@ -262,19 +282,19 @@ namespace mi
         busy_ = nullptr;
         if (e != hipSuccess && error_.empty())
         {
-          error_ = std::string("releasing a granule: ") + hipGetErrorString(e);
+          error_ = std::string("releasing a run of granules: ") + hipGetErrorString(e);
         }
         done_.notify_all();
       }
     }
 
     int device_;
-    std::size_t granule_;
     std::mutex mutex_;
     std::condition_variable wake_;
     std::condition_variable done_;
     std::deque<Item> queue_;
     const char *busy_ = nullptr;
+    std::size_t busy_bytes_ = 0;
     bool stop_ = false;
     std::string error_;
     std::thread thread_;
@@ -295,7 +315,7 @@ namespace mi
     hip_check(hipGetDevice(&device_), "hipGetDevice");
     prop_ = device_prop(device_);
     granule_ = mapping_unit(prop_);
-    releaser_ = std::make_unique<GranuleReleaser>(device_, granule_);
+    releaser_ = std::make_unique<GranuleReleaser>(device_);
     for (int t = 0; t < kTierCount; ++t)
     {
       Range &r = ranges_[t];
@@ -306,40 +326,70 @@ namespace mi
       {
         continue;
       }
+      // A guard granule, never mapped, before the range: no mapping ever
+      // ends where the range begins (the driver takes a mapping that ends
+      // at an address for the one that begins there when access is granted
+      // from it, and refuses it when their lengths differ).
       void *base = nullptr;
-      const hipError_t e = hipMemAddressReserve(&base, r.reserved, granule_, nullptr, 0);
+      const hipError_t e = hipMemAddressReserve(&base, r.reserved + granule_, granule_, nullptr, 0);
       if (e != hipSuccess)
       {
         for (int u = 0; u < t; ++u)
         {
-          if (ranges_[u].base != nullptr)
+          if (ranges_[u].reservation != nullptr)
           {
-            (void)hipMemAddressFree(ranges_[u].base, ranges_[u].reserved);
+            (void)hipMemAddressFree(ranges_[u].reservation, ranges_[u].reserved + granule_);
           }
         }
         hip_check(e, "hipMemAddressReserve");
       }
-      r.base = static_cast<char *>(base);
+      r.reservation = static_cast<char *>(base);
+      r.base = r.reservation + granule_;
     }
+    void *scratch = nullptr;
+    const hipError_t e = hipMemAddressReserve(&scratch, (kMaxRunGranules + 1) * granule_,
+                                              granule_, nullptr, 0);
+    if (e != hipSuccess)
+    {
+      for (Range &r : ranges_)
+      {
+        if (r.reservation != nullptr)
+        {
+          (void)hipMemAddressFree(r.reservation, r.reserved + granule_);
+        }
+      }
+      hip_check(e, "hipMemAddressReserve");
+    }
+    scratch_reservation_ = static_cast<char *>(scratch);
+    scratch_ = scratch_reservation_ + granule_;
   }
 
   PagedKVCache::~PagedKVCache()
   {
+    // Nothing here can be reported to a caller; a failure is dropped, and
+    // the thread's last error cleared so that no later call reports it.
     (void)hipDeviceSynchronize();
     releaser_.reset(); // finishes every release queued
     for (Range &r : ranges_)
     {
-      for (std::size_t g = r.granules.size(); g-- > 0;)
+      for (std::size_t i = r.runs.size(); i-- > 0;)
       {
-        (void)hipMemUnmap(r.base + g * granule_, granule_);
-        (void)hipMemRelease(r.granules[g]);
+        const Run &run = r.runs[i];
+        (void)hipMemUnmap(r.base + run.first * granule_, run.count * granule_);
+        (void)hipMemRelease(run.handle);
       }
-      r.granules.clear();
-      if (r.base != nullptr)
+      r.runs.clear();
+      r.mapped = 0;
+      if (r.reservation != nullptr)
       {
-        (void)hipMemAddressFree(r.base, r.reserved);
+        (void)hipMemAddressFree(r.reservation, r.reserved + granule_);
       }
     }
+    if (scratch_reservation_ != nullptr)
+    {
+      (void)hipMemAddressFree(scratch_reservation_, (kMaxRunGranules + 1) * granule_);
+    }
+    (void)hipGetLastError();
   }
 
   void PagedKVCache::check_tier(int tier)
@@ -591,58 +641,64 @@ namespace mi
 
   void PagedKVCache::replace(PageKey key, PageKey staged) { replace_pages({{key, staged}}); }
 
+  hipMemGenericAllocationHandle_t PagedKVCache::create_physical(std::size_t granules)
+  {
+    if (g_fail_granules > 0)
+    {
+      --g_fail_granules;
+      throw OutOfMemory("hipMemCreate: out of memory (injected by the test hook)");
+    }
+    hipMemGenericAllocationHandle_t handle;
+    hipError_t created = hipMemCreate(&handle, granules * granule_, &prop_, 0);
+    if (created == hipErrorOutOfMemory || created == hipErrorMemoryAllocation)
+    {
+      // Memory the releaser has yet to give back may be what is short.
+      (void)hipGetLastError();
+      releaser_->wait_for(nullptr);
+      created = hipMemCreate(&handle, granules * granule_, &prop_, 0);
+    }
+    hip_check(created, "hipMemCreate");
+    return handle;
+  }
+
   void PagedKVCache::map_to(Range &r, std::size_t count)
   {
-    // Each granule is made and mapped on its own (so that each can be
-    // given back on its own); the access to the whole new span is granted
-    // in one call, the driver's dearest of the three.
-    const std::size_t first = r.granules.size();
+    // The new granules in runs of up to kMaxRunGranules, each one physical
+    // allocation mapped by one call; access is then granted in one call
+    // over the range from its base.
+    const std::size_t first_run = r.runs.size();
+    const std::size_t first = r.mapped;
     const auto undo = [&]() {
-      for (std::size_t g = first; g < r.granules.size(); ++g)
+      for (std::size_t i = first_run; i < r.runs.size(); ++i)
       {
-        (void)hipMemUnmap(r.base + g * granule_, granule_);
-        (void)hipMemRelease(r.granules[g]);
+        const Run &run = r.runs[i];
+        (void)hipMemUnmap(r.base + run.first * granule_, run.count * granule_);
+        (void)hipMemRelease(run.handle);
       }
-      r.granules.resize(first);
+      r.runs.resize(first_run);
+      r.mapped = first;
     };
     try
     {
-      while (r.granules.size() < count)
+      while (r.mapped < count)
       {
-        if (g_fail_granules > 0)
-        {
-          --g_fail_granules;
-          throw OutOfMemory("hipMemCreate: out of memory (injected by the test hook)");
-        }
-        char *at = r.base + r.granules.size() * granule_;
-        // The address may be one the releaser still holds.
-        releaser_->wait_for(at);
-        hipMemGenericAllocationHandle_t handle;
-        hipError_t created = hipMemCreate(&handle, granule_, &prop_, 0);
-        if (created == hipErrorOutOfMemory || created == hipErrorMemoryAllocation)
-        {
-          // Memory the releaser has yet to give back may be what is short.
-          (void)hipGetLastError();
-          releaser_->wait_for(nullptr);
-          created = hipMemCreate(&handle, granule_, &prop_, 0);
-        }
-        hip_check(created, "hipMemCreate");
-        const hipError_t mapped = hipMemMap(at, granule_, 0, handle, 0);
+        const std::size_t n = std::min(count - r.mapped, kMaxRunGranules);
+        char *at = r.base + r.mapped * granule_;
+        // The addresses may be ones the releaser still holds.
+        releaser_->wait_for(at, n * granule_);
+        const hipMemGenericAllocationHandle_t handle = create_physical(n);
+        const hipError_t mapped = hipMemMap(at, n * granule_, 0, handle, 0);
         if (mapped != hipSuccess)
         {
           (void)hipMemRelease(handle);
           hip_check(mapped, "hipMemMap");
         }
-        r.granules.push_back(handle);
+        r.runs.push_back({r.mapped, n, handle});
+        r.mapped += n;
       }
-      if (r.granules.size() > first)
+      if (r.mapped > first)
       {
-        hipMemAccessDesc access{};
-        access.location = prop_.location;
-        access.flags = hipMemAccessFlagsProtReadWrite;
-        hip_check(hipMemSetAccess(r.base + first * granule_, (r.granules.size() - first) * granule_,
-                                  &access, 1),
-                  "hipMemSetAccess");
+        grant_access(r, first, r.mapped);
       }
     }
     catch (...)
@@ -652,15 +708,151 @@ namespace mi
     }
   }
 
+  void PagedKVCache::grant_access(Range &r, std::size_t from, std::size_t granules)
+  {
+    hipMemAccessDesc access{};
+    access.location = prop_.location;
+    access.flags = hipMemAccessFlagsProtReadWrite;
+    // The driver grants access over a span only where no mapping ends at
+    // its start and none lies past its end: it is granted from the range's
+    // base (which has an unmapped guard granule before it) once every run
+    // given up before has been unmapped.
+    releaser_->wait_for(nullptr);
+    hip_check(hipMemSetAccess(r.base, granules * granule_, &access, 1), "hipMemSetAccess");
+    // Every new run reads and writes before any page there is used.
+    for (const Run &run : r.runs)
+    {
+      if (run.first + run.count <= from)
+      {
+        continue;
+      }
+      for (const std::size_t g : {run.first, run.first + run.count - 1})
+      {
+        unsigned long long flags = 0;
+        hip_check(hipMemGetAccess(&flags, &prop_.location, r.base + g * granule_),
+                  "hipMemGetAccess");
+        if (flags != hipMemAccessFlagsProtReadWrite)
+        {
+          throw DeviceError("granule " + std::to_string(g) + " of a range is mapped without "
+                            "read and write access");
+        }
+      }
+    }
+  }
+
+  void PagedKVCache::split_run(Range &r, std::size_t keep)
+  {
+    Run &run = r.runs.back();
+    const std::size_t n = keep - run.first;
+    char *at = r.base + run.first * granule_;
+    // Whatever reads or writes the run (the call's compaction copies, a
+    // launch still queued anywhere) is done (the caller synchronised): for a
+    // moment its addresses hold nothing.
+    hipMemGenericAllocationHandle_t handle;
+    try
+    {
+      handle = create_physical(n);
+    }
+    catch (const OutOfMemory &)
+    {
+      // No room for the shorter copy: the run stays whole, its granules
+      // past `keep` mapped until the range next retracts.
+      r.mapped = run.first + run.count;
+      return;
+    }
+    hipMemAccessDesc access{};
+    access.location = prop_.location;
+    access.flags = hipMemAccessFlagsProtReadWrite;
+    hipError_t e = hipMemMap(scratch_, n * granule_, 0, handle, 0);
+    if (e == hipSuccess)
+    {
+      // The scratch span has a guard granule before it, like the ranges.
+      e = hipMemSetAccess(scratch_, n * granule_, &access, 1);
+      unsigned long long flags = 0;
+      for (const std::size_t g : {std::size_t{0}, n - 1})
+      {
+        if (e == hipSuccess)
+        {
+          e = hipMemGetAccess(&flags, &prop_.location, scratch_ + g * granule_);
+          if (e == hipSuccess && flags != hipMemAccessFlagsProtReadWrite)
+          {
+            e = hipErrorInvalidValue;
+          }
+        }
+      }
+      if (e == hipSuccess)
+      {
+        e = hipMemcpy(scratch_, at, n * granule_, hipMemcpyDeviceToDevice);
+      }
+      const hipError_t unmapped = hipMemUnmap(scratch_, n * granule_);
+      e = e == hipSuccess ? unmapped : e;
+    }
+    if (e != hipSuccess)
+    {
+      (void)hipMemRelease(handle);
+      hip_check(e, "splitting a run of granules (the copy)");
+    }
+    // The old run goes; the copy takes its place at the same addresses.
+    e = hipMemUnmap(at, run.count * granule_);
+    if (e != hipSuccess)
+    {
+      (void)hipMemRelease(handle);
+      hip_check(e, "hipMemUnmap a split run");
+    }
+    (void)hipMemRelease(run.handle);
+    e = hipMemMap(at, n * granule_, 0, handle, 0);
+    if (e != hipSuccess)
+    {
+      // The driver failed between the two mappings: the run is gone.
+      (void)hipMemRelease(handle);
+      r.mapped = run.first;
+      r.runs.pop_back();
+      hip_check(e, "hipMemMap a split run");
+    }
+    run.handle = handle;
+    run.count = n;
+    r.mapped = keep;
+    grant_access(r, run.first, keep);
+  }
+
+  void PagedKVCache::retract(Range &r, std::size_t keep)
+  {
+    std::vector<GranuleReleaser::Retired> going;
+    while (!r.runs.empty() && r.runs.back().first >= keep)
+    {
+      const Run &run = r.runs.back();
+      going.push_back({r.base + run.first * granule_, run.count * granule_, run.handle});
+      r.mapped -= run.count;
+      r.runs.pop_back();
+    }
+    if (r.mapped > keep)
+    {
+      // A run that `keep` cuts is remapped now, and access granted over the
+      // range: the runs past it are unmapped first, here, once the launches
+      // that may read them (this call's compaction copies) are done.
+      hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize before a run is split");
+      for (const GranuleReleaser::Retired &run : going)
+      {
+        hip_check(hipMemUnmap(run.at, run.bytes), "hipMemUnmap a run given up");
+        hip_check(hipMemRelease(run.handle), "hipMemRelease a run given up");
+      }
+      split_run(r, keep);
+      return;
+    }
+    // Whole runs go off the caller's path, once the launches queued so far
+    // (which may read them) are done.
+    releaser_->retire(std::move(going), runtime_stream());
+  }
+
   void PagedKVCache::fit(Range &r, bool map_spares)
   {
     const std::size_t needed = round_up(r.owners.size() * r.page_bytes, granule_) / granule_;
     const std::size_t keep = std::min(needed + r.spare, r.reserved / granule_);
-    if (r.granules.size() < needed)
+    if (r.mapped < needed)
     {
       map_to(r, needed);
     }
-    if (map_spares && r.granules.size() < keep)
+    if (map_spares && r.mapped < keep)
     {
       try
       {
@@ -671,15 +863,9 @@ namespace mi
         // A spare is room kept for later, not room a page needs now.
       }
     }
-    if (r.granules.size() > keep)
+    if (r.mapped > keep)
     {
-      std::vector<std::pair<char *, hipMemGenericAllocationHandle_t>> going;
-      for (std::size_t g = keep; g < r.granules.size(); ++g)
-      {
-        going.emplace_back(r.base + g * granule_, r.granules[g]);
-      }
-      r.granules.resize(keep);
-      releaser_->retire(std::move(going), runtime_stream());
+      retract(r, keep);
     }
   }
 

@@ -139,6 +139,10 @@ namespace mi
 
   class GranuleReleaser;
 
+  // The longest run of granules one physical allocation backs (64 MiB at
+  // 2 MiB granules): bounds the bytes a split copies.
+  constexpr std::size_t kMaxRunGranules = 32;
+
   // ADR-0007's allocator (reference: paged_kv_cache.h:88-227): one reserved
   // virtual range per tier, pages packed from slot 0 with no holes, physical
   // granules mapped only as far as the packed pages reach and given back as
@@ -172,10 +176,7 @@ namespace mi
     // Pages a tier holds: the slot the next allocation there takes.
     std::size_t held(int tier) const { return ranges_.at(tier).owners.size(); }
     std::size_t reserved_bytes(int tier) const { return ranges_.at(tier).reserved; }
-    std::size_t mapped_bytes(int tier) const
-    {
-      return ranges_.at(tier).granules.size() * granule_;
-    }
+    std::size_t mapped_bytes(int tier) const { return ranges_.at(tier).mapped * granule_; }
     void keep_spare_granules(int tier, std::size_t granules);
     std::size_t spare_granules(int tier) const { return ranges_.at(tier).spare; }
     std::size_t granule() const { return granule_; }
@@ -197,14 +198,26 @@ namespace mi
     void unwatch(PlacementObserver *o);
 
   private:
+    // Granules [first, first + count) of a range backed by one physical
+    // allocation, mapped by one call: the driver's unmap costs the same for
+    // a run of any length, so a range given back in runs costs a call a run,
+    // not a call a granule.
+    struct Run
+    {
+      std::size_t first;
+      std::size_t count;
+      hipMemGenericAllocationHandle_t handle;
+    };
     struct Range
     {
+      char *reservation = nullptr; // a guard granule, never mapped, then the range
       char *base = nullptr;
       std::size_t reserved = 0;
       std::size_t page_bytes = 0;
       std::size_t capacity = 0;
       std::vector<std::uint64_t> owners; // slot -> packed key
-      std::vector<hipMemGenericAllocationHandle_t> granules;
+      std::vector<Run> runs;             // in address order, from granule 0
+      std::size_t mapped = 0;            // granules the runs hold
       std::size_t spare = 0;
     };
     static void check_tier(int tier);
@@ -219,8 +232,21 @@ namespace mi
     }
     void release_keys(const std::vector<PageKey> &keys);
     void fit(Range &r, bool map_spares);
-    // Maps granules at the range's end until it has `count`; all or none.
+    // Maps granules at the range's end until it has `count`, in runs of at
+    // most kMaxRunGranules; all or none.
     void map_to(Range &r, std::size_t count);
+    // Gives back the granules from `keep` on: whole runs to the releaser;
+    // a run that `keep` cuts is replaced by a shorter one holding the same
+    // bytes (made at the scratch address, filled by a device copy, then
+    // mapped in its place), so exactly `keep` granules stay mapped.
+    void retract(Range &r, std::size_t keep);
+    void split_run(Range &r, std::size_t keep);
+    hipMemGenericAllocationHandle_t create_physical(std::size_t granules);
+    // Grants read and write over the range's first `granules` granules, and
+    // checks that granules [from, granules) have it.
+    void grant_access(Range &r, std::size_t from, std::size_t granules);
+    char *scratch_reservation_ = nullptr;
+    char *scratch_ = nullptr; // kMaxRunGranules of address space, for splits
     void tell_placed(std::uint64_t key, int tier, std::size_t slot);
     void tell_removed(std::uint64_t key);
 
