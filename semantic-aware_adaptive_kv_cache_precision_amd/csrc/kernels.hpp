@@ -51,16 +51,31 @@ namespace mi
     std::uint32_t to;
   };
 
+  // A launch's page pairs: in device memory (`pairs`), or, for a few, held
+  // in the launch's own arguments (`pairs` null), so that a small batch
+  // (a single move, a free's one tail move) uploads nothing first.
+  constexpr int kHeldRefs = 4;
+  struct RefList
+  {
+    const RefPair *pairs;
+    RefPair held[kHeldRefs];
+  };
+  // Pairs [first, first + count) of `host` as a RefList: held when count is
+  // at most kHeldRefs, else `uploaded` (where `host` was uploaded whole) +
+  // first.
+  RefList ref_list(const std::vector<RefPair> &host, std::size_t first, std::size_t count,
+                   const RefPair *uploaded);
+
   // Copies pair i's page from `from` to `to`: the destination space's page
   // size (an FP16 page when either side is a shadow). No copy may read
   // what another writes.
-  void launch_copy_refs(const RefPair *pairs, int count, const PageSpaces &spaces,
+  void launch_copy_refs(const RefList &pairs, int count, const PageSpaces &spaces,
                         hipStream_t stream);
   // Quantises pair i's FP16 page (a slot of the FP16 range, or a shadow) to
   // `tier` into its destination slot. head_dim 64 or 128, 32-token pages and
   // kv_heads * head_dim >= 128 take the register quantiser (a lane a task of
   // 64 elements, nothing staged); any other shape the LDS one.
-  void launch_requant_refs(const RefPair *pairs, int count, int tier, const PageSpaces &spaces,
+  void launch_requant_refs(const RefList &pairs, int count, int tier, const PageSpaces &spaces,
                            int page_tokens, int kv_heads, int head_dim, hipStream_t stream);
   // The register quantiser over pages named by address (launch_quantise_pages'
   // arguments): false, launching nothing, for a shape it does not take

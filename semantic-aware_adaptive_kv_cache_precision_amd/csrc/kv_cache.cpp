@@ -220,14 +220,15 @@ namespace mi
     allocator_.unwatch(this);
     try
     {
-      // Newest first, so that each free takes its tier's last page.
+      // Every page in one free: the ranges retract once, whole runs going.
+      std::vector<PageKey> held;
       for (int page = pages_ - 1; page >= 0; --page)
       {
         for (int layer = layers_ - 1; layer >= 0; --layer)
         {
           if (!evicted({layer, page}))
           {
-            allocator_.free({layer, page});
+            held.push_back({layer, page});
           }
         }
       }
@@ -237,13 +238,21 @@ namespace mi
         {
           for (int layer = layers_ - 1; layer >= 0; --layer)
           {
-            allocator_.free({layer, kOpenPages[k]});
+            held.push_back({layer, kOpenPages[k]});
           }
         }
       }
+      allocator_.free_pages(held);
     }
     catch (...)
     {
+    }
+    for (hipEvent_t e : move_events_)
+    {
+      if (e != nullptr)
+      {
+        (void)hipEventDestroy(e);
+      }
     }
   }
 
@@ -785,11 +794,26 @@ namespace mi
     PageSpaces spaces = allocator_.spaces();
     spaces.shadows = shadows_.device_table(stream);
     spaces.staging = staging_ ? reinterpret_cast<unsigned long long>(staging_->raw()) : 0;
-    const Clock::time_point device_began = Clock::now();
-    const RefPair *on_device = pairs_upload_.send(all, stream);
+    // A launch of a few pairs holds them in its arguments; the rest are
+    // uploaded together, once.
+    const bool upload = shadows_out.size() > kHeldRefs || restores.size() > kHeldRefs ||
+                        restage.size() > kHeldRefs ||
+                        std::any_of(requant.begin(), requant.end(),
+                                    [](const std::vector<RefPair> &r) { return r.size() > kHeldRefs; });
+    const RefPair *on_device = upload ? pairs_upload_.send(all, stream) : nullptr;
     std::size_t at = 0;
-    launch_copy_refs(on_device + at, static_cast<int>(shadows_out.size()), spaces, stream);
-    at += shadows_out.size();
+    const auto group = [&](std::size_t count) {
+      const RefList l = ref_list(all, at, count, on_device);
+      at += count;
+      return l;
+    };
+    if (shadow_seconds != nullptr)
+    {
+      ensure_move_events();
+      hip_check(hipEventRecord(move_events_[0], stream), "hipEventRecord before a move's copies");
+    }
+    launch_copy_refs(group(shadows_out.size()), static_cast<int>(shadows_out.size()), spaces,
+                     stream);
     phases_[0] = since(entered);
     const Clock::time_point allocating = Clock::now();
 
@@ -822,22 +846,16 @@ namespace mi
       throw;
     }
     phases_[1] = since(allocating);
-    launch_copy_refs(on_device + at, static_cast<int>(restores.size()), spaces, stream);
-    at += restores.size();
-    launch_copy_refs(on_device + at, static_cast<int>(restage.size()), spaces, stream);
-    at += restage.size();
+    launch_copy_refs(group(restores.size()), static_cast<int>(restores.size()), spaces, stream);
+    launch_copy_refs(group(restage.size()), static_cast<int>(restage.size()), spaces, stream);
     for (int t = kINT8; t <= kINT2; ++t)
     {
-      launch_requant_refs(on_device + at, static_cast<int>(requant[t].size()), t, spaces,
+      launch_requant_refs(group(requant[t].size()), static_cast<int>(requant[t].size()), t, spaces,
                           page_tokens_, kv_heads_, head_dim_, stream);
-      at += requant[t].size();
     }
     if (shadow_seconds != nullptr)
     {
-      // A single move reports what its shadow's trip over the host link
-      // took: the device work that reads or writes the shadow.
-      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize after a move's copies");
-      *shadow_seconds = touches_shadow ? since(device_began) : 0.0;
+      hip_check(hipEventRecord(move_events_[1], stream), "hipEventRecord after a move's copies");
     }
 
     // 3. The page table names the new pages; the old ones go together.
@@ -851,6 +869,26 @@ namespace mi
     allocator_.replace_pages(pairs);
     hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize after a batch");
     phases_[2] = since(finishing);
+    if (shadow_seconds != nullptr)
+    {
+      // A single move reports what its shadow's trip over the host link
+      // took: the device time of the work that reads or writes the shadow.
+      float ms = 0.0f;
+      hip_check(hipEventElapsedTime(&ms, move_events_[0], move_events_[1]),
+                "hipEventElapsedTime of a move's copies");
+      *shadow_seconds = touches_shadow ? ms * 1e-3 : 0.0;
+    }
+  }
+
+  void KVPages::ensure_move_events()
+  {
+    for (hipEvent_t &e : move_events_)
+    {
+      if (e == nullptr)
+      {
+        hip_check(hipEventCreate(&e), "hipEventCreate for a move's timing");
+      }
+    }
   }
 
   // ---- attention ---------------------------------------------------------------------

@@ -346,22 +346,6 @@ namespace mi
       r.reservation = static_cast<char *>(base);
       r.base = r.reservation + granule_;
     }
-    void *scratch = nullptr;
-    const hipError_t e = hipMemAddressReserve(&scratch, (kMaxRunGranules + 1) * granule_,
-                                              granule_, nullptr, 0);
-    if (e != hipSuccess)
-    {
-      for (Range &r : ranges_)
-      {
-        if (r.reservation != nullptr)
-        {
-          (void)hipMemAddressFree(r.reservation, r.reserved + granule_);
-        }
-      }
-      hip_check(e, "hipMemAddressReserve");
-    }
-    scratch_reservation_ = static_cast<char *>(scratch);
-    scratch_ = scratch_reservation_ + granule_;
   }
 
   PagedKVCache::~PagedKVCache()
@@ -385,10 +369,7 @@ namespace mi
         (void)hipMemAddressFree(r.reservation, r.reserved + granule_);
       }
     }
-    if (scratch_reservation_ != nullptr)
-    {
-      (void)hipMemAddressFree(scratch_reservation_, (kMaxRunGranules + 1) * granule_);
-    }
+    split_buffer_.reset();
     (void)hipGetLastError();
   }
 
@@ -584,7 +565,10 @@ namespace mi
     if (!copies.empty())
     {
       const hipStream_t stream = runtime_stream();
-      launch_copy_refs(moves_upload_.send(copies, stream), static_cast<int>(copies.size()),
+      const RefPair *uploaded =
+          copies.size() > static_cast<std::size_t>(kHeldRefs) ? moves_upload_.send(copies, stream)
+                                                              : nullptr;
+      launch_copy_refs(ref_list(copies, 0, copies.size(), uploaded), static_cast<int>(copies.size()),
                        spaces(), stream);
     }
     for (int t = 0; t < kTierCount; ++t)
@@ -745,54 +729,32 @@ namespace mi
     Run &run = r.runs.back();
     const std::size_t n = keep - run.first;
     char *at = r.base + run.first * granule_;
-    // Whatever reads or writes the run (the call's compaction copies, a
-    // launch still queued anywhere) is done (the caller synchronised): for a
-    // moment its addresses hold nothing.
+    // The caller synchronised the device: nothing reads or writes the run
+    // while, for a moment, its addresses hold nothing. The shorter run's
+    // memory is made first, so that a failure changes nothing.
     hipMemGenericAllocationHandle_t handle;
     try
     {
       handle = create_physical(n);
+      if (split_buffer_ == nullptr)
+      {
+        split_buffer_ = std::make_unique<DeviceBuffer>(kMaxRunGranules * granule_);
+      }
     }
-    catch (const OutOfMemory &)
+    catch (const std::exception &)
     {
       // No room for the shorter copy: the run stays whole, its granules
       // past `keep` mapped until the range next retracts.
       r.mapped = run.first + run.count;
       return;
     }
-    hipMemAccessDesc access{};
-    access.location = prop_.location;
-    access.flags = hipMemAccessFlagsProtReadWrite;
-    hipError_t e = hipMemMap(scratch_, n * granule_, 0, handle, 0);
-    if (e == hipSuccess)
-    {
-      // The scratch span has a guard granule before it, like the ranges.
-      e = hipMemSetAccess(scratch_, n * granule_, &access, 1);
-      unsigned long long flags = 0;
-      for (const std::size_t g : {std::size_t{0}, n - 1})
-      {
-        if (e == hipSuccess)
-        {
-          e = hipMemGetAccess(&flags, &prop_.location, scratch_ + g * granule_);
-          if (e == hipSuccess && flags != hipMemAccessFlagsProtReadWrite)
-          {
-            e = hipErrorInvalidValue;
-          }
-        }
-      }
-      if (e == hipSuccess)
-      {
-        e = hipMemcpy(scratch_, at, n * granule_, hipMemcpyDeviceToDevice);
-      }
-      const hipError_t unmapped = hipMemUnmap(scratch_, n * granule_);
-      e = e == hipSuccess ? unmapped : e;
-    }
+    hipError_t e = hipMemcpy(split_buffer_->raw(), at, n * granule_, hipMemcpyDeviceToDevice);
     if (e != hipSuccess)
     {
       (void)hipMemRelease(handle);
-      hip_check(e, "splitting a run of granules (the copy)");
+      hip_check(e, "hipMemcpy a split run's bytes out");
     }
-    // The old run goes; the copy takes its place at the same addresses.
+    // The old run goes; the new one takes its place at the same addresses.
     e = hipMemUnmap(at, run.count * granule_);
     if (e != hipSuccess)
     {
@@ -813,6 +775,8 @@ namespace mi
     run.count = n;
     r.mapped = keep;
     grant_access(r, run.first, keep);
+    hip_check(hipMemcpy(at, split_buffer_->raw(), n * granule_, hipMemcpyDeviceToDevice),
+              "hipMemcpy a split run's bytes back");
   }
 
   void PagedKVCache::retract(Range &r, std::size_t keep)

@@ -52,11 +52,26 @@ namespace mi
 
     // ---- batches by reference ------------------------------------------------
 
+    __device__ inline RefPair ref_at(const RefList &l, long long i)
+    {
+      if (l.pairs != nullptr)
+      {
+        return l.pairs[i];
+      }
+      RefPair p = l.held[0];
+#pragma unroll
+      for (int k = 1; k < kHeldRefs; ++k)
+      {
+        p = i == k ? l.held[k] : p;
+      }
+      return p;
+    }
+
     // Page blockIdx.y of the batch: the blocks of x stride over its bytes.
     __global__ void __launch_bounds__(kThreads)
-        copy_refs_kernel(const RefPair *__restrict__ pairs, PageSpaces s)
+        copy_refs_kernel(RefList pairs, int first, PageSpaces s)
     {
-      const RefPair p = pairs[blockIdx.y];
+      const RefPair p = ref_at(pairs, first + blockIdx.y);
       const auto *src = reinterpret_cast<const uint4 *>(resolve(s, p.from));
       auto *dst = reinterpret_cast<uint4 *>(resolve(s, p.to));
       const unsigned long long bytes = page_size(s, p.to);
@@ -78,8 +93,7 @@ namespace mi
     // is task (lane % W) of pair (lane / W).
     template <int Bits, int HD>
     __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
-        requant_refs_kernel(const RefPair *__restrict__ pairs, int count, PageSpaces s,
-                            PageLayout L, int kv_heads)
+        requant_refs_kernel(RefList pairs, int count, PageSpaces s, PageLayout L, int kv_heads)
     {
       const int W = kv_heads * HD;
       const long long lane = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
@@ -88,7 +102,7 @@ namespace mi
       {
         return; // whole waves: W is a multiple of 64
       }
-      const RefPair p = pairs[pair];
+      const RefPair p = ref_at(pairs, pair);
       const auto *src = reinterpret_cast<const std::uint16_t *>(resolve(s, p.from));
       std::uint8_t *dst = resolve(s, p.to);
       const Rows keys{src, src, kP, W};
@@ -129,11 +143,11 @@ namespace mi
     // staged whole (quant_core::quantise_in_lds).
     template <int Bits>
     __global__ void __launch_bounds__(kThreads)
-        requant_refs_lds_kernel(const RefPair *__restrict__ pairs, PageSpaces s, PageLayout L,
-                                int page_tokens, int kv_heads, int head_dim)
+        requant_refs_lds_kernel(RefList pairs, PageSpaces s, PageLayout L, int page_tokens,
+                                int kv_heads, int head_dim)
     {
       extern __shared__ uint4 lds_raw[];
-      const RefPair p = pairs[blockIdx.x];
+      const RefPair p = ref_at(pairs, blockIdx.x);
       const std::size_t half = static_cast<std::size_t>(page_tokens) * kv_heads * head_dim * 2;
       auto *in = reinterpret_cast<std::uint8_t *>(lds_raw);
       std::uint8_t *out = in + ((2 * half + 15) / 16) * 16;
@@ -335,29 +349,55 @@ namespace mi
 
   } // namespace
 
-  void launch_copy_refs(const RefPair *pairs, int count, const PageSpaces &spaces,
+  RefList ref_list(const std::vector<RefPair> &host, std::size_t first, std::size_t count,
+                   const RefPair *uploaded)
+  {
+    RefList l{};
+    if (count > static_cast<std::size_t>(kHeldRefs))
+    {
+      l.pairs = uploaded + first;
+      return l;
+    }
+    for (std::size_t i = 0; i < count; ++i)
+    {
+      l.held[i] = host[first + i];
+    }
+    return l;
+  }
+
+  void launch_copy_refs(const RefList &pairs, int count, const PageSpaces &spaces,
                         hipStream_t stream)
   {
     if (count <= 0)
     {
       return;
     }
+    if (pairs.pairs == nullptr && count > kHeldRefs)
+    {
+      throw InvalidArgument("a copy launch holds at most " + std::to_string(kHeldRefs) +
+                            " pairs in its arguments; got " + std::to_string(count));
+    }
     // Pages are tens of KiB: a few workgroups each, the batch in y.
     for (int first = 0; first < count; first += 65535)
     {
       const int n = std::min(65535, count - first);
-      hipLaunchKernelGGL(copy_refs_kernel, dim3(4, n), dim3(kThreads), 0, stream, pairs + first,
+      hipLaunchKernelGGL(copy_refs_kernel, dim3(4, n), dim3(kThreads), 0, stream, pairs, first,
                          spaces);
       hip_check(hipGetLastError(), "copy refs kernel launch");
     }
   }
 
-  void launch_requant_refs(const RefPair *pairs, int count, int tier, const PageSpaces &spaces,
+  void launch_requant_refs(const RefList &pairs, int count, int tier, const PageSpaces &spaces,
                            int page_tokens, int kv_heads, int head_dim, hipStream_t stream)
   {
     if (count <= 0)
     {
       return;
+    }
+    if (pairs.pairs == nullptr && count > kHeldRefs)
+    {
+      throw InvalidArgument("a requantise launch holds at most " + std::to_string(kHeldRefs) +
+                            " pairs in its arguments; got " + std::to_string(count));
     }
     const PageLayout L = page_layout(tier, page_tokens, kv_heads, head_dim);
     with_bits(tier, [&](auto bits) {

@@ -139,9 +139,9 @@ namespace mi
 
   class GranuleReleaser;
 
-  // The longest run of granules one physical allocation backs (64 MiB at
+  // The longest run of granules one physical allocation backs (32 MiB at
   // 2 MiB granules): bounds the bytes a split copies.
-  constexpr std::size_t kMaxRunGranules = 32;
+  constexpr std::size_t kMaxRunGranules = 16;
 
   // ADR-0007's allocator (reference: paged_kv_cache.h:88-227): one reserved
   // virtual range per tier, pages packed from slot 0 with no holes, physical
@@ -237,16 +237,15 @@ namespace mi
     void map_to(Range &r, std::size_t count);
     // Gives back the granules from `keep` on: whole runs to the releaser;
     // a run that `keep` cuts is replaced by a shorter one holding the same
-    // bytes (made at the scratch address, filled by a device copy, then
-    // mapped in its place), so exactly `keep` granules stay mapped.
+    // bytes (copied out to a device buffer and back), so exactly `keep`
+    // granules stay mapped.
     void retract(Range &r, std::size_t keep);
     void split_run(Range &r, std::size_t keep);
     hipMemGenericAllocationHandle_t create_physical(std::size_t granules);
     // Grants read and write over the range's first `granules` granules, and
     // checks that granules [from, granules) have it.
     void grant_access(Range &r, std::size_t from, std::size_t granules);
-    char *scratch_reservation_ = nullptr;
-    char *scratch_ = nullptr; // kMaxRunGranules of address space, for splits
+    std::unique_ptr<DeviceBuffer> split_buffer_; // a run's kept bytes during a split
     void tell_placed(std::uint64_t key, int tier, std::size_t slot);
     void tell_removed(std::uint64_t key);
 
@@ -582,6 +581,9 @@ namespace mi
     // The tier moves of a batch: validated already, every page held.
     void run_moves(const std::vector<PageKey> &keys, const std::vector<int> &from,
                    const std::vector<int> &targets, double *shadow_seconds);
+    // Two timing events around a single move's copies, made on first use.
+    void ensure_move_events();
+    hipEvent_t move_events_[2] = {nullptr, nullptr};
     double phases_[3] = {0.0, 0.0, 0.0}; // the last run_moves': prepare, allocate, finish
     void require_layer(int layer) const;
     std::size_t bytes_at(int tier) const;
