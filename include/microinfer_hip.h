@@ -385,6 +385,21 @@ int mi_kv_attention_at(mi_kv_pages *kv, int layer, const void *q, const void *k_
                        int heads, int kv_heads, int head_dim, const void *keys,
                        const void *values);
 int mi_kv_stored_on_device(mi_kv_pages *kv, int end);
+/* Beyond the reference: a decode row's RoPE and store as one launch, for a
+ * cache that does not seal (FP16 pages), where the reference makes three
+ * calls (rmsnorm.cu:87-109, rope.cu:57-68 and KVPages.store,
+ * kv_pages.h:161-180). qk holds q_heads then kv_heads rows of head_dim fp16;
+ * they are rotated into qk_out at *position with rope's angles, and the
+ * rotated k rows and `values` (kv_heads * head_dim fp16) are stored at that
+ * position of `layer`. When x is not NULL, the RMSNorm of that fp32 row of
+ * `hidden` values (weight norm_weight, eps) is written to `normed` in the
+ * same launch. The bits are those of mi_rmsnorm, mi_rope_from_table and
+ * mi_kv_store. The position must be reserved and below rope's positions
+ * (read when the kernel runs: outside the reserved positions nothing is
+ * stored). qk == qk_out is refused. */
+int mi_kv_rope_store(mi_kv_pages *kv, int layer, const void *qk, void *qk_out, int q_heads,
+                     const int32_t *position, mi_rope_table *rope, const void *values,
+                     const float *x, const void *norm_weight, void *normed, int hidden, float eps);
 
 /* ---- a whole decode step as one HIP graph (beyond the reference) ---------
  * The reference sequences a decode step from the host, a device call at a

@@ -1302,6 +1302,23 @@ int mi_kv_attention_at(mi_kv_pages *kv, int layer, const void *q, const void *k_
   });
 }
 
+int mi_kv_rope_store(mi_kv_pages *kv, int layer, const void *qk, void *qk_out, int q_heads,
+                     const int32_t *position, mi_rope_table *rope, const void *values,
+                     const float *x, const void *norm_weight, void *normed, int hidden, float eps)
+{
+  return guarded([&] {
+    need(kv, "kv");
+    need(position, "position");
+    need(rope, "rope");
+    if (qk == qk_out)
+    {
+      throw mi::InvalidArgument("rope cannot write over its input");
+    }
+    kv->impl.rope_store(layer, qk, qk_out, q_heads, position, rope->impl, values, x, norm_weight,
+                        normed, hidden, eps);
+  });
+}
+
 int mi_kv_stored_on_device(mi_kv_pages *kv, int end)
 {
   return guarded([&] {

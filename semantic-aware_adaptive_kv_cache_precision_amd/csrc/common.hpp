@@ -268,6 +268,52 @@ namespace mi
     return v;
   }
 
+  __device__ inline float widen_value(const float *x, std::size_t i) { return x[i]; }
+  __device__ inline float widen_value(const std::uint16_t *x, std::size_t i) { return h2f(x[i]); }
+
+  // 1 / RMS of one row, in the summation order every RMSNorm here shares
+  // (the standalone kernel, the decode step's fused norms, the row launch),
+  // so that their normed rows agree to the bit: lanes 0..255 each sum the
+  // squares of the elements i = lane (mod 256) in order, a wave adds its
+  // lanes by an xor butterfly, and the four wave sums are added in wave
+  // order (reference arithmetic: rmsnorm.cu:33-84, fp32 throughout).
+  // `partial` is four floats of LDS; every thread of the block calls it.
+  template <typename In>
+  __device__ inline float inv_rms(const In *x, int hidden, float eps, float *partial)
+  {
+    float acc = 0.0f;
+    if (threadIdx.x < 256)
+    {
+      for (int i = threadIdx.x; i < hidden; i += 256)
+      {
+        const float v = widen_value(x, i);
+        acc += v * v;
+      }
+    }
+    for (int offset = 32; offset > 0; offset >>= 1)
+    {
+      acc += __shfl_xor(acc, offset);
+    }
+    if (threadIdx.x < 256 && threadIdx.x % 64 == 0)
+    {
+      partial[threadIdx.x / 64] = acc;
+    }
+    __syncthreads();
+    const float total = ((partial[0] + partial[1]) + partial[2]) + partial[3];
+    return rsqrtf(total / static_cast<float>(hidden) + eps);
+  }
+
+  // One EWMA step of a page's importance score (reference:
+  // importance_scores.cu:31-50): `observed` is the heads' mean mass (summed
+  // in head order, then divided); the new score is alpha * observed +
+  // (1 - alpha) * old, each operation rounded once, and a page never
+  // observed (NaN) takes the observation.
+  __device__ inline float ewma_step(float old, float observed, float alpha)
+  {
+    return isnan(old) ? observed
+                      : __fadd_rn(__fmul_rn(alpha, observed), __fmul_rn(__fsub_rn(1.0f, alpha), old));
+  }
+
   // The group's scale (reference: quant.cu:44-56): its range over the
   // 2^bits - 1 steps, formed in fp64 and rounded to the nearest fp16, then
   // one fp16 ulp up if that fell short of the exact value, so that the last

@@ -1982,9 +1982,7 @@ namespace mi
           total = __fadd_rn(total, s_share[h][lane]);
         }
         const float observed = __fdiv_rn(total, static_cast<float>(a.heads));
-        scores[page] = isnan(old) ? observed
-                                  : __fadd_rn(__fmul_rn(a.alpha, observed),
-                                              __fmul_rn(__fsub_rn(1.0f, a.alpha), old));
+        scores[page] = ewma_step(old, observed, a.alpha);
       }
     }
 

@@ -169,6 +169,32 @@ namespace mi
     int head_dim;
   };
   void launch_rope_rows(const RopeRows &r, hipStream_t stream);
+  // One decode row's RMSNorm (x: one fp32 row, optional), the RoPE of its q
+  // and k heads (qk: q_heads then kv_heads rows of head_dim fp16) at
+  // *position with the table's angles, and the rotated k and the values
+  // stored in the layer's FP16 page at that position (pages: the layer's
+  // page addresses; positions outside [0, positions) store nothing).
+  struct RowPrep
+  {
+    const float *x;
+    const std::uint16_t *norm_weight;
+    std::uint16_t *normed;
+    int hidden;
+    float eps;
+    const std::uint16_t *qk;
+    std::uint16_t *qk_out;
+    int q_heads;
+    int kv_heads;
+    int head_dim;
+    const std::int32_t *position;
+    const float *table;
+    int table_positions;
+    const std::uint16_t *values;
+    const unsigned long long *pages;
+    int page_tokens;
+    int positions;
+  };
+  void launch_row_prep(const RowPrep &r, hipStream_t stream);
   void launch_rmsnorm(const void *x, bool x_is_f32, const void *weight, void *out, int rows,
                       int hidden, float eps, hipStream_t stream);
   void launch_swiglu(const void *gate, const void *up, void *out, std::size_t count,

@@ -1173,6 +1173,51 @@ namespace mi
     attend_open_[layer] = current_open_[layer];
   }
 
+  void KVPages::rope_store(int layer, const void *qk, void *qk_out, int q_heads,
+                           const int *position, const RopeTable &rope, const void *values,
+                           const float *x, const void *norm_weight, void *normed, int hidden,
+                           float eps)
+  {
+    require_layer(layer);
+    if (seals_)
+    {
+      throw LogicError("the row launch stores into FP16 pages; this cache seals its pages");
+    }
+    if (rope.head_dim() != head_dim_ || rope.data() == nullptr)
+    {
+      throw InvalidArgument("the RoPE table is for head_dim " + std::to_string(rope.head_dim()) +
+                            " with " + std::to_string(rope.positions()) +
+                            " positions; the cache's head_dim is " + std::to_string(head_dim_));
+    }
+    if (q_heads < 0 || qk == nullptr || qk_out == nullptr || values == nullptr ||
+        (x != nullptr && (norm_weight == nullptr || normed == nullptr || hidden <= 0)))
+    {
+      throw InvalidArgument("the row launch needs q and k rows, their output, the values and, "
+                            "with x, the norm weight, its output and a positive hidden size");
+    }
+    const hipStream_t stream = runtime_stream();
+    sync_tables(stream);
+    RowPrep r{};
+    r.x = x;
+    r.norm_weight = static_cast<const std::uint16_t *>(norm_weight);
+    r.normed = static_cast<std::uint16_t *>(normed);
+    r.hidden = hidden;
+    r.eps = eps;
+    r.qk = static_cast<const std::uint16_t *>(qk);
+    r.qk_out = static_cast<std::uint16_t *>(qk_out);
+    r.q_heads = q_heads;
+    r.kv_heads = kv_heads_;
+    r.head_dim = head_dim_;
+    r.position = position;
+    r.table = rope.data();
+    r.table_positions = rope.positions();
+    r.values = static_cast<const std::uint16_t *>(values);
+    r.pages = table_.addresses() + static_cast<std::size_t>(layer) * table_.stride();
+    r.page_tokens = page_tokens_;
+    r.positions = capacity_tokens();
+    launch_row_prep(r, stream);
+  }
+
   StepStore KVPages::step_store(int layer, const void *keys, const void *values,
                                 const int *position)
   {

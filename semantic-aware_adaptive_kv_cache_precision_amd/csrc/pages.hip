@@ -16,37 +16,47 @@ namespace mi
   namespace
   {
 
-    // Copy page blockIdx.y: `units` of Unit from from[y] to to[y], the
-    // blocks of x striding over them (reference: page_copy.cu:25-37).
+    // The bytes a workgroup of the page copy moves: 256 threads, four
+    // 16-byte units each.
+    constexpr std::size_t kCopyChunk = 256 * 4 * 16;
+
+    // A batch of page copies (from[p] to to[p], `units` of Unit each):
+    // workgroup x copies chunk x % chunks of page first + x / chunks, a Unit
+    // a thread a pass over the chunk.
     template <typename Unit>
-    __global__ void copy_pages_kernel(const void *const *__restrict__ from,
-                                      void *const *__restrict__ to, std::size_t units, int first)
+    __global__ void __launch_bounds__(256)
+        copy_pages_kernel(const void *const *__restrict__ from, void *const *__restrict__ to,
+                          std::size_t units, std::size_t chunks, int first)
     {
-      const auto *src = static_cast<const Unit *>(from[first + blockIdx.y]);
-      auto *dst = static_cast<Unit *>(to[first + blockIdx.y]);
-      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-           i < units; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+      constexpr std::size_t kChunkUnits = kCopyChunk / sizeof(Unit);
+      const std::size_t page = first + blockIdx.x / chunks;
+      const std::size_t begin = (blockIdx.x % chunks) * kChunkUnits;
+      const std::size_t end = begin + kChunkUnits < units ? begin + kChunkUnits : units;
+      const Unit *src = static_cast<const Unit *>(from[page]);
+      Unit *dst = static_cast<Unit *>(to[page]);
+      for (std::size_t i = begin + threadIdx.x; i < end; i += 256)
       {
         dst[i] = src[i];
       }
     }
 
-    // One thread per fp16 element of the n rows: token i / row at position
-    // start + i / row (reference: kv_pages.cu:26-43).
+    // Rows start .. start + n of one layer into its FP16 pages (pages: the
+    // layer's page addresses; a page holds page_tokens key rows, then as many
+    // value rows): workgroup y takes row y, its threads the row's channels.
     __global__ void store_pages_kernel(const std::uint16_t *__restrict__ keys,
                                        const std::uint16_t *__restrict__ values,
                                        const unsigned long long *__restrict__ pages,
-                                       int page_tokens, std::size_t row, int start,
-                                       std::size_t count)
+                                       int page_tokens, int width, int start)
     {
-      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-           i < count; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+      const int position = start + static_cast<int>(blockIdx.y);
+      auto *page = reinterpret_cast<std::uint16_t *>(pages[position / page_tokens]);
+      std::uint16_t *k_row = page + static_cast<std::size_t>(position % page_tokens) * width;
+      std::uint16_t *v_row = k_row + static_cast<std::size_t>(page_tokens) * width;
+      const std::size_t from = static_cast<std::size_t>(blockIdx.y) * width;
+      for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < width; c += gridDim.x * blockDim.x)
       {
-        const int position = start + static_cast<int>(i / row);
-        auto *page = reinterpret_cast<std::uint16_t *>(pages[position / page_tokens]);
-        std::uint16_t *key = page + static_cast<std::size_t>(position % page_tokens) * row + i % row;
-        key[0] = keys[i];
-        key[static_cast<std::size_t>(page_tokens) * row] = values[i];
+        k_row[c] = keys[from + c];
+        v_row[c] = values[from + c];
       }
     }
 
@@ -59,25 +69,25 @@ namespace mi
       }
     }
 
-    // One thread per page (reference: importance_scores.cu:31-50). The
-    // library is built with -ffp-contract=off, so nothing below fuses.
+    // The fold of one layer's page masses (heads rows of `pages`) into its
+    // scores: a thread a page, the heads' masses added in head order, their
+    // mean, then ewma_step. The library is built with -ffp-contract=off, so
+    // nothing here fuses.
     __global__ void fold_kernel(float *__restrict__ scores, const float *__restrict__ mass,
                                 int heads, int pages, float alpha)
     {
-      for (int page = blockIdx.x * blockDim.x + threadIdx.x; page < pages;
-           page += gridDim.x * blockDim.x)
+      const int page = blockIdx.x * blockDim.x + threadIdx.x;
+      if (page >= pages)
       {
-        float total = 0.0f;
-        for (int h = 0; h < heads; ++h)
-        {
-          total = __fadd_rn(total, mass[static_cast<std::size_t>(h) * pages + page]);
-        }
-        const float observed = __fdiv_rn(total, static_cast<float>(heads));
-        const float old = scores[page];
-        scores[page] = isnan(old) ? observed
-                                  : __fadd_rn(__fmul_rn(alpha, observed),
-                                              __fmul_rn(__fsub_rn(1.0f, alpha), old));
+        return;
       }
+      float total = 0.0f;
+      const float *column = mass + page;
+      for (int h = 0; h < heads; ++h, column += pages)
+      {
+        total = __fadd_rn(total, *column);
+      }
+      scores[page] = ewma_step(scores[page], __fdiv_rn(total, static_cast<float>(heads)), alpha);
     }
 
     int grid_for(std::size_t count, int threads, int cap = 65536)
@@ -98,18 +108,18 @@ namespace mi
     {
       return;
     }
-    const int threads = 256;
     const auto go = [&](auto unit) {
       using Unit = decltype(unit);
       const std::size_t units = bytes / sizeof(Unit);
-      // A few workgroups a page: a page is tens of KiB, and a batch holds
-      // thousands, so the grid fills the device either way.
-      const int blocks = static_cast<int>(std::min<std::size_t>((units + threads - 1) / threads, 8));
-      for (int first = 0; first < count; first += kMaxGridY)
+      const std::size_t chunks = (bytes + kCopyChunk - 1) / kCopyChunk;
+      // A launch's x dimension holds 2^31 - 1 workgroups.
+      const int per_launch = static_cast<int>(std::min<std::size_t>(
+          count, std::max<std::size_t>(1, 0x7fffffffULL / chunks)));
+      for (int first = 0; first < count; first += per_launch)
       {
-        const int n = std::min(kMaxGridY, count - first);
-        hipLaunchKernelGGL(copy_pages_kernel<Unit>, dim3(blocks, n), dim3(threads), 0, stream,
-                           from, to, units, first);
+        const int n = std::min(per_launch, count - first);
+        hipLaunchKernelGGL(copy_pages_kernel<Unit>, dim3(static_cast<unsigned>(n * chunks)),
+                           dim3(256), 0, stream, from, to, units, chunks, first);
         hip_check(hipGetLastError(), "copy pages kernel launch");
       }
     };
@@ -128,15 +138,20 @@ namespace mi
   void launch_store_pages(const void *keys, const void *values, const unsigned long long *pages,
                           int page_tokens, std::size_t row, int start, int n, hipStream_t stream)
   {
-    const std::size_t count = static_cast<std::size_t>(n) * row;
-    if (count == 0)
+    if (n <= 0 || row == 0)
     {
       return;
     }
-    hipLaunchKernelGGL(store_pages_kernel, dim3(grid_for(count, 256)), dim3(256), 0, stream,
-                       static_cast<const std::uint16_t *>(keys),
-                       static_cast<const std::uint16_t *>(values), pages, page_tokens, row, start,
-                       count);
+    const int threads = 256;
+    const int blocks_x = static_cast<int>((row + threads - 1) / threads);
+    for (int first = 0; first < n; first += kMaxGridY)
+    {
+      const int rows = std::min(kMaxGridY, n - first);
+      hipLaunchKernelGGL(store_pages_kernel, dim3(blocks_x, rows), dim3(threads), 0, stream,
+                         static_cast<const std::uint16_t *>(keys) + static_cast<std::size_t>(first) * row,
+                         static_cast<const std::uint16_t *>(values) + static_cast<std::size_t>(first) * row,
+                         pages, page_tokens, static_cast<int>(row), start + first);
+    }
     hip_check(hipGetLastError(), "store pages kernel launch");
   }
 
@@ -158,7 +173,7 @@ namespace mi
     {
       return;
     }
-    hipLaunchKernelGGL(fold_kernel, dim3(grid_for(pages, 256)), dim3(256), 0, stream, scores, mass,
+    hipLaunchKernelGGL(fold_kernel, dim3((pages + 255) / 256), dim3(256), 0, stream, scores, mass,
                        heads, pages, alpha);
     hip_check(hipGetLastError(), "fold kernel launch");
   }

@@ -20,6 +20,7 @@ namespace mi
 {
   namespace
   {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
     __device__ inline void rope_angle(double position, int j, int head_dim, double theta,
                                       double *s, double *c)
@@ -28,36 +29,53 @@ namespace mi
       sincos(position * inv_freq, s, c);
     }
 
-    // One workgroup per (token, head); a lane per rotation pair.
+    // Rotates pair j of the row at `row` (channels j and j + half) by the
+    // angle whose fp32 cosine and sine are cs, writing the fp16 results to
+    // `out` (and to `also`, where given): each product and difference
+    // rounded in fp32, then to fp16 (reference arithmetic: rope.cu:32-54).
+    __device__ inline void rotate_pair(const std::uint16_t *row, int j, int half, float2 cs,
+                                       std::uint16_t *out, std::uint16_t *also = nullptr)
+    {
+      const float x1 = h2f(row[j]);
+      const float x2 = h2f(row[j + half]);
+      const std::uint16_t lo = __half_as_ushort(__float2half(x1 * cs.x - x2 * cs.y));
+      const std::uint16_t hi = __half_as_ushort(__float2half(x2 * cs.x + x1 * cs.y));
+      out[j] = lo;
+      out[j + half] = hi;
+      if (also != nullptr)
+      {
+        also[j] = lo;
+        also[j + half] = hi;
+      }
+    }
+
+    // RoPE with the angle formed per pair in fp64: a thread a rotation pair
+    // of every (token, head) row, the grid striding over them.
     __global__ void rope_kernel(const std::uint16_t *__restrict__ x,
                                 const std::int32_t *__restrict__ positions,
                                 std::uint16_t *__restrict__ out, int heads, int head_dim,
-                                double theta)
+                                double theta, std::size_t pairs)
     {
-      const int token = blockIdx.x / heads;
-      const std::size_t base = static_cast<std::size_t>(blockIdx.x) * head_dim;
       const int half = head_dim / 2;
-      const double pos = static_cast<double>(positions[token]);
-      for (int j = threadIdx.x; j < half; j += blockDim.x)
+      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+           i < pairs; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
       {
+        const std::size_t row = i / half;
+        const int j = static_cast<int>(i % half);
         double s, c;
-        rope_angle(pos, j, head_dim, theta, &s, &c);
-        const float sf = static_cast<float>(s);
-        const float cf = static_cast<float>(c);
-        const float x1 = h2f(x[base + j]);
-        const float x2 = h2f(x[base + j + half]);
-        out[base + j] = __half_as_ushort(__float2half(x1 * cf - x2 * sf));
-        out[base + j + half] = __half_as_ushort(__float2half(x2 * cf + x1 * sf));
+        rope_angle(static_cast<double>(positions[row / heads]), j, head_dim, theta, &s, &c);
+        const std::size_t base = row * head_dim;
+        rotate_pair(x + base, j, half, make_float2(static_cast<float>(c), static_cast<float>(s)),
+                    out + base);
       }
     }
 
     // RoPE of up to two row sets (a chunk's q and k) with the angles read
     // from a RopeTable ({cos, sin} in fp32 per (position, j), filled by
     // rope_table_kernel from the same double-precision angle rope_kernel
-    // forms): a thread a rotation pair, the rotation the RoPE kernel's fp32
-    // arithmetic, so the rows are rope_kernel's to the bit. A position past
-    // the table reads its last row (the launcher's caller covers every
-    // position first).
+    // forms): a thread a rotation pair, the rotation rope_kernel's, so the
+    // rows are its to the bit. A position past the table reads its last row
+    // (the launcher's caller covers every position first).
     __global__ void rope_rows_kernel(RopeRows r)
     {
       const int half = r.head_dim / 2;
@@ -75,12 +93,8 @@ namespace mi
         const float2 cs = *reinterpret_cast<const float2 *>(
             r.table + 2 * (static_cast<std::size_t>(position) * half + j));
         const std::size_t base = row * r.head_dim;
-        const auto *x = static_cast<const std::uint16_t *>(r.x[set]);
-        auto *out = static_cast<std::uint16_t *>(r.out[set]);
-        const float x1 = h2f(x[base + j]);
-        const float x2 = h2f(x[base + j + half]);
-        out[base + j] = __half_as_ushort(__float2half(x1 * cs.x - x2 * cs.y));
-        out[base + j + half] = __half_as_ushort(__float2half(x2 * cs.x + x1 * cs.y));
+        rotate_pair(static_cast<const std::uint16_t *>(r.x[set]) + base, j, half, cs,
+                    static_cast<std::uint16_t *>(r.out[set]) + base);
       }
     }
 
@@ -121,93 +135,145 @@ namespace mi
       }
     }
 
-    __device__ inline float widen(const std::uint16_t *x, std::size_t i)
+    // x * scale * w for the row's elements, one fp16 rounding each, eight a
+    // thread through 16-byte stores where the row allows, else one.
+    template <typename In>
+    __device__ inline void normed_row(const In *x, const std::uint16_t *w, std::uint16_t *out,
+                                      int hidden, float scale)
     {
-      return h2f(x[i]);
+      const bool wide = hidden % 8 == 0 && (reinterpret_cast<std::uintptr_t>(out) |
+                                            reinterpret_cast<std::uintptr_t>(w)) % 16 == 0;
+      if (wide)
+      {
+        for (int r = threadIdx.x; r < hidden / 8; r += blockDim.x)
+        {
+          const u32x4 wv = *reinterpret_cast<const u32x4 *>(w + 8 * r);
+          u32x4 o;
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+          {
+            const float a = widen_value(x, 8 * r + 2 * k) * scale * h2f(static_cast<std::uint16_t>(wv[k]));
+            const float b =
+                widen_value(x, 8 * r + 2 * k + 1) * scale * h2f(static_cast<std::uint16_t>(wv[k] >> 16));
+            o[k] = static_cast<unsigned>(__half_as_ushort(__float2half(a))) |
+                   (static_cast<unsigned>(__half_as_ushort(__float2half(b))) << 16);
+          }
+          *reinterpret_cast<u32x4 *>(out + 8 * r) = o;
+        }
+        return;
+      }
+      for (int i = threadIdx.x; i < hidden; i += blockDim.x)
+      {
+        out[i] = __half_as_ushort(__float2half(widen_value(x, i) * scale * h2f(w[i])));
+      }
     }
-    __device__ inline float widen(const float *x, std::size_t i) { return x[i]; }
 
+    // RMSNorm: a 256-thread workgroup a row, the scale by inv_rms.
     template <typename In>
     __global__ void __launch_bounds__(256)
         rmsnorm_kernel(const In *__restrict__ x, const std::uint16_t *__restrict__ weight,
                        std::uint16_t *__restrict__ out, int hidden, float eps)
     {
-      __shared__ float partial[256 / 64];
-      __shared__ float scale;
+      __shared__ float partial[4];
       const std::size_t row = static_cast<std::size_t>(blockIdx.x) * hidden;
-      float acc = 0.0f;
-      for (int i = threadIdx.x; i < hidden; i += blockDim.x)
+      const float scale = inv_rms(x + row, hidden, eps, partial);
+      normed_row(x + row, weight, out + row, hidden, scale);
+    }
+
+    // One decode row's work that precedes its attention, as one launch:
+    // workgroup 0 the RMSNorm of r.x (when given); the rest a thread a
+    // rotation pair of the q and k heads at *position (angles from the
+    // table), the k heads' rotated pairs also written into the layer's FP16
+    // page at that position, then a thread a value channel into the page's
+    // value row. A position outside [0, r.positions) stores nothing.
+    __global__ void __launch_bounds__(256) row_prep_kernel(RowPrep r)
+    {
+      int block = blockIdx.x;
+      if (r.x != nullptr)
       {
-        const float v = widen(x, row + i);
-        acc += v * v;
-      }
-      for (int offset = warpSize / 2; offset > 0; offset /= 2)
-      {
-        acc += __shfl_xor(acc, offset);
-      }
-      const int wave = threadIdx.x / warpSize;
-      if (threadIdx.x % warpSize == 0)
-      {
-        partial[wave] = acc;
-      }
-      __syncthreads();
-      if (threadIdx.x == 0)
-      {
-        float total = 0.0f;
-        for (int w = 0; w < static_cast<int>(blockDim.x / warpSize); ++w)
+        if (block == 0)
         {
-          total += partial[w];
+          __shared__ float partial[4];
+          const float scale = inv_rms(r.x, r.hidden, r.eps, partial);
+          normed_row(r.x, r.norm_weight, r.normed, r.hidden, scale);
+          return;
         }
-        scale = rsqrtf(total / static_cast<float>(hidden) + eps);
+        --block;
       }
-      __syncthreads();
-      for (int i = threadIdx.x; i < hidden; i += blockDim.x)
+      const int half = r.head_dim / 2;
+      const int width = r.kv_heads * r.head_dim;
+      const int pairs = (r.q_heads + r.kv_heads) * half;
+      const int i = block * 256 + static_cast<int>(threadIdx.x);
+      const int position = *r.position;
+      const bool stored = position >= 0 && position < r.positions;
+      std::uint16_t *page = nullptr;
+      if (stored)
       {
-        const float v = widen(x, row + i) * scale * h2f(weight[i]);
-        out[row + i] = __half_as_ushort(__float2half(v));
+        page = reinterpret_cast<std::uint16_t *>(r.pages[position / r.page_tokens]) +
+               static_cast<std::size_t>(position % r.page_tokens) * width;
+      }
+      if (i < pairs)
+      {
+        const int head = i / half;
+        const int j = i % half;
+        const int at = min(max(position, 0), r.table_positions - 1);
+        const float2 cs =
+            *reinterpret_cast<const float2 *>(r.table + 2 * (static_cast<std::size_t>(at) * half + j));
+        const std::size_t base = static_cast<std::size_t>(head) * r.head_dim;
+        std::uint16_t *key_row =
+            stored && head >= r.q_heads ? page + (head - r.q_heads) * r.head_dim : nullptr;
+        rotate_pair(r.qk + base, j, half, cs, r.qk_out + base, key_row);
+      }
+      else if (i < pairs + width && stored)
+      {
+        const int c = i - pairs;
+        page[static_cast<std::size_t>(r.page_tokens) * width + c] = r.values[c];
       }
     }
 
+    // SiLU(g) * u of one fp16 pair (reference arithmetic: swiglu.cu:26-38):
+    // g / (1 + e^-g) and the product in fp32, one rounding to fp16.
+    __device__ inline std::uint16_t swiglu_value(std::uint16_t g, std::uint16_t u)
+    {
+      const float gf = h2f(g);
+      const float silu = gf / (1.0f + expf(-gf));
+      return __half_as_ushort(__float2half(silu * h2f(u)));
+    }
+
+    // SwiGLU over `count` values: with Wide, eight a thread through 16-byte
+    // loads and stores for the first count / 8 * 8 and one a thread for the
+    // rest; else one a thread throughout.
+    template <bool Wide>
     __global__ void swiglu_kernel(const std::uint16_t *__restrict__ gate,
                                   const std::uint16_t *__restrict__ up,
                                   std::uint16_t *__restrict__ out, std::size_t count)
     {
+      const std::size_t groups = Wide ? count / 8 : 0;
+      const std::size_t items = groups + (count - 8 * groups);
       for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-           i < count; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+           i < items; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
       {
-        const float g = h2f(gate[i]);
-        const float silu = g / (1.0f + expf(-g));
-        out[i] = __half_as_ushort(__float2half(silu * h2f(up[i])));
-      }
-    }
-
-    // The same, eight values a thread through 16-byte loads and stores.
-    __global__ void swiglu8_kernel(const uint4 *__restrict__ gate, const uint4 *__restrict__ up,
-                                   uint4 *__restrict__ out, std::size_t groups)
-    {
-      for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-           i < groups; i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
-      {
-        const uint4 gw = gate[i];
-        const uint4 uw = up[i];
-        const unsigned gs[4] = {gw.x, gw.y, gw.z, gw.w};
-        const unsigned us[4] = {uw.x, uw.y, uw.z, uw.w};
-        unsigned os[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
+        if (i < groups)
         {
-          unsigned word = 0;
+          const u32x4 g = *reinterpret_cast<const u32x4 *>(gate + 8 * i);
+          const u32x4 u = *reinterpret_cast<const u32x4 *>(up + 8 * i);
+          u32x4 o;
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
+          for (int k = 0; k < 4; ++k)
           {
-            const float g = h2f(static_cast<std::uint16_t>(gs[k] >> (16 * h)));
-            const float silu = g / (1.0f + expf(-g));
-            const float u = h2f(static_cast<std::uint16_t>(us[k] >> (16 * h)));
-            word |= static_cast<unsigned>(__half_as_ushort(__float2half(silu * u))) << (16 * h);
+            o[k] = static_cast<unsigned>(swiglu_value(static_cast<std::uint16_t>(g[k]),
+                                                      static_cast<std::uint16_t>(u[k]))) |
+                   (static_cast<unsigned>(swiglu_value(static_cast<std::uint16_t>(g[k] >> 16),
+                                                       static_cast<std::uint16_t>(u[k] >> 16)))
+                    << 16);
           }
-          os[k] = word;
+          *reinterpret_cast<u32x4 *>(out + 8 * i) = o;
         }
-        out[i] = uint4{os[0], os[1], os[2], os[3]};
+        else
+        {
+          const std::size_t e = 8 * groups + (i - groups);
+          out[e] = swiglu_value(gate[e], up[e]);
+        }
       }
     }
 
@@ -236,10 +302,25 @@ namespace mi
     {
       return;
     }
-    hipLaunchKernelGGL(rope_kernel, dim3(seq * heads), dim3(64), 0, stream,
+    const std::size_t pairs = static_cast<std::size_t>(seq) * heads * (head_dim / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0, stream,
                        static_cast<const std::uint16_t *>(x), positions,
-                       static_cast<std::uint16_t *>(out), heads, head_dim, theta);
+                       static_cast<std::uint16_t *>(out), heads, head_dim, theta, pairs);
     hip_check(hipGetLastError(), "rope kernel launch");
+  }
+
+  void launch_row_prep(const RowPrep &r, hipStream_t stream)
+  {
+    if (r.head_dim <= 0 || r.head_dim % 2 != 0 || r.table == nullptr || r.table_positions <= 0 ||
+        r.q_heads < 0 || r.kv_heads <= 0 || r.page_tokens <= 0 || r.pages == nullptr)
+    {
+      throw InvalidArgument("the row launch takes an even head_dim, a filled RoPE table and the "
+                            "layer's pages");
+    }
+    const int items = (r.q_heads + r.kv_heads) * (r.head_dim / 2) + r.kv_heads * r.head_dim;
+    const int blocks = (items + 255) / 256 + (r.x != nullptr ? 1 : 0);
+    hipLaunchKernelGGL(row_prep_kernel, dim3(blocks), dim3(256), 0, stream, r);
+    hip_check(hipGetLastError(), "row prep kernel launch");
   }
 
   void launch_rope_rows(const RopeRows &r, hipStream_t stream)
@@ -317,19 +398,19 @@ namespace mi
     const auto aligned = [](const void *p) {
       return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0;
     };
-    if (count % 8 == 0 && aligned(gate) && aligned(up) && aligned(out))
+    const auto *g = static_cast<const std::uint16_t *>(gate);
+    const auto *u = static_cast<const std::uint16_t *>(up);
+    auto *o = static_cast<std::uint16_t *>(out);
+    if (aligned(gate) && aligned(up) && aligned(out))
     {
-      const std::size_t groups = count / 8;
-      hipLaunchKernelGGL(swiglu8_kernel, dim3(grid_for(groups, 256)), dim3(256), 0, stream,
-                         static_cast<const uint4 *>(gate), static_cast<const uint4 *>(up),
-                         static_cast<uint4 *>(out), groups);
+      const std::size_t items = count / 8 + count % 8;
+      hipLaunchKernelGGL(swiglu_kernel<true>, dim3(grid_for(items, 256)), dim3(256), 0, stream, g,
+                         u, o, count);
     }
     else
     {
-      hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(count, 256)), dim3(256), 0, stream,
-                         static_cast<const std::uint16_t *>(gate),
-                         static_cast<const std::uint16_t *>(up), static_cast<std::uint16_t *>(out),
-                         count);
+      hipLaunchKernelGGL(swiglu_kernel<false>, dim3(grid_for(count, 256)), dim3(256), 0, stream, g,
+                         u, o, count);
     }
     hip_check(hipGetLastError(), "swiglu kernel launch");
   }

@@ -505,6 +505,16 @@ namespace mi
     // the positions before `end` were stored.
     void prepare_step(int max_seq_k, int heads, int head_dim);
     void store_step(int layer, const void *keys, const void *values, const int *position);
+    // For a cache that does not seal (FP16 pages throughout): one decode
+    // row's RoPE (qk: q_heads then kv_heads rows of head_dim fp16, rotated
+    // into qk_out at *position with `rope`'s angles) and its store at that
+    // position (the rotated k heads and `values`), with the RMSNorm of an
+    // independent fp32 row (x, when not null) in the same launch: the bits
+    // of launch_rmsnorm, launch_rope_rows and store for that row. The
+    // position must be reserved and covered by the table.
+    void rope_store(int layer, const void *qk, void *qk_out, int q_heads, const int *position,
+                    const RopeTable &rope, const void *values, const float *x,
+                    const void *norm_weight, void *normed, int hidden, float eps);
     // The layer's store target for a step whose projection writes its row
     // (launch_qkv_step): the open page (the step's row goes there unless it
     // is the page's last) and the page table row for the seal; `keys` and

@@ -75,37 +75,6 @@ namespace mi
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef const __attribute__((address_space(1))) f32x4 *g_f32x4;
 
-    // RMSNorm's scale of the residual row, summed as the RMSNorm kernel sums
-    // it (256 lanes, each over its stride, a wave reduction, the four waves
-    // in order), so that the normed row is that kernel's to the bit.
-    __device__ inline float norm_scale(const float *x, int hidden, float eps, float *partial)
-    {
-      float acc = 0.0f;
-      if (threadIdx.x < 256)
-      {
-        for (int i = threadIdx.x; i < hidden; i += 256)
-        {
-          const float v = x[i];
-          acc += v * v;
-        }
-      }
-      for (int offset = 32; offset > 0; offset >>= 1)
-      {
-        acc += __shfl_xor(acc, offset);
-      }
-      if (threadIdx.x < 256 && threadIdx.x % 64 == 0)
-      {
-        partial[threadIdx.x / 64] = acc;
-      }
-      __syncthreads();
-      float total = 0.0f;
-      for (int w = 0; w < 4; ++w)
-      {
-        total += partial[w];
-      }
-      return rsqrtf(total / static_cast<float>(hidden) + eps);
-    }
-
     // Run r (eight values) of RMSNorm of the residual: x * scale * w, one
     // rounding to fp16, as the RMSNorm kernel stores it.
     __device__ inline u32x4 normed_run(const float *residual, const std::uint16_t *weight,
@@ -241,7 +210,7 @@ namespace mi
       }
       else if (p.norm_weight != nullptr)
       {
-        const float scale = norm_scale(p.residual, p.in, p.eps, s_partial);
+        const float scale = inv_rms(p.residual, p.in, p.eps, s_partial);
         for (int r = threadIdx.x; r < runs; r += kBlockThreads)
         {
           x_lds[r] = normed_run(p.residual, p.norm_weight, scale, r);
@@ -436,7 +405,7 @@ namespace mi
       {
         load(item);
       }
-      const float scale = norm_scale(p.residual, p.in, p.eps, s_partial);
+      const float scale = inv_rms(p.residual, p.in, p.eps, s_partial);
       for (int r = threadIdx.x; r < runs; r += kBlockThreads)
       {
         x_lds[r] = normed_run(p.residual, p.norm_weight, scale, r);

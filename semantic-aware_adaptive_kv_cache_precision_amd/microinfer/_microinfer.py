@@ -78,6 +78,7 @@ SIGNATURES = {
     "mi_kv_store_at": ((_vp, _i, _vp, _vp, _vp), C.c_int),
     "mi_kv_attention_at": ((_vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp), C.c_int),
     "mi_kv_stored_on_device": ((_vp, _i), C.c_int),
+    "mi_kv_rope_store": ((_vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f), C.c_int),
     "mi_decode_step_create": ((C.POINTER(_vp), _vp, C.POINTER(_ModelShape), _vp, _vp, _vp,
                                C.POINTER(_LayerWeights), _vp, _i), C.c_int),
     "mi_decode_step_destroy": ((_vp,), C.c_int),
@@ -1102,6 +1103,35 @@ class KVPages:
                                       seq_k.address, max_seq_k, heads, kv_heads, head_dim,
                                       _need(_span(keys), width, "keys"),
                                       _need(_span(values), width, "values")))
+
+    def rope_store(self, layer: int, qk, qk_out, q_heads: int, position: DeviceIndex,
+                   rope: "RopeTable", values, norm=None) -> None:
+        """Beyond the reference's surface, for a cache that does not seal: a
+        decode row's RoPE and store in one launch. qk holds q_heads then
+        kv_heads rows of head_dim; they are rotated into qk_out at the
+        position held in device memory (rope's angles), and the rotated k
+        rows and `values` are stored there. norm = (x, weight, out, eps)
+        adds the RMSNorm of the fp32 row x to the same launch. The bits of
+        rmsnorm_f32, rope_from_table and store."""
+        width = self.kv_width
+        rows = q_heads * rope.head_dim + width
+        qa = _need(_span(qk), rows, "qk")
+        oa = _need(_span(qk_out), rows, "qk_out")
+        if qa == oa:
+            raise ValueError("rope cannot write over its input")
+        if position.count < 1:
+            raise ValueError("the position holds no value")
+        xa = wa = na = None
+        hidden, eps = 0, 0.0
+        if norm is not None:
+            x, weight, out, eps = norm
+            hidden = x.numel
+            xa = x.address
+            wa = _need(_span(weight), hidden, "norm weight")
+            na = _need(_span(out), hidden, "normed")
+        _check(lib.mi_kv_rope_store(self._h, layer, qa, oa, q_heads, position.address, rope._h,
+                                    _need(_span(values), width, "values"), xa, wa, na, hidden,
+                                    float(eps)))
 
     def stored_on_device(self, end: int) -> None:
         """Records that the positions before `end` were stored by store_at."""

@@ -142,7 +142,8 @@ def test_rope_rmsnorm_swiglu_are_the_float64_references():
         want = pointwise.rope(x, pos, 1e6)
         ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
         assert np.all(np.abs(got - want) <= 2 * ulp + 1e-6 * np.abs(x).max())
-    for hidden in (896, 2048):
+    # Eight values a thread (hidden a multiple of 8) and one a thread (1001).
+    for hidden in (896, 2048, 1001):
         announce("rmsnorm", hidden)
         x = fp16_exact(rng.standard_normal((3, hidden)))
         w = fp16_exact(rng.uniform(0.5, 1.5, hidden))

@@ -190,6 +190,64 @@ def test_decode_over_a_cache_that_does_not_seal_is_the_oracle():
                           "paged mass")
 
 
+def test_the_row_launch_is_rmsnorm_rope_and_store_to_the_bit():
+    """rope_store (config 2's row work as one launch) against the three
+    calls it replaces on a twin cache: the normed row, the rotated q and k
+    and every page byte agree to the bit, at the 0.5B and 1.5B head shapes,
+    mid-page, at a page's last row and its first; a position past the
+    reserved ones rotates but stores nothing. The three calls are held to
+    the float64 references by the pointwise and decode tests."""
+    m = mi()
+    d = m.device
+    for heads, kv, hd, hidden, positions in ((14, 2, 64, 896, (100, 127, 128)),
+                                             (12, 2, 128, 1536, (33, 63))):
+        rng = np.random.default_rng(hd)
+        rope = d.RopeTable(hd, 1e6)
+        rope.cover(4096)
+        seq = 160
+        k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+        (alloc_a, a), (alloc_b, b) = pages_for(32, kv, hd, 0), pages_for(32, kv, hd, 0)
+        for cache in (a, b):
+            store_in_runs(cache, 1, k, v, [seq])
+        norm_w = put(rng.uniform(0.5, 1.5, hidden))
+        for pos in positions + (seq,):
+            announce("row launch", heads, kv, hd, pos)
+            x = d.upload_f32(rng.standard_normal(hidden).astype(np.float32))
+            raw = put(normal(rng, heads + kv, hd))
+            vals = put(normal(rng, kv, hd))
+            at = d.DeviceIndex([pos])
+            rows = (heads + kv) * hd
+            # The three calls.
+            n_a, qk_a = d.empty(hidden), d.empty(rows)
+            d.rmsnorm_f32(x, norm_w, n_a, 1, hidden, 1e-6)
+            d.rope_from_table(raw, at, rope, qk_a, 1, heads + kv, hd)
+            if pos < seq:
+                a.store(1, d.view(qk_a, heads * hd, kv * hd), vals, pos, 1)
+            # The one launch.
+            n_b, qk_b = d.empty(hidden), d.empty(rows)
+            b.rope_store(1, raw, qk_b, heads, at, rope, vals, norm=(x, norm_w, n_b, 1e-6))
+            np.testing.assert_array_equal(n_b.to_numpy(), n_a.to_numpy())
+            np.testing.assert_array_equal(qk_b.to_numpy(), qk_a.to_numpy())
+            for page in range(seq // 32):
+                np.testing.assert_array_equal(alloc_b.read(1, page), alloc_a.read(1, page))
+        # Without the norm: the rows alone, and layer 0 left as it was.
+        before = alloc_b.read(0, 1)
+        raw = put(normal(rng, heads + kv, hd))
+        qk_a, qk_b = d.empty((heads + kv) * hd), d.empty((heads + kv) * hd)
+        at = d.DeviceIndex([40])
+        d.rope_from_table(raw, at, rope, qk_a, 1, heads + kv, hd)
+        b.rope_store(1, raw, qk_b, heads, at, rope, put(normal(rng, kv, hd)))
+        np.testing.assert_array_equal(qk_b.to_numpy(), qk_a.to_numpy())
+        np.testing.assert_array_equal(alloc_b.read(0, 1), before)
+    # A cache that seals refuses it.
+    _, sealing = pages_for(32, 2, 64, 1)
+    rope = d.RopeTable(64, 1e6)
+    rope.cover(64)
+    with pytest.raises(Exception, match="seals"):
+        sealing.rope_store(0, put(np.zeros(16 * 64)), d.empty(16 * 64), 14, d.DeviceIndex([0]),
+                           rope, put(np.zeros(128)))
+
+
 def test_asking_for_the_mass_changes_no_output_bit():
     for P in (16, 32):
         for tier in (0, 2):
