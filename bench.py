@@ -215,6 +215,19 @@ def decode_legs(m, shape, context, layers, steps, warmup):
     log(f"per-layer, fold once: {ms * 1e3:.1f} us/token, {step_bytes / ms / 1e6:.0f} GB/s")
     out["kept"] = ms
 
+    # The floor of the headline's structure, live: a graph of as many
+    # dependent launches (2 a layer and the fold), each writing one float.
+    dummy = d.empty_f32(1)
+    launches = 2 * layers + 1
+
+    def empty_launches():
+        for _ in range(launches):
+            m._check(m.lib.mi_fill_f32(dummy.address, 1, 0.0, None))
+
+    out["launch_floor"] = timed_graph(m, stream, empty_launches, steps, warmup) / launches
+    log(f"dependent launch floor: {out['launch_floor'] * 1e3:.2f} us a launch, "
+        f"{out['launch_floor'] * launches * 1e3:.1f} us for the headline's {launches}")
+
     # The fold fused into each layer's combine.
     outs_fused = [d.empty(heads * hd) for _ in range(layers)]
     scores_fused = d.ImportanceScores(layers, context // P)
@@ -1221,8 +1234,12 @@ def main() -> int:
                          "one_launch": leg_gbs(times["one_launch"]),
                          "key_bias_on": leg_gbs(times["bias"])},
             "one_launch_vs_per_layer_gap": round(times["one_launch_gap"], 6),
+            "dependent_launch_floor_us": round(times["launch_floor"] * 1e3, 3),
+            "per_layer_launch_floor_us_per_token": round(
+                times["launch_floor"] * 1e3 * (2 * shape.layers + 1), 1),
             "note": "same bytes; the one launch takes every layer's query at once, not the "
-                    "per-layer decode order"},
+                    "per-layer decode order; the launch floor is a graph of as many dependent "
+                    "one-float launches as the headline's (2 a layer + the fold), timed live"},
         "decode_by_tier": tier_rows,
         "config2": c2,
         "decode_step": steps_out,

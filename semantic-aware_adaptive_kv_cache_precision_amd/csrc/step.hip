@@ -184,14 +184,25 @@ namespace mi
       const auto up_weights = [&](int row) {
         return Two ? p.seg[1].w + static_cast<std::size_t>(row) * p.in : nullptr;
       };
-      // The wave's first row's runs, before the input.
+      // The wave's first row's runs, and with Pipe its second's, before the
+      // input.
       int g = blockIdx.x * kSlots + slot;
       u32x4 a[Ahead], b[Ahead];
+      u32x4 na[Pipe ? Ahead : 1], nb[Pipe ? Ahead : 1];
       if (g < total)
       {
         int seg, row;
         const std::uint16_t *w0 = row_weights(g, seg, row);
         load_part<Ahead, Two>(a, b, w0, up_weights(row), begin, end, lane);
+      }
+      if constexpr (Pipe)
+      {
+        if (g + stride < total)
+        {
+          int nseg, nrow;
+          const std::uint16_t *w0 = row_weights(g + stride, nseg, nrow);
+          load_part<Ahead, Two>(na, nb, w0, up_weights(nrow), begin, end, lane);
+        }
       }
       // A row split over waves reads x (no RMSNorm) straight from global
       // memory, a lane its own runs, with the weights: staging a long input
@@ -227,25 +238,16 @@ namespace mi
       }
       float best = -FLT_MAX;
       int at = INT_MAX;
-      // Every wave of the workgroup takes the same number of turns (the
-      // parts of a row meet at a barrier); a slot past the rows idles.
-      for (int base = blockIdx.x * kSlots; base < total; base += stride, g += stride)
-      {
+      // One turn: the row g the registers (wa, wb) hold, its dot (the parts
+      // of a split row meet at a barrier), its output; then wa and wb take
+      // the row `ahead` turns on (the next, or with Pipe the one after: the
+      // other buffer holds the next, in flight meanwhile).
+      const auto turn = [&](u32x4 (&wa)[Ahead], u32x4 (&wb)[Ahead], int ahead) {
         const bool live = g < total;
         int seg = 0, row = 0;
         if (live)
         {
           row = locate(p, Two, g, seg);
-        }
-        u32x4 na[Pipe ? Ahead : 1], nb[Pipe ? Ahead : 1];
-        if constexpr (Pipe)
-        {
-          if (g + stride < total)
-          {
-            int nseg, nrow;
-            const std::uint16_t *w0 = row_weights(g + stride, nseg, nrow);
-            load_part<Ahead, Two>(na, nb, w0, up_weights(nrow), begin, end, lane);
-          }
         }
         float acc0 = 0.0f, acc1 = 0.0f;
         if (live)
@@ -265,10 +267,10 @@ namespace mi
               {
                 xv = x_lds[r];
               }
-              acc0 = dot_run(a[i], xv, acc0);
+              acc0 = dot_run(wa[i], xv, acc0);
               if constexpr (Two)
               {
-                acc1 = dot_run(b[i], xv, acc1);
+                acc1 = dot_run(wb[i], xv, acc1);
               }
             }
           }
@@ -290,32 +292,20 @@ namespace mi
           }
           __syncthreads();
         }
-        if constexpr (Pipe)
-        {
-#pragma unroll
-          for (int i = 0; i < Ahead; ++i)
-          {
-            a[i] = na[i];
-            if constexpr (Two)
-            {
-              b[i] = nb[i];
-            }
-          }
-        }
-        else if (g + stride < total)
+        if (g + ahead * stride < total)
         {
           int nseg, nrow;
-          const std::uint16_t *w0 = row_weights(g + stride, nseg, nrow);
-          load_part<Ahead, Two>(a, b, w0, up_weights(nrow), begin, end, lane);
+          const std::uint16_t *w0 = row_weights(g + ahead * stride, nseg, nrow);
+          load_part<Ahead, Two>(wa, wb, w0, up_weights(nrow), begin, end, lane);
         }
         if (!live || part != 0)
         {
-          continue;
+          return;
         }
         if (lane != 0)
         {
           keep_better(best, at, dot, row);
-          continue;
+          return;
         }
         const ProjectSegment &sg = p.seg[seg];
         switch (p.mode)
@@ -345,6 +335,28 @@ namespace mi
           break;
         }
         keep_better(best, at, dot, row);
+      };
+      // Every wave of the workgroup takes the same number of turns (the
+      // parts of a row meet at a barrier); a slot past the rows idles. With
+      // Pipe the two buffers alternate, so that a turn waits only for its
+      // own row.
+      for (int base = blockIdx.x * kSlots; base < total; base += stride, g += stride)
+      {
+        if constexpr (Pipe)
+        {
+          turn(a, b, 2);
+          base += stride;
+          g += stride;
+          if (base >= total)
+          {
+            break;
+          }
+          turn(na, nb, 2);
+        }
+        else
+        {
+          turn(a, b, 1);
+        }
       }
       if (p.mode == ProjectMode::kLogits)
       {

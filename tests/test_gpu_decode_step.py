@@ -302,8 +302,11 @@ def test_one_step_at_full_model_widths_takes_the_real_gemv_variants(name):
     per-block bests reduced right over every block of the resident grid).
     The shapes reach the GEMV variants the real steps run, and the test
     asserts that they did: the down projection's long input split over four
-    waves a row, read as it comes; gate/up and the head on the device's
-    resident grid, each wave taking several rows with the next in flight."""
+    waves a row, read as it comes; the head (and Qwen's gate/up, 8,960 rows
+    of pairs) on the device's resident grid, each wave taking several rows
+    with the next in flight; Llama's gate/up (8,192) a row a wave in one
+    grid where the device holds that many workgroups, else on the resident
+    grid."""
     from microinfer import workloads as w
     shape = w.SHAPES[name]
     s = dict(w.model_dict(shape), layers=2)
@@ -316,12 +319,18 @@ def test_one_step_at_full_model_widths_takes_the_real_gemv_variants(name):
     assert plans["output"]["split"] == 1
     assert plans["down"]["n_in"] == shape.intermediate and plans["down"]["split"] == 4
     assert not plans["down"]["pipelined"]
-    assert plans["gate_up"]["rows"] == shape.intermediate and plans["gate_up"]["pipelined"]
+    gate_up = plans["gate_up"]
+    assert gate_up["rows"] == shape.intermediate
+    assert gate_up["pipelined"] or name.startswith("llama")
     head = plans["head"]
     assert head["rows"] == shape.vocab and head["pipelined"]
-    # The resident grid: fewer workgroups than a row a wave would need.
+    # The resident grid: fewer workgroups than a row a wave would need; one
+    # grid: a row a wave.
     assert head["blocks"] * head["waves"] < shape.vocab
-    assert plans["gate_up"]["blocks"] * plans["gate_up"]["waves"] < shape.intermediate
+    if gate_up["pipelined"]:
+        assert gate_up["blocks"] * gate_up["waves"] < shape.intermediate
+    else:
+        assert gate_up["blocks"] * gate_up["waves"] == shape.intermediate
 
 
 @pytest.mark.skip(reason="its process ended in a host segmentation fault in an object finalizer at "
