@@ -649,14 +649,17 @@ def quantise_batches(m, stream, steps, warmup, seed=4, single_launch_graphs=Fals
 def link_rates(m, nbytes=256 << 20, reps=3):
     """The host link as the moves use it, GB/s: DMA copies between device
     memory and pinned host memory each way, and the page-copy kernel writing
-    into pinned host memory mapped for the device (how shadows are taken)."""
+    into pinned host memory mapped for the device (how shadows are taken)
+    and reading from it (how a restore brings them back)."""
     host = m.HostBuffer(nbytes)
     arena = m.DeviceArena(nbytes)
-    best = {"d2h_dma": 0.0, "h2d_dma": 0.0, "d2h_kernel": 0.0}
+    best = {"d2h_dma": 0.0, "h2d_dma": 0.0, "d2h_kernel": 0.0, "h2d_kernel": 0.0}
     page = 32768
     count = nbytes // page
     to_host = m.PageCopy([arena.address + i * page for i in range(count)],
                          [host.address + i * page for i in range(count)], page)
+    from_host = m.PageCopy([host.address + i * page for i in range(count)],
+                           [arena.address + i * page for i in range(count)], page)
     for _ in range(reps):
         for name, kind in (("d2h_dma", 1), ("h2d_dma", 0)):
             m.synchronize()
@@ -665,12 +668,13 @@ def link_rates(m, nbytes=256 << 20, reps=3):
                 (arena.address, host.array.ctypes.data)
             m._check(m.lib.mi_memcpy(dst, src, nbytes, kind))
             best[name] = max(best[name], nbytes / (time.perf_counter() - t0) / 1e9)
-        timer = m.Timer()
-        timer.start()
-        to_host.launch()
-        timer.stop()
-        m.synchronize()
-        best["d2h_kernel"] = max(best["d2h_kernel"], nbytes / (timer.elapsed_ms() * 1e-3) / 1e9)
+        for name, copy in (("d2h_kernel", to_host), ("h2d_kernel", from_host)):
+            timer = m.Timer()
+            timer.start()
+            copy.launch()
+            timer.stop()
+            m.synchronize()
+            best[name] = max(best[name], nbytes / (timer.elapsed_ms() * 1e-3) / 1e9)
     return {k: round(v, 2) for k, v in best.items()}
 
 

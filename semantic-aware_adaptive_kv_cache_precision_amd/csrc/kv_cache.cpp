@@ -779,8 +779,8 @@ namespace mi
     std::vector<RefPair> all;
     all.reserve(2 * n);
     all.insert(all.end(), shadows_out.begin(), shadows_out.end());
-    all.insert(all.end(), restores.begin(), restores.end());
     all.insert(all.end(), restage.begin(), restage.end());
+    all.insert(all.end(), restores.begin(), restores.end());
     for (const auto &r : requant)
     {
       all.insert(all.end(), r.begin(), r.end());
@@ -812,8 +812,11 @@ namespace mi
       ensure_move_events();
       hip_check(hipEventRecord(move_events_[0], stream), "hipEventRecord before a move's copies");
     }
+    // Shadows out, and the shadows that restores quantise from brought into
+    // device staging: neither needs the new pages.
     launch_copy_refs(group(shadows_out.size()), static_cast<int>(shadows_out.size()), spaces,
                      stream);
+    launch_copy_refs(group(restage.size()), static_cast<int>(restage.size()), spaces, stream);
     phases_[0] = since(entered);
     const Clock::time_point allocating = Clock::now();
 
@@ -847,7 +850,6 @@ namespace mi
     }
     phases_[1] = since(allocating);
     launch_copy_refs(group(restores.size()), static_cast<int>(restores.size()), spaces, stream);
-    launch_copy_refs(group(restage.size()), static_cast<int>(restage.size()), spaces, stream);
     for (int t = kINT8; t <= kINT2; ++t)
     {
       launch_requant_refs(group(requant[t].size()), static_cast<int>(requant[t].size()), t, spaces,

@@ -647,9 +647,10 @@ namespace mi
 
   void PagedKVCache::map_to(Range &r, std::size_t count)
   {
-    // The new granules in runs of up to kMaxRunGranules, each one physical
-    // allocation mapped by one call; access is then granted in one call
-    // over the range from its base.
+    // A run the tail cut still holds its granules: those are counted back
+    // first. Then the new granules in runs of up to kMaxRunGranules, each
+    // one physical allocation mapped by one call; access is then granted in
+    // one call over the range from its base.
     const std::size_t first_run = r.runs.size();
     const std::size_t first = r.mapped;
     const auto undo = [&]() {
@@ -664,6 +665,8 @@ namespace mi
     };
     try
     {
+      r.mapped = std::max(r.mapped, std::min(count, r.runs_end()));
+      const std::size_t held = r.mapped;
       while (r.mapped < count)
       {
         const std::size_t n = std::min(count - r.mapped, kMaxRunGranules);
@@ -680,9 +683,9 @@ namespace mi
         r.runs.push_back({r.mapped, n, handle});
         r.mapped += n;
       }
-      if (r.mapped > first)
+      if (r.mapped > held)
       {
-        grant_access(r, first, r.mapped);
+        grant_access(r, held, r.mapped);
       }
     }
     catch (...)
@@ -743,9 +746,8 @@ namespace mi
     }
     catch (const std::exception &)
     {
-      // No room for the shorter copy: the run stays whole, its granules
-      // past `keep` mapped until the range next retracts.
-      r.mapped = run.first + run.count;
+      // No room for the shorter copy: the run stays whole and cut, its
+      // granules past `keep` given back when a later settle can make it.
       return;
     }
     hipError_t e = hipMemcpy(split_buffer_->raw(), at, n * granule_, hipMemcpyDeviceToDevice);
@@ -786,26 +788,39 @@ namespace mi
     {
       const Run &run = r.runs.back();
       going.push_back({r.base + run.first * granule_, run.count * granule_, run.handle});
-      r.mapped -= run.count;
       r.runs.pop_back();
     }
-    if (r.mapped > keep)
-    {
-      // A run that `keep` cuts is remapped now, and access granted over the
-      // range: the runs past it are unmapped first, here, once the launches
-      // that may read them (this call's compaction copies) are done.
-      hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize before a run is split");
-      for (const GranuleReleaser::Retired &run : going)
-      {
-        hip_check(hipMemUnmap(run.at, run.bytes), "hipMemUnmap a run given up");
-        hip_check(hipMemRelease(run.handle), "hipMemRelease a run given up");
-      }
-      split_run(r, keep);
-      return;
-    }
+    // A run that `keep` cuts stays whole (its bytes past `keep` are past
+    // the tail) until settle_cuts; the granules are no longer counted.
+    r.mapped = std::min(r.mapped, keep);
     // Whole runs go off the caller's path, once the launches queued so far
     // (which may read them) are done.
     releaser_->retire(std::move(going), runtime_stream());
+  }
+
+  void PagedKVCache::settle_cuts()
+  {
+    bool cut = false;
+    for (const Range &r : ranges_)
+    {
+      cut = cut || r.runs_end() > r.mapped;
+    }
+    if (!cut)
+    {
+      return;
+    }
+    // Nothing may read or write a cut run while, for a moment, its
+    // addresses hold nothing; and access is granted over a range only once
+    // nothing is mapped past it (the runs given up are unmapped first).
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize before a cut run is settled");
+    releaser_->wait_for(nullptr);
+    for (Range &r : ranges_)
+    {
+      if (r.runs_end() > r.mapped)
+      {
+        split_run(r, r.mapped);
+      }
+    }
   }
 
   void PagedKVCache::fit(Range &r, bool map_spares)
@@ -841,7 +856,11 @@ namespace mi
     fit(r, true);
   }
 
-  void PagedKVCache::drain_releases() { releaser_->wait_for(nullptr); }
+  void PagedKVCache::drain_releases()
+  {
+    releaser_->wait_for(nullptr);
+    settle_cuts();
+  }
 
   std::vector<PageKey> PagedKVCache::pages(int tier) const
   {

@@ -181,7 +181,8 @@ namespace mi
     std::size_t spare_granules(int tier) const { return ranges_.at(tier).spare; }
     std::size_t granule() const { return granule_; }
     std::uint64_t generation() const { return generation_; }
-    // Waits until every granule given up so far is back with the driver.
+    // Waits until every granule given up so far is back with the driver
+    // (a run the tail cut is settled here).
     void drain_releases();
     // Valid until the next allocator operation: for the cache's own launches.
     char *address(PageKey key, std::size_t bytes) const;
@@ -217,8 +218,12 @@ namespace mi
       std::size_t capacity = 0;
       std::vector<std::uint64_t> owners; // slot -> packed key
       std::vector<Run> runs;             // in address order, from granule 0
-      std::size_t mapped = 0;            // granules the runs hold
+      // Granules the range counts as mapped. The last run may reach past
+      // them: a run the tail cut, whose granules past `mapped` are given
+      // back when the cut is settled (or counted back by the next growth).
+      std::size_t mapped = 0;
       std::size_t spare = 0;
+      std::size_t runs_end() const { return runs.empty() ? 0 : runs.back().first + runs.back().count; }
     };
     static void check_tier(int tier);
     // The location word kept per key: tier in the top byte, slot below.
@@ -235,11 +240,15 @@ namespace mi
     // Maps granules at the range's end until it has `count`, in runs of at
     // most kMaxRunGranules; all or none.
     void map_to(Range &r, std::size_t count);
-    // Gives back the granules from `keep` on: whole runs to the releaser;
-    // a run that `keep` cuts is replaced by a shorter one holding the same
-    // bytes (copied out to a device buffer and back), so exactly `keep`
-    // granules stay mapped.
+    // Gives back the granules from `keep` on: whole runs to the releaser; a
+    // run that `keep` cuts stays whole until the cut is settled, its
+    // granules past `keep` no longer counted.
     void retract(Range &r, std::size_t keep);
+    // Settles every range's cut: the run is replaced by a shorter one
+    // holding the same bytes (copied out to a device buffer and back), so
+    // that exactly the counted granules stay mapped. Synchronises the
+    // device first; a range whose shorter run cannot be made stays cut.
+    void settle_cuts();
     void split_run(Range &r, std::size_t keep);
     hipMemGenericAllocationHandle_t create_physical(std::size_t granules);
     // Grants read and write over the range's first `granules` granules, and
