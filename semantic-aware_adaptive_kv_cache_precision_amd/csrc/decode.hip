@@ -499,7 +499,10 @@ namespace mi
 #pragma unroll
         for (int e = 0; e < 8; ++e)
         {
-          const float ab = static_cast<float>(q1[e]) * y1[e] + static_cast<float>(q2[e]) * y2[e];
+          // Two mixed-precision fmas, q read as fp16 (q2 y2 rounded once,
+          // as a product is).
+          const float ab = __builtin_fmaf(static_cast<float>(q1[e]), y1[e],
+                                          __builtin_fmaf(static_cast<float>(q2[e]), y2[e], 0.0f));
           _Float16 hi, lo;
           split_half(ab, hi, lo);
           ab_hi[e] = hi;
