@@ -75,6 +75,25 @@ namespace mi
   // `tier` into its destination slot. head_dim 64 or 128, 32-token pages and
   // kv_heads * head_dim >= 128 take the register quantiser (a lane a task of
   // 64 elements, nothing staged); any other shape the LDS one.
+  // One page's move as one launch (one workgroup): the page's FP16 bytes to
+  // its shadow (shadow.from -> shadow.to) when has_shadow, the page at its
+  // new tier (page.from, FP16 rows, -> page.to: the register quantiser at
+  // `tier`), then, after a barrier, the compaction copies of the tier the
+  // page left, which may overwrite what came before them. It applies to a
+  // move from FP16 at a shape the register quantiser takes
+  // (move_one_applies); anything else takes the separate launches.
+  struct OneMove
+  {
+    RefPair shadow;
+    RefPair page;
+    RefPair compact[kHeldRefs];
+    int has_shadow;
+    int tier;
+    int compact_count;
+  };
+  bool launch_move_one(const OneMove &m, const PageSpaces &spaces, int page_tokens, int kv_heads,
+                       int head_dim, hipStream_t stream);
+  bool move_one_applies(int from, int tier, int page_tokens, int kv_heads, int head_dim);
   void launch_requant_refs(const RefList &pairs, int count, int tier, const PageSpaces &spaces,
                            int page_tokens, int kv_heads, int head_dim, hipStream_t stream);
   // The register quantiser over pages named by address (launch_quantise_pages'

@@ -692,9 +692,108 @@ namespace mi
                               phases_[0], phases_[1], phases_[2]};
   }
 
+  bool KVPages::run_one_move(PageKey key, int from, int target, double *shadow_seconds)
+  {
+    if (!move_one_applies(from, target, page_tokens_, kv_heads_, head_dim_))
+    {
+      return false;
+    }
+    const hipStream_t stream = runtime_stream();
+    const bool first_downgrade = from == kFP16 && !shadows_.contains(key);
+    shadows_.reserve(first_downgrade ? 1 : 0);
+    // The page's FP16 rows (the page itself, or its shadow) and, before its
+    // first downgrade, its shadow's place.
+    const std::size_t shadows_before = shadows_.count();
+    OneMove m{};
+    m.page.from = allocator_.ref_of(key);
+    if (first_downgrade)
+    {
+      m.has_shadow = 1;
+      m.shadow = {m.page.from, page_ref(kShadowSpace, shadows_.add(key))};
+    }
+    m.tier = target;
+    // The new page at the target tier's tail, under a staging key; a page
+    // that landed anywhere else is refused before the device names it.
+    const PageKey staged{key.layer, kBatchStagingPage};
+    m.page.to = page_ref(target, static_cast<std::uint32_t>(allocator_.held(target)));
+    try
+    {
+      allocator_.allocate_run({staged}, target, false);
+      if (allocator_.ref_of(staged) != m.page.to)
+      {
+        allocator_.free(staged);
+        throw LogicError("a staged page did not land in the slot its move named");
+      }
+    }
+    catch (...)
+    {
+      shadows_.truncate(shadows_before);
+      throw;
+    }
+    PageSpaces spaces = allocator_.spaces();
+    spaces.shadows = shadows_.device_table(stream);
+    // The page table names the new page and the old one goes; its tier's
+    // compaction copies ride in the move's launch, after the reads of the
+    // old page, and the granules that tier gives up are released after it.
+    std::vector<RefPair> compaction;
+    allocator_.defer_copies(&compaction);
+    try
+    {
+      allocator_.replace_pages({{key, staged}});
+    }
+    catch (...)
+    {
+      allocator_.finish_deferred();
+      throw;
+    }
+    may_be_at_[target] = true;
+    const std::size_t held = std::min<std::size_t>(compaction.size(), kHeldRefs);
+    m.compact_count = static_cast<int>(held);
+    for (std::size_t i = 0; i < held; ++i)
+    {
+      m.compact[i] = compaction[i];
+    }
+    try
+    {
+      ensure_move_events();
+      hip_check(hipEventRecord(move_events_[0], stream), "hipEventRecord before a move");
+      launch_move_one(m, spaces, page_tokens_, kv_heads_, head_dim_, stream);
+      hip_check(hipEventRecord(move_events_[1], stream), "hipEventRecord after a move");
+      if (compaction.size() > held)
+      {
+        // More than a launch holds (never for one free): the rest after it.
+        const std::vector<RefPair> rest(compaction.begin() + held, compaction.end());
+        const RefPair *up = rest.size() > kHeldRefs ? pairs_upload_.send(rest, stream) : nullptr;
+        launch_copy_refs(ref_list(rest, 0, rest.size(), up), static_cast<int>(rest.size()),
+                         spaces, stream);
+      }
+    }
+    catch (...)
+    {
+      allocator_.finish_deferred();
+      throw;
+    }
+    allocator_.finish_deferred();
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize after a move");
+    if (shadow_seconds != nullptr)
+    {
+      // The launch that takes the shadow also makes the page: its device
+      // time, when it takes one.
+      float ms = 0.0f;
+      hip_check(hipEventElapsedTime(&ms, move_events_[0], move_events_[1]),
+                "hipEventElapsedTime of a move");
+      *shadow_seconds = first_downgrade ? ms * 1e-3 : 0.0;
+    }
+    return true;
+  }
+
   void KVPages::run_moves(const std::vector<PageKey> &keys, const std::vector<int> &from,
                           const std::vector<int> &targets, double *shadow_seconds)
   {
+    if (keys.size() == 1 && run_one_move(keys[0], from[0], targets[0], shadow_seconds))
+    {
+      return;
+    }
     const hipStream_t stream = runtime_stream();
     const std::size_t n = keys.size();
     const Clock::time_point entered = Clock::now();

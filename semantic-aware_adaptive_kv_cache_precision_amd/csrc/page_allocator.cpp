@@ -562,7 +562,11 @@ namespace mi
       tell_removed(w);
     }
     ++generation_;
-    if (!copies.empty())
+    if (!copies.empty() && deferred_copies_ != nullptr)
+    {
+      deferred_copies_->insert(deferred_copies_->end(), copies.begin(), copies.end());
+    }
+    else if (!copies.empty())
     {
       const hipStream_t stream = runtime_stream();
       const RefPair *uploaded =
@@ -793,8 +797,29 @@ namespace mi
     // A run that `keep` cuts stays whole (its bytes past `keep` are past
     // the tail) until settle_cuts; the granules are no longer counted.
     r.mapped = std::min(r.mapped, keep);
+    if (deferred_copies_ != nullptr)
+    {
+      // The caller's launch may still read them: released after it.
+      for (const GranuleReleaser::Retired &run : going)
+      {
+        deferred_runs_.push_back({run.at, run.bytes, run.handle});
+      }
+      return;
+    }
     // Whole runs go off the caller's path, once the launches queued so far
     // (which may read them) are done.
+    releaser_->retire(std::move(going), runtime_stream());
+  }
+
+  void PagedKVCache::finish_deferred()
+  {
+    deferred_copies_ = nullptr;
+    std::vector<GranuleReleaser::Retired> going;
+    for (const HeldRun &run : deferred_runs_)
+    {
+      going.push_back({run.at, run.bytes, run.handle});
+    }
+    deferred_runs_.clear();
     releaser_->retire(std::move(going), runtime_stream());
   }
 

@@ -112,6 +112,56 @@ namespace mi
                           Emit::kCodes);
     }
 
+    // A workgroup's copy of one page's bytes (16 bytes a thread a pass, then
+    // any last bytes one by one).
+    // A workgroup's copy of one page's bytes (16 bytes a thread a pass, then
+    // any last bytes one by one).
+    __device__ inline void block_copy_page(std::uint8_t *dst, const std::uint8_t *src,
+                                           unsigned long long bytes)
+    {
+      const unsigned long long units = bytes / 16;
+      for (unsigned long long i = threadIdx.x; i < units; i += kThreads)
+      {
+        reinterpret_cast<uint4 *>(dst)[i] = reinterpret_cast<const uint4 *>(src)[i];
+      }
+      if (threadIdx.x < bytes % 16)
+      {
+        dst[16 * units + threadIdx.x] = src[16 * units + threadIdx.x];
+      }
+    }
+
+    // One page's move from FP16 (OneMove), a workgroup: the shadow copy and
+    // the page at its new tier (the register quantiser, its W tasks over the
+    // workgroup's lanes), then, after the barrier that waits for every read
+    // of the page, the compaction copies.
+    template <int Bits, int HD>
+    __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+        move_one_kernel(OneMove m, PageSpaces s, PageLayout L, int kv_heads)
+    {
+      if (m.has_shadow)
+      {
+        block_copy_page(resolve(s, m.shadow.to), resolve(s, m.shadow.from), s.shadow_bytes);
+      }
+      {
+        const int W = kv_heads * HD;
+        const auto *src = reinterpret_cast<const std::uint16_t *>(resolve(s, m.page.from));
+        std::uint8_t *dst = resolve(s, m.page.to);
+        const Rows keys{src, src, kP, W};
+        const Rows values{src + static_cast<std::size_t>(kP) * W,
+                          src + static_cast<std::size_t>(kP) * W, kP, W};
+        for (int task = threadIdx.x; task < W; task += kThreads)
+        {
+          page_task<Bits, HD>(task, keys, values, kv_heads, dst, L, Emit::kCodes, Emit::kCodes);
+        }
+      }
+      __syncthreads();
+      for (int k = 0; k < m.compact_count; ++k)
+      {
+        const RefPair p = m.compact[k];
+        block_copy_page(resolve(s, p.to), resolve(s, p.from), page_size(s, p.to));
+      }
+    }
+
     // The register quantiser over pages named by address (the batch API):
     // page i's keys at rows[i] (or row0), its values `values_offset` bytes
     // on, quantised into pages[i] (or page0); lane (blockIdx.x * 256 + tid)
@@ -385,6 +435,43 @@ namespace mi
                          spaces);
       hip_check(hipGetLastError(), "copy refs kernel launch");
     }
+  }
+
+  bool move_one_applies(int from, int tier, int page_tokens, int kv_heads, int head_dim)
+  {
+    // A workgroup's reads of host memory are latency-bound: a move from a
+    // shadow keeps the wide launches.
+    return from == kFP16 && tier != kFP16 && register_shape(page_tokens, kv_heads, head_dim);
+  }
+
+  bool launch_move_one(const OneMove &m, const PageSpaces &spaces, int page_tokens, int kv_heads,
+                       int head_dim, hipStream_t stream)
+  {
+    if (m.compact_count < 0 || m.compact_count > kHeldRefs)
+    {
+      throw InvalidArgument("a move's launch holds at most " + std::to_string(kHeldRefs) +
+                            " compaction copies; got " + std::to_string(m.compact_count));
+    }
+    if (m.tier == kFP16 || !register_shape(page_tokens, kv_heads, head_dim))
+    {
+      return false;
+    }
+    const PageLayout L = page_layout(m.tier, page_tokens, kv_heads, head_dim);
+    with_bits(m.tier, [&](auto bits) {
+      constexpr int B = decltype(bits)::value;
+      if (head_dim == 128)
+      {
+        hipLaunchKernelGGL((move_one_kernel<B, 128>), dim3(1), dim3(kThreads), 0, stream, m,
+                           spaces, L, kv_heads);
+      }
+      else
+      {
+        hipLaunchKernelGGL((move_one_kernel<B, 64>), dim3(1), dim3(kThreads), 0, stream, m,
+                           spaces, L, kv_heads);
+      }
+    });
+    hip_check(hipGetLastError(), "move kernel launch");
+    return true;
   }
 
   void launch_requant_refs(const RefList &pairs, int count, int tier, const PageSpaces &spaces,

@@ -167,6 +167,13 @@ namespace mi
     void free_pages(const std::vector<PageKey> &keys);
     void replace(PageKey key, PageKey staged);
     void replace_pages(const std::vector<std::pair<PageKey, PageKey>> &pairs);
+    // While a sink is set, the compaction copies of frees and replaces are
+    // appended to it instead of launched, and the runs a range gives up are
+    // held back: the caller launches the copies itself (after the work that
+    // reads the freed pages) and then calls finish_deferred, which queues
+    // the held runs for release behind what the stream has been given.
+    void defer_copies(std::vector<RefPair> *sink) { deferred_copies_ = sink; }
+    void finish_deferred();
     void write(PageKey key, const void *host, std::size_t bytes);
     void read(PageKey key, void *host, std::size_t bytes) const;
     PageLocation locate(PageKey key) const;
@@ -267,6 +274,14 @@ namespace mi
     std::vector<PlacementObserver *> observers_;
     std::unique_ptr<GranuleReleaser> releaser_;
     UploadBuffer moves_upload_;
+    std::vector<RefPair> *deferred_copies_ = nullptr;
+    struct HeldRun
+    {
+      char *at;
+      std::size_t bytes;
+      hipMemGenericAllocationHandle_t handle;
+    };
+    std::vector<HeldRun> deferred_runs_;
   };
 
   // FP16 shadows of downgraded pages in pinned host memory mapped for the
@@ -600,6 +615,9 @@ namespace mi
     // The tier moves of a batch: validated already, every page held.
     void run_moves(const std::vector<PageKey> &keys, const std::vector<int> &from,
                    const std::vector<int> &targets, double *shadow_seconds);
+    // One page's move from FP16 as one launch (launch_move_one), where its
+    // shape allows: false, and nothing changed, where it does not.
+    bool run_one_move(PageKey key, int from, int target, double *shadow_seconds);
     // Two timing events around a single move's copies, made on first use.
     void ensure_move_events();
     hipEvent_t move_events_[2] = {nullptr, nullptr};
