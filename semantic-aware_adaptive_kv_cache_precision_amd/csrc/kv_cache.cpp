@@ -757,7 +757,10 @@ namespace mi
     {
       ensure_move_events();
       hip_check(hipEventRecord(move_events_[0], stream), "hipEventRecord before a move");
-      launch_move_one(m, spaces, page_tokens_, kv_heads_, head_dim_, stream);
+      if (!launch_move_one(m, spaces, page_tokens_, kv_heads_, head_dim_, stream))
+      {
+        throw LogicError("a single move's launch refused a shape move_one_applies took");
+      }
       hip_check(hipEventRecord(move_events_[1], stream), "hipEventRecord after a move");
       if (compaction.size() > held)
       {

@@ -417,13 +417,37 @@ namespace mi
       {
         load(item);
       }
+      // The position, and the first item's bias and angle, asked for with
+      // its weights, before the input's norm: none waits behind the dots.
+      const int position = *p.position;
+      const int first_item = item;
+      const auto epilogue_inputs = [&](int it, float &b0, float &b1, float &c, float &sn) {
+        int seg, head, j;
+        item_rows(it, seg, head, j);
+        const std::size_t r0 = static_cast<std::size_t>(head) * p.head_dim + j;
+        const std::uint16_t *bias = p.b[seg];
+        b0 = bias != nullptr ? h2f(bias[r0]) : 0.0f;
+        b1 = bias != nullptr ? h2f(bias[r0 + half]) : 0.0f;
+        c = 1.0f;
+        sn = 0.0f;
+        if (seg != 2)
+        {
+          const float *cs = p.rope + (static_cast<std::size_t>(position) * half + j) * 2;
+          c = cs[0];
+          sn = cs[1];
+        }
+      };
+      float first_b0 = 0.0f, first_b1 = 0.0f, first_c = 1.0f, first_sn = 0.0f;
+      if (item < total && lane == 0)
+      {
+        epilogue_inputs(item, first_b0, first_b1, first_c, first_sn);
+      }
       const float scale = inv_rms(p.residual, p.in, p.eps, s_partial);
       for (int r = threadIdx.x; r < runs; r += kBlockThreads)
       {
         x_lds[r] = normed_run(p.residual, p.norm_weight, scale, r);
       }
       __syncthreads();
-      const int position = *p.position;
       const int row = position % kPage;
       const std::size_t W = static_cast<std::size_t>(p.kv_heads) * p.head_dim;
       for (; item < total; item += stride)
@@ -454,9 +478,13 @@ namespace mi
         item_rows(item, seg, head, j);
         const std::size_t r0 = static_cast<std::size_t>(head) * p.head_dim + j;
         const std::size_t r1 = r0 + half;
-        const std::uint16_t *bias = p.b[seg];
-        const unsigned h0 = to_half(d0 + (bias != nullptr ? h2f(bias[r0]) : 0.0f));
-        const unsigned h1 = to_half(d1 + (bias != nullptr ? h2f(bias[r1]) : 0.0f));
+        float b0 = first_b0, b1 = first_b1, c = first_c, sn = first_sn;
+        if (item != first_item)
+        {
+          epilogue_inputs(item, b0, b1, c, sn);
+        }
+        const unsigned h0 = to_half(d0 + b0);
+        const unsigned h1 = to_half(d1 + b1);
         if (seg == 2)
         {
           p.v[r0] = static_cast<std::uint16_t>(h0);
@@ -472,9 +500,6 @@ namespace mi
         // RoPE of the rounded pair, as the RoPE kernel rotates it.
         const float x1 = h2f(static_cast<std::uint16_t>(h0));
         const float x2 = h2f(static_cast<std::uint16_t>(h1));
-        const float *cs = p.rope + (static_cast<std::size_t>(position) * half + j) * 2;
-        const float c = cs[0];
-        const float sn = cs[1];
         const std::uint16_t o1 = to_half(x1 * c - x2 * sn);
         const std::uint16_t o2 = to_half(x2 * c + x1 * sn);
         const std::size_t at = static_cast<std::size_t>(seg == 0 ? head : p.heads + head) *
