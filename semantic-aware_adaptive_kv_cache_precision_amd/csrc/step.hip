@@ -20,7 +20,8 @@
 // and a wave reduction leaves the row's dot in every lane. The input row is
 // staged once a workgroup in LDS -- or, where an RMSNorm feeds the
 // projection, formed there from the fp32 residual to the RMSNorm kernel's
-// bits -- after each wave's first weight loads are already on their way.
+// bits -- its reads asked for before the weights', in one trip that does
+// not queue behind them.
 // A row a wave (a long row split over four or eight waves) when the
 // device holds the whole grid at once; otherwise as many workgroups as it
 // holds, each wave taking several rows with the next row's runs in flight
@@ -75,26 +76,89 @@ namespace mi
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef const __attribute__((address_space(1))) f32x4 *g_f32x4;
 
-    // Run r (eight values) of RMSNorm of the residual: x * scale * w, one
-    // rounding to fp16, as the RMSNorm kernel stores it.
-    __device__ inline u32x4 normed_run(const float *residual, const std::uint16_t *weight,
-                                       float scale, int r)
+    // RMSNorm of the fp32 residual row staged in LDS as fp16 runs, with the
+    // RMSNorm kernel's bits (inv_rms's sum in its order, then x * scale * w
+    // rounded once), every global read asked for in one trip: `ask` reads
+    // the values inv_rms sums (thread t < 256: t + 256 k) and the runs the
+    // thread forms (t + Threads m) of the residual and the norm weight; a
+    // kernel asks before its weights' loads, so that these do not queue
+    // behind them. `stage` sums, meets the workgroup at a barrier and writes
+    // the runs (the caller's barrier publishes them). The input is at most
+    // 512 Ahead values (Ahead runs a lane of a wave).
+    template <int Threads, int Ahead>
+    struct NormedInput
     {
-      const f32x4 a = *((g_f32x4)(residual + 8 * static_cast<std::size_t>(r)));
-      const f32x4 b = *((g_f32x4)(residual + 8 * static_cast<std::size_t>(r) + 4));
-      const u32x4 wv = *((g_u32x4)(weight + 8 * static_cast<std::size_t>(r)));
-      const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-      u32x4 out;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
+      static constexpr int kSquares = 2 * Ahead;
+      static constexpr int kRuns = (64 * Ahead + Threads - 1) / Threads;
+      float sq[kSquares];
+      f32x4 lo[kRuns], hi[kRuns];
+      u32x4 w[kRuns];
+
+      __device__ void ask(const float *residual, const std::uint16_t *weight, int in)
       {
-        const unsigned wi = wv[i];
-        const unsigned lo = to_half(v[2 * i] * scale * h2f(static_cast<std::uint16_t>(wi)));
-        const unsigned hi = to_half(v[2 * i + 1] * scale * h2f(static_cast<std::uint16_t>(wi >> 16)));
-        out[i] = lo | (hi << 16);
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < kSquares; ++k)
+        {
+          const int i = t + 256 * k;
+          sq[k] = t < 256 && i < in ? residual[i] : 0.0f;
+        }
+#pragma unroll
+        for (int m = 0; m < kRuns; ++m)
+        {
+          const int r = t + Threads * m;
+          if (r < in / 8)
+          {
+            lo[m] = *((g_f32x4)(residual + 8 * static_cast<std::size_t>(r)));
+            hi[m] = *((g_f32x4)(residual + 8 * static_cast<std::size_t>(r) + 4));
+            w[m] = *((g_u32x4)(weight + 8 * static_cast<std::size_t>(r)));
+          }
+        }
       }
-      return out;
-    }
+
+      __device__ void stage(int in, float eps, float *partial, u32x4 *x_lds)
+      {
+        // inv_rms's sum: the zeros past the row add nothing.
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kSquares; ++k)
+        {
+          acc += sq[k] * sq[k];
+        }
+        for (int offset = 32; offset > 0; offset >>= 1)
+        {
+          acc += __shfl_xor(acc, offset);
+        }
+        if (threadIdx.x < 256 && threadIdx.x % 64 == 0)
+        {
+          partial[threadIdx.x / 64] = acc;
+        }
+        __syncthreads();
+        const float total = ((partial[0] + partial[1]) + partial[2]) + partial[3];
+        const float scale = rsqrtf(total / static_cast<float>(in) + eps);
+#pragma unroll
+        for (int m = 0; m < kRuns; ++m)
+        {
+          const int r = threadIdx.x + Threads * m;
+          if (r < in / 8)
+          {
+            const float v[8] = {lo[m][0], lo[m][1], lo[m][2], lo[m][3],
+                                hi[m][0], hi[m][1], hi[m][2], hi[m][3]};
+            u32x4 out;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+              const unsigned wi = w[m][i];
+              const unsigned l = to_half(v[2 * i] * scale * h2f(static_cast<std::uint16_t>(wi)));
+              const unsigned h =
+                  to_half(v[2 * i + 1] * scale * h2f(static_cast<std::uint16_t>(wi >> 16)));
+              out[i] = l | (h << 16);
+            }
+            x_lds[r] = out;
+          }
+        }
+      }
+    };
 
     // The better of two (value, index) candidates, as argmax.cu chooses: the
     // larger value, the lower index on equal values; NaN never wins.
@@ -152,7 +216,7 @@ namespace mi
     // workgroup holds Waves / Split rows at a time; with Pipe a wave's next
     // row is loaded while the current one is used (the head: many rows a
     // wave). The input -- x, or RMSNorm of the residual -- is staged once a
-    // workgroup in LDS, after each wave's first loads are on their way.
+    // workgroup in LDS, its reads asked for before the wave's first loads.
     template <int Waves, int Ahead, bool Two, int Split, bool Pipe>
     __global__ void __launch_bounds__(64 * Waves) project_kernel(ProjectArgs p)
     {
@@ -184,8 +248,44 @@ namespace mi
       const auto up_weights = [&](int row) {
         return Two ? p.seg[1].w + static_cast<std::size_t>(row) * p.in : nullptr;
       };
-      // The wave's first row's runs, and with Pipe its second's, before the
-      // input.
+      // The input is asked for first, then the wave's first row's runs (and
+      // with Pipe its second's): the input's one trip does not queue behind
+      // the weights'. A row split over waves reads x (no RMSNorm) straight
+      // from global memory, a lane its own runs: staging a long input once a
+      // workgroup would read it more times than the weights' bytes.
+      // Otherwise x, or RMSNorm of the residual, is staged in LDS.
+      constexpr bool kDirect = Split > 1;
+      constexpr int kStagedRuns = (64 * Ahead + kBlockThreads - 1) / kBlockThreads;
+      const bool normed = !kDirect && p.norm_weight != nullptr;
+      u32x4 xd[kDirect ? Ahead : 1];
+      u32x4 xs[kDirect ? 1 : kStagedRuns];
+      NormedInput<kBlockThreads, kDirect ? 1 : Ahead> norm;
+      if constexpr (kDirect)
+      {
+#pragma unroll
+        for (int i = 0; i < Ahead; ++i)
+        {
+          const int r = begin + lane + 64 * i;
+          xd[i] = r < end ? *((g_u32x4)(p.x + 8 * static_cast<std::size_t>(r)))
+                          : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+      else if (normed)
+      {
+        norm.ask(p.residual, p.norm_weight, p.in);
+      }
+      else
+      {
+#pragma unroll
+        for (int m = 0; m < kStagedRuns; ++m)
+        {
+          const int r = threadIdx.x + kBlockThreads * m;
+          if (r < runs)
+          {
+            xs[m] = *((g_u32x4)(p.x + 8 * static_cast<std::size_t>(r)));
+          }
+        }
+      }
       int g = blockIdx.x * kSlots + slot;
       u32x4 a[Ahead], b[Ahead];
       u32x4 na[Pipe ? Ahead : 1], nb[Pipe ? Ahead : 1];
@@ -204,35 +304,23 @@ namespace mi
           load_part<Ahead, Two>(na, nb, w0, up_weights(nrow), begin, end, lane);
         }
       }
-      // A row split over waves reads x (no RMSNorm) straight from global
-      // memory, a lane its own runs, with the weights: staging a long input
-      // once a workgroup would read it more times than the weights' bytes.
-      constexpr bool kDirect = Split > 1;
-      u32x4 xd[kDirect ? Ahead : 1];
-      if constexpr (kDirect)
+      if constexpr (!kDirect)
       {
+        if (normed)
+        {
+          norm.stage(p.in, p.eps, s_partial, x_lds);
+        }
+        else
+        {
 #pragma unroll
-        for (int i = 0; i < Ahead; ++i)
-        {
-          const int r = begin + lane + 64 * i;
-          xd[i] = r < end ? *((g_u32x4)(p.x + 8 * static_cast<std::size_t>(r)))
-                          : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-      else if (p.norm_weight != nullptr)
-      {
-        const float scale = inv_rms(p.residual, p.in, p.eps, s_partial);
-        for (int r = threadIdx.x; r < runs; r += kBlockThreads)
-        {
-          x_lds[r] = normed_run(p.residual, p.norm_weight, scale, r);
-        }
-        __syncthreads();
-      }
-      else
-      {
-        for (int r = threadIdx.x; r < runs; r += kBlockThreads)
-        {
-          x_lds[r] = *((g_u32x4)(p.x + 8 * static_cast<std::size_t>(r)));
+          for (int m = 0; m < kStagedRuns; ++m)
+          {
+            const int r = threadIdx.x + kBlockThreads * m;
+            if (r < runs)
+            {
+              x_lds[r] = xs[m];
+            }
+          }
         }
         __syncthreads();
       }
@@ -412,13 +500,17 @@ namespace mi
         load_part<Ahead, true>(a, b, p.w[seg] + r0 * p.in, p.w[seg] + (r0 + half) * p.in, 0,
                                runs, lane);
       };
+      // The input's RMSNorm reads first, then the first item's weights.
+      NormedInput<kBlockThreads, Ahead> norm;
+      norm.ask(p.residual, p.norm_weight, p.in);
       int item = blockIdx.x * Waves + wave;
       if (item < total)
       {
         load(item);
       }
       // The position, and the first item's bias and angle, asked for with
-      // its weights, before the input's norm: none waits behind the dots.
+      // its weights, before the input's norm is staged: none waits behind
+      // the dots.
       const int position = *p.position;
       const int first_item = item;
       const auto epilogue_inputs = [&](int it, float &b0, float &b1, float &c, float &sn) {
@@ -442,11 +534,7 @@ namespace mi
       {
         epilogue_inputs(item, first_b0, first_b1, first_c, first_sn);
       }
-      const float scale = inv_rms(p.residual, p.in, p.eps, s_partial);
-      for (int r = threadIdx.x; r < runs; r += kBlockThreads)
-      {
-        x_lds[r] = normed_run(p.residual, p.norm_weight, scale, r);
-      }
+      norm.stage(p.in, p.eps, s_partial, x_lds);
       __syncthreads();
       const int row = position % kPage;
       const std::size_t W = static_cast<std::size_t>(p.kv_heads) * p.head_dim;
