@@ -25,7 +25,7 @@
 // A row a wave (a long row split over four or eight waves) when the
 // device holds the whole grid at once; otherwise as many workgroups as it
 // holds, each wave taking several rows with the next row's runs in flight
-// while one is used (the head's vocabulary, gate and up). The projections a step makes
+// while one is used (the head's vocabulary). The projections a step makes
 // from one input run in one launch: q, k and v (three weight matrices, one
 // grid over their rows), gate and up (a wave both rows of one output, the
 // SwiGLU in the epilogue).
@@ -758,9 +758,12 @@ namespace mi
     };
 
     // A wave a row (Split waves with a long input) in one grid when the
-    // device holds that many workgroups at once; otherwise as many
-    // workgroups as it holds, each wave over several rows with the next
-    // row's runs in flight while one is used.
+    // device holds that many workgroups at once -- for gate/up when it
+    // holds four fifths of them, the rest a short second round (faster
+    // than the resident grid, whose waves hold two rows' registers and so
+    // fit fewer a SIMD); otherwise as many workgroups as it holds,
+    // each wave over several rows with the next row's runs in flight while
+    // one is used.
     ProjectPlan plan_projection(const ProjectArgs &p)
     {
       const bool two = p.mode == ProjectMode::kSwiglu;
@@ -789,7 +792,8 @@ namespace mi
       const std::size_t lds = split > 1 ? 0 : static_cast<std::size_t>(p.in) * 2;
       const long long needed = (rows + slots - 1) / slots;
       ProjectFn plain = project_variant(ahead, waves, two, split, false);
-      if (split > 1 || needed <= resident_blocks(plain, 64 * waves, lds))
+      const long long held_plain = resident_blocks(plain, 64 * waves, lds);
+      if (split > 1 || needed <= held_plain || (two && 4 * needed <= 5 * held_plain))
       {
         return {plain, waves, static_cast<int>(needed), lds, split, false};
       }
