@@ -64,6 +64,7 @@ namespace mi
     typedef _Float16 half8 __attribute__((ext_vector_type(8)));
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
     constexpr int kP = 32;              // keys a page, and a key tile
     // Probabilities are held x2^14 for PV (14 added in the exponent).
@@ -290,6 +291,90 @@ namespace mi
         f.k = u32x4{0, 0, 0, 0};
         f.v = u32x4{0, 0, 0, 0};
       }
+    }
+
+    // Word 3 of a raw buffer descriptor on gfx9-family parts (gfx950).
+    constexpr int kBufferWord3 = 0x00020000;
+
+    // A thread's byte offsets into a sealed page for its (key t, chunk c),
+    // the same at every step: an FP16 page's key and value rows, the codes'
+    // element index (the row's first channel), the key channels' scales
+    // and zeros, the value row's scale and zero.
+    struct ItemOffsets
+    {
+      int fp16_k;
+      int fp16_v;
+      int elem;
+      int kmeta;
+      int vgroup;
+    };
+
+    template <int HD>
+    __device__ inline ItemOffsets item_offsets(int kv_heads, int kvh, int t, int c)
+    {
+      const int row = kv_heads * HD;
+      const int at = kvh * HD + 8 * c;
+      ItemOffsets o;
+      o.elem = t * row + at;
+      o.fp16_k = 2 * o.elem;
+      o.fp16_v = 2 * ((kP + t) * row + at);
+      o.kmeta = 2 * at;
+      o.vgroup = 2 * (t * kv_heads + kvh);
+      return o;
+    }
+
+    // fetch's sealed-page branch for a page the whole wave stages: its
+    // address and tier uniform, so one buffer over the page with the
+    // regions as scalar offsets and the thread's offsets fixed; the same
+    // words as fetch reads. An FP16 page (no quantised layout: lay[kFP16]
+    // is left empty) is its 2 x 32 rows of kv_heads * HD halves.
+    template <int HD>
+    __device__ inline void fetch_sealed(const PrefillArgs &a, unsigned long long page, int tier,
+                                        const ItemOffsets &o, Fetched &f)
+    {
+      if (tier == kFP16)
+      {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void *>(page), 0, 4 * kP * a.kv_heads * HD, kBufferWord3);
+        f.k = __builtin_amdgcn_raw_buffer_load_b128(rs, o.fp16_k, 0, 0);
+        f.v = __builtin_amdgcn_raw_buffer_load_b128(rs, o.fp16_v, 0, 0);
+        f.tier = kFP16;
+        return;
+      }
+      const PageLayout &L = a.lay[tier];
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          reinterpret_cast<void *>(page), 0, static_cast<int>(L.page_bytes), kBufferWord3);
+      const int kc = static_cast<int>(L.key_codes);
+      const int vc = static_cast<int>(L.value_codes);
+      f.k = u32x4{0, 0, 0, 0};
+      f.v = u32x4{0, 0, 0, 0};
+      if (tier == kINT8)
+      {
+        const u32x2 k2 = __builtin_amdgcn_raw_buffer_load_b64(rs, o.elem, kc, 0);
+        const u32x2 v2 = __builtin_amdgcn_raw_buffer_load_b64(rs, o.elem, vc, 0);
+        f.k.x = k2.x;
+        f.k.y = k2.y;
+        f.v.x = v2.x;
+        f.v.y = v2.y;
+      }
+      else if (tier == kINT4)
+      {
+        f.k.x = __builtin_amdgcn_raw_buffer_load_b32(rs, o.elem / 2, kc, 0);
+        f.v.x = __builtin_amdgcn_raw_buffer_load_b32(rs, o.elem / 2, vc, 0);
+      }
+      else
+      {
+        f.k.x = __builtin_amdgcn_raw_buffer_load_b16(rs, o.elem / 4, kc, 0);
+        f.v.x = __builtin_amdgcn_raw_buffer_load_b16(rs, o.elem / 4, vc, 0);
+      }
+      f.ks = __builtin_amdgcn_raw_buffer_load_b128(rs, o.kmeta, static_cast<int>(L.key_scales), 0);
+      f.kz = __builtin_amdgcn_raw_buffer_load_b128(rs, o.kmeta, static_cast<int>(L.key_zeros), 0);
+      f.vsz = static_cast<unsigned>(__builtin_amdgcn_raw_buffer_load_b16(
+                  rs, o.vgroup, static_cast<int>(L.value_scales), 0)) |
+              (static_cast<unsigned>(__builtin_amdgcn_raw_buffer_load_b16(
+                   rs, o.vgroup, static_cast<int>(L.value_zeros), 0))
+               << 16);
+      f.tier = tier;
     }
 
     __device__ inline std::uint16_t half_of(const u32x4 &w, int e)
@@ -581,15 +666,29 @@ namespace mi
         }
       };
       // Whether an item has anything to read: an unread sealed page has not.
+      // Its table entry (every lane read the same one, a step earlier) is
+      // made uniform here, so that what follows it branches on scalars.
       const auto settle = [&](Step &st) {
 #pragma unroll
         for (int j = 0; j < NP; ++j)
         {
+          st.tier[j] = __builtin_amdgcn_readfirstlane(st.tier[j]);
+          const unsigned long long raw = st.page[j];
+          st.page[j] =
+              static_cast<unsigned long long>(
+                  static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(raw)))) |
+              (static_cast<unsigned long long>(static_cast<unsigned>(
+                   __builtin_amdgcn_readfirstlane(static_cast<int>(raw >> 32))))
+               << 32);
           st.live[j] = st.p[j] < p_end &&
                        !(causal && st.version[j] == kSealed && st.tier[j] == kUnreadPage);
         }
       };
 
+      // A thread's items keep their (key, chunk) from step to step, and a
+      // page's items are whole waves (kItems is a multiple of 64): each
+      // wave stages one page a slot, its entry uniform.
+      static_assert(kItems % 64 == 0, "a page's staging items are whole waves");
       Fetched f[kFetch];
       f32x4 cs[kFetch][4];
       const auto fetch_step = [&](const Step &st) {
@@ -599,15 +698,25 @@ namespace mi
           const int item = threadIdx.x + u * threads;
           if (item < kStepItems)
           {
-            const int j = item / kItems;
+            const int j = __builtin_amdgcn_readfirstlane(item / kItems);
             const int t = (item % kItems) % kP;
             const int c = (item % kItems) / kP;
             const int p = st.p[j];
             f[u].tier = -1;
-            if (st.live[j])
+            // (With a key bias the general fetch: the buffer path's registers
+            // would spill there.)
+            if (!kBias && st.live[j] && causal && st.version[j] == kSealed)
+            {
+              fetch_sealed<HD>(a, st.page[j], st.tier[j], item_offsets<HD>(a.kv_heads, kvh, t, c),
+                           f[u]);
+            }
+            else if (st.live[j])
             {
               const Entry e{st.page[j], st.tier[j]};
               fetch<HD>(a, p, st.version[j], e, kvh, t, c, f[u]);
+            }
+            if (st.live[j])
+            {
               if constexpr (kBias)
               {
                 if (p * kP + t < a.seq_k)
@@ -626,7 +735,7 @@ namespace mi
           const int item = threadIdx.x + u * threads;
           if (item < kStepItems)
           {
-            const int j = item / kItems;
+            const int j = __builtin_amdgcn_readfirstlane(item / kItems);
             if (st.live[j])
             {
               commit<HD, kBias>(f[u], cs[u], b_first[u], b_second[u], (item % kItems) % kP,
@@ -664,28 +773,30 @@ namespace mi
         if (computes)
         {
           const std::uint16_t *stages = smem + buf * NP * kStage;
-          // S^T = K . Q^T, two 16-key tiles a page.
+          // S^T = K . Q^T, two 16-key tiles a page, each started from the
+          // product's zero operand; a dead item's scores are zeros (the
+          // softmax masks it whole).
+          const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
           f32x4 s[TPW][2 * NP];
-          #pragma unroll
-          for (int tt = 0; tt < TPW; ++tt)
-          {
-#pragma unroll
-            for (int kt = 0; kt < 2 * NP; ++kt)
-            {
-              s[tt][kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
-          }
 #pragma unroll
           for (int j = 0; j < NP; ++j)
           {
             if (!cur.live[j])
             {
+              #pragma unroll
+              for (int tt = 0; tt < TPW; ++tt)
+              {
+                s[tt][2 * j] = zero;
+                s[tt][2 * j + 1] = zero;
+              }
               continue;
             }
             const std::uint16_t *k_hi = stages + j * kStage;
             const std::uint16_t *k_lo = k_hi + kP * KS;
+#pragma unroll
             for (int kt = 0; kt < 2; ++kt)
             {
+#pragma unroll
               for (int cc = 0; cc < HD / 32; ++cc)
               {
                 const int off = (16 * kt + col) * KS + 32 * cc + 8 * g;
@@ -693,7 +804,7 @@ namespace mi
                 #pragma unroll
                 for (int tt = 0; tt < TPW; ++tt)
                 {
-                  s[tt][2 * j + kt] = mfma(ka, qf[tt][cc], s[tt][2 * j + kt]);
+                  s[tt][2 * j + kt] = mfma(ka, qf[tt][cc], cc == 0 ? zero : s[tt][2 * j + kt]);
                 }
                 if constexpr (kBias)
                 {
@@ -715,7 +826,8 @@ namespace mi
           #pragma unroll
           for (int tt = 0; tt < TPW; ++tt)
           {
-            float sc[8 * NP];
+            // A masked key's score becomes -inf in place; an item every row
+            // sees whole keeps its scores as they are.
             float top = -INFINITY;
 #pragma unroll
             for (int j = 0; j < NP; ++j)
@@ -743,24 +855,20 @@ namespace mi
               {
                 limit = -1;
               }
-              if (live && full)
-              {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                {
-                  sc[8 * j + e] = s[tt][2 * j + e / 4][e % 4];
-                  top = fmaxf(top, sc[8 * j + e]);
-                }
-              }
-              else
+              if (!(live && full))
               {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
                 {
                   const int key = p * kP + key_of(e / 4, g, e % 4);
-                  sc[8 * j + e] = key <= limit ? s[tt][2 * j + e / 4][e % 4] : -INFINITY;
-                  top = fmaxf(top, sc[8 * j + e]);
+                  s[tt][2 * j + e / 4][e % 4] =
+                      key <= limit ? s[tt][2 * j + e / 4][e % 4] : -INFINITY;
                 }
+              }
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+              {
+                top = fmaxf(top, s[tt][2 * j + e / 4][e % 4]);
               }
             }
             // Scores to base 2: the scale is positive, so the scaled maximum
@@ -779,7 +887,7 @@ namespace mi
 #pragma unroll
               for (int e = 0; e < 8; ++e)
               {
-                const float ps = exp2_fast(fmaf(sc[8 * j + e], a.scale2, bias2));
+                const float ps = exp2_fast(fmaf(s[tt][2 * j + e / 4][e % 4], a.scale2, bias2));
                 sum += ps;
                 _Float16 h, h_lo;
                 split_half(ps, h, h_lo);
