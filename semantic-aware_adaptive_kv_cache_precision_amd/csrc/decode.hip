@@ -52,6 +52,7 @@
 #include <map>
 #include <mutex>
 #include <numeric>
+#include <tuple>
 #include <vector>
 
 namespace mi
@@ -165,6 +166,13 @@ namespace mi
       // seal_block - 1; 0: none.
       StepStore seal;
       int seal_block;
+      // The workgroups a KV head's split launch holds at once (0: no bound).
+      // When the live splits exceed it, busy_splits workgroups take the
+      // pages: each its own kWaves, and the pages past busy_splits * kWaves
+      // a wave each as a second page (kWaves * busy_splits on from its
+      // first); the splits past them are written as empty partials, so that
+      // readers of live_splits partials see the same layout.
+      int busy_splits;
     };
 
     __device__ inline half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
@@ -747,7 +755,12 @@ namespace mi
       const int li = blockIdx.z;
       const int layer = a.first_layer + li;
       go_live(a);
-      if (split >= a.live_splits)
+      // (The key-bias kernel keeps one split a workgroup: its launches are
+      // never bounded.)
+      const int busy = !kBias && a.busy_splits > 0 && a.busy_splits < a.live_splits
+                           ? a.busy_splits
+                           : a.live_splits;
+      if (split >= busy)
       {
         return; // past the live pages: the combine reads no partial of this split
       }
@@ -766,6 +779,18 @@ namespace mi
       const std::uint8_t *tiers = a.tiers != nullptr ? a.tiers + layer * a.table_stride : nullptr;
       const int own = a.causal ? (a.seq_k - 1) / kPageTokens : -1;
       const int p0 = (split * kWaves + wave) * a.pages_per_wave;
+      // The wave's pages: p0 and the next pages_per_wave - 1 (several a
+      // wave), or p0 and every kWaves * busy pages on (the pages past the
+      // busy splits).
+      int p_step = 1, p_count = a.pages_per_wave, p_bound = a.live_pages;
+      if constexpr (!kBias)
+      {
+        if (a.pages_per_wave == 1)
+        {
+          p_step = kWaves * busy;
+          p_count = INT_MAX;
+        }
+      }
       // A pack's rows: its first KV head's heads, then its second's; lane
       // groups 0-1 hold the first head's 64 channels, 2-3 the second's.
       const int head_row = kvh * G + (r < G ? r : 0);
@@ -826,7 +851,7 @@ namespace mi
       // prologue, whose angle-row copy then shares its trip to memory.
       int first_tier_lane = 0;
       unsigned long long first_page_raw = 0;
-      if (p0 < a.live_pages)
+      if (p0 < p_bound)
       {
         entry(p0, first_tier_lane, first_page_raw);
       }
@@ -849,10 +874,10 @@ namespace mi
                              ? reinterpret_cast<const std::uint16_t *>(a.open_table[layer])
                              : a.open;
       bool first = true;
-      for (int i = 0; i < a.pages_per_wave; ++i)
+      for (int i = 0; i < p_count; ++i)
       {
-        const int p = p0 + i;
-        if (p >= a.live_pages)
+        const int p = p0 + i * p_step;
+        if (p >= p_bound)
         {
           break;
         }
@@ -1025,6 +1050,27 @@ namespace mi
         else
         {
           part[h * out_hd + col - 2] = acc;
+        }
+      }
+      // Splits past the busy ones: empty partials (max -inf, sum and
+      // outputs 0), which weigh nothing where they are folded.
+      for (int empty = busy + split; !kBias && empty < a.live_splits; empty += busy)
+      {
+        float *epart = a.partials +
+                       ((static_cast<std::size_t>(li) * a.kv_heads + kvh) * a.splits + empty) * G * out_hd;
+        for (int idx = threadIdx.x; idx < G * (out_hd + 2); idx += kThreads)
+        {
+          const int h = idx / (out_hd + 2);
+          const int col = idx % (out_hd + 2);
+          if (col < 2)
+          {
+            ml[(static_cast<std::size_t>(h) * a.splits + empty) * 2 + col] =
+                col == 0 ? -INFINITY : 0.0f;
+          }
+          else
+          {
+            epart[h * out_hd + col - 2] = 0.0f;
+          }
         }
       }
     }
@@ -2036,6 +2082,32 @@ namespace mi
       return waves;
     }
 
+    // Workgroups of a pages-kernel variant the current device holds at once
+    // with `lds` bytes of LDS each: whole workgroups a CU times the CUs.
+    long long resident_pages_blocks(const void *kernel, std::size_t lds)
+    {
+      static std::mutex lock;
+      static std::map<std::tuple<int, const void *, std::size_t>, long long> known;
+      int device = 0;
+      hip_check(hipGetDevice(&device), "hipGetDevice");
+      std::lock_guard<std::mutex> guard(lock);
+      const auto key = std::make_tuple(device, kernel, lds);
+      const auto found = known.find(key);
+      if (found != known.end())
+      {
+        return found->second;
+      }
+      int blocks = 0;
+      hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kThreads, lds),
+                "hipOccupancyMaxActiveBlocksPerMultiprocessor decode pages");
+      int cus = 0;
+      hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                "hipDeviceGetAttribute CUs");
+      const long long held = static_cast<long long>(std::max(blocks, 1)) * cus;
+      known.emplace(key, held);
+      return held;
+    }
+
   } // namespace
 
   float *stream_workspace(hipStream_t stream, std::size_t count)
@@ -2280,7 +2352,22 @@ namespace mi
                                         static_cast<int>(lds)),
                     "hipFuncSetAttribute decode LDS");
         }
-        hipLaunchKernelGGL(pages_kernel, dim3(d.splits, d.kv_heads, ls.layers), dim3(kThreads),
+        // One layer split a page a wave (no key bias): no more workgroups a
+        // KV head than the device holds at once (past that, second pages
+        // for some waves).
+        int grid_splits = d.splits;
+        if (ls.split && d.k_bias == nullptr)
+        {
+          const long long per = resident_pages_blocks(reinterpret_cast<const void *>(pages_kernel),
+                                                      lds) /
+                                (static_cast<long long>(d.kv_heads) * ls.layers);
+          if (per < d.splits)
+          {
+            d.busy_splits = static_cast<int>(std::max<long long>(per, 1));
+            grid_splits = d.busy_splits;
+          }
+        }
+        hipLaunchKernelGGL(pages_kernel, dim3(grid_splits, d.kv_heads, ls.layers), dim3(kThreads),
                            lds, stream, d);
         hip_check(hipGetLastError(), "decode pages kernel launch");
       }

@@ -630,16 +630,20 @@ def test_chained_store_and_decode_steps_across_a_seal_at_llama_shape():
     np.testing.assert_array_equal(scores.download(), ewma.host_ewma(folded, LAYERS, max_pages))
 
 
-def test_llama_shape_at_16k_two_kv_heads_a_wave_is_the_oracle():
+@pytest.mark.parametrize("extra", [10, 700])
+def test_llama_shape_at_16k_two_kv_heads_a_wave_is_the_oracle(extra):
     """At the Llama-3.2-1B shape and 16K positions (more waves of one KV head
     each than the device holds at once) the decode takes two KV heads a wave
     as one 128-channel unit: output and masses against the float64 causal
     view of a 30/40/30 FP16/INT8/INT4 cache, and the scores the oracle's
-    fold of the kernel's masses, to the bit."""
+    fold of the kernel's masses, to the bit. Past 512 pages (65 and 67
+    splits a KV-head pair here, against the 64 workgroups a pair the device
+    holds at once) the busy workgroups take balanced runs of pages and the
+    splits past them are empty partials."""
     from microinfer import workloads as w
     P, shape = 32, w.LLAMA_1B
     heads, kv, hd = shape.heads, shape.kv_heads, shape.head_dim
-    seq = 16384 + 10
+    seq = 16384 + extra
     pages = seq // P + 1
     tmap = w.tier_map(1, LAYERS, pages, w.MIX_CONFIG5)
     announce("llama 16K decode", seq)
