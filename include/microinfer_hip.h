@@ -400,6 +400,20 @@ int mi_kv_stored_on_device(mi_kv_pages *kv, int end);
 int mi_kv_rope_store(mi_kv_pages *kv, int layer, const void *qk, void *qk_out, int q_heads,
                      const int32_t *position, mi_rope_table *rope, const void *values,
                      const float *x, const void *norm_weight, void *normed, int hidden, float eps);
+/* Beyond the reference: mi_kv_rope_store at position seq_k - 1 and
+ * mi_kv_attention's one-query split decode over the positions before seq_k
+ * (kv_pages.h:163-179 KVPages.attention with partials) as two launches, the
+ * pages launch and its combine, for a cache that does not seal. The pages
+ * launch turns q and the row's k by RoPE in the waves that read them, stores
+ * the turned k rows and `values` at seq_k - 1 by the wave that reads that
+ * page, forms the RMSNorm of x (when not NULL) in one more workgroup, and
+ * writes the turned rows to qk_out when it is not NULL. The bits of
+ * mi_kv_rope_store then mi_kv_attention with partials. q_heads a whole
+ * number of heads a KV head (at most 16); head_dim 64 or 128; 32-token pages;
+ * rope covers seq_k positions; rows 16-byte aligned. */
+int mi_kv_attend_row(mi_kv_pages *kv, int layer, const void *qk, void *qk_out, int q_heads,
+                     int seq_k, mi_rope_table *rope, const void *values, void *out,
+                     const float *x, const void *norm_weight, void *normed, int hidden, float eps);
 
 /* ---- a whole decode step as one HIP graph (beyond the reference) ---------
  * The reference sequences a decode step from the host, a device call at a

@@ -1319,6 +1319,22 @@ int mi_kv_rope_store(mi_kv_pages *kv, int layer, const void *qk, void *qk_out, i
   });
 }
 
+int mi_kv_attend_row(mi_kv_pages *kv, int layer, const void *qk, void *qk_out, int q_heads,
+                     int seq_k, mi_rope_table *rope, const void *values, void *out,
+                     const float *x, const void *norm_weight, void *normed, int hidden, float eps)
+{
+  return guarded([&] {
+    need(kv, "kv");
+    need(rope, "rope");
+    if (qk_out != nullptr && qk == qk_out)
+    {
+      throw mi::InvalidArgument("rope cannot write over its input");
+    }
+    kv->impl.attend_row(layer, qk, qk_out, q_heads, seq_k, rope->impl, values, out, x,
+                        norm_weight, normed, hidden, eps);
+  });
+}
+
 int mi_kv_stored_on_device(mi_kv_pages *kv, int end)
 {
   return guarded([&] {

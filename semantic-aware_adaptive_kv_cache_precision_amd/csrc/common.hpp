@@ -303,6 +303,51 @@ namespace mi
     return rsqrtf(total / static_cast<float>(hidden) + eps);
   }
 
+  // x * scale * w for the row's elements, one fp16 rounding each, eight a
+  // thread through 16-byte stores where the row allows, else one.
+  template <typename In>
+  __device__ inline void normed_row(const In *x, const std::uint16_t *w, std::uint16_t *out,
+                                    int hidden, float scale)
+  {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const bool wide = hidden % 8 == 0 && (reinterpret_cast<std::uintptr_t>(out) |
+                                          reinterpret_cast<std::uintptr_t>(w)) % 16 == 0;
+    if (wide)
+    {
+      for (int r = threadIdx.x; r < hidden / 8; r += blockDim.x)
+      {
+        const u32x4 wv = *reinterpret_cast<const u32x4 *>(w + 8 * r);
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+          const float a = widen_value(x, 8 * r + 2 * k) * scale * h2f(static_cast<std::uint16_t>(wv[k]));
+          const float b =
+              widen_value(x, 8 * r + 2 * k + 1) * scale * h2f(static_cast<std::uint16_t>(wv[k] >> 16));
+          o[k] = static_cast<unsigned>(__half_as_ushort(__float2half(a))) |
+                 (static_cast<unsigned>(__half_as_ushort(__float2half(b))) << 16);
+        }
+        *reinterpret_cast<u32x4 *>(out + 8 * r) = o;
+      }
+      return;
+    }
+    for (int i = threadIdx.x; i < hidden; i += blockDim.x)
+    {
+      out[i] = __half_as_ushort(__float2half(widen_value(x, i) * scale * h2f(w[i])));
+    }
+  }
+
+  // RoPE of one pair (reference: rope.cu:32-54): channel j's value x1 and
+  // channel j + hd/2's x2 turned by the angle's cos c and sin s, each result
+  // rounded once to fp16. Every rotation here goes through this, so that
+  // they agree to the bit.
+  __device__ inline void rope_pair(float x1, float x2, float c, float s, std::uint16_t &lo,
+                                   std::uint16_t &hi)
+  {
+    lo = __half_as_ushort(__float2half(x1 * c - x2 * s));
+    hi = __half_as_ushort(__float2half(x2 * c + x1 * s));
+  }
+
   // One EWMA step of a page's importance score (reference:
   // importance_scores.cu:31-50): `observed` is the heads' mean mass (summed
   // in head order, then divided); the new score is alpha * observed +

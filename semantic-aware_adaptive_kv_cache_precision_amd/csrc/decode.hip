@@ -173,9 +173,28 @@ namespace mi
       // first); the splits past them are written as empty partials, so that
       // readers of live_splits partials see the same layout.
       int busy_splits;
+      // The row launch's work in the pages launch (decode_pages_kernel with
+      // kRow; a cache that does not seal, no key bias): q and the current
+      // row's k are row_qk's raw rows (q_heads then kv_heads), turned by RoPE
+      // at position seq_k - 1 from row_table as each wave needs them; the
+      // current row's values are row_v; the wave reading the current page
+      // takes that row from registers and stores it into the page. One more
+      // workgroup forms RMSNorm(row_x) into row_normed when row_x is given.
+      // The turned q and k rows go to row_qk_out when it is given.
+      const std::uint16_t *row_qk;
+      std::uint16_t *row_qk_out;
+      const std::uint16_t *row_v;
+      const float *row_table;
+      int row_q_heads;
+      const float *row_x;
+      const std::uint16_t *row_norm_weight;
+      std::uint16_t *row_normed;
+      int row_hidden;
+      float row_eps;
     };
 
     __device__ inline half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
+    __device__ inline u32x4 as_u32x4(half8 v) { return __builtin_bit_cast(u32x4, v); }
 
     // The launch's position, when it lives on the device: seq_k, the first
     // chunk row (a decode step brings one) and the live bounds.
@@ -708,14 +727,70 @@ namespace mi
       }
     }
 
+    // RoPE of a lane's run of a head's row (HD/4 channels from g HD/4) at
+    // one position: the run's raw words and the cos and sin of its angles,
+    // asked for first (TurnIn::ask) and turned once they are in (turn). A
+    // run's partner channels, hd/2 away, are lane ^ 32's: lane groups 0-1
+    // form x1 c - x2 s, groups 2-3 x2 c + x1 s, as rope_pair does.
+    template <int HD>
+    struct TurnIn
+    {
+      u32x4 raw[HD / 32];
+      f32x4 cs[HD / 8]; // {cos, sin} of two angles a vector
+
+      __device__ void ask(const std::uint16_t *run, const float *table, int position, int g)
+      {
+        constexpr int kRun = HD / 4;
+        const float *angles =
+            table + 2 * (static_cast<std::size_t>(position) * (HD / 2) + (g % 2) * kRun);
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s)
+        {
+          raw[s] = *((g_u32x4)(run + 8 * s));
+        }
+#pragma unroll
+        for (int i = 0; i < HD / 8; ++i)
+        {
+          cs[i] = *reinterpret_cast<const f32x4 *>(angles + 4 * i);
+        }
+      }
+
+      __device__ void turn(half8 *dst, const u32x4 *words, int g) const
+      {
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s)
+        {
+          u32x4 out;
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+          {
+            float lo_word, hi_word;
+            lane_pair32(__uint_as_float(words[s][w]), lo_word, hi_word);
+            const unsigned x1w = __float_as_uint(lo_word), x2w = __float_as_uint(hi_word);
+            const f32x4 a = cs[4 * s + w];
+            std::uint16_t lo0, hi0, lo1, hi1;
+            rope_pair(h2f(static_cast<std::uint16_t>(x1w)), h2f(static_cast<std::uint16_t>(x2w)),
+                      a[0], a[1], lo0, hi0);
+            rope_pair(h2f(static_cast<std::uint16_t>(x1w >> 16)),
+                      h2f(static_cast<std::uint16_t>(x2w >> 16)), a[2], a[3], lo1, hi1);
+            out[w] = g < 2 ? (static_cast<unsigned>(lo0) | (static_cast<unsigned>(lo1) << 16))
+                           : (static_cast<unsigned>(hi0) | (static_cast<unsigned>(hi1) << 16));
+          }
+          dst[s] = as_half8(out);
+        }
+      }
+    };
+
     // A page of FP16 rows from global memory: keys at k0/k1 (rows r and
     // 16 + r, the lane's run), values at v0/v1, all requested at once so that
-    // the page costs one trip to memory.
-    template <int HD, bool kBias = false>
+    // the page costs one trip to memory. With kCurrent, row `cur_row` (-1:
+    // none) is cur_k and cur_v from registers instead.
+    template <int HD, bool kBias = false, bool kCurrent = false>
     __device__ inline void fp16_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
                                      const std::uint16_t *k0, const std::uint16_t *k1,
                                      const std::uint16_t *v0, const std::uint16_t *v1,
-                                     const KeyBias<HD> *bias = nullptr)
+                                     const KeyBias<HD> *bias = nullptr, int cur_row = -1,
+                                     const half8 *cur_k = nullptr, const half8 *cur_v = nullptr)
     {
       constexpr int S = HD / 32;
       half8 k[2][S], v[2][S];
@@ -723,6 +798,22 @@ namespace mi
       load_fp16_run<HD>(k[1], k1);
       load_fp16_run<HD>(v[0], v0);
       load_fp16_run<HD>(v[1], v1);
+      if constexpr (kCurrent)
+      {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+        {
+          if (kb * 16 + c.r == cur_row)
+          {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+            {
+              k[kb][s] = cur_k[s];
+              v[kb][s] = cur_v[s];
+            }
+          }
+        }
+      }
       f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
       // The key bias's scores while the keys are on their way.
       if constexpr (kBias)
@@ -735,7 +826,10 @@ namespace mi
       fp16_values<HD>(run, c, v, p_hi, p_lo);
     }
 
-    template <int HD, bool kBias>
+    // kCurrent: the row launch's work done here too (the DecodeArgs row_*
+    // fields; one split layer, FP16 pages of a cache that does not seal, no
+    // key bias, no pack).
+    template <int HD, bool kBias, bool kCurrent = false>
     __global__ void __launch_bounds__(kThreads) decode_pages_kernel(DecodeArgs a)
     {
       constexpr int S = HD / 32;  // K steps of q.K^T
@@ -754,6 +848,19 @@ namespace mi
       const int kvh = blockIdx.y;
       const int li = blockIdx.z;
       const int layer = a.first_layer + li;
+      if constexpr (kCurrent)
+      {
+        // The workgroups past the splits: the first forms RMSNorm(row_x).
+        if (split == static_cast<int>(gridDim.x) - 1 && a.row_x != nullptr)
+        {
+          if (kvh == 0)
+          {
+            const float scale = inv_rms(a.row_x, a.row_hidden, a.row_eps, lds);
+            normed_row(a.row_x, a.row_norm_weight, a.row_normed, a.row_hidden, scale);
+          }
+          return;
+        }
+      }
       go_live(a);
       // (The key-bias kernel keeps one split a workgroup: its launches are
       // never bounded.)
@@ -826,9 +933,40 @@ namespace mi
       {
         qb[si] = as_half8(u32x4{0u, 0u, 0u, 0u});
       }
-      if (!q_off)
+      // The current row (kCurrent): its position, its page and row there,
+      // and whether this wave reads that page. q's raw run and angles (and
+      // with the page, the row's raw k and its values) are asked for here
+      // and turned once the first page's entry is asked for too.
+      const int cur_pos = a.seq_k - 1;
+      const int cur_page = cur_pos / kPageTokens;
+      const int cur_t = cur_pos % kPageTokens;
+      half8 cur_k[kCurrent ? S : 1], cur_v[kCurrent ? S : 1];
+      u32x4 k_raw[kCurrent ? S : 1];
+      TurnIn<kCurrent ? HD : 32> turn_in;
+      bool holds_cur = false;
+      if constexpr (kCurrent)
       {
-        load_fp16_run<HD>(qb, q_row);
+        const int ahead = cur_page - p0;
+        holds_cur = ahead >= 0 && ahead % p_step == 0 && ahead / p_step < p_count;
+        turn_in.ask(q_row, a.row_table, cur_pos, g);
+        if (holds_cur)
+        {
+          const std::uint16_t *k_row =
+              a.row_qk + (static_cast<std::size_t>(a.row_q_heads) + kvh) * HD + g * kRun;
+#pragma unroll
+          for (int si = 0; si < S; ++si)
+          {
+            k_raw[si] = *((g_u32x4)(k_row + 8 * si));
+          }
+          load_fp16_run<HD>(cur_v, a.row_v + run0);
+        }
+      }
+      if constexpr (!kCurrent)
+      {
+        if (!q_off)
+        {
+          load_fp16_run<HD>(qb, q_row);
+        }
       }
 
       // Where the tiers and addresses are read from: q (always readable)
@@ -854,6 +992,35 @@ namespace mi
       if (p0 < p_bound)
       {
         entry(p0, first_tier_lane, first_page_raw);
+      }
+      if constexpr (kCurrent)
+      {
+        turn_in.turn(qb, turn_in.raw, g);
+        if (holds_cur)
+        {
+          turn_in.turn(cur_k, k_raw, g);
+        }
+        // The turned q rows out, once (split 0's first wave), and the
+        // turned k row by the wave that stores it.
+        if (a.row_qk_out != nullptr && split == 0 && wave == 0 && r < G)
+        {
+#pragma unroll
+          for (int si = 0; si < S; ++si)
+          {
+            *reinterpret_cast<u32x4 *>(a.row_qk_out + static_cast<std::size_t>(head_row) * HD +
+                                       g * kRun + 8 * si) = as_u32x4(qb[si]);
+          }
+        }
+        if (a.row_qk_out != nullptr && holds_cur && r == 0)
+        {
+#pragma unroll
+          for (int si = 0; si < S; ++si)
+          {
+            *reinterpret_cast<u32x4 *>(a.row_qk_out +
+                                       (static_cast<std::size_t>(a.row_q_heads) + kvh) * HD +
+                                       g * kRun + 8 * si) = as_u32x4(cur_k[si]);
+          }
+        }
       }
 
       // The key bias: lane i holds b_i and b_i' of this KV head; the
@@ -968,10 +1135,34 @@ namespace mi
         default:
         {
           const auto *h = reinterpret_cast<const std::uint16_t *>(page);
-          fp16_page<HD, kBias>(run, c, qb, h + static_cast<std::size_t>(r) * W + run0,
-                        h + static_cast<std::size_t>(16 + r) * W + run0,
-                        h + static_cast<std::size_t>(kPageTokens + r) * W + run0,
-                        h + static_cast<std::size_t>(kPageTokens + 16 + r) * W + run0, page_bias);
+          if constexpr (kCurrent)
+          {
+            const bool here = holds_cur && p == cur_page;
+            fp16_page<HD, kBias, true>(run, c, qb, h + static_cast<std::size_t>(r) * W + run0,
+                                       h + static_cast<std::size_t>(16 + r) * W + run0,
+                                       h + static_cast<std::size_t>(kPageTokens + r) * W + run0,
+                                       h + static_cast<std::size_t>(kPageTokens + 16 + r) * W + run0,
+                                       page_bias, here ? cur_t : -1, cur_k, cur_v);
+            // The current row into its page: its four lanes of row cur_t
+            // (each row's k and v runs are read by this wave only).
+            if (here && (cur_t % 16) == r)
+            {
+              auto *row = const_cast<std::uint16_t *>(h) + static_cast<std::size_t>(cur_t) * W + run0;
+#pragma unroll
+              for (int si = 0; si < S; ++si)
+              {
+                *reinterpret_cast<u32x4 *>(row + 8 * si) = as_u32x4(cur_k[si]);
+                *reinterpret_cast<u32x4 *>(row + kPageTokens * W + 8 * si) = as_u32x4(cur_v[si]);
+              }
+            }
+          }
+          else
+          {
+            fp16_page<HD, kBias>(run, c, qb, h + static_cast<std::size_t>(r) * W + run0,
+                          h + static_cast<std::size_t>(16 + r) * W + run0,
+                          h + static_cast<std::size_t>(kPageTokens + r) * W + run0,
+                          h + static_cast<std::size_t>(kPageTokens + 16 + r) * W + run0, page_bias);
+          }
           break;
         }
         }
@@ -2252,6 +2443,35 @@ namespace mi
         d.seal.lay[t] = page_layout(t, kPageTokens, d.seal.kv_heads, a.head_dim);
       }
     }
+    const RowPrep *row = ls.row;
+    if (row != nullptr)
+    {
+      if (!ls.split || ls.layers != 1 || ls.live_seq_k != nullptr || ls.seal != nullptr ||
+          ls.keep_ml != nullptr || kv.layout != Layout::kPaged || a.k_bias != nullptr ||
+          a.mass != nullptr || a.scores != nullptr || row->head_dim != a.head_dim ||
+          row->kv_heads != a.kv_heads || row->q_heads != a.heads || row->qk != a.q ||
+          row->table == nullptr || row->table_positions < a.seq_k || row->values == nullptr ||
+          !aligned16(row->values) || !aligned16(row->table) ||
+          (row->qk_out != nullptr && !aligned16(row->qk_out)) ||
+          (row->x != nullptr &&
+           (row->norm_weight == nullptr || row->normed == nullptr || row->hidden <= 0)))
+      {
+        throw InvalidArgument("the pages launch takes the row launch's work for one split layer "
+                              "of FP16 pages with no key bias, mass or scores, q and k rows of "
+                              "the cache's shape, 16-byte aligned rows and a RoPE table covering "
+                              "the current position");
+      }
+      d.row_qk = row->qk;
+      d.row_qk_out = row->qk_out;
+      d.row_v = row->values;
+      d.row_table = row->table;
+      d.row_q_heads = row->q_heads;
+      d.row_x = row->x;
+      d.row_norm_weight = row->norm_weight;
+      d.row_normed = row->normed;
+      d.row_hidden = row->hidden;
+      d.row_eps = row->eps;
+    }
     int stream_blocks = 0;
     if (streaming)
     {
@@ -2296,7 +2516,8 @@ namespace mi
     // resident at once: below that, halving the waves halves the launch's
     // parallelism (Qwen2.5-0.5B at 8K: 6.8 us a layer unpacked, 9.9 packed).
     const bool packed =
-        !streaming && a.head_dim == 64 && d.k_bias == nullptr && a.kv_heads % 2 == 0 &&
+        !streaming && row == nullptr && a.head_dim == 64 && d.k_bias == nullptr &&
+        a.kv_heads % 2 == 0 &&
         2 * group <= kMaxGroup &&
         static_cast<long long>(pages) * a.kv_heads * ls.layers >
             resident_pages_waves_64(pages_kernel_lds(group, 64, false));
@@ -2367,8 +2588,11 @@ namespace mi
             grid_splits = d.busy_splits;
           }
         }
-        hipLaunchKernelGGL(pages_kernel, dim3(grid_splits, d.kv_heads, ls.layers), dim3(kThreads),
-                           lds, stream, d);
+        // With the row's RMSNorm: one more column of workgroups (the first
+        // forms it; the rest end at once).
+        const int norm_splits = row != nullptr && row->x != nullptr ? 1 : 0;
+        hipLaunchKernelGGL(pages_kernel, dim3(grid_splits + norm_splits, d.kv_heads, ls.layers),
+                           dim3(kThreads), lds, stream, d);
         hip_check(hipGetLastError(), "decode pages kernel launch");
       }
       const int combine_blocks = a.heads * (hd / (4 * kQuads)) + mass_blocks +
@@ -2379,7 +2603,22 @@ namespace mi
                          dim3(kCombineThreads), 0, stream, d);
       hip_check(hipGetLastError(), "decode combine kernel launch");
     };
-    if (a.head_dim == 128)
+    if (row != nullptr)
+    {
+      if (a.head_dim == 128)
+      {
+        run(decode_pages_kernel<128, false, true>, decode_stream_kernel<128>,
+            decode_combine_kernel<128, false>, decode_combine_kernel<128, true>, 128,
+            stream_kernel_lds<128>(), 128);
+      }
+      else
+      {
+        run(decode_pages_kernel<64, false, true>, decode_stream_kernel<64>,
+            decode_combine_kernel<64, false>, decode_combine_kernel<64, true>, 64,
+            stream_kernel_lds<64>(), 64);
+      }
+    }
+    else if (a.head_dim == 128)
     {
       if (d.k_bias != nullptr)
       {

@@ -375,6 +375,15 @@ namespace mi
     // (the page quantised, or copied at FP16, from the open page's rows and
     // the step's k and v rows into its slot). Null: no seal.
     const StepStore *seal;
+    // The row launch's work done by the pages launch (one split layer of
+    // FP16 pages of a cache that does not seal, no key bias): RMSNorm of
+    // row->x by one more workgroup, q and the current row's k (position
+    // AttentionArgs::seq_k - 1, which row->table covers) turned by RoPE in
+    // the waves that read them, and that row's k and values stored into its
+    // page (row->pages) by the wave that reads the page. AttentionArgs::q is
+    // row->qk's raw q rows; row->qk_out (optional) receives the turned rows.
+    // Null: none.
+    const RowPrep *row;
   };
   // Whether the fast path takes this decode: one query, no key bias, 32-token
   // pages, head_dim 64 or 128, a group of at most 16 heads, 16-byte aligned

@@ -1322,6 +1322,81 @@ namespace mi
     launch_row_prep(r, stream);
   }
 
+  void KVPages::attend_row(int layer, const void *qk, void *qk_out, int q_heads, int seq_k,
+                           const RopeTable &rope, const void *values, void *out, const float *x,
+                           const void *norm_weight, void *normed, int hidden, float eps)
+  {
+    require_layer(layer);
+    if (seals_)
+    {
+      throw LogicError("the row's attention stores into FP16 pages; this cache seals its pages");
+    }
+    if (rope.head_dim() != head_dim_ || rope.data() == nullptr || rope.positions() < seq_k)
+    {
+      throw InvalidArgument("the RoPE table is for head_dim " + std::to_string(rope.head_dim()) +
+                            " with " + std::to_string(rope.positions()) +
+                            " positions; the row needs head_dim " + std::to_string(head_dim_) +
+                            " covering " + std::to_string(seq_k));
+    }
+    if (seq_k <= 0 || seq_k > capacity_tokens())
+    {
+      throw OutOfRange("seq_k " + std::to_string(seq_k) + " is not a position on pages (1 to " +
+                       std::to_string(capacity_tokens()) + ")");
+    }
+    if (q_heads <= 0 || q_heads % kv_heads_ != 0 || qk == nullptr || values == nullptr ||
+        out == nullptr ||
+        (x != nullptr && (norm_weight == nullptr || normed == nullptr || hidden <= 0)))
+    {
+      throw InvalidArgument("the row's attention needs q and k rows (a whole number of q heads "
+                            "a KV head), the values, the output and, with x, the norm weight, "
+                            "its output and a positive hidden size");
+    }
+    const hipStream_t stream = runtime_stream();
+    sync_tables(stream);
+    const std::size_t table_row = static_cast<std::size_t>(layer) * table_.stride();
+    RowPrep r{};
+    r.x = x;
+    r.norm_weight = static_cast<const std::uint16_t *>(norm_weight);
+    r.normed = static_cast<std::uint16_t *>(normed);
+    r.hidden = hidden;
+    r.eps = eps;
+    r.qk = static_cast<const std::uint16_t *>(qk);
+    r.qk_out = static_cast<std::uint16_t *>(qk_out);
+    r.q_heads = q_heads;
+    r.kv_heads = kv_heads_;
+    r.head_dim = head_dim_;
+    r.table = rope.data();
+    r.table_positions = rope.positions();
+    r.values = static_cast<const std::uint16_t *>(values);
+    r.pages = table_.addresses() + table_row;
+    r.page_tokens = page_tokens_;
+    r.positions = capacity_tokens();
+    AttentionArgs a{};
+    a.q = r.qk;
+    a.out = static_cast<std::uint16_t *>(out);
+    a.seq_q = 1;
+    a.seq_k = seq_k;
+    a.heads = q_heads;
+    a.kv_heads = kv_heads_;
+    a.head_dim = head_dim_;
+    a.workspace = &workspace_;
+    KVSource kv{};
+    kv.page_tokens = page_tokens_;
+    kv.layout = Layout::kPaged;
+    kv.pages = r.pages;
+    kv.may_be_at[kFP16] = true;
+    if (!decode_fast_applies(kv, a))
+    {
+      throw InvalidArgument("the row's attention takes 32-token pages, head_dim 64 or 128, at "
+                            "most 16 q heads a KV head and 16-byte aligned rows");
+    }
+    DecodeLayers one{};
+    one.split = true;
+    one.layers = 1;
+    one.row = &r;
+    launch_decode_layers(kv, a, one, stream);
+  }
+
   StepStore KVPages::step_store(int layer, const void *keys, const void *values,
                                 const int *position)
   {

@@ -36,10 +36,8 @@ namespace mi
     __device__ inline void rotate_pair(const std::uint16_t *row, int j, int half, float2 cs,
                                        std::uint16_t *out, std::uint16_t *also = nullptr)
     {
-      const float x1 = h2f(row[j]);
-      const float x2 = h2f(row[j + half]);
-      const std::uint16_t lo = __half_as_ushort(__float2half(x1 * cs.x - x2 * cs.y));
-      const std::uint16_t hi = __half_as_ushort(__float2half(x2 * cs.x + x1 * cs.y));
+      std::uint16_t lo, hi;
+      rope_pair(h2f(row[j]), h2f(row[j + half]), cs.x, cs.y, lo, hi);
       out[j] = lo;
       out[j + half] = hi;
       if (also != nullptr)
@@ -132,39 +130,6 @@ namespace mi
         const __half lo = __float2half_rn(value - __half2float(hi));
         angles[2 * t * head_dim + c] = __half_as_ushort(hi);
         angles[(2 * t + 1) * head_dim + c] = __half_as_ushort(lo);
-      }
-    }
-
-    // x * scale * w for the row's elements, one fp16 rounding each, eight a
-    // thread through 16-byte stores where the row allows, else one.
-    template <typename In>
-    __device__ inline void normed_row(const In *x, const std::uint16_t *w, std::uint16_t *out,
-                                      int hidden, float scale)
-    {
-      const bool wide = hidden % 8 == 0 && (reinterpret_cast<std::uintptr_t>(out) |
-                                            reinterpret_cast<std::uintptr_t>(w)) % 16 == 0;
-      if (wide)
-      {
-        for (int r = threadIdx.x; r < hidden / 8; r += blockDim.x)
-        {
-          const u32x4 wv = *reinterpret_cast<const u32x4 *>(w + 8 * r);
-          u32x4 o;
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-          {
-            const float a = widen_value(x, 8 * r + 2 * k) * scale * h2f(static_cast<std::uint16_t>(wv[k]));
-            const float b =
-                widen_value(x, 8 * r + 2 * k + 1) * scale * h2f(static_cast<std::uint16_t>(wv[k] >> 16));
-            o[k] = static_cast<unsigned>(__half_as_ushort(__float2half(a))) |
-                   (static_cast<unsigned>(__half_as_ushort(__float2half(b))) << 16);
-          }
-          *reinterpret_cast<u32x4 *>(out + 8 * r) = o;
-        }
-        return;
-      }
-      for (int i = threadIdx.x; i < hidden; i += blockDim.x)
-      {
-        out[i] = __half_as_ushort(__float2half(widen_value(x, i) * scale * h2f(w[i])));
       }
     }
 

@@ -539,6 +539,14 @@ namespace mi
     void rope_store(int layer, const void *qk, void *qk_out, int q_heads, const int *position,
                     const RopeTable &rope, const void *values, const float *x,
                     const void *norm_weight, void *normed, int hidden, float eps);
+    // For a cache that does not seal: rope_store at position seq_k - 1 and
+    // attention's one-query decode over the positions before seq_k, as the
+    // pages launch and its combine (the pages launch turns q and the row's
+    // k, stores the row in its page and forms the RMSNorm when x is given):
+    // the bits of rope_store then attention given partials (split).
+    void attend_row(int layer, const void *qk, void *qk_out, int q_heads, int seq_k,
+                    const RopeTable &rope, const void *values, void *out, const float *x,
+                    const void *norm_weight, void *normed, int hidden, float eps);
     // The layer's store target for a step whose projection writes its row
     // (launch_qkv_step): the open page (the step's row goes there unless it
     // is the page's last) and the page table row for the seal; `keys` and

@@ -586,10 +586,9 @@ namespace mi
           continue;
         }
         // RoPE of the rounded pair, as the RoPE kernel rotates it.
-        const float x1 = h2f(static_cast<std::uint16_t>(h0));
-        const float x2 = h2f(static_cast<std::uint16_t>(h1));
-        const std::uint16_t o1 = to_half(x1 * c - x2 * sn);
-        const std::uint16_t o2 = to_half(x2 * c + x1 * sn);
+        std::uint16_t o1, o2;
+        rope_pair(h2f(static_cast<std::uint16_t>(h0)), h2f(static_cast<std::uint16_t>(h1)), c, sn,
+                  o1, o2);
         const std::size_t at = static_cast<std::size_t>(seg == 0 ? head : p.heads + head) *
                                    p.head_dim + j;
         p.qk[at] = o1;

@@ -79,6 +79,8 @@ SIGNATURES = {
     "mi_kv_attention_at": ((_vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp), C.c_int),
     "mi_kv_stored_on_device": ((_vp, _i), C.c_int),
     "mi_kv_rope_store": ((_vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f), C.c_int),
+    "mi_kv_attend_row": ((_vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _f),
+                         C.c_int),
     "mi_decode_step_create": ((C.POINTER(_vp), _vp, C.POINTER(_ModelShape), _vp, _vp, _vp,
                                C.POINTER(_LayerWeights), _vp, _i), C.c_int),
     "mi_decode_step_destroy": ((_vp,), C.c_int),
@@ -1131,6 +1133,34 @@ class KVPages:
             na = _need(_span(out), hidden, "normed")
         _check(lib.mi_kv_rope_store(self._h, layer, qa, oa, q_heads, position.address, rope._h,
                                     _need(_span(values), width, "values"), xa, wa, na, hidden,
+                                    float(eps)))
+
+    def attend_row(self, layer: int, qk, qk_out, q_heads: int, seq_k: int, rope: "RopeTable",
+                   values, out, norm=None) -> None:
+        """Beyond the reference's surface, for a cache that does not seal:
+        rope_store at position seq_k - 1 then attention's one-query split
+        decode over the positions before seq_k, as two launches (the pages
+        launch turns q and the row's k, stores the row and forms the
+        RMSNorm; then the combine). qk_out, when not None, receives the
+        turned rows. The bits of rope_store then attention with partials."""
+        width = self.kv_width
+        hd = rope.head_dim
+        rows = q_heads * hd + width
+        qa = _need(_span(qk), rows, "qk")
+        oa = _need(_span(qk_out), rows, "qk_out") if qk_out is not None else None
+        if qa == oa:
+            raise ValueError("rope cannot write over its input")
+        xa = wa = na = None
+        hidden, eps = 0, 0.0
+        if norm is not None:
+            x, weight, normed, eps = norm
+            hidden = x.numel
+            xa = x.address
+            wa = _need(_span(weight), hidden, "norm weight")
+            na = _need(_span(normed), hidden, "normed")
+        _check(lib.mi_kv_attend_row(self._h, layer, qa, oa, q_heads, seq_k, rope._h,
+                                    _need(_span(values), width, "values"),
+                                    _need(_span(out), q_heads * hd, "out"), xa, wa, na, hidden,
                                     float(eps)))
 
     def stored_on_device(self, end: int) -> None:

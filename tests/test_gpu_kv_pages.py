@@ -248,6 +248,76 @@ def test_the_row_launch_is_rmsnorm_rope_and_store_to_the_bit():
                            rope, put(np.zeros(128)))
 
 
+def test_the_row_attention_is_rope_store_then_attention_to_the_bit():
+    """attend_row (config 2's layer as two launches: the pages launch turns
+    q and the row's k, stores the row and forms the RMSNorm, then the
+    combine) against rope_store then attention with partials on a twin
+    cache: the output, the normed row, the turned rows and every page byte
+    agree to the bit, at the 0.5B and 1.5B head shapes mid-page, at a page's
+    last row and a page's first, and at a Llama shape long enough that the
+    launch is bounded to the resident workgroups (the current page is then a
+    wave's second). The two calls are held to the float64 references by the
+    row launch and decode tests."""
+    m = mi()
+    d = m.device
+    for heads, kv, hd, hidden, seq, positions in ((14, 2, 64, 896, 160, (100, 127, 128)),
+                                                  (12, 2, 128, 1536, 96, (33, 63, 64)),
+                                                  (32, 8, 128, 4096, 16448, (16447,))):
+        rng = np.random.default_rng(hd + kv)
+        rope = d.RopeTable(hd, 1e6)
+        rope.cover(seq + 64)
+        k, v = normal(rng, seq, kv, hd), normal(rng, seq, kv, hd)
+        (alloc_a, a), (alloc_b, b) = pages_for(32, kv, hd, 0), pages_for(32, kv, hd, 0)
+        for cache in (a, b):
+            store_in_runs(cache, 1, k, v, [seq])
+            cache.reserve(seq + 1)
+        norm_w = put(rng.uniform(0.5, 1.5, hidden))
+        partials = d.empty_f32(d.attention_partials(hd))
+        rows = (heads + kv) * hd
+        for pos in positions:
+            for with_norm in (True, False):
+                announce("row attention", heads, kv, hd, pos, with_norm)
+                x = d.upload_f32(rng.standard_normal(hidden).astype(np.float32))
+                raw = put(normal(rng, heads + kv, hd))
+                vals = put(normal(rng, kv, hd))
+                n_a, qk_a, out_a = d.empty(hidden), d.empty(rows), d.empty(heads * hd)
+                n_b, qk_b, out_b = d.empty(hidden), d.empty(rows), d.empty(heads * hd)
+                a.rope_store(1, raw, qk_a, heads, d.DeviceIndex([pos]), rope, vals,
+                             norm=(x, norm_w, n_a, 1e-6) if with_norm else None)
+                a.attention(1, d.view(qk_a, 0, heads * hd), None, None, out_a, 1, pos + 1, heads,
+                            kv, hd, None, None, None, partials)
+                b.attend_row(1, raw, qk_b, heads, pos + 1, rope, vals, out_b,
+                             norm=(x, norm_w, n_b, 1e-6) if with_norm else None)
+                got = out_b.to_numpy()
+                assert np.isfinite(got).all()
+                np.testing.assert_array_equal(got, out_a.to_numpy())
+                np.testing.assert_array_equal(qk_b.to_numpy(), qk_a.to_numpy())
+                if with_norm:
+                    np.testing.assert_array_equal(n_b.to_numpy(), n_a.to_numpy())
+                page = pos // 32
+                for near in range(max(0, page - 1), page + 1):
+                    np.testing.assert_array_equal(alloc_b.read(1, near), alloc_a.read(1, near))
+        # Without qk_out: the same output and page.
+        pos = positions[0]
+        raw, vals = put(normal(rng, heads + kv, hd)), put(normal(rng, kv, hd))
+        out_a, out_b = d.empty(heads * hd), d.empty(heads * hd)
+        b.attend_row(1, raw, d.empty(rows), heads, pos + 1, rope, vals, out_a)
+        b.attend_row(1, raw, None, heads, pos + 1, rope, vals, out_b)
+        np.testing.assert_array_equal(out_b.to_numpy(), out_a.to_numpy())
+    # A cache that seals, and a table short of the position, are refused.
+    _, sealing = pages_for(32, 2, 64, 1)
+    rope = d.RopeTable(64, 1e6)
+    rope.cover(64)
+    with pytest.raises(Exception, match="seals"):
+        sealing.attend_row(0, put(np.zeros(16 * 64)), None, 14, 1, rope, put(np.zeros(128)),
+                           d.empty(14 * 64))
+    _, plain = pages_for(32, 2, 64, 0)
+    plain.reserve(256)
+    with pytest.raises(Exception, match="covering"):
+        plain.attend_row(0, put(np.zeros(16 * 64)), None, 14, 200, rope, put(np.zeros(128)),
+                         d.empty(14 * 64))
+
+
 def test_asking_for_the_mass_changes_no_output_bit():
     for P in (16, 32):
         for tier in (0, 2):
