@@ -755,8 +755,13 @@ namespace mi
         }
       }
 
+      // Lane groups 0-1 hold x1 (own) and need x1 c - x2 s; groups 2-3 hold
+      // x2 and need x2 c + x1 s. Both are own c + partner' s, where
+      // partner' is x2 with its sign flipped (exact) for groups 0-1 and x1
+      // for groups 2-3: the products and the sum round as rope_pair's do.
       __device__ void turn(half8 *dst, const u32x4 *words, int g) const
       {
+        const unsigned flip = g < 2 ? 0x80008000u : 0u;
 #pragma unroll
         for (int s = 0; s < HD / 32; ++s)
         {
@@ -766,15 +771,15 @@ namespace mi
           {
             float lo_word, hi_word;
             lane_pair32(__uint_as_float(words[s][w]), lo_word, hi_word);
-            const unsigned x1w = __float_as_uint(lo_word), x2w = __float_as_uint(hi_word);
-            const f32x4 a = cs[4 * s + w];
-            std::uint16_t lo0, hi0, lo1, hi1;
-            rope_pair(h2f(static_cast<std::uint16_t>(x1w)), h2f(static_cast<std::uint16_t>(x2w)),
-                      a[0], a[1], lo0, hi0);
-            rope_pair(h2f(static_cast<std::uint16_t>(x1w >> 16)),
-                      h2f(static_cast<std::uint16_t>(x2w >> 16)), a[2], a[3], lo1, hi1);
-            out[w] = g < 2 ? (static_cast<unsigned>(lo0) | (static_cast<unsigned>(lo1) << 16))
-                           : (static_cast<unsigned>(hi0) | (static_cast<unsigned>(hi1) << 16));
+            const unsigned own = words[s][w];
+            const unsigned partner = __float_as_uint(g < 2 ? hi_word : lo_word) ^ flip;
+            const f32x4 a = cs[4 * s + w]; // cos, sin of the word's two angles
+            const float r0 = h2f(static_cast<std::uint16_t>(own)) * a[0] +
+                             h2f(static_cast<std::uint16_t>(partner)) * a[1];
+            const float r1 = h2f(static_cast<std::uint16_t>(own >> 16)) * a[2] +
+                             h2f(static_cast<std::uint16_t>(partner >> 16)) * a[3];
+            out[w] = static_cast<unsigned>(__half_as_ushort(__float2half(r0))) |
+                     (static_cast<unsigned>(__half_as_ushort(__float2half(r1))) << 16);
           }
           dst[s] = as_half8(out);
         }
@@ -785,12 +790,18 @@ namespace mi
     // 16 + r, the lane's run), values at v0/v1, all requested at once so that
     // the page costs one trip to memory. With kCurrent, row `cur_row` (-1:
     // none) is cur_k and cur_v from registers instead.
-    template <int HD, bool kBias = false, bool kCurrent = false>
+    struct NoHook
+    {
+      __device__ void operator()() const {}
+    };
+
+    template <int HD, bool kBias = false, bool kCurrent = false, typename Hook = NoHook>
     __device__ inline void fp16_page(Running<HD> &run, const PageCtx &c, const half8 *qb,
                                      const std::uint16_t *k0, const std::uint16_t *k1,
                                      const std::uint16_t *v0, const std::uint16_t *v1,
                                      const KeyBias<HD> *bias = nullptr, int cur_row = -1,
-                                     const half8 *cur_k = nullptr, const half8 *cur_v = nullptr)
+                                     const half8 *cur_k = nullptr, const half8 *cur_v = nullptr,
+                                     Hook hook = {})
     {
       constexpr int S = HD / 32;
       half8 k[2][S], v[2][S];
@@ -800,6 +811,7 @@ namespace mi
       load_fp16_run<HD>(v[1], v1);
       if constexpr (kCurrent)
       {
+        hook(); // work that needs no page byte, while the page's are in flight
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
         {
@@ -993,15 +1005,15 @@ namespace mi
       {
         entry(p0, first_tier_lane, first_page_raw);
       }
-      if constexpr (kCurrent)
-      {
+      // (kCurrent) q and the current row's k turned, and the turned rows
+      // out: split 0's first wave writes q's, the wave that stores the row
+      // its k. Run while the wave's first page's bytes are in flight.
+      const auto turn_rows = [&]() {
         turn_in.turn(qb, turn_in.raw, g);
         if (holds_cur)
         {
           turn_in.turn(cur_k, k_raw, g);
         }
-        // The turned q rows out, once (split 0's first wave), and the
-        // turned k row by the wave that stores it.
         if (a.row_qk_out != nullptr && split == 0 && wave == 0 && r < G)
         {
 #pragma unroll
@@ -1021,7 +1033,7 @@ namespace mi
                                        g * kRun + 8 * si) = as_u32x4(cur_k[si]);
           }
         }
-      }
+      };
 
       // The key bias: lane i holds b_i and b_i' of this KV head; the
       // workgroup's angle rows follow the epilogue's LDS.
@@ -1040,133 +1052,166 @@ namespace mi
       const auto *open = a.open_table != nullptr
                              ? reinterpret_cast<const std::uint16_t *>(a.open_table[layer])
                              : a.open;
-      bool first = true;
-      for (int i = 0; i < p_count; ++i)
+      if constexpr (kCurrent)
       {
-        const int p = p0 + i * p_step;
-        if (p >= p_bound)
-        {
-          break;
-        }
-        const bool sealed = !a.causal || p < own;
-        int tier_lane = first_tier_lane;
-        unsigned long long page_raw = first_page_raw;
-        if (i > 0)
-        {
-          entry(p, tier_lane, page_raw);
-        }
-        const int tier_raw = __builtin_amdgcn_readfirstlane(tier_lane);
-        const int tier = !a.causal ? static_cast<int>(kFP16) : (p < own ? tier_raw : kOwnPage);
-        const auto *page = reinterpret_cast<const std::uint8_t *>(sealed ? page_raw : 0ull);
-        PageCtx c;
-        c.r = r;
-        c.g = g;
-        c.group = G;
-        c.last = a.seq_k - 1 - p * kPageTokens;
-        c.partial = c.last < kPageTokens - 1;
-        c.first = first;
-        c.scale = a.scale;
-        {
-          const int h = kvh * G + r; // rows past the group are never stored
-          c.stat = stats + ((static_cast<std::size_t>(h / SG) * a.pages + p) * SG + h % SG) * 2;
-        }
-        KeyBias<HD> bias;
-        if constexpr (kBias)
-        {
-          bias.b = bias_b;
-          bias.b2 = bias_b2;
-          bias.lds = reinterpret_cast<float *>(meta + HD);
-          bias.lane = lane;
-          // cos and sin of the lane's angle at the page's first row.
-          bias.turn = *reinterpret_cast<const float2 *>(
-              a.rope + 2 * (static_cast<std::size_t>(p) * kPageTokens * (HD / 2) + lane % (HD / 2)));
-          bias.rows = angle_rows;
-        }
-        const KeyBias<HD> *page_bias = &bias;
-        if (tier == kUnreadPage)
-        {
-          if (g == 0 && r < G)
+        // FP16 pages of a cache that does not seal: page i of the wave's,
+        // its first with the turn while its bytes are in flight (the first
+        // page outside the loop, so that the turn's registers end there).
+        const auto fp16_at = [&](int i, auto hook) {
+          const int p = p0 + i * p_step;
+          unsigned long long page_raw = first_page_raw;
+          if (i > 0)
           {
-            *reinterpret_cast<float2 *>(c.stat) = make_float2(-INFINITY, 0.0f);
+            int tier_lane;
+            entry(p, tier_lane, page_raw);
           }
-          continue;
-        }
-        switch (tier)
-        {
-        case kINT8:
-          quantised_page<HD, 8, kBias>(run, c, qb, page, a.lay[kINT8], W, kvh,
-                                         a.value_kv_heads, value_kvh, lane, meta, page_bias);
-          break;
-        case kINT4:
-          quantised_page<HD, 4, kBias>(run, c, qb, page, a.lay[kINT4], W, kvh,
-                                         a.value_kv_heads, value_kvh, lane, meta, page_bias);
-          break;
-        case kINT2:
-          quantised_page<HD, 2, kBias>(run, c, qb, page, a.lay[kINT2], W, kvh,
-                                         a.value_kv_heads, value_kvh, lane, meta, page_bias);
-          break;
-        case kOwnPage:
-        {
-          // Rows before `start` from the open page, the rest from the chunk;
-          // rows past the last key read row 0 (masked).
-          const int t_start = a.start - p * kPageTokens;
-          const std::uint16_t *ck = a.chunk_k + li * a.chunk_stride;
-          const std::uint16_t *cv = a.chunk_v + li * a.chunk_stride;
-          const std::uint16_t *rk[2], *rv[2];
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+          PageCtx c;
+          c.r = r;
+          c.g = g;
+          c.group = G;
+          c.last = a.seq_k - 1 - p * kPageTokens;
+          c.partial = c.last < kPageTokens - 1;
+          c.first = i == 0;
+          c.scale = a.scale;
           {
-            const int t = kb * 16 + r;
-            const int tt = t <= c.last ? t : 0;
-            if (tt < t_start)
+            const int h = kvh * G + r; // rows past the group are never stored
+            c.stat = stats + ((static_cast<std::size_t>(h / SG) * a.pages + p) * SG + h % SG) * 2;
+          }
+          const auto *h = reinterpret_cast<const std::uint16_t *>(page_raw);
+          const bool here = holds_cur && p == cur_page;
+          fp16_page<HD, false, true>(run, c, qb, h + static_cast<std::size_t>(r) * W + run0,
+                                     h + static_cast<std::size_t>(16 + r) * W + run0,
+                                     h + static_cast<std::size_t>(kPageTokens + r) * W + run0,
+                                     h + static_cast<std::size_t>(kPageTokens + 16 + r) * W + run0,
+                                     nullptr, here ? cur_t : -1, cur_k, cur_v, hook);
+          // The current row into its page: its four lanes of row cur_t
+          // (each row's k and v runs are read by this wave only).
+          if (here && (cur_t % 16) == r)
+          {
+            auto *row = const_cast<std::uint16_t *>(h) + static_cast<std::size_t>(cur_t) * W + run0;
+#pragma unroll
+            for (int si = 0; si < S; ++si)
             {
-              rk[kb] = open + static_cast<std::size_t>(tt) * W + run0;
-              rv[kb] = open + static_cast<std::size_t>(kPageTokens + tt) * W + run0;
-            }
-            else
-            {
-              rk[kb] = ck + static_cast<std::size_t>(tt - t_start) * W + run0;
-              rv[kb] = cv + static_cast<std::size_t>(tt - t_start) * W + run0;
+              *reinterpret_cast<u32x4 *>(row + 8 * si) = as_u32x4(cur_k[si]);
+              *reinterpret_cast<u32x4 *>(row + kPageTokens * W + 8 * si) = as_u32x4(cur_v[si]);
             }
           }
-          fp16_page<HD, kBias>(run, c, qb, rk[0], rk[1], rv[0], rv[1], page_bias);
-          break;
-        }
-        default:
+        };
+        if (p0 < p_bound)
         {
-          const auto *h = reinterpret_cast<const std::uint16_t *>(page);
-          if constexpr (kCurrent)
+          fp16_at(0, turn_rows);
+          for (int i = 1; i < p_count && p0 + i * p_step < p_bound; ++i)
           {
-            const bool here = holds_cur && p == cur_page;
-            fp16_page<HD, kBias, true>(run, c, qb, h + static_cast<std::size_t>(r) * W + run0,
-                                       h + static_cast<std::size_t>(16 + r) * W + run0,
-                                       h + static_cast<std::size_t>(kPageTokens + r) * W + run0,
-                                       h + static_cast<std::size_t>(kPageTokens + 16 + r) * W + run0,
-                                       page_bias, here ? cur_t : -1, cur_k, cur_v);
-            // The current row into its page: its four lanes of row cur_t
-            // (each row's k and v runs are read by this wave only).
-            if (here && (cur_t % 16) == r)
+            fp16_at(i, NoHook{});
+          }
+        }
+      }
+      else
+      {
+        bool first = true;
+        for (int i = 0; i < p_count; ++i)
+        {
+          const int p = p0 + i * p_step;
+          if (p >= p_bound)
+          {
+            break;
+          }
+          const bool sealed = !a.causal || p < own;
+          int tier_lane = first_tier_lane;
+          unsigned long long page_raw = first_page_raw;
+          if (i > 0)
+          {
+            entry(p, tier_lane, page_raw);
+          }
+          const int tier_raw = __builtin_amdgcn_readfirstlane(tier_lane);
+          const int tier = !a.causal ? static_cast<int>(kFP16) : (p < own ? tier_raw : kOwnPage);
+          const auto *page = reinterpret_cast<const std::uint8_t *>(sealed ? page_raw : 0ull);
+          PageCtx c;
+          c.r = r;
+          c.g = g;
+          c.group = G;
+          c.last = a.seq_k - 1 - p * kPageTokens;
+          c.partial = c.last < kPageTokens - 1;
+          c.first = first;
+          c.scale = a.scale;
+          {
+            const int h = kvh * G + r; // rows past the group are never stored
+            c.stat = stats + ((static_cast<std::size_t>(h / SG) * a.pages + p) * SG + h % SG) * 2;
+          }
+          KeyBias<HD> bias;
+          if constexpr (kBias)
+          {
+            bias.b = bias_b;
+            bias.b2 = bias_b2;
+            bias.lds = reinterpret_cast<float *>(meta + HD);
+            bias.lane = lane;
+            // cos and sin of the lane's angle at the page's first row.
+            bias.turn = *reinterpret_cast<const float2 *>(
+                a.rope + 2 * (static_cast<std::size_t>(p) * kPageTokens * (HD / 2) + lane % (HD / 2)));
+            bias.rows = angle_rows;
+          }
+          const KeyBias<HD> *page_bias = &bias;
+          if (tier == kUnreadPage)
+          {
+            if (g == 0 && r < G)
             {
-              auto *row = const_cast<std::uint16_t *>(h) + static_cast<std::size_t>(cur_t) * W + run0;
-#pragma unroll
-              for (int si = 0; si < S; ++si)
+              *reinterpret_cast<float2 *>(c.stat) = make_float2(-INFINITY, 0.0f);
+            }
+            continue;
+          }
+          switch (tier)
+          {
+          case kINT8:
+            quantised_page<HD, 8, kBias>(run, c, qb, page, a.lay[kINT8], W, kvh,
+                                           a.value_kv_heads, value_kvh, lane, meta, page_bias);
+            break;
+          case kINT4:
+            quantised_page<HD, 4, kBias>(run, c, qb, page, a.lay[kINT4], W, kvh,
+                                           a.value_kv_heads, value_kvh, lane, meta, page_bias);
+            break;
+          case kINT2:
+            quantised_page<HD, 2, kBias>(run, c, qb, page, a.lay[kINT2], W, kvh,
+                                           a.value_kv_heads, value_kvh, lane, meta, page_bias);
+            break;
+          case kOwnPage:
+          {
+            // Rows before `start` from the open page, the rest from the chunk;
+            // rows past the last key read row 0 (masked).
+            const int t_start = a.start - p * kPageTokens;
+            const std::uint16_t *ck = a.chunk_k + li * a.chunk_stride;
+            const std::uint16_t *cv = a.chunk_v + li * a.chunk_stride;
+            const std::uint16_t *rk[2], *rv[2];
+  #pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+            {
+              const int t = kb * 16 + r;
+              const int tt = t <= c.last ? t : 0;
+              if (tt < t_start)
               {
-                *reinterpret_cast<u32x4 *>(row + 8 * si) = as_u32x4(cur_k[si]);
-                *reinterpret_cast<u32x4 *>(row + kPageTokens * W + 8 * si) = as_u32x4(cur_v[si]);
+                rk[kb] = open + static_cast<std::size_t>(tt) * W + run0;
+                rv[kb] = open + static_cast<std::size_t>(kPageTokens + tt) * W + run0;
+              }
+              else
+              {
+                rk[kb] = ck + static_cast<std::size_t>(tt - t_start) * W + run0;
+                rv[kb] = cv + static_cast<std::size_t>(tt - t_start) * W + run0;
               }
             }
+            fp16_page<HD, kBias>(run, c, qb, rk[0], rk[1], rv[0], rv[1], page_bias);
+            break;
           }
-          else
+          default:
           {
+            const auto *h = reinterpret_cast<const std::uint16_t *>(page);
             fp16_page<HD, kBias>(run, c, qb, h + static_cast<std::size_t>(r) * W + run0,
                           h + static_cast<std::size_t>(16 + r) * W + run0,
                           h + static_cast<std::size_t>(kPageTokens + r) * W + run0,
                           h + static_cast<std::size_t>(kPageTokens + 16 + r) * W + run0, page_bias);
+            break;
           }
-          break;
+          }
+          first = false;
         }
-        }
-        first = false;
       }
 
       // The workgroup's waves into one partial: each wave's state to LDS,
