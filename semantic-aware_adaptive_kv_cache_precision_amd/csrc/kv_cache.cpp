@@ -755,13 +755,23 @@ namespace mi
     }
     try
     {
-      ensure_move_events();
-      hip_check(hipEventRecord(move_events_[0], stream), "hipEventRecord before a move");
+      // The shadow's time is reported for a first downgrade only: the
+      // events cost ~1.3 us of host time a move, so no other move records
+      // them.
+      const bool timed = shadow_seconds != nullptr && first_downgrade;
+      if (timed)
+      {
+        ensure_move_events();
+        hip_check(hipEventRecord(move_events_[0], stream), "hipEventRecord before a move");
+      }
       if (!launch_move_one(m, spaces, page_tokens_, kv_heads_, head_dim_, stream))
       {
         throw LogicError("a single move's launch refused a shape move_one_applies took");
       }
-      hip_check(hipEventRecord(move_events_[1], stream), "hipEventRecord after a move");
+      if (timed)
+      {
+        hip_check(hipEventRecord(move_events_[1], stream), "hipEventRecord after a move");
+      }
       if (compaction.size() > held)
       {
         // More than a launch holds (never for one free): the rest after it.
@@ -783,9 +793,12 @@ namespace mi
       // The launch that takes the shadow also makes the page: its device
       // time, when it takes one.
       float ms = 0.0f;
-      hip_check(hipEventElapsedTime(&ms, move_events_[0], move_events_[1]),
-                "hipEventElapsedTime of a move");
-      *shadow_seconds = first_downgrade ? ms * 1e-3 : 0.0;
+      if (first_downgrade)
+      {
+        hip_check(hipEventElapsedTime(&ms, move_events_[0], move_events_[1]),
+                  "hipEventElapsedTime of a move");
+      }
+      *shadow_seconds = ms * 1e-3;
     }
     return true;
   }
