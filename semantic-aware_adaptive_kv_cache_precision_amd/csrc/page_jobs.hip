@@ -112,17 +112,35 @@ namespace mi
                           Emit::kCodes);
     }
 
-    // A workgroup's copy of one page's bytes (16 bytes a thread a pass, then
-    // any last bytes one by one).
-    // A workgroup's copy of one page's bytes (16 bytes a thread a pass, then
-    // any last bytes one by one).
+    // A workgroup's copy of one page's bytes, 16 bytes a thread a pass and
+    // any last bytes one by one. Up to kCopyBatch passes' loads are issued
+    // before any of their stores, so that a page (32 KiB: 8 passes) is one
+    // trip to its source, not a trip a pass: the source may be host memory
+    // or the far side of the device, and a store may alias a later load
+    // for all the compiler knows. A thread past the last unit copies the
+    // last unit again (the same bytes to the same place), so that nothing
+    // in the batch is conditional: a branch's join would wait for its load.
+    constexpr int kCopyBatch = 8;
     __device__ inline void block_copy_page(std::uint8_t *dst, const std::uint8_t *src,
                                            unsigned long long bytes)
     {
+      typedef unsigned copy_unit __attribute__((ext_vector_type(4)));
       const unsigned long long units = bytes / 16;
-      for (unsigned long long i = threadIdx.x; i < units; i += kThreads)
+      for (unsigned long long base = 0; base < units; base += kCopyBatch * kThreads)
       {
-        reinterpret_cast<uint4 *>(dst)[i] = reinterpret_cast<const uint4 *>(src)[i];
+        copy_unit v[kCopyBatch];
+#pragma unroll
+        for (int j = 0; j < kCopyBatch; ++j)
+        {
+          const unsigned long long i = base + j * kThreads + threadIdx.x;
+          v[j] = reinterpret_cast<const copy_unit *>(src)[i < units ? i : units - 1];
+        }
+#pragma unroll
+        for (int j = 0; j < kCopyBatch; ++j)
+        {
+          const unsigned long long i = base + j * kThreads + threadIdx.x;
+          reinterpret_cast<copy_unit *>(dst)[i < units ? i : units - 1] = v[j];
+        }
       }
       if (threadIdx.x < bytes % 16)
       {
@@ -133,9 +151,11 @@ namespace mi
     // One page's move from FP16 (OneMove), a workgroup: the shadow copy and
     // the page at its new tier (the register quantiser, its W tasks over the
     // workgroup's lanes), then, after the barrier that waits for every read
-    // of the page, the compaction copies.
+    // of the page, the compaction copies. The launch is one workgroup, so
+    // its registers are not capped for occupancy (the batch quantiser's
+    // four waves a SIMD would spill its tasks here).
     template <int Bits, int HD>
-    __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+    __global__ void __launch_bounds__(kThreads)
         move_one_kernel(OneMove m, PageSpaces s, PageLayout L, int kv_heads)
     {
       if (m.has_shadow)
