@@ -76,12 +76,16 @@ namespace mi
   // kv_heads * head_dim >= 128 take the register quantiser (a lane a task of
   // 64 elements, nothing staged); any other shape the LDS one.
   // One page's move as one launch (one workgroup): the page's FP16 bytes to
-  // its shadow (shadow.from -> shadow.to) when has_shadow, the page at its
-  // new tier (page.from, FP16 rows, -> page.to: the register quantiser at
-  // `tier`), then, after a barrier, the compaction copies of the tier the
-  // page left, which may overwrite what came before them. It applies to a
-  // move from FP16 at a shape the register quantiser takes
-  // (move_one_applies); anything else takes the separate launches.
+  // its shadow (shadow.from -> shadow.to) when has_shadow; the shadow's rows
+  // into device staging (stage.from -> stage.to) when has_stage, then a
+  // barrier; the page at its new tier (page.from, FP16 rows, -> page.to: the
+  // register quantiser at `tier`, or a copy at FP16); then, after a barrier,
+  // the compaction copies of the tier the page left, which may overwrite
+  // what came before them. It applies at a shape the register quantiser
+  // takes (move_one_applies): a move from FP16 (its rows the page), and a
+  // move of a page that has a shadow (its rows the shadow: copied at FP16,
+  // staged first for a quantised tier, whose quantiser reads its rows
+  // twice); anything else takes the separate launches.
   struct OneMove
   {
     RefPair shadow;
@@ -90,6 +94,8 @@ namespace mi
     int has_shadow;
     int tier;
     int compact_count;
+    RefPair stage;
+    int has_stage;
   };
   bool launch_move_one(const OneMove &m, const PageSpaces &spaces, int page_tokens, int kv_heads,
                        int head_dim, hipStream_t stream);

@@ -702,14 +702,36 @@ namespace mi
     const bool first_downgrade = from == kFP16 && !shadows_.contains(key);
     shadows_.reserve(first_downgrade ? 1 : 0);
     // The page's FP16 rows (the page itself, or its shadow) and, before its
-    // first downgrade, its shadow's place.
+    // first downgrade, its shadow's place. A quantised page's rows are its
+    // shadow's: copied as they are to FP16, or staged in device memory
+    // first for a quantised tier.
+    const std::size_t fp16_bytes = bytes_at(kFP16);
+    if (from != kFP16 && target != kFP16 &&
+        (staging_ == nullptr || staging_->bytes() < fp16_bytes))
+    {
+      staging_.reset(); // waits for launches that may read the old one
+      staging_ = std::make_unique<DeviceBuffer>(fp16_bytes);
+    }
     const std::size_t shadows_before = shadows_.count();
     OneMove m{};
-    m.page.from = allocator_.ref_of(key);
-    if (first_downgrade)
+    if (from == kFP16)
     {
-      m.has_shadow = 1;
-      m.shadow = {m.page.from, page_ref(kShadowSpace, shadows_.add(key))};
+      m.page.from = allocator_.ref_of(key);
+      if (first_downgrade)
+      {
+        m.has_shadow = 1;
+        m.shadow = {m.page.from, page_ref(kShadowSpace, shadows_.add(key))};
+      }
+    }
+    else
+    {
+      m.page.from = page_ref(kShadowSpace, shadows_.number(key));
+      if (target != kFP16)
+      {
+        m.has_stage = 1;
+        m.stage = {m.page.from, page_ref(kStagingSpace, 0)};
+        m.page.from = m.stage.to;
+      }
     }
     m.tier = target;
     // The new page at the target tier's tail, under a staging key; a page
@@ -732,6 +754,7 @@ namespace mi
     }
     PageSpaces spaces = allocator_.spaces();
     spaces.shadows = shadows_.device_table(stream);
+    spaces.staging = staging_ ? reinterpret_cast<unsigned long long>(staging_->raw()) : 0;
     // The page table names the new page and the old one goes; its tier's
     // compaction copies ride in the move's launch, after the reads of the
     // old page, and the granules that tier gives up are released after it.
@@ -755,10 +778,11 @@ namespace mi
     }
     try
     {
-      // The shadow's time is reported for a first downgrade only: the
-      // events cost ~1.3 us of host time a move, so no other move records
-      // them.
-      const bool timed = shadow_seconds != nullptr && first_downgrade;
+      // The shadow's time (the launch's device time) is reported for a move
+      // that writes or reads a shadow only: the events cost ~1.3 us of host
+      // time a move, so no other move records them.
+      const bool touches_shadow = first_downgrade || from != kFP16;
+      const bool timed = shadow_seconds != nullptr && touches_shadow;
       if (timed)
       {
         ensure_move_events();
@@ -793,7 +817,7 @@ namespace mi
       // The launch that takes the shadow also makes the page: its device
       // time, when it takes one.
       float ms = 0.0f;
-      if (first_downgrade)
+      if (first_downgrade || from != kFP16)
       {
         hip_check(hipEventElapsedTime(&ms, move_events_[0], move_events_[1]),
                   "hipEventElapsedTime of a move");

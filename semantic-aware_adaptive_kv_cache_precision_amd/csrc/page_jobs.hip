@@ -148,12 +148,13 @@ namespace mi
       }
     }
 
-    // One page's move from FP16 (OneMove), a workgroup: the shadow copy and
+    // One page's move (OneMove), a workgroup: the shadow copy, the shadow's
+    // rows staged (then a barrier, so that every wave reads them whole), and
     // the page at its new tier (the register quantiser, its W tasks over the
-    // workgroup's lanes), then, after the barrier that waits for every read
-    // of the page, the compaction copies. The launch is one workgroup, so
-    // its registers are not capped for occupancy (the batch quantiser's
-    // four waves a SIMD would spill its tasks here).
+    // workgroup's lanes; Bits 16: a copy at FP16), then, after the barrier
+    // that waits for every read of the old page, the compaction copies. The
+    // launch is one workgroup, so its registers are not capped for occupancy
+    // (the batch quantiser's four waves a SIMD would spill its tasks here).
     template <int Bits, int HD>
     __global__ void __launch_bounds__(kThreads)
         move_one_kernel(OneMove m, PageSpaces s, PageLayout L, int kv_heads)
@@ -162,6 +163,16 @@ namespace mi
       {
         block_copy_page(resolve(s, m.shadow.to), resolve(s, m.shadow.from), s.shadow_bytes);
       }
+      if (m.has_stage)
+      {
+        block_copy_page(resolve(s, m.stage.to), resolve(s, m.stage.from), s.shadow_bytes);
+        __syncthreads();
+      }
+      if constexpr (Bits == 16)
+      {
+        block_copy_page(resolve(s, m.page.to), resolve(s, m.page.from), s.shadow_bytes);
+      }
+      else
       {
         const int W = kv_heads * HD;
         const auto *src = reinterpret_cast<const std::uint16_t *>(resolve(s, m.page.from));
@@ -459,9 +470,9 @@ namespace mi
 
   bool move_one_applies(int from, int tier, int page_tokens, int kv_heads, int head_dim)
   {
-    // A workgroup's reads of host memory are latency-bound: a move from a
-    // shadow keeps the wide launches.
-    return from == kFP16 && tier != kFP16 && register_shape(page_tokens, kv_heads, head_dim);
+    // A move from a shadow reads host memory, a page in one trip (the
+    // copies issue a batch of loads before their stores).
+    return from != tier && register_shape(page_tokens, kv_heads, head_dim);
   }
 
   bool launch_move_one(const OneMove &m, const PageSpaces &spaces, int page_tokens, int kv_heads,
@@ -472,9 +483,26 @@ namespace mi
       throw InvalidArgument("a move's launch holds at most " + std::to_string(kHeldRefs) +
                             " compaction copies; got " + std::to_string(m.compact_count));
     }
-    if (m.tier == kFP16 || !register_shape(page_tokens, kv_heads, head_dim))
+    if (!register_shape(page_tokens, kv_heads, head_dim))
     {
       return false;
+    }
+    if (m.tier == kFP16)
+    {
+      // A restore: the shadow's rows copied into the new page.
+      const PageLayout none{};
+      if (head_dim == 128)
+      {
+        hipLaunchKernelGGL((move_one_kernel<16, 128>), dim3(1), dim3(kThreads), 0, stream, m,
+                           spaces, none, kv_heads);
+      }
+      else
+      {
+        hipLaunchKernelGGL((move_one_kernel<16, 64>), dim3(1), dim3(kThreads), 0, stream, m,
+                           spaces, none, kv_heads);
+      }
+      hip_check(hipGetLastError(), "move kernel launch");
+      return true;
     }
     const PageLayout L = page_layout(m.tier, page_tokens, kv_heads, head_dim);
     with_bits(m.tier, [&](auto bits) {

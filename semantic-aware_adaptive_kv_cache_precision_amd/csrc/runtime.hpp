@@ -623,8 +623,8 @@ namespace mi
     // The tier moves of a batch: validated already, every page held.
     void run_moves(const std::vector<PageKey> &keys, const std::vector<int> &from,
                    const std::vector<int> &targets, double *shadow_seconds);
-    // One page's move from FP16 as one launch (launch_move_one), where its
-    // shape allows: false, and nothing changed, where it does not.
+    // One page's move as one launch (launch_move_one), where its shape
+    // allows: false, and nothing changed, where it does not.
     bool run_one_move(PageKey key, int from, int target, double *shadow_seconds);
     // Two timing events around a single move's copies, made on first use.
     void ensure_move_events();
