@@ -645,48 +645,95 @@ namespace mi
 
   void KVPages::move_pages(const std::vector<PageMove> &moves)
   {
+    const hipStream_t stream = runtime_stream();
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize before a batch");
+    const Clock::time_point began = Clock::now();
+    const std::size_t n = moves.size();
     std::vector<PageKey> keys;
     std::vector<int> from, targets;
-    std::vector<std::uint64_t> named;
-    keys.reserve(moves.size());
-    for (const PageMove &m : moves)
-    {
-      const PageKey key = require_held(m.key.layer, m.key.page, "move");
-      named.push_back(pack(key));
-      if (m.target < 0 || m.target >= kTierCount)
-      {
-        throw InvalidArgument("tier " + std::to_string(m.target) + " is not one of the four");
-      }
-      const int now = page_tier(key);
-      if (now == m.target)
-      {
-        throw InvalidArgument(page_name(key) + " is already at " + tier_name(now));
-      }
-      if (now != kFP16 && !shadows_.contains(key))
-      {
-        throw InvalidArgument(page_name(key) + " was born at " + tier_name(now) +
-                              " and has no FP16 shadow to move from; only a page sealed at FP16 "
-                              "moves");
-      }
-      require_page_size(m.target, "a page of positions");
-      keys.push_back(key);
-      from.push_back(now);
-      targets.push_back(m.target);
-    }
-    std::sort(named.begin(), named.end());
-    const auto dup = std::adjacent_find(named.begin(), named.end());
-    if (dup != named.end())
-    {
-      throw InvalidArgument(page_name(unpack(*dup)) +
-                            " is named twice in one batch; a batch moves a page once, to the "
-                            "tier it ends at");
-    }
-    hip_check(hipStreamSynchronize(runtime_stream()), "hipStreamSynchronize before a batch");
-    const Clock::time_point began = Clock::now();
+    keys.reserve(n);
+    from.reserve(n);
+    targets.reserve(n);
+    // A large batch's first downgrades: each page's shadow is numbered as
+    // the page is validated, and every kShadowPiece of them start over the
+    // host link at once, so that the link (the batch's bound) is busy while
+    // the host validates and plans the rest. A later refusal forgets the
+    // shadows (the copies into their places are harmless: the places are
+    // free again, and a later copy into one is ordered after them).
+    constexpr std::size_t kShadowPiece = 1024;
+    const bool early_shadows = n >= 256;
     const std::size_t shadows_before = shadows_.count();
-    if (!keys.empty())
+    if (early_shadows)
     {
-      run_moves(keys, from, targets, nullptr);
+      shadow_pairs_.reserve(n);
+    }
+    std::size_t staged = 0, sent = 0;
+    const auto send_shadows = [&]() {
+      PageSpaces spaces = allocator_.spaces();
+      spaces.shadows = shadows_.device_table(stream);
+      RefList l{};
+      l.pairs = shadow_pairs_.send(sent, staged - sent, stream);
+      launch_copy_refs(l, static_cast<int>(staged - sent), spaces, stream);
+      sent = staged;
+    };
+    // Pages named so far, one bit a (layer, page) position.
+    const std::size_t stride = static_cast<std::size_t>(pages_);
+    std::vector<std::uint64_t> named((static_cast<std::size_t>(layers_) * stride + 63) / 64, 0);
+    try
+    {
+      for (const PageMove &m : moves)
+      {
+        const PageKey key = require_held(m.key.layer, m.key.page, "move");
+        if (m.target < 0 || m.target >= kTierCount)
+        {
+          throw InvalidArgument("tier " + std::to_string(m.target) + " is not one of the four");
+        }
+        const std::size_t bit = static_cast<std::size_t>(key.layer) * stride + key.page;
+        if ((named[bit / 64] >> (bit % 64)) & 1u)
+        {
+          throw InvalidArgument(page_name(key) +
+                                " is named twice in one batch; a batch moves a page once, to the "
+                                "tier it ends at");
+        }
+        named[bit / 64] |= std::uint64_t{1} << (bit % 64);
+        const int now = page_tier(key);
+        if (now == m.target)
+        {
+          throw InvalidArgument(page_name(key) + " is already at " + tier_name(now));
+        }
+        if (now != kFP16 && !shadows_.contains(key))
+        {
+          throw InvalidArgument(page_name(key) + " was born at " + tier_name(now) +
+                                " and has no FP16 shadow to move from; only a page sealed at "
+                                "FP16 moves");
+        }
+        require_page_size(m.target, "a page of positions");
+        keys.push_back(key);
+        from.push_back(now);
+        targets.push_back(m.target);
+        if (early_shadows && now == kFP16 && !shadows_.contains(key))
+        {
+          shadow_pairs_.host()[staged++] = {allocator_.ref_of(key),
+                                            page_ref(kShadowSpace, shadows_.add(key))};
+          if (staged - sent == kShadowPiece)
+          {
+            send_shadows();
+          }
+        }
+      }
+      if (staged > sent)
+      {
+        send_shadows();
+      }
+      if (!keys.empty())
+      {
+        run_moves(keys, from, targets, nullptr);
+      }
+    }
+    catch (...)
+    {
+      shadows_.truncate(shadows_before);
+      throw;
     }
     last_batch_ = BatchRecord{keys.size(), shadows_.count() - shadows_before, since(began),
                               phases_[0], phases_[1], phases_[2]};

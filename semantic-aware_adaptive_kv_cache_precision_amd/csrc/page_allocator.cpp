@@ -126,6 +126,50 @@ namespace mi
     return buffer_->raw();
   }
 
+  StagedPairs::~StagedPairs()
+  {
+    if (host_ != nullptr)
+    {
+      (void)hipDeviceSynchronize(); // a queued copy may still read it
+      (void)hipHostFree(host_);
+    }
+  }
+
+  void StagedPairs::reserve(std::size_t count)
+  {
+    if (count <= capacity_)
+    {
+      return;
+    }
+    if (host_ != nullptr)
+    {
+      (void)hipDeviceSynchronize();
+      (void)hipHostFree(host_);
+      host_ = nullptr;
+    }
+    device_.reset();
+    capacity_ = 0;
+    const std::size_t room = std::max<std::size_t>(count, 4096);
+    void *host = nullptr;
+    hip_check(hipHostMalloc(&host, room * sizeof(RefPair), 0), "hipHostMalloc page pairs");
+    host_ = static_cast<RefPair *>(host);
+    device_ = std::make_unique<DeviceBuffer>(room * sizeof(RefPair));
+    capacity_ = room;
+  }
+
+  const RefPair *StagedPairs::send(std::size_t first, std::size_t count, hipStream_t stream)
+  {
+    if (first + count > capacity_)
+    {
+      throw LogicError("page pairs past the staged capacity");
+    }
+    RefPair *dst = device_->as<RefPair>() + first;
+    hip_check(hipMemcpyAsync(dst, host_ + first, count * sizeof(RefPair), hipMemcpyHostToDevice,
+                             stream),
+              "hipMemcpyAsync page pairs");
+    return dst;
+  }
+
   std::size_t granule_bytes()
   {
     int device = 0;

@@ -86,6 +86,29 @@ namespace mi
     std::unique_ptr<DeviceBuffer> buffer_;
   };
 
+  // Page pairs sent to the device in pieces while the launches of earlier
+  // pieces run: a pinned host area and a device area of one capacity, grown
+  // only while the stream is idle (a batch's start), each piece written at
+  // its own offset, so that no copy waits for the stream and none overwrites
+  // what a queued copy still reads.
+  class StagedPairs
+  {
+  public:
+    StagedPairs() = default;
+    StagedPairs(const StagedPairs &) = delete;
+    StagedPairs &operator=(const StagedPairs &) = delete;
+    ~StagedPairs();
+    void reserve(std::size_t count);
+    RefPair *host() const { return host_; }
+    // Pairs [first, first + count) of host() to the device; their device copy.
+    const RefPair *send(std::size_t first, std::size_t count, hipStream_t stream);
+
+  private:
+    RefPair *host_ = nullptr;
+    std::unique_ptr<DeviceBuffer> device_;
+    std::size_t capacity_ = 0;
+  };
+
   // A workspace of one owner's: a device buffer grown on demand. A buffer it
   // outgrows is kept until the owner goes, so that an address a captured
   // graph holds stays valid as long as the owner does.
@@ -670,6 +693,7 @@ namespace mi
     std::unique_ptr<DeviceBuffer> open_table_;
     std::vector<unsigned long long> open_uploaded_;
     UploadBuffer pairs_upload_;
+    StagedPairs shadow_pairs_; // a batch's first-downgrade shadows, sent as validated
     // FP16 pages brought from their shadows to device memory before they are
     // quantised (read once over the host link, then twice from HBM).
     std::unique_ptr<DeviceBuffer> staging_;
