@@ -18,8 +18,8 @@
 //     the runtime stream without waiting for it;
 //   - granules are mapped in runs (one physical allocation and one map call
 //     for up to kMaxRunGranules of them): the driver's unmap costs the same
-//     ~0.26 ms for a run of any length, so a range gives back a 704 MB tail
-//     in a dozen calls, not 352;
+//     ~0.2 ms for a run of any length, so a range gives back a 704 MB tail
+//     in six calls, not 352;
 //   - whole runs the tail gives up are unmapped by the releaser thread once
 //     an event recorded after the call's copies has completed, so no caller
 //     waits for the driver's unmap; a run the new tail cuts is replaced, on

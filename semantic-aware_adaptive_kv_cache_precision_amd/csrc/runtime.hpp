@@ -162,9 +162,11 @@ namespace mi
 
   class GranuleReleaser;
 
-  // The longest run of granules one physical allocation backs (32 MiB at
-  // 2 MiB granules): bounds the bytes a split copies.
-  constexpr std::size_t kMaxRunGranules = 16;
+  // The longest run of granules one physical allocation backs (128 MiB at
+  // 2 MiB granules): bounds the bytes a split copies, and sets how many
+  // unmap calls (~0.2 ms each, whatever a run's length) a shrinking range
+  // makes: a 704 MB tail is six.
+  constexpr std::size_t kMaxRunGranules = 64;
 
   // ADR-0007's allocator (reference: paged_kv_cache.h:88-227): one reserved
   // virtual range per tier, pages packed from slot 0 with no holes, physical
