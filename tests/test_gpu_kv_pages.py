@@ -508,6 +508,44 @@ def test_downgrade_upgrade_and_moves_are_quantise_of_the_shadow():
             assert cache.page_tier(layer, page) == tier
 
 
+def test_a_refused_large_batch_leaves_no_shadow_and_the_retry_is_exact():
+    """A batch of at least 256 moves takes its first downgrades' shadows in
+    pieces of 1,024 while it is validated: refused at its last move (a page
+    named twice) after a piece has gone out, it leaves no shadow, tier or
+    page byte changed; the same batch without that move then leaves every
+    page at quantise_page of its rows and every shadow at the page's FP16
+    bytes (the places the refused piece wrote are taken again)."""
+    m = mi()
+    P, kv, hd = 32, 2, 64
+    rng = np.random.default_rng(8)
+    pages = 560
+    k, v = normal(rng, P * pages, kv, hd), normal(rng, P * pages, kv, hd)
+    alloc, cache = pages_for(P, kv, hd, 0, always_seal=True)
+    for layer in range(LAYERS):
+        store_in_runs(cache, layer, k, v, [P * pages])
+    plan = [(layer, page, 1 + (layer * pages + page) % 3)
+            for layer in range(LAYERS) for page in range(pages - 1)]
+    assert len(plan) > 1024
+    before = [alloc.read(layer, page) for layer, page, _ in plan[:40]]
+    shadows = cache.shadow_count
+    announce("refused large batch", len(plan) + 1)
+    with pytest.raises(Exception, match="twice"):
+        cache.move_pages(plan + [plan[7]])
+    assert cache.shadow_count == shadows
+    assert (cache.page_tiers()[:, :pages] == 0).all()
+    for (layer, page, _), want in zip(plan[:40], before):
+        np.testing.assert_array_equal(alloc.read(layer, page), want)
+    announce("large batch", len(plan))
+    cache.move_pages(plan)
+    assert cache.last_batch["shadows_taken"] == len(plan)
+    for layer, page, tier in plan[::9] + plan[1020:1030] + plan[-3:]:
+        kp = k[page * P:(page + 1) * P].astype(np.float16)
+        vp = v[page * P:(page + 1) * P].astype(np.float16)
+        assert cache.page_tier(layer, page) == tier
+        np.testing.assert_array_equal(cache.shadow(layer, page), quant.fp16_page(kp, vp))
+        np.testing.assert_array_equal(alloc.read(layer, page), quant.quantise_page(kp, vp, tier, P))
+
+
 def plan_tier(plan, layer, page):
     return next(t for l, p, t in plan if l == layer and p == page)
 
