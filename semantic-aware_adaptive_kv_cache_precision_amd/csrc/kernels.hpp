@@ -76,7 +76,9 @@ namespace mi
   // kv_heads * head_dim >= 128 take the register quantiser (a lane a task of
   // 64 elements, nothing staged); any other shape the LDS one.
   // One page's move as one launch (one workgroup): the page's FP16 bytes to
-  // its shadow (shadow.from -> shadow.to) when has_shadow; the shadow's rows
+  // its shadow (shadow.from -> shadow_at, the new shadow's mapped address,
+  // so that the launch needs no upload of the shadow table) when has_shadow;
+  // the shadow's rows
   // into device staging (stage.from -> stage.to) when has_stage, then a
   // barrier; the page at its new tier (page.from, FP16 rows, -> page.to: the
   // register quantiser at `tier`, or a copy at FP16); then, after a barrier,
@@ -96,6 +98,7 @@ namespace mi
     int compact_count;
     RefPair stage;
     int has_stage;
+    unsigned long long shadow_at;
   };
   bool launch_move_one(const OneMove &m, const PageSpaces &spaces, int page_tokens, int kv_heads,
                        int head_dim, hipStream_t stream);

@@ -768,6 +768,7 @@ namespace mi
       {
         m.has_shadow = 1;
         m.shadow = {m.page.from, page_ref(kShadowSpace, shadows_.add(key))};
+        m.shadow_at = shadows_.device_address(m.shadow.to & kRefIndexMask);
       }
     }
     else
@@ -800,7 +801,11 @@ namespace mi
       throw;
     }
     PageSpaces spaces = allocator_.spaces();
-    spaces.shadows = shadows_.device_table(stream);
+    // The shadow table is brought up to date only for a move that reads a
+    // shadow (its upload from pageable memory costs a first downgrade, which
+    // writes its new shadow by address, a few microseconds); later launches
+    // that read shadows send what is pending first.
+    spaces.shadows = from != kFP16 ? shadows_.device_table(stream) : nullptr;
     spaces.staging = staging_ ? reinterpret_cast<unsigned long long>(staging_->raw()) : 0;
     // The page table names the new page and the old one goes; its tier's
     // compaction copies ride in the move's launch, after the reads of the

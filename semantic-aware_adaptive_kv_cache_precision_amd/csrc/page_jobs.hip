@@ -161,7 +161,8 @@ namespace mi
     {
       if (m.has_shadow)
       {
-        block_copy_page(resolve(s, m.shadow.to), resolve(s, m.shadow.from), s.shadow_bytes);
+        block_copy_page(reinterpret_cast<std::uint8_t *>(m.shadow_at), resolve(s, m.shadow.from),
+                        s.shadow_bytes);
       }
       if (m.has_stage)
       {

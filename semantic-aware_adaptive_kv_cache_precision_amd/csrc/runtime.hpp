@@ -335,6 +335,8 @@ namespace mi
     void truncate(std::size_t count);
     bool contains(PageKey key) const { return number_.count(pack(key)) != 0; }
     std::uint32_t number(PageKey key) const;
+    // Shadow `number`'s mapped address (what the device table holds for it).
+    unsigned long long device_address(std::uint32_t number) const { return device_[number]; }
     const std::uint8_t *shadow(PageKey key) const;
     std::size_t page_bytes() const { return page_bytes_; }
     std::size_t count() const { return host_.size(); }
