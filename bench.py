@@ -974,8 +974,9 @@ def blas_threads() -> int:
 
 
 def config1_pass_bytes(m, shape) -> int:
-    """BASELINE.md's configuration-1 pass, per tier: the 64 FP16 pages in
-    (1 MiB), the pages' codes and metadata out, q and out, the masses."""
+    """The configuration-1 pass (a 0.5B layer of 2048 positions, 64 pages),
+    per quantised tier: the 64 FP16 pages in (1 MiB), the pages' codes and
+    metadata out, q and out, the masses."""
     sizes = tier_sizes(m, shape)
     q_out = 2 * 2 * shape.heads * shape.head_dim
     mass = 4 * shape.heads * 64
