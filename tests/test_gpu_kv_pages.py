@@ -254,8 +254,9 @@ def test_the_row_attention_is_rope_store_then_attention_to_the_bit():
     combine) against rope_store then attention with partials on a twin
     cache: the output, the normed row, the turned rows and every page byte
     agree to the bit, at the 0.5B and 1.5B head shapes at position 0 (one
-    row to attend), mid-page, at a page's last row and a page's first, and
-    at a Llama shape long enough that the
+    row to attend), mid-page, at a page's last row and a page's first, at
+    the largest group (16 q heads a KV head), and at a Llama shape long
+    enough that the
     launch is bounded to the resident workgroups (the current page is then a
     wave's second). The two calls are held to the float64 references by the
     row launch and decode tests."""
@@ -263,6 +264,7 @@ def test_the_row_attention_is_rope_store_then_attention_to_the_bit():
     d = m.device
     for heads, kv, hd, hidden, seq, positions in ((14, 2, 64, 896, 160, (0, 100, 127, 128)),
                                                   (12, 2, 128, 1536, 96, (33, 63, 64)),
+                                                  (32, 2, 128, 2048, 96, (40,)),
                                                   (32, 8, 128, 4096, 16448, (16447,))):
         rng = np.random.default_rng(hd + kv)
         rope = d.RopeTable(hd, 1e6)
