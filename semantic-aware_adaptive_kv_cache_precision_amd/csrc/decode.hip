@@ -347,8 +347,15 @@ namespace mi
 
     // Scores (base-2 units) from the two 16-key accumulators, masked past
     // the last key; the page's max and sum over the lane group, its stats,
-    // and the running softmax merged; returns P (hi, lo) for P.V.
-    template <int HD>
+    // and the running softmax merged; returns P (hi, lo) for P.V. With
+    // kEveryPage every page, the first too, takes the merge with no branch
+    // (the stream kernel's walk, whose state starts each group at max -inf,
+    // sum 0, outputs 0): the rescale factor is exactly 1 wherever a head's
+    // maximum did not rise and 0 on a group's first page (exp2(-inf)), and
+    // the page's own factor exactly 1 there, so the bits are those of the
+    // branches, and the compiler keeps the accumulators in place instead of
+    // copying them around them.
+    template <int HD, bool kEveryPage = false>
     __device__ inline void softmax_page(const f32x4 (&acc)[2], const PageCtx &c, Running<HD> &run,
                                         half8 &p_hi, half8 &p_lo)
     {
@@ -395,7 +402,7 @@ namespace mi
         *reinterpret_cast<float2 *>(c.stat) = make_float2(m_page, l_page);
       }
       float f_page = 1.0f;
-      if (c.first)
+      if (!kEveryPage && c.first)
       {
         run.m = m_page;
         run.l = l_page;
@@ -408,7 +415,7 @@ namespace mi
         f_page = exp2_fast(m_page - m_new_from);
         run.l = run.l * f_old + l_page * f_page;
         // o needs rescaling only where this page raised a head's maximum.
-        if (__builtin_amdgcn_ballot_w64(m_page > run.m) != 0)
+        if (kEveryPage || __builtin_amdgcn_ballot_w64(m_page > run.m) != 0)
         {
 #pragma unroll
           for (int db = 0; db < HD / 16; ++db)
@@ -553,7 +560,7 @@ namespace mi
     // scores starting from `start`. `ks` and `kz` point at the KV head's key
     // scales and key zeros (HD halves each) in LDS, read 32 channels at a
     // time.
-    template <int HD, int Bits>
+    template <int HD, int Bits, bool kEveryPage = false>
     __device__ inline void quantised_compute(Running<HD> &run, const PageCtx &c, const half8 *qb,
                                              const QuantRaw<HD, Bits> &raw, const unsigned *ks,
                                              const unsigned *kz, const f32x4 (&start)[2])
@@ -588,7 +595,7 @@ namespace mi
         }
       }
       half8 p_hi, p_lo;
-      softmax_page<HD>(acc, c, run, p_hi, p_lo);
+      softmax_page<HD, kEveryPage>(acc, c, run, p_hi, p_lo);
       // Values: one scale and zero a row (token) of this KV head.
       u32x4 sv[2], zv[2];
 #pragma unroll
@@ -1692,8 +1699,8 @@ namespace mi
       *reinterpret_cast<u32x2 *>(meta + 8 * lane) = km;
       next();
       const f32x4 zero[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-      quantised_compute<HD, Bits>(run, c, qb, raw, reinterpret_cast<const unsigned *>(meta),
-                                  reinterpret_cast<const unsigned *>(meta + 256), zero);
+      quantised_compute<HD, Bits, true>(run, c, qb, raw, reinterpret_cast<const unsigned *>(meta),
+                                        reinterpret_cast<const unsigned *>(meta + 256), zero);
     }
 
     // Each range of (layer, KV-head block, page) units (at most 64 of them)
@@ -1877,7 +1884,7 @@ namespace mi
           f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
           fp16_scores<HD>(acc, k, qb);
           half8 p_hi, p_lo;
-          softmax_page<HD>(acc, c, run, p_hi, p_lo);
+          softmax_page<HD, true>(acc, c, run, p_hi, p_lo);
           fp16_values<HD>(run, c, v, p_hi, p_lo);
           first = false;
           break;
